@@ -1,0 +1,324 @@
+"""Pins the CPU oracle (oracle/gguf_oracle.py) before anything is checked against it.
+
+dequant   bit-exact against the reference's golden rows (fp32 gguf-py b11211 output on real
+          GGUF rows, tests/fixtures/dequant of the reference, copied to tests/golden/dequant).
+tables    against the reference header itself (oracle/_ref/ref_tables, built by oracle/Makefile
+          from ggml-common.h where it lies) when that is built, and against invariants always.
+q8_1      closed-form properties plus independent scalar restatements on small inputs; planted
+          mistakes (x*(1/d) rounding, sequential sum order, half-even rounding) must be told
+          apart from the real arithmetic.
+dots      brute-force int64 loops on tiny inputs; the dequant identity on real rows.
+"""
+
+import glob
+import json
+import os
+import subprocess
+
+import numpy as np
+import pytest
+from conftest import GOLDEN, ORACLE
+
+import gguf_oracle as o
+
+FILES = sorted(glob.glob(os.path.join(GOLDEN, "dequant", "*.npz")))
+IDS = [os.path.basename(f)[:-4] for f in FILES]
+TYPES = [o.IQ3_S, o.Q4_K, o.IQ4_XS, o.Q6_K]
+
+
+def _load(path):
+    z = np.load(path, allow_pickle=False)
+    return z["raw"], z["ref"], int(z["ggml_type"])
+
+
+def test_manifest_matches_files():
+    m = json.load(open(os.path.join(GOLDEN, "dequant", "manifest.json")))
+    assert {f["file"] for f in m["fixtures"]} == {os.path.basename(f) for f in FILES}
+    assert set(m["types"]) == {o.TYPE_NAMES[t] for t in TYPES}
+    assert len(FILES) == 36
+
+
+@pytest.mark.parametrize("path", FILES, ids=IDS)
+def test_dequant_bit_exact_vs_golden(path):
+    raw, ref, qt = _load(path)
+    y = o.dequantize(raw, qt)
+    np.testing.assert_array_equal(y.view(np.uint32), ref.view(np.uint32))
+
+
+def test_golden_rows_reach_every_iq3s_grid_entry():
+    """Every one of the 512 grid entries is used by the golden rows, so the bit-exact dequant
+    above pins the whole grid (a blocks' d is never 0 on these rows)."""
+    seen = set()
+    for f in FILES:
+        raw, _, qt = _load(f)
+        if qt != o.IQ3_S:
+            continue
+        b = raw.reshape(-1, 110).astype(np.int64)
+        assert (b[:, 0] | b[:, 1]).all()
+        g = np.arange(64)
+        seen |= set((b[:, 2:66] | (((b[:, 66:74][:, g // 8] >> (g % 8)) & 1) << 8)).ravel().tolist())
+    assert seen == set(range(512))
+
+
+def test_tables_invariants():
+    g = o.IQ3S_GRID
+    assert g.shape == (512, 4)
+    assert set(np.unique(g).tolist()) <= {1, 3, 5, 7, 9, 11, 13, 15}
+    u = o.IQ3S_GRID_U32.astype(np.int64)
+    assert (np.diff(u) > 0).all()                    # ascending, hence distinct
+    assert u[0] == 0x01010101 and u[-1] == 0x0F0F0101
+    kv = o.KVALUES_IQ4NL.astype(int)
+    assert (np.diff(kv) > 0).all() and kv[0] == -127 and kv[-1] == 113
+
+
+def _ref_tables():
+    exe = os.path.join(ORACLE, "_ref", "ref_tables")
+    if not os.path.exists(exe):
+        pytest.skip("oracle/_ref not built (needs the reference tree; `make -C oracle`)")
+    out = subprocess.run([exe], capture_output=True, text=True, check=True).stdout.split("\n")
+    grid = [int(l.split()[2]) for l in out if l.startswith("iq3s_grid")]
+    kv = [int(l.split()[2]) for l in out if l.startswith("kvalues_iq4nl")]
+    sizes = [l for l in out if l.startswith("sizeof")][0].split()
+    return grid, kv, dict(zip(sizes[1::2], map(int, sizes[2::2])))
+
+
+def test_tables_equal_reference_header():
+    grid, kv, sizes = _ref_tables()
+    assert o.IQ3S_GRID_U32.astype(np.int64).tolist() == grid
+    assert o.KVALUES_IQ4NL.astype(int).tolist() == kv
+    assert sizes == {"block_iq3_s": 110, "block_q4_K": 144, "block_q6_K": 210,
+                     "block_iq4_xs": 136, "block_q8_1": 36}
+    assert o.BLOCK_BYTES == {o.IQ3_S: 110, o.Q4_K: 144, o.Q6_K: 210, o.IQ4_XS: 136}
+
+
+# ------------------------------------------------------------------------------------ q8_1
+def _x(n, k, seed=0, dtype="float32"):
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(n, k, generator=g)
+    x[:, torch.randperm(k, generator=g)[: max(1, k // 256)]] *= 20
+    return x.to(getattr(torch, dtype))
+
+
+def _ties(n, k, seed):
+    """Tie-heavy float32 blocks: values at (j + 1/2) * amax/127, where x/d lands on or next to
+    a rounding tie (random inputs almost never do)."""
+    rng = np.random.default_rng(seed)
+    amax = np.exp2(rng.uniform(-4, 4, (n, k // 32))).astype(np.float32)
+    j = rng.integers(-126, 126, (n, k // 32, 32)).astype(np.float32)
+    x = ((j + np.float32(0.5)) * (amax / np.float32(127))[..., None]).astype(np.float32)
+    x[..., 0] = amax
+    return x.reshape(n, k)
+
+
+def _q8_scalar(xrow):
+    """Independent scalar restatement of one block_q8_1 (lcpp_shim.cu:274-294), float32 ops
+    through numpy scalars, the butterfly spelled out lane by lane."""
+    f = np.float32
+    x = [f(v) for v in xrow]
+    amax = f(0)
+    for v in x:
+        amax = max(amax, f(abs(v)))
+    lanes = list(x)
+    for off in (16, 8, 4, 2, 1):
+        lanes = [f(lanes[i] + lanes[i ^ off]) for i in range(32)]
+    d = f(amax / f(127))
+    q = []
+    for v in x:
+        if amax == 0:
+            q.append(0)
+            continue
+        t = f(v / d)
+        r = int(np.trunc(t))
+        if abs(float(t) - r) >= 0.5:
+            r += 1 if t > 0 else -1
+        q.append(r)
+    return d, lanes[0], q
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16", "float16"])
+def test_q8_1_matches_scalar_restatement(dtype):
+    x = _x(2, 512, seed=3, dtype=dtype)
+    q8 = o.quantize_q8_1(x)
+    q, d, s = o.dequant_q8_1(q8, 2, 512)
+    xf = x.float().numpy()
+    for r in range(2):
+        for b in range(16):
+            dd, ss, qq = _q8_scalar(xf[r, 32 * b:32 * b + 32])
+            assert d[r, b] == np.float32(np.float16(dd))
+            assert s[r, b] == np.float32(np.float16(ss))
+            assert q[r, 32 * b:32 * b + 32].tolist() == qq
+
+
+def test_q8_1_properties():
+    x = _x(4, 4096, seed=1).numpy()
+    x[1, :32] = 0                                    # an all-zero block
+    q8 = o.quantize_q8_1(x)
+    assert q8.size == 4 * 4096 // 32 * 36
+    q, d, s = o.dequant_q8_1(q8, 4, 4096)
+    assert (np.abs(q.astype(int)) <= 127).all()
+    assert d[1, 0] == 0 and s[1, 0] == 0 and (q[1, :32] == 0).all()
+    # d = half(amax/127): every block with amax > 0 reaches |q| = 127 at its amax element
+    b = np.abs(q.reshape(4, -1, 32).astype(int)).max(-1)
+    nz = np.abs(x.reshape(4, -1, 32)).max(-1) > 0
+    assert (b[nz] == 127).all()
+    # dequant within half a step (fp32 d, before the half rounding of the stored scale)
+    d32 = np.abs(x.reshape(4, -1, 32)).max(-1) / np.float32(127)
+    err = np.abs(q.reshape(4, -1, 32) * d32[..., None] - x.reshape(4, -1, 32))
+    assert (err <= d32[..., None] * 0.5000001 + 1e-30).all()
+
+
+def test_q8_1_planted_mistakes_are_visible():
+    """The tests above would notice each of these plausible mistakes on ordinary inputs."""
+    xr = _x(8, 4096, seed=2).numpy()
+    n, k = xr.shape
+    x = _ties(n, k, seed=11)
+    good = o.dequant_q8_1(o.quantize_q8_1(x), n, k)
+    b = x.reshape(n, -1, 32)
+    amax = np.abs(b).max(-1)
+    d = (amax / np.float32(127)).astype(np.float32)
+    # (1) x * (1/d) instead of x / d
+    q_mul = o._roundf((b * (np.float32(1) / d)[..., None]).astype(np.float32)).astype(np.int8)
+    # (2) half-to-even instead of roundf
+    q_even = np.rint((b / d[..., None]).astype(np.float32)).astype(np.int8)
+    # (3) sequential sum instead of the butterfly (random inputs)
+    br = xr.reshape(n, -1, 32)
+    seq = br[..., 0].copy()
+    for i in range(1, 32):
+        seq = (seq + br[..., i]).astype(np.float32)
+    good_r = o.dequant_q8_1(o.quantize_q8_1(xr), n, k)
+    diffs = [
+        (q_mul.reshape(n, k) != good[0]).any(),
+        (q_even.reshape(n, k) != good[0]).any(),
+        (seq.astype(np.float16) != good_r[2].astype(np.float16)).any(),
+    ]
+    assert all(diffs), diffs
+
+
+def test_q8_1_mmq_layout_and_rounding():
+    x = _x(3, 1024, seed=4).numpy()
+    x[2, 128:160] = 0
+    for qt in (o.IQ3_S, o.Q4_K):
+        q8 = o.quantize_q8_1_mmq(x, qt)
+        assert q8.size == 3 * 1024 // 128 * 144
+        q, d = o.dequant_q8_1_mmq(q8, 3, 1024, qt)
+        blk = q8.reshape(1024 // 128, 3, 144)
+        # block (k/128)*n + row holds row's values k..k+127
+        assert np.array_equal(blk[1, 2, 16:].view(np.int8), q[2, 128:256])
+        assert (q[2, 128:160] == 0).all() and d[2, 4] == 0
+        # scalar restatement: q = roundf(x * (127/amax)), d = 1/(127/amax)
+        for r, b in ((0, 0), (1, 17), (2, 31)):
+            xb = x[r, 32 * b:32 * b + 32].astype(np.float32)
+            dinv = np.float32(127) / np.float32(np.abs(xb).max())
+            qq = o._roundf((xb * dinv).astype(np.float32))
+            assert np.array_equal(q[r, 32 * b:32 * b + 32], qq.astype(np.int8))
+            dd = np.float32(1) / dinv
+            want = np.float32(np.float16(dd)) if qt == o.Q4_K else dd
+            assert d[r, b] == want
+    # the two layouts round differently somewhere (x/d vs x*(127/amax))
+    qa, _, _ = o.dequant_q8_1(o.quantize_q8_1(x), 3, 1024)
+    qb, _ = o.dequant_q8_1_mmq(o.quantize_q8_1_mmq(x, o.IQ3_S), 3, 1024, o.IQ3_S)
+    big = _ties(16, 4096, seed=9)
+    qa2, _, _ = o.dequant_q8_1(o.quantize_q8_1(big), 16, 4096)
+    qb2, _ = o.dequant_q8_1_mmq(o.quantize_q8_1_mmq(big, o.IQ3_S), 16, 4096, o.IQ3_S)
+    assert (qa2 != qb2).any() and np.abs(qa2.astype(int) - qb2.astype(int)).max() == 1
+
+
+# ------------------------------------------------------------------------------------ dots
+def _brute_dots(raw, qt, q):
+    """Pure-Python loops over a tiny case: decode every value from the block bytes directly
+    (struct-free bit arithmetic on Python ints), multiply by q8, sum per slice."""
+    rows = raw.shape[0]
+    n, k = q.shape
+    bs = o.BLOCK_BYTES[qt]
+    grid = [int(v) for v in o.IQ3S_GRID_U32]
+    kv = [int(v) for v in o.KVALUES_IQ4NL]
+    out = {}
+    for xr in range(n):
+        for wr in range(rows):
+            for s in range(k // 32):
+                blk = [int(v) for v in raw[wr, (s // 8) * bs:(s // 8 + 1) * bs]]
+                u = s % 8
+                acc, acc_m = 0, 0
+                for j in range(32):
+                    i = 32 * u + j
+                    qx = int(q[xr, 32 * s + j])
+                    if qt == o.IQ3_S:
+                        gidx = blk[2 + i // 4] | (((blk[66 + i // 32] >> ((i // 4) % 8)) & 1) << 8)
+                        gv = (grid[gidx] >> (8 * (i % 4))) & 0xFF
+                        sign = -1 if (blk[74 + i // 8] >> (i % 8)) & 1 else 1
+                        acc += sign * gv * qx
+                    elif qt == o.IQ4_XS:
+                        byte = blk[8 + 16 * u + (j % 16)]
+                        acc += kv[(byte >> (4 * (j // 16))) & 0xF] * qx
+                    elif qt == o.Q4_K:
+                        byte = blk[16 + 32 * (u // 2) + j]
+                        acc += ((byte >> (4 * (u % 2))) & 0xF) * qx
+                        acc_m += qx
+                    elif qt == o.Q6_K:
+                        h, v = i // 128, i % 128
+                        lo = (blk[64 * h + (v % 64)] >> (4 * (v // 64))) & 0xF
+                        hi = (blk[128 + 32 * h + (v % 32)] >> (2 * (v // 32))) & 3
+                        sc = blk[192 + i // 16]
+                        sc = sc - 256 if sc > 127 else sc
+                        acc += sc * ((lo | (hi << 4)) - 32) * qx
+                if qt == o.IQ3_S:
+                    ls = (blk[106 + u // 2] >> (4 * (u % 2))) & 0xF
+                    acc *= 1 + 2 * ls
+                elif qt == o.IQ4_XS:
+                    sh = blk[2] | (blk[3] << 8)
+                    ls = ((blk[4 + u // 2] >> (4 * (u % 2))) & 0xF) | (((sh >> (2 * u)) & 3) << 4)
+                    acc *= ls - 32
+                elif qt == o.Q4_K:
+                    sc12 = blk[4:16]
+                    if u < 4:
+                        scv, mv = sc12[u] & 63, sc12[u + 4] & 63
+                    else:
+                        scv = (sc12[u + 4] & 0xF) | ((sc12[u - 4] >> 6) << 4)
+                        mv = (sc12[u + 4] >> 4) | ((sc12[u] >> 6) << 4)
+                    acc *= scv
+                    acc_m *= mv
+                out[(xr, wr, s)] = (acc, acc_m)
+    return out
+
+
+@pytest.mark.parametrize("qt", TYPES, ids=lambda t: o.TYPE_NAMES[t])
+def test_slice_dots_brute_force(qt):
+    rng = np.random.default_rng(5)
+    raw = o.random_blocks(rng, qt, 3, 512)
+    q = rng.integers(-127, 128, size=(2, 512)).astype(np.int8)
+    dots = o.slice_dots(raw, qt, q)
+    brute = _brute_dots(raw, qt, q)
+    for (xr, wr, s), (a, m) in brute.items():
+        assert dots["dot"][xr, wr, s] == a
+        if qt == o.Q4_K:
+            assert dots["m"][xr, wr, s] == m
+
+
+@pytest.mark.parametrize("path", [f for f in FILES if "__r0" in f], ids=lambda p: os.path.basename(p)[:-4])
+def test_slice_dots_scale_identity_on_golden_rows(path):
+    """d_w * (integer slice dot) * d8 summed over slices == dequant(W) . (q * d8), both in
+    float64, to 1e-12 relative: the integer dots carry every sub-scale of the format."""
+    raw, ref, qt = _load(path)
+    k = ref.size
+    x = _x(2, k, seed=6).numpy()
+    q, d8, _ = o.dequant_q8_1(o.quantize_q8_1(x), 2, k)
+    dots = o.slice_dots(raw.reshape(1, -1), qt, q)
+    t = o.decode_int(raw, qt)
+    dw = np.repeat(t["d"].astype(np.float64), 8)
+    y = (dots["dot"][:, 0, :] * dw[None] * d8).sum(-1)
+    if qt == o.Q4_K:
+        y -= (dots["m"][:, 0, :] * np.repeat(t["dmin"].astype(np.float64), 8)[None] * d8).sum(-1)
+    want = (q.astype(np.float64).reshape(2, -1, 32) * d8[..., None]).reshape(2, k) @ ref.astype(np.float64)
+    np.testing.assert_allclose(y, want, rtol=1e-12, atol=1e-12 * np.abs(want).max())
+
+
+def test_q81_model_close_to_full_and_not_equal():
+    rng = np.random.default_rng(7)
+    raw = o.random_blocks(rng, o.IQ3_S, 64, 2048)
+    x = _x(4, 2048, seed=8)
+    y81 = o.q81_model(raw, o.IQ3_S, x)
+    yf = o.full_model(raw, o.IQ3_S, x)
+    e = o.rel_l2(y81, yf)
+    assert 1e-4 < e < 2e-2, e
