@@ -1,0 +1,63 @@
+"""The C-ABI library loads without a GPU and exports every symbol include/gguf_mi355x.h declares;
+its host-side helpers answer without touching the GPU."""
+
+import ctypes
+import os
+import re
+
+from conftest import ROOT
+
+from vllm_gguf_plugin import _capi
+
+HEADER = os.path.join(ROOT, "include", "gguf_mi355x.h")
+
+
+def _declared():
+    src = open(HEADER).read()
+    return sorted(set(re.findall(r"GGUF_API\s+[\w\s\*]+?\b(gguf_\w+)\s*\(", src)))
+
+
+def test_header_declares_the_op_surface():
+    names = _declared()
+    assert len(names) == 17
+    for op in _capi.OPS:
+        assert "gguf_" + op in names
+    assert "gguf_lcpp_quantize_q8_1" in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in _declared():
+        assert hasattr(lib, name), name
+        assert isinstance(getattr(lib, name), ctypes._CFuncPtr)
+    assert set(_declared()) == set(_capi.EXPORTS)
+
+
+def test_no_other_exports():
+    import subprocess
+
+    out = subprocess.run(["nm", "-D", "--defined-only", _capi.LIB_PATH], capture_output=True, text=True).stdout
+    exported = {l.split()[-1] for l in out.splitlines() if " T " in l}
+    assert exported == set(_declared())
+
+
+def test_host_helpers(lib):
+    assert lib.gguf_version().startswith(b"gguf_mi355x")
+    assert lib.gguf_q8_1_bytes(4, 5120, 0) == 4 * 5120 // 32 * 36
+    assert lib.gguf_q8_1_bytes(512, 5120, 1) == 2949120
+    # decode ops need the q8_1 copy of X unless x_q8 is given; GEMM ops always the MMQ copy
+    assert lib.gguf_op_workspace_bytes(0, 21, 17408, 5120, 4, 0) >= 4 * 5120 // 32 * 36
+    assert lib.gguf_op_workspace_bytes(0, 21, 17408, 5120, 4, 1) == 0
+    assert lib.gguf_op_workspace_bytes(1, 21, 17408, 5120, 48, 1) >= 48 * 5120 // 128 * 144
+    # whole 16-row tiles, at most 64 MiB (or the whole tensor if smaller)
+    assert lib.gguf_iq3_pack_scratch_bytes(17408, 2200) == 17408 * 2200
+    assert lib.gguf_iq3_pack_scratch_bytes(65536, 2200) == (64 << 20) // (16 * 2200) * 16 * 2200
+
+
+def test_guard_call_does_not_need_a_gpu(lib):
+    import torch
+
+    W = torch.zeros(32, 2200, dtype=torch.uint8)
+    X = torch.zeros(2, 5120, dtype=torch.bfloat16)
+    rc = lib.gguf_check_op(0, _capi.ref(_capi.view(W)), _capi.ref(_capi.view(X)), 21, 32, None)
+    assert rc == _capi.GGUF_EINVAL
+    assert _capi.error(lib).endswith("W and X must be CUDA tensors")

@@ -1,0 +1,331 @@
+"""Parity of the gfx950 kernels with the CPU oracle, through the C ABI (torch.ops._C_gguf ->
+libgguf_mi355x.so). Needs an MI355X.
+
+Bars:
+  * q8_1 bytes (both layouts): bit-exact with the oracle;
+  * int32 slice dots: bit-exact, checked through the real product kernels in an exact-integer
+    mode (block scales d = dmin = 1, X integer-valued with one 127 per slice so every q8_1 scale
+    is 1): every partial sum is then an integer below 2^24, so the fp32 output must equal the
+    oracle's int64 sum of slice dots exactly;
+  * fp32 outputs (fp32 X): within 1e-3 relative L2 (max over activation rows) of the q81 model
+    dequant(W) @ dequant(q8_1(X)) in float64; 16-bit X/Y: within the reference's tight bars
+    (5e-3 bf16, 2.5e-3 fp16, tests/gpu/test_kernel_parity.py:40) since Y is rounded to X's dtype;
+  * bit-identical outputs across hipGraph replays.
+"""
+
+import glob
+import os
+
+import numpy as np
+import pytest
+import torch
+from conftest import GOLDEN
+
+import _tile
+import gguf_oracle as o
+
+pytestmark = pytest.mark.gpu
+
+TYPES = [o.IQ3_S, o.Q4_K, o.IQ4_XS, o.Q6_K]
+TN = {t: o.TYPE_NAMES[t] for t in TYPES}
+VEC_OP = {o.IQ3_S: "lcpp_mul_mat_vec_iq3", o.Q4_K: "lcpp_mul_mat_vec_own", o.IQ4_XS: "lcpp_mul_mat_vec_q",
+          o.Q6_K: "lcpp_mul_mat_vec_q"}
+GEMM_OP = {o.IQ3_S: "lcpp_mul_mat_q", o.Q4_K: "lcpp_mul_mat_mma_k", o.IQ4_XS: "lcpp_mul_mat_mma_k",
+           o.Q6_K: "lcpp_mul_mat_q"}
+TIGHT = {torch.float32: 1e-3, torch.bfloat16: 5e-3, torch.float16: 2.5e-3}
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _ops():
+    assert torch.cuda.is_available(), "GPU tests need an MI355X"
+    from vllm_gguf_plugin import ops  # noqa: F401  registers torch.ops._C_gguf (fails if not built)
+
+    return torch.ops._C_gguf
+
+
+def C():
+    return torch.ops._C_gguf
+
+
+def _x(n, k, seed, dtype=torch.float32):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(n, k, generator=g)
+    x[:, torch.randperm(k, generator=g)[: max(1, k // 256)]] *= 20
+    return x.to(dtype)
+
+
+def _w(qt, rows, k, seed):
+    return o.random_blocks(np.random.default_rng(seed), qt, rows, k)
+
+
+def _dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _exact_weights(qt, rows, k, seed):
+    """Random codes with every block scale 1.0 (Q6_K sub-scales kept within +-31)."""
+    w = _w(qt, rows, k, seed)
+    b = w.reshape(-1, o.BLOCK_BYTES[qt])
+    one = np.array([0x00, 0x3C], dtype=np.uint8)  # fp16 1.0
+    if qt == o.Q6_K:
+        b[:, 208:210] = one
+        sc = np.random.default_rng(seed + 1).integers(-31, 32, size=(b.shape[0], 16)).astype(np.int8)
+        b[:, 192:208] = sc.view(np.uint8)
+    else:
+        b[:, 0:2] = one
+        if qt == o.Q4_K:
+            b[:, 2:4] = one
+    return w
+
+
+def _exact_x(n, k, seed, dtype=torch.bfloat16):
+    """Integers in [-2, 2] with one +-127 per 32-slice: every q8_1 scale is exactly 1."""
+    rng = np.random.default_rng(seed)
+    x = rng.integers(-2, 3, size=(n, k)).astype(np.float32)
+    pos = rng.integers(0, 32, size=(n, k // 32)) + 32 * np.arange(k // 32)
+    x[np.arange(n)[:, None], pos] = 127 * rng.choice([-1.0, 1.0], size=(n, k // 32))
+    return torch.from_numpy(x).to(dtype)
+
+
+def _exact_ref(raw, qt, x):
+    q, d, _ = o.dequant_q8_1(o.quantize_q8_1(x), x.shape[0], x.shape[1])
+    assert (d == 1).all()
+    dots = o.slice_dots(raw, qt, q)
+    y = dots["dot"].sum(-1)
+    if qt == o.Q4_K:
+        y = y - dots["m"].sum(-1)
+    assert np.abs(y).max() < 2 ** 24
+    return y
+
+
+# ------------------------------------------------------------------------------------ q8_1
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16], ids=str)
+@pytest.mark.parametrize("n,k", [(1, 512), (3, 5120), (8, 17408), (48, 5120)])
+def test_quantize_q8_1_bit_exact(dtype, n, k):
+    x = _x(n, k, seed=n + k, dtype=dtype)
+    x[0, 64:96] = 0                                   # an all-zero block
+    got = C().lcpp_quantize_q8_1(x.cuda(), o.IQ3_S, False, False).cpu().numpy()
+    np.testing.assert_array_equal(got, o.quantize_q8_1(x))
+
+
+@pytest.mark.parametrize("qt", [o.IQ3_S, o.Q4_K], ids=lambda t: TN[t])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=str)
+@pytest.mark.parametrize("n,k", [(1, 512), (9, 5120), (64, 2048)])
+def test_quantize_q8_1_mmq_bit_exact(qt, dtype, n, k):
+    x = _x(n, k, seed=3 * n + k, dtype=dtype)
+    x[-1, 128:160] = 0
+    got = C().lcpp_quantize_q8_1(x.cuda(), qt, True, False).cpu().numpy()
+    np.testing.assert_array_equal(got, o.quantize_q8_1_mmq(x, qt))
+
+
+def test_quantize_strided_rows():
+    x = _x(4, 1024 + 64, seed=5)[:, :1024]           # row stride > K
+    got = C().lcpp_quantize_q8_1(x.cuda(), o.IQ3_S, False, False).cpu().numpy()
+    np.testing.assert_array_equal(got, o.quantize_q8_1(x.contiguous()))
+
+
+# ------------------------------------------------------------------------------------ exact ints
+@pytest.mark.parametrize("qt", TYPES, ids=lambda t: TN[t])
+@pytest.mark.parametrize("n", [1, 2, 4, 5, 8])
+def test_gemv_exact_integer_dots(qt, n):
+    rows, k = 64, 512
+    raw = _exact_weights(qt, rows, k, seed=10 + n)
+    x = _exact_x(n, k, seed=20 + n)
+    y = getattr(C(), VEC_OP[qt])(_dev(raw), x.cuda(), qt, rows).float().cpu().numpy()
+    np.testing.assert_array_equal(y.astype(np.int64), _exact_ref(raw, qt, x))
+    assert (y == y.astype(np.int64)).all()
+
+
+@pytest.mark.parametrize("qt", TYPES, ids=lambda t: TN[t])
+@pytest.mark.parametrize("n", [9, 16, 33, 64])
+def test_gemm_exact_integer_dots(qt, n):
+    rows, k = 48, 512
+    raw = _exact_weights(qt, rows, k, seed=30 + n)
+    x = _exact_x(n, k, seed=40 + n, dtype=torch.float32)
+    op = GEMM_OP[qt] if n <= 64 else "lcpp_mul_mat_q"
+    y = getattr(C(), op)(_dev(raw), x.cuda(), qt, rows).cpu().numpy()
+    np.testing.assert_array_equal(y.astype(np.int64), _exact_ref(raw, qt, x))
+    assert (y == y.astype(np.int64)).all()
+
+
+def test_packed_exact_integer_dots():
+    from vllm_gguf_plugin.quantization import iq3_pack
+
+    rows, k = 64, 512
+    raw = _exact_weights(o.IQ3_S, rows, k, seed=50)
+    w = iq3_pack.pack(_dev(raw), o.IQ3_S)
+    for n, op in ((1, "lcpp_mul_mat_vec_iq3_mma_packed"), (8, "lcpp_mul_mat_vec_iq3_mma_packed"),
+                  (24, "lcpp_mul_mat_vec_iq3_mma_packed"), (40, "lcpp_mul_mat_iq3_packed")):
+        x = _exact_x(n, k, seed=60 + n, dtype=torch.float32)
+        y = getattr(C(), op)(w, x.cuda(), o.IQ3_S, rows).cpu().numpy()
+        np.testing.assert_array_equal(y.astype(np.int64), _exact_ref(raw, o.IQ3_S, x), err_msg=f"{op} n={n}")
+
+
+# ------------------------------------------------------------------------------------ q81 model
+@pytest.mark.parametrize("qt", TYPES, ids=lambda t: TN[t])
+@pytest.mark.parametrize("n", [1, 3, 4, 8])
+@pytest.mark.parametrize("rows,k", [(96, 2048), (100, 512)])
+def test_gemv_vs_q81(qt, n, rows, k):
+    raw = _w(qt, rows + 4, k, seed=n * 7 + rows)    # W has more rows than the product uses
+    x = _x(n, k, seed=n + 100)
+    y = getattr(C(), VEC_OP[qt])(_dev(raw), x.cuda(), qt, rows).cpu().numpy()
+    ref = o.q81_model(raw[:rows], qt, x)
+    assert o.rel_l2(y, ref) <= 1e-3, o.rel_l2(y, ref)
+    assert o.rel_l2(y, o.full_model(raw[:rows], qt, x)) <= 3e-2
+
+
+@pytest.mark.parametrize("qt", TYPES, ids=lambda t: TN[t])
+@pytest.mark.parametrize("n", [9, 17, 32, 48, 130])
+def test_gemm_vs_q81(qt, n):
+    rows, k = 80, 1024
+    raw = _w(qt, rows, k, seed=n * 11)
+    x = _x(n, k, seed=n + 200)
+    op = GEMM_OP[qt] if n <= 64 else "lcpp_mul_mat_q"
+    y = getattr(C(), op)(_dev(raw), x.cuda(), qt, rows).cpu().numpy()
+    ref = o.q81_model(raw, qt, x, layout="mmq")
+    assert o.rel_l2(y, ref) <= 1e-3, o.rel_l2(y, ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
+@pytest.mark.parametrize("qt", TYPES, ids=lambda t: TN[t])
+@pytest.mark.parametrize("n", [1, 4, 16])
+def test_16bit_x(qt, n, dtype):
+    rows, k = 64, 1024
+    raw = _w(qt, rows, k, seed=n * 13)
+    x = _x(n, k, seed=n + 300, dtype=dtype)
+    op = VEC_OP[qt] if n <= 8 else GEMM_OP[qt]
+    y = getattr(C(), op)(_dev(raw), x.cuda(), qt, rows)
+    assert y.dtype == dtype and y.shape == (n, rows)
+    ref = o.q81_model(raw, qt, x, layout="mmvq" if n <= 8 else "mmq")
+    assert o.rel_l2(y.float().cpu().numpy(), ref) <= TIGHT[dtype]
+
+
+def _golden(qt):
+    files = sorted(glob.glob(os.path.join(GOLDEN, "dequant", f"{TN[qt]}__*.npz")))
+    rows = {}
+    for f in files:
+        raw = np.load(f, allow_pickle=False)["raw"]
+        rows.setdefault(raw.size, []).append(raw)
+    return rows
+
+
+@pytest.mark.parametrize("qt", TYPES, ids=lambda t: TN[t])
+@pytest.mark.parametrize("n", [1, 4, 16, 48])
+def test_golden_rows(qt, n):
+    """Real GGUF rows of the reference's fixtures, 32 rows cycled per K."""
+    for same_k in _golden(qt).values():
+        raw = np.stack([same_k[i % len(same_k)] for i in range(32)])
+        k = raw.shape[1] // o.BLOCK_BYTES[qt] * 256
+        x = _x(n, k, seed=n + 400)
+        op = VEC_OP[qt] if n <= 8 else GEMM_OP[qt]
+        y = getattr(C(), op)(_dev(raw), x.cuda(), qt, 32).cpu().numpy()
+        ref = o.q81_model(raw, qt, x, layout="mmvq" if n <= 8 else "mmq")
+        assert o.rel_l2(y, ref) <= 1e-3, (k, o.rel_l2(y, ref))
+
+
+# ------------------------------------------------------------------------------------ packed
+def test_pack_is_the_tile_layout_and_roundtrips():
+    from vllm_gguf_plugin.quantization import iq3_pack
+
+    raw = _w(o.IQ3_S, 272, 1024, seed=70)
+    w = _dev(raw)
+    p = iq3_pack.pack(w, o.IQ3_S)
+    np.testing.assert_array_equal(p.cpu().numpy(), _tile.pack(raw))
+    np.testing.assert_array_equal(iq3_pack.unpack(p, o.IQ3_S).cpu().numpy(), raw)
+
+
+def test_pack_inplace_inside_padded_buffer():
+    from vllm_gguf_plugin.quantization import iq3_pack
+
+    raw = _w(o.IQ3_S, 48, 512, seed=71)
+    buf = torch.full((80, raw.shape[1] + 64), 7, dtype=torch.uint8, device="cuda")
+    run = buf[16:16 + 48].view(-1)[: raw.size].view(48, raw.shape[1])
+    run.copy_(_dev(raw))
+    before = buf.clone()
+    iq3_pack.pack_(run, o.IQ3_S)
+    np.testing.assert_array_equal(run.cpu().numpy(), _tile.pack(raw))
+    outside = torch.ones_like(buf, dtype=torch.bool)
+    outside.view(-1)[16 * buf.shape[1]:16 * buf.shape[1] + raw.size] = False
+    assert torch.equal(buf[outside], before[outside])
+
+
+@pytest.mark.parametrize("n", [1, 2, 4, 8, 12, 32, 33, 130])
+@pytest.mark.parametrize("k", [512, 5120])
+def test_packed_ops_vs_q81(n, k):
+    from vllm_gguf_plugin.quantization import iq3_pack
+
+    rows = 64
+    raw = _w(o.IQ3_S, rows, k, seed=n + k)
+    w = iq3_pack.pack(_dev(raw), o.IQ3_S)
+    x = _x(n, k, seed=n + 500)
+    op = "lcpp_mul_mat_vec_iq3_mma_packed" if n <= 32 else "lcpp_mul_mat_iq3_packed"
+    y = getattr(C(), op)(w, x.cuda(), o.IQ3_S, rows).cpu().numpy()
+    ref = o.q81_model(raw, o.IQ3_S, x, layout="mmvq" if n <= 8 else "mmq")
+    assert o.rel_l2(y, ref) <= 1e-3, o.rel_l2(y, ref)
+
+
+# ------------------------------------------------------------------------------------ x_q8, graphs
+@pytest.mark.parametrize("qt", TYPES, ids=lambda t: TN[t])
+def test_shared_x_q8_equals_own_quantize(qt):
+    rows, k, n = 64, 1024, 4
+    raw = _dev(_w(qt, rows, k, seed=80))
+    x = _x(n, k, seed=81, dtype=torch.bfloat16).cuda()
+    q8 = C().lcpp_quantize_q8_1(x, qt, False, False)
+    a = getattr(C(), VEC_OP[qt])(raw, x, qt, rows)
+    b = getattr(C(), VEC_OP[qt])(raw, x, qt, rows, q8)
+    assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("op,qt,n,packed", [
+    ("lcpp_mul_mat_vec_iq3_mma_packed", o.IQ3_S, 4, True),
+    ("lcpp_mul_mat_iq3_packed", o.IQ3_S, 32, True),
+    ("lcpp_mul_mat_vec_own", o.Q4_K, 4, False),
+    ("lcpp_mul_mat_mma_k", o.Q4_K, 16, False),
+    ("lcpp_mul_mat_q", o.Q6_K, 48, False),
+    ("lcpp_mul_mat_vec_q", o.IQ4_XS, 1, False),
+])
+def test_graph_replay_bit_exact(op, qt, n, packed):
+    from vllm_gguf_plugin.quantization import iq3_pack
+
+    rows, k = 256, 2048
+    w = _dev(_w(qt, rows, k, seed=90))
+    if packed:
+        w = iq3_pack.pack(w, qt)
+    fn = getattr(C(), op)
+    xs = [_x(n, k, seed=91 + i, dtype=torch.bfloat16).cuda() for i in range(3)]
+    eager = [fn(w, x, qt, rows).clone() for x in xs]
+    static_x = xs[0].clone()
+    fn(w, static_x, qt, rows)  # warm up outside the capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        y = fn(w, static_x, qt, rows)
+    for rep in range(2):
+        for i, x in enumerate(xs):
+            static_x.copy_(x)
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(y, eager[i]), (op, rep, i)
+
+
+# ------------------------------------------------------------------------------------ full sizes
+@pytest.mark.parametrize("n", [1, 4])
+def test_full_size_iq3s_gate_packed(n):
+    """BASELINE config 2 at its real shape (17408 x 5120), M = 1 and 4, through the packed path."""
+    from vllm_gguf_plugin.quantization import iq3_pack
+
+    rows, k = 17408, 5120
+    raw = _w(o.IQ3_S, rows, k, seed=2)
+    w = iq3_pack.pack(_dev(raw), o.IQ3_S)
+    x = _x(n, k, seed=3, dtype=torch.bfloat16)
+    y = C().lcpp_mul_mat_vec_iq3_mma_packed(w, x.cuda(), o.IQ3_S, rows).float().cpu().numpy()
+    assert o.rel_l2(y, o.q81_model(raw, o.IQ3_S, x)) <= TIGHT[torch.bfloat16]
+
+
+def test_full_size_q4k_cpu_config():
+    """Q4_K 4096 x 4096, X 1 x 4096 fp32 N(0,1), seed 0."""
+    rows = k = 4096
+    raw = _w(o.Q4_K, rows, k, seed=0)
+    x = torch.from_numpy(np.random.default_rng(0).standard_normal((1, k)).astype(np.float32))
+    y = C().lcpp_mul_mat_vec_q(_dev(raw), x.cuda(), o.Q4_K, rows).cpu().numpy()
+    assert o.rel_l2(y, o.q81_model(raw, o.Q4_K, x)) <= 1e-3

@@ -1,0 +1,309 @@
+// C ABI of libgguf_mi355x.so (declared in include/gguf_mi355x.h): guards, workspace sizing and
+// dispatch to the gfx950 kernels. Host code only; nothing here touches the GPU until every
+// guard has passed.
+//
+// The guards restate the reference's run() type checks (lcpp_shim.cu:767-791) and check_inputs
+// (lcpp_shim.cu:690-732) in the same order with the same message fragments, so callers (and the
+// CPU guard tests) see the same rejections. Types served by this build: Q4_K, Q6_K, IQ3_S,
+// IQ4_XS; the reference's other Route L types report "unsupported ggml type".
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/gguf_mi355x.h"
+#include "gguf_common.h"
+
+namespace gguf {
+hipError_t launch_quantize(const void* x, int dtype, int64_t n, int64_t k, int64_t s01, int type, bool mmq, void* y,
+                           hipStream_t stream);
+hipError_t launch_gemv_raw(int type, const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n,
+                           void* y, int y_dtype, hipStream_t stream);
+hipError_t launch_gemm(int type, const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n,
+                       void* y, int y_dtype, hipStream_t stream);
+hipError_t launch_gemv_packed(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n,
+                              void* y, int y_dtype, hipStream_t stream);
+hipError_t launch_gemm_packed(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n,
+                              void* y, int y_dtype, hipStream_t stream);
+hipError_t launch_iq3_pack(uint8_t* w, int64_t rows, int64_t row_bytes, bool unpack, uint8_t* scratch,
+                           size_t scratch_bytes, hipStream_t stream);
+size_t iq3_pack_scratch_bytes(int64_t rows, int64_t row_bytes);
+}  // namespace gguf
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return GGUF_EINVAL;
+}
+
+int hip_fail(hipError_t e, const char* op, const char* what) {
+  char buf[512];
+  snprintf(buf, sizeof(buf), "%s: HIP error in %s: %s", op, what, hipGetErrorString(e));
+  g_err = buf;
+  return GGUF_EHIP;
+}
+
+const char* op_name(int op) {
+  switch (op) {
+    case GGUF_OP_MUL_MAT_VEC_Q: return "lcpp_mul_mat_vec_q";
+    case GGUF_OP_MUL_MAT_Q: return "lcpp_mul_mat_q";
+    case GGUF_OP_MUL_MAT_VEC_IQ3: return "lcpp_mul_mat_vec_iq3";
+    case GGUF_OP_MUL_MAT_VEC_IQ3_MMA: return "lcpp_mul_mat_vec_iq3_mma";
+    case GGUF_OP_MUL_MAT_VEC_OWN: return "lcpp_mul_mat_vec_own";
+    case GGUF_OP_MUL_MAT_MMA_K: return "lcpp_mul_mat_mma_k";
+    case GGUF_OP_MUL_MAT_VEC_IQ3_MMA_PACKED: return "lcpp_mul_mat_vec_iq3_mma_packed";
+    case GGUF_OP_MUL_MAT_IQ3_PACKED: return "lcpp_mul_mat_iq3_packed";
+    default: return "gguf_mul_mat";
+  }
+}
+
+bool type_served(int64_t t) {
+  return t == gguf::kQ4_K || t == gguf::kQ6_K || t == gguf::kIQ3_S || t == gguf::kIQ4_XS;
+}
+
+// the reference's Route L type ids that the IQ3 / own / mma_k checks name
+constexpr int64_t kIQ3_XXS = 18, kIQ2_S = 22, kIQ1_M = 29;
+
+bool is_float(int32_t dt) { return dt == GGUF_DT_F32 || dt == GGUF_DT_F16 || dt == GGUF_DT_BF16; }
+
+int64_t elem_size(int32_t dt) { return dt == GGUF_DT_F32 ? 4 : dt == GGUF_DT_U8 ? 1 : 2; }
+
+bool op_packed(int op) { return op == GGUF_OP_MUL_MAT_VEC_IQ3_MMA_PACKED || op == GGUF_OP_MUL_MAT_IQ3_PACKED; }
+bool op_gemm(int op) {
+  return op == GGUF_OP_MUL_MAT_Q || op == GGUF_OP_MUL_MAT_MMA_K || op == GGUF_OP_MUL_MAT_IQ3_PACKED;
+}
+bool op_iq3(int op) {
+  return op == GGUF_OP_MUL_MAT_VEC_IQ3 || op == GGUF_OP_MUL_MAT_VEC_IQ3_MMA || op_packed(op);
+}
+// activation-row limits of the ops (lcpp_shim.cu:775-777; mma_k_max_cols = 64)
+int64_t op_max_rows(int op) {
+  if (op == GGUF_OP_MUL_MAT_Q || op == GGUF_OP_MUL_MAT_IQ3_PACKED) return 0;
+  if (op == GGUF_OP_MUL_MAT_MMA_K) return 64;
+  if (op == GGUF_OP_MUL_MAT_VEC_IQ3_MMA_PACKED) return 32;
+  return 8;
+}
+
+// check_inputs (lcpp_shim.cu:690-732). Returns K, or -1 with g_err set.
+int64_t check_inputs(const gguf_view* W, const gguf_view* X, int64_t type, int64_t row, int64_t max_rows,
+                     const char* op) {
+  if (!type_served(type)) return fail("%s: unsupported ggml type %lld", op, (long long)type), -1;
+  if (W->ndim != 2 || X->ndim != 2) return fail("%s: W and X must be 2-D", op), -1;
+  if (W->dtype != GGUF_DT_U8) return fail("%s: W must be uint8", op), -1;
+  if (!is_float(X->dtype)) return fail("%s: X must be fp32, fp16 or bf16", op), -1;
+  const int64_t ts = gguf::block_bytes((int)type);
+  const int64_t row_bytes = W->size[1];
+  if (!(row_bytes > 0 && row_bytes % ts == 0))
+    return fail("%s: W row bytes %lld not a multiple of the block size %lld", op, (long long)row_bytes,
+                (long long)ts), -1;
+  const int64_t k = row_bytes / ts * gguf::kQK;
+  if (k % 512 != 0)
+    return fail("%s: K=%lld must be a multiple of 512 (no weight tail padding)", op, (long long)k), -1;
+  if (!(k <= INT_MAX && W->size[0] <= INT_MAX)) return fail("%s: W too large", op), -1;
+  if (!(row > 0 && row <= W->size[0]))
+    return fail("%s: row=%lld out of range (W has %lld rows)", op, (long long)row, (long long)W->size[0]), -1;
+  if (W->stride[1] != 1) return fail("%s: W inner stride must be 1", op), -1;
+  if (!(W->size[0] == 1 || W->stride[0] == row_bytes))
+    return fail("%s: W rows must be contiguous (row stride %lld, row bytes %lld)", op, (long long)W->stride[0],
+                (long long)row_bytes), -1;
+  if (reinterpret_cast<uintptr_t>(W->data) % 16 != 0) return fail("%s: W data must be 16-byte aligned", op), -1;
+  if (X->size[1] != k)
+    return fail("%s: X has %lld columns, W rows hold K=%lld", op, (long long)X->size[1], (long long)k), -1;
+  if (!(X->stride[1] == 1 && (X->size[0] <= 1 || X->stride[0] >= k))) return fail("%s: X inner stride must be 1", op), -1;
+  if (max_rows > 0 && X->size[0] > max_rows)
+    return fail("%s: at most %lld rows, got %lld", op, (long long)max_rows, (long long)X->size[0]), -1;
+  if (X->size[0] > INT_MAX) return fail("%s: X too large", op), -1;
+  // device checks last, so host views exercise every guard above and are then rejected
+  if (W->device < 0 || X->device < 0) return fail("%s: W and X must be CUDA tensors", op), -1;
+  if (W->device != X->device) return fail("%s: W and X must be on the same device", op), -1;
+  return k;
+}
+
+// run()'s checks (lcpp_shim.cu:767-791) then check_inputs; returns K or -1.
+int64_t check_op(int op, const gguf_view* W, const gguf_view* X, int64_t type, int64_t row, const gguf_view* x_q8) {
+  if (op < 0 || op >= GGUF_OP_COUNT) return fail("gguf_mul_mat: unknown op %d", op), -1;
+  const char* name = op_name(op);
+  if (!W || !X) return fail("%s: W and X must be given", name), -1;
+  if (op_iq3(op) && !(type == gguf::kIQ3_S || type == kIQ3_XXS))
+    return fail("%s: IQ3_S or IQ3_XXS only, got type %lld", name, (long long)type), -1;
+  if (op == GGUF_OP_MUL_MAT_VEC_OWN && !(type == gguf::kQ4_K || type == kIQ2_S))
+    return fail("%s: Q4_K or IQ2_S only, got type %lld", name, (long long)type), -1;
+  if (op == GGUF_OP_MUL_MAT_MMA_K && !(type == gguf::kQ4_K || type == gguf::kIQ4_XS || type == kIQ2_S))
+    return fail("%s: Q4_K, IQ4_XS or IQ2_S only, got type %lld", name, (long long)type), -1;
+  if (op == GGUF_OP_MUL_MAT_Q && type == kIQ1_M) return fail("%s: no MMQ for IQ1_M", name), -1;
+  if (op_packed(op) && row % 16 != 0)
+    return fail("%s: row=%lld must be a multiple of 16 (packed 16-row tiles)", name, (long long)row), -1;
+  const int64_t k = check_inputs(W, X, type, row, op_max_rows(op), name);
+  if (k < 0) return -1;
+  if (x_q8) {
+    const int64_t q8_bytes = X->size[0] * k / gguf::kQ81 * 36;
+    if (!(x_q8->dtype == GGUF_DT_U8 && x_q8->ndim == 1 && x_q8->stride[0] == 1 && x_q8->size[0] >= q8_bytes))
+      return fail("%s: x_q8 must be contiguous uint8 with at least %lld bytes", name, (long long)q8_bytes), -1;
+    if (reinterpret_cast<uintptr_t>(x_q8->data) % 16 != 0) return fail("%s: x_q8 must be 16-byte aligned", name), -1;
+    if (!(x_q8->device >= 0 && x_q8->device == X->device)) return fail("%s: x_q8 must be on X's device", name), -1;
+  }
+  return k;
+}
+
+size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+// Makes `device` current for the call when it is not already (the reference's DeviceGuard,
+// lcpp_shim.cu:796), restoring the caller's device after; no device call when nothing changes,
+// so a call inside stream capture makes no device switch.
+struct DeviceScope {
+  int prev = -1;
+  hipError_t err = hipSuccess;
+  explicit DeviceScope(int device) {
+    int cur = -1;
+    err = hipGetDevice(&cur);
+    if (err == hipSuccess && cur != device) {
+      err = hipSetDevice(device);
+      if (err == hipSuccess) prev = cur;
+    }
+  }
+  ~DeviceScope() {
+    if (prev >= 0) (void)hipSetDevice(prev);
+  }
+};
+
+}  // namespace
+
+extern "C" {
+
+const char* gguf_last_error(void) { return g_err.c_str(); }
+
+const char* gguf_version(void) { return "gguf_mi355x 0.1 (gfx950)"; }
+
+int gguf_check_op(int op, const gguf_view* W, const gguf_view* X, int64_t type, int64_t row, const gguf_view* x_q8) {
+  g_err.clear();
+  return check_op(op, W, X, type, row, x_q8) < 0 ? GGUF_EINVAL : GGUF_OK;
+}
+
+size_t gguf_q8_1_bytes(int64_t n, int64_t k, int mmq) {
+  return mmq ? (size_t)(n * k / 128 * 144) : (size_t)(n * k / gguf::kQ81 * 36);
+}
+
+size_t gguf_op_workspace_bytes(int op, int64_t type, int64_t row, int64_t k, int64_t n, int has_x_q8) {
+  (void)type;
+  (void)row;
+  if (n <= 0) return 0;
+  if (op_gemm(op)) return align256(gguf_q8_1_bytes(n, k, 1));
+  if (op == GGUF_OP_MUL_MAT_VEC_IQ3_MMA_PACKED && n > 8) return align256(gguf_q8_1_bytes(n, k, 1));
+  return has_x_q8 ? 0 : align256(gguf_q8_1_bytes(n, k, 0));
+}
+
+int gguf_mul_mat(int op, const gguf_view* W, const gguf_view* X, int64_t type, int64_t row, const gguf_view* x_q8,
+                 void* y, size_t y_bytes, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err.clear();
+  const int64_t k = check_op(op, W, X, type, row, x_q8);
+  if (k < 0) return GGUF_EINVAL;
+  const char* name = op_name(op);
+  const int64_t n = X->size[0];
+  if (n == 0) return GGUF_OK;
+  if (type == kIQ3_XXS) return fail("%s: unsupported ggml type %lld", name, (long long)type);
+  if (y_bytes < (size_t)(n * row * elem_size(X->dtype))) return fail("%s: output buffer too small", name);
+  const bool packed = op_packed(op);
+  const bool gemm = op_gemm(op) || (op == GGUF_OP_MUL_MAT_VEC_IQ3_MMA_PACKED && n > 8);
+  const size_t need = gguf_op_workspace_bytes(op, type, row, k, n, x_q8 != nullptr && !gemm);
+  if (workspace_bytes < need || (need > 0 && !workspace))
+    return fail("%s: workspace of %zu bytes needed, got %zu", name, need, workspace_bytes);
+  if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0) return fail("%s: workspace must be 16-byte aligned", name);
+
+  hipStream_t s = (hipStream_t)stream;
+  const DeviceScope scope(X->device);
+  if (scope.err != hipSuccess) return hip_fail(scope.err, name, "device select");
+  hipError_t e;
+  const int64_t s01 = n == 1 ? k : X->stride[0];
+  const uint8_t* w = (const uint8_t*)W->data;
+  const int64_t row_bytes = W->size[1];
+  const int ydt = X->dtype;
+
+  if (gemm) {
+    e = gguf::launch_quantize(X->data, X->dtype, n, k, s01, (int)type, true, workspace, s);
+    if (e != hipSuccess) return hip_fail(e, name, "quantize");
+    e = packed ? gguf::launch_gemm_packed(w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace, (int)n, y, ydt, s)
+               : gguf::launch_gemm((int)type, w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace, (int)n, y,
+                                   ydt, s);
+    if (e != hipSuccess) return hip_fail(e, name, "gemm");
+    return GGUF_OK;
+  }
+  const uint8_t* q8 = (const uint8_t*)workspace;
+  if (x_q8) {
+    q8 = (const uint8_t*)x_q8->data;
+  } else {
+    e = gguf::launch_quantize(X->data, X->dtype, n, k, s01, (int)type, false, workspace, s);
+    if (e != hipSuccess) return hip_fail(e, name, "quantize");
+  }
+  e = packed ? gguf::launch_gemv_packed(w, row_bytes, (int)row, (int)k, q8, (int)n, y, ydt, s)
+             : gguf::launch_gemv_raw((int)type, w, row_bytes, (int)row, (int)k, q8, (int)n, y, ydt, s);
+  if (e != hipSuccess) return hip_fail(e, name, "gemv");
+  return GGUF_OK;
+}
+
+#define GGUF_OP_Q8(fn, OP)                                                                                    \
+  int fn(const gguf_view* W, const gguf_view* X, int64_t type, int64_t row, const gguf_view* x_q8, void* y,   \
+         size_t y_bytes, void* ws, size_t ws_bytes, void* stream) {                                           \
+    return gguf_mul_mat(OP, W, X, type, row, x_q8, y, y_bytes, ws, ws_bytes, stream);                         \
+  }
+#define GGUF_OP_OWN(fn, OP)                                                                                  \
+  int fn(const gguf_view* W, const gguf_view* X, int64_t type, int64_t row, void* y, size_t y_bytes, void* ws, \
+         size_t ws_bytes, void* stream) {                                                                     \
+    return gguf_mul_mat(OP, W, X, type, row, nullptr, y, y_bytes, ws, ws_bytes, stream);                      \
+  }
+GGUF_OP_Q8(gguf_lcpp_mul_mat_vec_q, GGUF_OP_MUL_MAT_VEC_Q)
+GGUF_OP_OWN(gguf_lcpp_mul_mat_q, GGUF_OP_MUL_MAT_Q)
+GGUF_OP_Q8(gguf_lcpp_mul_mat_vec_iq3, GGUF_OP_MUL_MAT_VEC_IQ3)
+GGUF_OP_Q8(gguf_lcpp_mul_mat_vec_iq3_mma, GGUF_OP_MUL_MAT_VEC_IQ3_MMA)
+GGUF_OP_Q8(gguf_lcpp_mul_mat_vec_own, GGUF_OP_MUL_MAT_VEC_OWN)
+GGUF_OP_OWN(gguf_lcpp_mul_mat_mma_k, GGUF_OP_MUL_MAT_MMA_K)
+GGUF_OP_Q8(gguf_lcpp_mul_mat_vec_iq3_mma_packed, GGUF_OP_MUL_MAT_VEC_IQ3_MMA_PACKED)
+GGUF_OP_OWN(gguf_lcpp_mul_mat_iq3_packed, GGUF_OP_MUL_MAT_IQ3_PACKED)
+#undef GGUF_OP_Q8
+#undef GGUF_OP_OWN
+
+int gguf_lcpp_quantize_q8_1(const gguf_view* X, int64_t type, int mmq, int vendored, void* out, size_t out_bytes,
+                            void* stream) {
+  g_err.clear();
+  // lcpp_shim.cu:950-955: one combined guard
+  if (!(X && type_served(type) && X->device >= 0 && X->ndim == 2 && X->stride[1] == 1 && X->size[1] % 512 == 0 &&
+        is_float(X->dtype)))
+    return fail("lcpp_quantize_q8_1: bad arguments");
+  if (vendored) return fail("lcpp_quantize_q8_1: no vendored quantizer in this build (vendored must be false)");
+  const int64_t n = X->size[0], k = X->size[1];
+  if (out_bytes < gguf_q8_1_bytes(n, k, mmq)) return fail("lcpp_quantize_q8_1: output buffer too small");
+  if (n == 0) return GGUF_OK;
+  const DeviceScope scope(X->device);
+  if (scope.err != hipSuccess) return hip_fail(scope.err, "lcpp_quantize_q8_1", "device select");
+  hipError_t e;
+  const int64_t s01 = n == 1 ? k : X->stride[0];
+  e = gguf::launch_quantize(X->data, X->dtype, n, k, s01, (int)type, mmq != 0, out, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "lcpp_quantize_q8_1", "quantize");
+  return GGUF_OK;
+}
+
+size_t gguf_iq3_pack_scratch_bytes(int64_t rows, int64_t row_bytes) { return gguf::iq3_pack_scratch_bytes(rows, row_bytes); }
+
+int gguf_iq3_pack(void* w, int64_t rows, int64_t row_bytes, int unpack, void* scratch, size_t scratch_bytes,
+                  void* stream) {
+  g_err.clear();
+  if (!w || rows <= 0 || rows % 16 != 0 || row_bytes <= 0 || row_bytes % 110 != 0)
+    return fail("gguf_iq3_pack: rows must be a positive multiple of 16 and row bytes whole IQ3_S blocks");
+  if (reinterpret_cast<uintptr_t>(w) % 16 != 0) return fail("gguf_iq3_pack: W data must be 16-byte aligned");
+  if (scratch_bytes < gguf::iq3_pack_scratch_bytes(rows, row_bytes) || !scratch)
+    return fail("gguf_iq3_pack: scratch of %zu bytes needed", gguf::iq3_pack_scratch_bytes(rows, row_bytes));
+  const hipError_t e = gguf::launch_iq3_pack((uint8_t*)w, rows, row_bytes, unpack != 0, (uint8_t*)scratch,
+                                             scratch_bytes, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "gguf_iq3_pack", "pack");
+  return GGUF_OK;
+}
+
+}  // extern "C"

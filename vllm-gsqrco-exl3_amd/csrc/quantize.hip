@@ -1,0 +1,125 @@
+// q8_1 activation quantisation on gfx950.
+//
+// Two output layouts, both bit-exact with the reference's arithmetic:
+//  * block_q8_1 (decode GEMV input), lcpp_shim.cu:274-294: per 32 values d = amax/127 (IEEE
+//    division), q = amax == 0 ? 0 : roundf(x/d), sum by a 32-lane xor butterfly with offsets
+//    16, 8, 4, 2, 1, stored as half2(d, sum) followed by 32 int8; block (row, k/32) row-major.
+//  * block_q8_1_mmq (GEMM input), lcpp_shim.cu:298-355: per 32 values d_inv = 127/amax,
+//    q = roundf(x*d_inv), d = 1/d_inv; 144-byte blocks of 128 values, block index
+//    (k/128)*n + row, 16 bytes of scales (4 x fp32 d, or 4 x half2(d, sum) for Q4_K) then 128
+//    int8. An all-zero 32-block stores q = 0, d = 0 (the reference's NaN -> 0 conversion).
+//
+// Wave64 mapping: the MMVQ kernel gives each 32-lane half-wave one block (one value per lane);
+// the MMQ kernel gives each lane 4 consecutive values, 8 lanes per 32-block.
+#include "gguf_common.h"
+
+namespace gguf {
+
+template <int DT>
+__device__ __forceinline__ float ldx(const void* x, int64_t i) {
+  if constexpr (DT == kF32) {
+    return ((const float*)x)[i];
+  } else if constexpr (DT == kF16) {
+    return half_bits_to_float(((const uint16_t*)x)[i]);
+  } else {
+    return __uint_as_float((uint32_t)((const uint16_t*)x)[i] << 16);
+  }
+}
+
+template <int DT>
+__global__ void __launch_bounds__(256) quantize_q8_1_kernel(const void* __restrict__ x, uint8_t* __restrict__ y,
+                                                            int64_t k, int64_t s01) {
+  const int64_t i0 = (int64_t)blockIdx.x * 256 + threadIdx.x;  // column
+  const int64_t row = blockIdx.y;
+  if (i0 >= k) return;  // k % 512 == 0: whole 32-lane groups exit together
+  const float xi = ldx<DT>(x, row * s01 + i0);
+  float amax = fabsf(xi);
+  float sum = xi;
+#pragma unroll
+  for (int off = 16; off > 0; off >>= 1) {
+    amax = fmaxf(amax, __shfl_xor(amax, off, 32));
+    sum += __shfl_xor(sum, off, 32);
+  }
+  const float d = amax / 127.0f;
+  const int q = amax == 0.0f ? 0 : (int)roundf(xi / d);
+  const int64_t blk = (row * k + i0) / kQ81;
+  const int iqs = (int)(i0 % kQ81);
+  uint8_t* b = y + blk * 36;
+  b[4 + iqs] = (uint8_t)(int8_t)q;
+  if (iqs == 0) {
+    const uint32_t dh = __half_as_ushort(__float2half_rn(d));
+    const uint32_t sh = __half_as_ushort(__float2half_rn(sum));
+    *(uint32_t*)b = dh | (sh << 16);
+  }
+}
+
+template <int DT, bool DS4>
+__global__ void __launch_bounds__(128) quantize_q8_1_mmq_kernel(const void* __restrict__ x, uint8_t* __restrict__ y,
+                                                                int64_t k, int64_t s01, int n) {
+  const int64_t row = blockIdx.x;
+  const int64_t i0 = ((int64_t)blockIdx.y * 128 + threadIdx.x) * 4;
+  if (i0 >= k) return;  // k % 512 == 0: whole blocks exit together
+  const int64_t base = row * s01 + i0;
+  const float x0 = ldx<DT>(x, base), x1 = ldx<DT>(x, base + 1), x2 = ldx<DT>(x, base + 2),
+              x3 = ldx<DT>(x, base + 3);
+  float amax = fmaxf(fmaxf(fmaxf(fabsf(x0), fabsf(x1)), fabsf(x2)), fabsf(x3));
+  float sum = ((x0 + x1) + x2) + x3;
+#pragma unroll
+  for (int off = 4; off > 0; off >>= 1) {
+    amax = fmaxf(amax, __shfl_xor(amax, off, 8));
+    if constexpr (DS4) sum += __shfl_xor(sum, off, 8);
+  }
+  int q0 = 0, q1 = 0, q2 = 0, q3 = 0;
+  float d = 0.0f;
+  if (amax != 0.0f) {
+    const float d_inv = 127.0f / amax;
+    q0 = (int)roundf(x0 * d_inv);
+    q1 = (int)roundf(x1 * d_inv);
+    q2 = (int)roundf(x2 * d_inv);
+    q3 = (int)roundf(x3 * d_inv);
+    d = 1.0f / d_inv;
+  }
+  const int64_t ib = (i0 / 128) * n + row;
+  const int iqs = (int)(i0 % 128);
+  uint8_t* b = y + ib * 144;
+  *(uint32_t*)(b + 16 + iqs) = (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) |
+                               ((uint32_t)(q2 & 0xFF) << 16) | ((uint32_t)(q3 & 0xFF) << 24);
+  if (iqs % 32 == 0) {
+    if constexpr (DS4) {
+      const uint32_t dh = __half_as_ushort(__float2half_rn(d));
+      const uint32_t sh = __half_as_ushort(__float2half_rn(sum));
+      *(uint32_t*)(b + 4 * (iqs / 32)) = dh | (sh << 16);
+    } else {
+      *(float*)(b + 4 * (iqs / 32)) = d;
+    }
+  }
+}
+
+// X [n, k] (row stride s01 elements, dtype DT) -> q8 bytes at y.
+hipError_t launch_quantize(const void* x, int dtype, int64_t n, int64_t k, int64_t s01, int type, bool mmq,
+                           void* y, hipStream_t stream) {
+  if (n == 0) return hipSuccess;
+  if (!mmq) {
+    const dim3 grid((unsigned)((k + 255) / 256), (unsigned)n);
+    switch (dtype) {
+      case kF32: quantize_q8_1_kernel<kF32><<<grid, 256, 0, stream>>>(x, (uint8_t*)y, k, s01); break;
+      case kF16: quantize_q8_1_kernel<kF16><<<grid, 256, 0, stream>>>(x, (uint8_t*)y, k, s01); break;
+      default: quantize_q8_1_kernel<kBF16><<<grid, 256, 0, stream>>>(x, (uint8_t*)y, k, s01); break;
+    }
+    return hipGetLastError();
+  }
+  const dim3 grid((unsigned)n, (unsigned)((k + 511) / 512));
+  const bool ds4 = type == kQ4_K;
+#define GGUF_QMMQ(DT)                                                                                     \
+  if (ds4) quantize_q8_1_mmq_kernel<DT, true><<<grid, 128, 0, stream>>>(x, (uint8_t*)y, k, s01, (int)n); \
+  else quantize_q8_1_mmq_kernel<DT, false><<<grid, 128, 0, stream>>>(x, (uint8_t*)y, k, s01, (int)n);
+  switch (dtype) {
+    case kF32: GGUF_QMMQ(kF32) break;
+    case kF16: GGUF_QMMQ(kF16) break;
+    default: GGUF_QMMQ(kBF16) break;
+  }
+#undef GGUF_QMMQ
+  return hipGetLastError();
+}
+
+}  // namespace gguf
