@@ -130,10 +130,21 @@ def test_quantize_strided_rows():
 def test_gemv_exact_integer_dots(qt, n):
     rows, k = 64, 512
     raw = _exact_weights(qt, rows, k, seed=10 + n)
-    x = _exact_x(n, k, seed=20 + n)
-    y = getattr(C(), VEC_OP[qt])(_dev(raw), x.cuda(), qt, rows).float().cpu().numpy()
+    x = _exact_x(n, k, seed=20 + n, dtype=torch.float32)
+    y = getattr(C(), VEC_OP[qt])(_dev(raw), x.cuda(), qt, rows).cpu().numpy()
     np.testing.assert_array_equal(y.astype(np.int64), _exact_ref(raw, qt, x))
     assert (y == y.astype(np.int64)).all()
+
+
+@pytest.mark.parametrize("qt", TYPES, ids=lambda t: TN[t])
+def test_gemv_exact_integer_bf16_output_is_rounded_exact(qt):
+    """bf16 X: the fp32 result is the exact integer, stored with round-to-nearest-even."""
+    rows, k, n = 64, 512, 3
+    raw = _exact_weights(qt, rows, k, seed=15)
+    x = _exact_x(n, k, seed=25)
+    y = getattr(C(), VEC_OP[qt])(_dev(raw), x.cuda(), qt, rows).cpu()
+    want = torch.from_numpy(_exact_ref(raw, qt, x).astype(np.float32)).to(torch.bfloat16)
+    assert torch.equal(y.view(torch.int16), want.view(torch.int16))
 
 
 @pytest.mark.parametrize("qt", TYPES, ids=lambda t: TN[t])

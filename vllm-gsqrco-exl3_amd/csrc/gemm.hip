@@ -19,6 +19,8 @@ namespace gguf {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
+__device__ const Iq3sSignedTable kIq3sSignedGemm = make_iq3s_signed_table();
+
 __device__ __forceinline__ v4i mfma16x16x32(long a, long b) {
   const v4i z = {0, 0, 0, 0};
   return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, z, 0, 0, 0);
@@ -28,9 +30,13 @@ template <int TYPE, int NT, bool TILE>
 __global__ void __launch_bounds__(256) gemm_mfma_kernel(const uint8_t* __restrict__ W, int64_t row_bytes, int nrows,
                                                         int k, const uint8_t* __restrict__ q8, int n,
                                                         void* __restrict__ y, int y_dtype) {
-  __shared__ uint32_t grid[TYPE == kIQ3_S ? 512 : 1];
+  __shared__ uint32_t grid[TYPE == kIQ3_S ? (TILE ? 8192 : 512) : 1];
   __shared__ float part[3][NT][4][64];
-  if constexpr (TYPE == kIQ3_S) {
+  if constexpr (TILE) {
+    const uint4* src = (const uint4*)kIq3sSignedGemm.v;
+    for (int i = threadIdx.x; i < 2048; i += blockDim.x) ((uint4*)grid)[i] = src[i];
+    __syncthreads();
+  } else if constexpr (TYPE == kIQ3_S) {
     for (int i = threadIdx.x; i < 512; i += blockDim.x) grid[i] = kIq3sGrid.v[i];
     __syncthreads();
   }

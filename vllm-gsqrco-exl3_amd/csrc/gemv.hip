@@ -152,26 +152,141 @@ hipError_t launch_gemv_raw(int type, const uint8_t* W, int64_t row_bytes, int nr
 
 
 // ---------------------------------------------------------------------------------------------
-// IQ3_S in the tile layout (iq3_tile.h): a workgroup owns one 16-row tile, its 4 waves split the
-// K blocks, and lane L = 8p + s of a wave decodes slice s of rows 2p, 2p+1 of each block it
-// visits, from one 16-byte, one 8-byte and three small loads, all contiguous across the wave.
-// The q8_1 block of X for the slice is loaded once per lane and used for both rows. Partial sums
-// are added over the 8 slice lanes (xor butterfly) and then over the 4 waves in wave order.
+// IQ3_S in the tile layout (iq3_tile.h). A workgroup owns one 16-row tile; its WPT waves split the
+// K blocks. Lane L = 8p + s decodes slice s of rows 2p, 2p+1 of each block it visits from one
+// 16-byte, one 8-byte and three small loads (contiguous across the wave), turning each 4-value
+// group into an index of the 32 KB signed-grid table in LDS with a byte permute: one LDS read per
+// group yields four signed int8 values. The next block's weight and q8_1 loads are issued before
+// the current block is computed. The q8_1 block of X for the slice serves both rows. Partial sums
+// are added over the 8 slice lanes (xor butterfly), then over the waves in wave order.
+
+__device__ const Iq3sSignedTable kIq3sSignedDev = make_iq3s_signed_table();
+
+struct TileFrag {
+  uint4 qs;
+  uint2 e8;
+  uint32_t l2, sc, dd;
+};
+
+// Buffer-descriptor loads (raw buffer loads: SGPR descriptor + VGPR lane offset + SGPR offset +
+// immediate), so the K loop spends no vector instructions on addresses. gfx9 descriptor word 3.
+constexpr int kBufDword3 = 0x00020000;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, kBufDword3);
+}
+
+// per-lane byte offsets of a lane's data inside a tile-block (constant over the K loop)
+struct TileOffs {
+  uint32_t qs, e8, l2, sc, dd;
+};
+
+__device__ __forceinline__ TileOffs tile_offsets(int lane, int p, int s) {
+  return {(uint32_t)(16 * lane), (uint32_t)(8 * lane), (uint32_t)(2 * lane), (uint32_t)(2 * (4 * p + (s >> 1))),
+          (uint32_t)(4 * p)};
+}
+
+// tile-block at byte `boff` of the tile described by `rs`
+__device__ __forceinline__ void load_tile_frag(__amdgpu_buffer_rsrc_t rs, uint32_t boff, const TileOffs& o,
+                                               TileFrag& f) {
+  const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)o.qs, (int)boff, 0);
+  f.qs = make_uint4(q.x, q.y, q.z, q.w);
+  const auto e = __builtin_amdgcn_raw_buffer_load_b64(rs, (int)(o.e8 + kTe8), (int)boff, 0);
+  f.e8 = make_uint2(e[0], e[1]);
+  f.l2 = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)(o.l2 + kTl2), (int)boff, 0);
+  f.sc = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)(o.sc + kTsc), (int)boff, 0);
+  f.dd = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(o.dd + kTd), (int)boff, 0);
+}
+
 template <int NC>
-__global__ void __launch_bounds__(256) gemv_iq3s_tile_kernel(const uint8_t* __restrict__ W, int64_t row_bytes,
-                                                             int nrows, int k, const uint8_t* __restrict__ q8,
-                                                             void* __restrict__ y, int y_dtype) {
-  __shared__ uint32_t grid[512];
-  __shared__ float red[kGemvWaves][NC][kTileRows];
-  for (int i = threadIdx.x; i < 512; i += blockDim.x) grid[i] = kIq3sGrid.v[i];
-  __syncthreads();
+struct XFrag {
+  int q[NC][8];
+  float d[NC];
+};
+
+// q8_1 blocks of X at slice `slice0 + s` for every activation row c (row c starts nslices
+// blocks after row c-1): rs describes the whole q8_1 buffer, lane_off = 36 * s
+template <int NC>
+__device__ __forceinline__ void load_x_frag(__amdgpu_buffer_rsrc_t rs, uint32_t lane_off, int nslices, int slice0,
+                                            XFrag<NC>& x) {
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int so = (c * nslices + slice0) * 36;
+    x.d[c] = half_bits_to_float(__builtin_amdgcn_raw_buffer_load_b16(rs, (int)lane_off, so, 0));
+    const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)lane_off, so + 4, 0);
+    const u32x4 e = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)lane_off, so + 20, 0);
+    x.q[c][0] = (int)a.x; x.q[c][1] = (int)a.y; x.q[c][2] = (int)a.z; x.q[c][3] = (int)a.w;
+    x.q[c][4] = (int)e.x; x.q[c][5] = (int)e.y; x.q[c][6] = (int)e.z; x.q[c][7] = (int)e.w;
+  }
+}
+
+// signed-grid words of the table entries for the two groups a byte permute pairs in P
+__device__ __forceinline__ void tile_lookup2(const uint8_t* tbl, uint32_t P, int& w0, int& w1) {
+  w0 = *(const int*)(tbl + ((P & 0xFFFFu) << 2));
+  w1 = *(const int*)(tbl + (P >> 14));  // bits 14, 15 of P are zero (ex has 5 bits)
+}
+
+template <int NC>
+__device__ __forceinline__ void tile_compute(const uint8_t* tbl, const TileFrag& f, const XFrag<NC>& x, int s,
+                                             float (&acc)[2][NC]) {
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const uint32_t q0 = r == 0 ? f.qs.x : f.qs.z;
+    const uint32_t q1 = r == 0 ? f.qs.y : f.qs.w;
+    uint32_t lo, hi;
+    iq3_tile_ex(r == 0 ? f.e8.x : f.e8.y, f.l2, r, lo, hi);
+    int w[8];
+    tile_lookup2(tbl, __builtin_amdgcn_perm(lo, q0, 0x05010400u), w[0], w[1]);
+    tile_lookup2(tbl, __builtin_amdgcn_perm(lo, q0, 0x07030602u), w[2], w[3]);
+    tile_lookup2(tbl, __builtin_amdgcn_perm(hi, q1, 0x05010400u), w[4], w[5]);
+    tile_lookup2(tbl, __builtin_amdgcn_perm(hi, q1, 0x07030602u), w[6], w[7]);
+    const int ls = 1 + 2 * (((f.sc >> (8 * r)) >> (4 * (s & 1))) & 0xF);
+    const float dl = half_bits_to_float((f.dd >> (16 * r)) & 0xFFFF) * (float)ls;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      int sumi = 0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sumi = dot4(w[e], x.q[c][e], sumi);
+      acc[r][c] = fmaf((float)sumi, dl * x.d[c], acc[r][c]);
+    }
+  }
+}
+
+// the 32 KB signed-grid table, global -> LDS without VGPRs: 32 wave-wide 1 KB DMA loads shared
+// out over the workgroup's waves (global_load_lds_dwordx4)
+template <int WPT>
+__device__ __forceinline__ void table_to_lds(uint4* table, int wave, int lane) {
+  const uint4* src = (const uint4*)kIq3sSignedDev.v;
+#pragma unroll
+  for (int i = wave; i < 32; i += WPT)
+    __builtin_amdgcn_global_load_lds((const void*)(src + i * 64 + lane),
+                                     (__attribute__((address_space(3))) void*)(table + i * 64), 16, 0, 0);
+}
+
+template <int NC, int TPW, int WPT>
+__global__ void __launch_bounds__(64 * TPW * WPT) gemv_iq3s_tile_kernel(const uint8_t* __restrict__ W,
+                                                                        int64_t row_bytes, int nrows, int k,
+                                                                        const uint8_t* __restrict__ q8,
+                                                                        void* __restrict__ y, int y_dtype) {
+  __shared__ uint4 table[2048];  // the 8192-entry signed-grid table
+  __shared__ float red[TPW][WPT][NC][kTileRows];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave index, scalar
+  const int wave = wv % WPT;   // K part of the tile
+  const int tw = wv / WPT;     // tile of the workgroup
+  const int tile = blockIdx.x * TPW + tw;
+  const int ntiles = nrows / kTileRows;
   const int p = lane >> 3, s = lane & 7;
   const int nb = k / kQK;
   const int nslices = k / kQ81;
-  const int b_begin = wave * nb / kGemvWaves, b_end = (wave + 1) * nb / kGemvWaves;
-  const uint8_t* tb = W + (int64_t)blockIdx.x * kTileRows * row_bytes;
+  const bool active = tile < ntiles;
+  const int b_begin = active ? wave * nb / WPT : 0, b_end = active ? (wave + 1) * nb / WPT : 0;
+  const uint8_t* tb = W + (int64_t)(active ? tile : 0) * kTileRows * row_bytes;  // scalar
+  const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(tb, (uint32_t)(kTileRows * row_bytes));
+  const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(q8, (uint32_t)(NC * nslices * 36));
+  const uint8_t* tbl = (const uint8_t*)table;
+  const TileOffs off = tile_offsets(lane, p, s);
+  const uint32_t xoff = 36u * (uint32_t)s;
 
   float acc[2][NC];
 #pragma unroll
@@ -179,45 +294,28 @@ __global__ void __launch_bounds__(256) gemv_iq3s_tile_kernel(const uint8_t* __re
 #pragma unroll
     for (int c = 0; c < NC; ++c) acc[i][c] = 0.0f;
 
-  for (int b = b_begin; b < b_end; ++b) {
-    const uint8_t* t = tb + (int64_t)b * kTileBlockBytes;
-    const uint4 qs = *(const uint4*)(t + kTqs + 16 * lane);
-    const uint2 sg = *(const uint2*)(t + kTsg + 8 * lane);
-    const uint32_t qh = *(const uint16_t*)(t + kTqh + 2 * lane);
-    const uint32_t sc = *(const uint16_t*)(t + kTsc + 2 * (4 * p + (s >> 1)));
-    const uint32_t dd = *(const uint32_t*)(t + kTd + 4 * p);
-
-    int xq[NC][8];
-    float d8[NC];
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const uint8_t* xb = q8 + ((int64_t)c * nslices + b * 8 + s) * 36;
-      d8[c] = half_bits_to_float(*(const uint16_t*)xb);
-      const u32x4 a = ld128a4(xb + 4);
-      const u32x4 e = ld128a4(xb + 20);
-      xq[c][0] = (int)a.x; xq[c][1] = (int)a.y; xq[c][2] = (int)a.z; xq[c][3] = (int)a.w;
-      xq[c][4] = (int)e.x; xq[c][5] = (int)e.y; xq[c][6] = (int)e.z; xq[c][7] = (int)e.w;
+  // the first two weight blocks of the wave, then the table DMA; the wait before the barrier
+  // covers both. Two named weight buffers (A: blocks b, b+2, ...; B: b+1, b+3, ...) keep one
+  // block in flight while the other is computed, with no register copies; the q8_1 blocks of X
+  // (L1-resident) are loaded just before use.
+  TileFrag fa, fb;
+  if (b_begin < b_end) load_tile_frag(wrs, b_begin * kTileBlockBytes, off, fa);
+  if (b_begin + 1 < b_end) load_tile_frag(wrs, (b_begin + 1) * kTileBlockBytes, off, fb);
+  table_to_lds<TPW * WPT>(table, wv, lane);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int b = b_begin; b < b_end; b += 2) {
+    {
+      XFrag<NC> x;
+      load_x_frag<NC>(xrs, xoff, nslices, b * 8, x);
+      tile_compute<NC>(tbl, fa, x, s, acc);
     }
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const uint64_t q = i == 0 ? ((uint64_t)qs.y << 32 | qs.x) : ((uint64_t)qs.w << 32 | qs.z);
-      const uint32_t sgn = i == 0 ? sg.x : sg.y;
-      const uint32_t h = (qh >> (8 * i)) & 0xFF;
-      int w[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t idx = (uint32_t)((q >> (8 * e)) & 0xFF) | (((h >> e) & 1u) << 8);
-        w[e] = apply_signs(grid[idx], sgn >> (4 * e));
-      }
-      const int ls = 1 + 2 * (((sc >> (8 * i)) >> (4 * (s & 1))) & 0xF);
-      const float dw = half_bits_to_float((dd >> (16 * i)) & 0xFFFF);
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        int sumi = 0;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) sumi = dot4(w[e], xq[c][e], sumi);
-        acc[i][c] += (float)(sumi * ls) * (dw * d8[c]);
-      }
+    if (b + 2 < b_end) load_tile_frag(wrs, (b + 2) * kTileBlockBytes, off, fa);
+    if (b + 1 < b_end) {
+      XFrag<NC> x;
+      load_x_frag<NC>(xrs, xoff, nslices, (b + 1) * 8, x);
+      tile_compute<NC>(tbl, fb, x, s, acc);
+      if (b + 3 < b_end) load_tile_frag(wrs, (b + 3) * kTileBlockBytes, off, fb);
     }
   }
 
@@ -229,24 +327,30 @@ __global__ void __launch_bounds__(256) gemv_iq3s_tile_kernel(const uint8_t* __re
       v += __shfl_xor(v, 1, 64);
       v += __shfl_xor(v, 2, 64);
       v += __shfl_xor(v, 4, 64);
-      if (s == 0) red[wave][c][2 * p + i] = v;
+      if (s == 0) red[tw][wave][c][2 * p + i] = v;
     }
   }
   __syncthreads();
-  if (threadIdx.x < NC * kTileRows) {
-    const int c = threadIdx.x / kTileRows, r = threadIdx.x % kTileRows;
-    float v = red[0][c][r];
+  if (threadIdx.x < TPW * NC * kTileRows) {
+    const int t = threadIdx.x / (NC * kTileRows);
+    const int c = (threadIdx.x / kTileRows) % NC, r = threadIdx.x % kTileRows;
+    const int otile = blockIdx.x * TPW + t;
+    if (otile < ntiles) {
+      float v = red[t][0][c][r];
 #pragma unroll
-    for (int wv = 1; wv < kGemvWaves; ++wv) v += red[wv][c][r];
-    store_y(y, (int64_t)c * nrows + (int64_t)blockIdx.x * kTileRows + r, v, y_dtype);
+      for (int w2 = 1; w2 < WPT; ++w2) v += red[t][w2][c][r];
+      store_y(y, (int64_t)c * nrows + (int64_t)otile * kTileRows + r, v, y_dtype);
+    }
   }
 }
 
-// nrows % 16 == 0, n in 1..8
-hipError_t launch_gemv_packed(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n,
-                              void* y, int y_dtype, hipStream_t stream) {
-  const unsigned blocks = (unsigned)(nrows / kTileRows);
-#define GGUF_GT(NC) gemv_iq3s_tile_kernel<NC><<<blocks, 64 * kGemvWaves, 0, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype)
+template <int TPW, int WPT>
+static void launch_gemv_packed_w(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n,
+                                 void* y, int y_dtype, hipStream_t stream) {
+  const int tiles = nrows / kTileRows;
+  const unsigned blocks = (unsigned)((tiles + TPW - 1) / TPW);
+#define GGUF_GT(NC) \
+  gemv_iq3s_tile_kernel<NC, TPW, WPT><<<blocks, 64 * TPW * WPT, 0, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype)
   switch (n) {
     case 1: GGUF_GT(1); break;
     case 2: GGUF_GT(2); break;
@@ -258,6 +362,15 @@ hipError_t launch_gemv_packed(const uint8_t* W, int64_t row_bytes, int nrows, in
     default: GGUF_GT(8); break;
   }
 #undef GGUF_GT
+}
+
+// nrows % 16 == 0, n in 1..8.
+hipError_t launch_gemv_packed(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n,
+                              void* y, int y_dtype, hipStream_t stream) {
+  // One tile per workgroup. Eight waves split K for one or two columns (measured best at
+  // 17408 x 5120: 12.3 us at M=1); from three columns on, the register file allows four.
+  if (n <= 2) launch_gemv_packed_w<1, 8>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);
+  else launch_gemv_packed_w<1, 4>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);
   return hipGetLastError();
 }
 

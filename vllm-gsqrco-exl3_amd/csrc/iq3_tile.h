@@ -1,16 +1,20 @@
-// The build's IQ3_S tile layout (its own; the reference's iq3_pack.py layout serves its CUDA
-// mma fragments and is not reproduced).
+// The build's IQ3_S tile layout (its own; the reference's iq3_pack.py layout serves its CUDA mma
+// fragments and is not reproduced), and the signed-grid table the decode kernels read.
 //
 // Rows are grouped in tiles of 16. Tile t's bytes stay where rows 16t..16t+15 were; block b of
-// the tile becomes one 1760-byte "tile-block" at byte 1760*b of the tile. Inside a tile-block,
-// lane L = 8p + s of the decode GEMV (p = row pair 0..7, s = slice 0..7) finds its data as
-//   [   0, 1024)  16 B at 16L : qs[8s..8s+8) of row 2p, then of row 2p+1
-//   [1024, 1536)   8 B at 8L  : signs[4s..4s+4) of row 2p, then of row 2p+1
-//   [1536, 1664)   2 B at 2L  : qh[s] of row 2p, then of row 2p+1
-//   [1664, 1728)   2 B at 2(4p + j) : scales[j] of row 2p, then of row 2p+1 (j = 0..3)
-//   [1728, 1760)   4 B at 4p  : d of row 2p, then of row 2p+1
-// (block_iq3_s byte offsets: d 0, qs 2, qh 66, signs 74, scales 106.) A pure byte permutation:
-// bijective, same size, each load of the GEMV 16-byte aligned and contiguous across lanes.
+// the tile becomes one 1760-byte "tile-block" at byte 1760*b of the tile. Lane L = 8p + s of a
+// decode wave (p = row pair 0..7, s = 32-value slice 0..7) owns rows 2p, 2p+1 (r = 0, 1) of
+// slice s. For group e (values 4e..4e+3 of the slice, e = 0..7) of row r define the 5-bit
+//   ex(r, e) = sign nibble e of the slice's 4 sign bytes | (bit e of qh[s]) << 4
+// so that (qs byte | ex << 8) is a 13-bit index into the signed-grid table (below). The
+// tile-block holds, for every lane L:
+//   [   0, 1024)  QS  16 B at 16L : qs[8s..8s+8) of row 2p, then of row 2p+1
+//   [1024, 1536)  E8   8 B at 8L  : byte 4r+j (j = 0..3) = ex(r, j) | (ex(r, 4+j) & 7) << 5
+//   [1536, 1664)  L2   2 B at 2L  : bits 8r+2j, 8r+2j+1 = ex(r, 4+j) >> 3
+//   [1664, 1728)  SC   2 B at 2(4p + j) : scales[j] of row 2p, then of row 2p+1 (j = 0..3)
+//   [1728, 1760)  D    4 B at 4p  : d of row 2p, then of row 2p+1
+// (block_iq3_s byte offsets: d 0, qs 2, qh 66, signs 74, scales 106.) Same size, bijective, and
+// every load of the decode GEMV is contiguous across the wave (16 / 8 / 2 B per lane).
 #pragma once
 
 #include "gguf_common.h"
@@ -19,23 +23,86 @@ namespace gguf {
 
 constexpr int kTileRows = 16;
 constexpr int kTileBlockBytes = kTileRows * 110;  // 1760
-constexpr int kTqs = 0, kTsg = 1024, kTqh = 1536, kTsc = 1664, kTd = 1728;
+constexpr int kTqs = 0, kTe8 = 1024, kTl2 = 1536, kTsc = 1664, kTd = 1728;
 
-// tile-block byte j -> (row within the tile, byte within that row's block)
-__host__ __device__ inline void iq3_tile_source(int j, int& r, int& o) {
-  if (j < kTsg) {
-    const int L = j >> 4, i = j & 15;
-    r = 2 * (L >> 3) + (i >> 3);
-    o = 2 + 8 * (L & 7) + (i & 7);
-  } else if (j < kTqh) {
-    const int jj = j - kTsg, L = jj >> 3, i = jj & 7;
-    r = 2 * (L >> 3) + (i >> 2);
-    o = 74 + 4 * (L & 7) + (i & 3);
-  } else if (j < kTsc) {
-    const int jj = j - kTqh, L = jj >> 1;
-    r = 2 * (L >> 3) + (jj & 1);
-    o = 66 + (L & 7);
-  } else if (j < kTd) {
+// Signed-grid table: entry (qs | ex << 8) = the grid word of index qs | (ex >> 4) << 8 with the
+// bytes whose bit is set in ex & 0xF negated; 8192 x int8x4 = 32 KB, staged in LDS by the
+// decode kernels.
+struct Iq3sSignedTable {
+  uint32_t v[8192];
+};
+
+constexpr Iq3sSignedTable make_iq3s_signed_table() {
+  Iq3sSignedTable t{};
+  for (int idx = 0; idx < 8192; ++idx) {
+    const int ex = idx >> 8;
+    const uint32_t g = kIq3sGrid.v[(idx & 0xFF) | ((ex >> 4) << 8)];
+    uint32_t out = 0;
+    for (int b = 0; b < 4; ++b) {
+      uint32_t byte = (g >> (8 * b)) & 0xFF;
+      if ((ex >> b) & 1) byte = (256u - byte) & 0xFF;
+      out |= byte << (8 * b);
+    }
+    t.v[idx] = out;
+  }
+  return t;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Pack / unpack of one lane's share of a tile-block (host and device).
+
+// ex of group e (0..7) of a slice, from its 4 sign bytes (as a dword) and its qh byte
+__host__ __device__ inline uint32_t iq3_ex(uint32_t signs, uint32_t qh, int e) {
+  return ((signs >> (4 * e)) & 0xF) | (((qh >> e) & 1u) << 4);
+}
+
+// GGUF block pointers of rows 2p, 2p+1 -> lane L's QS / E8 / L2 bytes written at tb
+__host__ __device__ inline void iq3_tile_pack_lane(const uint8_t* const rowblk[2], int L, uint8_t* tb) {
+  const int s = L & 7;
+  uint8_t* qs = tb + kTqs + 16 * L;
+  uint8_t* e8 = tb + kTe8 + 8 * L;
+  uint32_t l2 = 0;
+  for (int r = 0; r < 2; ++r) {
+    const uint8_t* b = rowblk[r];
+    for (int i = 0; i < 8; ++i) qs[8 * r + i] = b[2 + 8 * s + i];
+    const uint32_t sg = (uint32_t)b[74 + 4 * s] | ((uint32_t)b[75 + 4 * s] << 8) | ((uint32_t)b[76 + 4 * s] << 16) |
+                        ((uint32_t)b[77 + 4 * s] << 24);
+    const uint32_t qh = b[66 + s];
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t lo = iq3_ex(sg, qh, j), hi = iq3_ex(sg, qh, 4 + j);
+      e8[4 * r + j] = (uint8_t)(lo | ((hi & 7u) << 5));
+      l2 |= (hi >> 3) << (8 * r + 2 * j);
+    }
+  }
+  tb[kTl2 + 2 * L] = (uint8_t)(l2 & 0xFF);
+  tb[kTl2 + 2 * L + 1] = (uint8_t)(l2 >> 8);
+}
+
+// lane L's QS / E8 / L2 bytes at tb -> qs, qh and sign bytes of rows 2p, 2p+1 (GGUF blocks)
+__host__ __device__ inline void iq3_tile_unpack_lane(const uint8_t* tb, int L, uint8_t* const rowblk[2]) {
+  const int s = L & 7;
+  const uint8_t* qs = tb + kTqs + 16 * L;
+  const uint8_t* e8 = tb + kTe8 + 8 * L;
+  const uint32_t l2 = (uint32_t)tb[kTl2 + 2 * L] | ((uint32_t)tb[kTl2 + 2 * L + 1] << 8);
+  for (int r = 0; r < 2; ++r) {
+    uint8_t* b = rowblk[r];
+    for (int i = 0; i < 8; ++i) b[2 + 8 * s + i] = qs[8 * r + i];
+    uint32_t sg = 0, qh = 0;
+    for (int e = 0; e < 8; ++e) {
+      const int j = e & 3;
+      const uint32_t byte = e8[4 * r + j];
+      const uint32_t ex = e < 4 ? (byte & 0x1F) : ((byte >> 5) | (((l2 >> (8 * r + 2 * j)) & 3u) << 3));
+      sg |= (ex & 0xF) << (4 * e);
+      qh |= ((ex >> 4) & 1u) << e;
+    }
+    for (int i = 0; i < 4; ++i) b[74 + 4 * s + i] = (uint8_t)(sg >> (8 * i));
+    b[66 + s] = (uint8_t)qh;
+  }
+}
+
+// SC and D bytes: tile-block byte j in [kTsc, 1760) <-> (row in tile, byte in the row's block)
+__host__ __device__ inline void iq3_tile_scale_source(int j, int& r, int& o) {
+  if (j < kTd) {
     const int jj = j - kTsc, m = jj >> 1;
     r = 2 * (m >> 2) + (jj & 1);
     o = 106 + (m & 3);
@@ -46,18 +113,35 @@ __host__ __device__ inline void iq3_tile_source(int j, int& r, int& o) {
   }
 }
 
-// Decode of values 8q..8q+7 (groups 2q, 2q+1) of slice u of row li (0..15) from a tile-block,
-// for the MFMA kernel's lane mapping.
-__device__ __forceinline__ void decode_iq3s_tile_q(const uint8_t* t, int li, int u, int q, const uint32_t* grid,
+// ---------------------------------------------------------------------------------------------
+// Decode helpers of the kernels
+
+// ex of the 4 groups 0..3 (lo) and 4..7 (hi) of row r, one per byte, from a lane's E8 dword of
+// row r and its L2 halfword
+__device__ __forceinline__ void iq3_tile_ex(uint32_t e8, uint32_t l2, int r, uint32_t& lo, uint32_t& hi) {
+  lo = e8 & 0x1F1F1F1Fu;
+  const uint32_t b = (l2 >> (8 * r)) & 0xFF;
+  const uint32_t t = (b | (b << 12)) & 0x000F000Fu;
+  const uint32_t t2 = (t | (t << 6)) & 0x03030303u;
+  hi = ((e8 >> 5) & 0x07070707u) | (t2 << 3);
+}
+
+// Values 8q..8q+7 (groups 2q, 2q+1) of slice u of row li (0..15) from a tile-block, through the
+// signed-grid table (in LDS), for the MFMA kernel's lane mapping.
+__device__ __forceinline__ void decode_iq3s_tile_q(const uint8_t* t, int li, int u, int q, const uint32_t* table,
                                                    int (&w)[2], float& d, int& ls) {
-  const int L = 8 * (li >> 1) + u, ri = li & 1;
-  const uint32_t qs = *(const uint16_t*)(t + kTqs + 16 * L + 8 * ri + 2 * q);
-  const uint32_t qh = t[kTqh + 2 * L + ri] >> (2 * q);
-  const uint32_t sg = t[kTsg + 8 * L + 4 * ri + q];
-  w[0] = apply_signs(grid[(qs & 0xFF) | ((qh & 1u) << 8)], sg);
-  w[1] = apply_signs(grid[(qs >> 8) | ((qh & 2u) << 7)], sg >> 4);
-  d = half_bits_to_float(*(const uint16_t*)(t + kTd + 4 * (li >> 1) + 2 * ri));
-  ls = 1 + 2 * ((t[kTsc + 2 * (4 * (li >> 1) + (u >> 1)) + ri] >> (4 * (u & 1))) & 0xF);
+  const int L = 8 * (li >> 1) + u, r = li & 1;
+  const uint32_t qs = *(const uint16_t*)(t + kTqs + 16 * L + 8 * r + 2 * q);
+  const uint32_t e8 = *(const uint32_t*)(t + kTe8 + 8 * L + 4 * r);
+  const uint32_t l2 = *(const uint16_t*)(t + kTl2 + 2 * L);
+  uint32_t lo, hi;
+  iq3_tile_ex(e8, l2, r, lo, hi);
+  const uint32_t ex = q < 2 ? lo : hi;
+  const int j = 2 * (q & 1);
+  w[0] = (int)table[(qs & 0xFF) | (((ex >> (8 * j)) & 0xFF) << 8)];
+  w[1] = (int)table[(qs >> 8) | (((ex >> (8 * j + 8)) & 0xFF) << 8)];
+  d = half_bits_to_float(*(const uint16_t*)(t + kTd + 4 * (li >> 1) + 2 * r));
+  ls = 1 + 2 * ((t[kTsc + 2 * (4 * (li >> 1) + (u >> 1)) + r] >> (4 * (u & 1))) & 0xF);
 }
 
 }  // namespace gguf
