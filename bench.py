@@ -1,9 +1,9 @@
 #!/usr/bin/env python3
 """Benchmark of the GGUF quantized-matmul hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-points] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-points] [--no-cpu] [--kernel-only]
 
-Workload (BASELINE.json configs[1]): IQ3_S decode GEMV at M = 1 and 4 on the two 27B-layer
+Workload: IQ3_S decode GEMV at M = 1 and 4 on the two 27B-layer
 shapes, gate/up 17408 x 5120 and down 5120 x 17408, bf16 activations N(0,1) quantised to q8_1,
 weights in IQ3_S super-blocks with uniform random codes and d ~ |N(0, 2e-3)|, in the build's
 packed tile layout (the route the linear method takes for IQ3_S). A step is one op call
@@ -17,6 +17,12 @@ Also reported: the dominant kernel's roofline (the packed decode GEMV kernel at 
 M = 1, timed alone with the q8_1 input precomputed), the metric's other points (IQ3_S and Q4_K at
 M = 1, 4, 16, 32, 48 on 17408 x 5120, each through the routing table's op), and the CPU oracle
 (numpy dequantise + torch fp32 matmul) timed on the host cores on a bounded sample.
+
+`traffic` (HBM bytes per launch of the dominant kernel) is read from the committed PMC summary
+profiles/gemv_iq3s_tile_17408x5120_m1.traffic.json when present (null otherwise). That summary
+comes from `rocprofv3 --pmc FETCH_SIZE` and `--pmc WRITE_SIZE` runs of `bench.py --kernel-only`,
+which times only the dominant kernel and then runs a plain elementwise copy of 256 MiB (read
+256 MiB, write 256 MiB) whose counter readings calibrate the counters' byte scale.
 """
 
 import argparse
@@ -31,6 +37,8 @@ sys.path.insert(0, os.path.join(ROOT, "vllm-gsqrco-exl3_amd"))
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 NBUF = 8                       # distinct weight copies per shape (defeats the 256 MB MALL)
+COPY_BYTES = 256 << 20         # calibration copy: bytes read (and written) per launch
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_iq3s_tile_17408x5120_m1.traffic.json")
 IQ3_S, Q4_K = 21, 12
 BLOCK = {IQ3_S: 110, Q4_K: 144}
 SCALE_OFFSETS = {IQ3_S: (0,), Q4_K: (0, 2)}
@@ -101,6 +109,54 @@ def cpu_baseline(torch):
                       f"median of 3: {t * 1e6:.0f} us/call"}
 
 
+def load_traffic():
+    """HBM bytes per launch of the dominant kernel from the committed PMC summary, or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return json.load(f)["traffic_bytes_per_launch"]
+    except (OSError, ValueError, KeyError):
+        return None
+
+
+def dominant_kernel(torch, C, ws, steps):
+    """The packed decode GEMV kernel alone (17408 x 5120, M = 1, q8_1 input precomputed): one graph
+    of one launch per weight copy, timed with HIP events on the stream the op launches on."""
+    rows, k, m = 17408, 5120, 1
+    x = torch.randn(m, k, device="cuda", dtype=torch.bfloat16)
+    q8 = C.lcpp_quantize_q8_1(x, IQ3_S, False, False)
+    kg = graph(torch, [lambda w=w: C.lcpp_mul_mat_vec_iq3_mma_packed(w, x, IQ3_S, rows, q8) for w in ws])
+    kernel_us = time_graphs(torch, [kg], max(5, steps)) * 1e3 / len(ws)
+    alg_bytes = ws[0].numel() + q8.numel() + m * rows * 2
+    achieved = alg_bytes / (kernel_us * 1e-6) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic(),
+            "kernel": "gemv_iq3s_tile_kernel<1,1,8> (17408x5120, M=1, q8_1 precomputed)",
+            "us_per_launch": round(kernel_us, 3), "alg_bytes_per_launch": alg_bytes}
+
+
+def copy_calibration(torch):
+    """A plain elementwise map over COPY_BYTES (torch.neg, float32 in, float32 out: COPY_BYTES read,
+    COPY_BYTES written), three launches, so that a PMC run can read what FETCH_SIZE / WRITE_SIZE
+    report for a known byte count."""
+    src = torch.randn(COPY_BYTES // 4, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+
+
+def kernel_only(torch, C, iq3_pack, steps):
+    """--kernel-only: the dominant kernel (as in the full run) and the calibration copy; prints one
+    JSON line with the roofline object."""
+    ws = [iq3_pack.pack(make_weights(torch, IQ3_S, 17408, 5120, i), IQ3_S) for i in range(NBUF)]
+    roofline = dominant_kernel(torch, C, ws, steps)
+    del ws
+    torch.cuda.empty_cache()
+    copy_calibration(torch)
+    print(json.dumps({"mode": "kernel-only", "roofline": roofline, "copy_bytes": COPY_BYTES}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -108,10 +164,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-points", action="store_true", help="skip the metric's other (type, M) points")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--kernel-only", action="store_true",
+                    help="time only the dominant kernel, then run the counter-calibration copy (for rocprofv3)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); the path "
-              "would shard along the weight rows, see DESIGN.md", file=sys.stderr)
+              "would shard along the weight rows, one slice of rows per GPU", file=sys.stderr)
         sys.exit(2)
 
     import torch
@@ -121,6 +179,9 @@ def main():
 
     C = torch.ops._C_gguf
     torch.cuda.set_device(0)
+    if args.kernel_only:
+        kernel_only(torch, C, iq3_pack, args.steps)
+        return
 
     # ------------------------------------------------------------------ headline workload
     cases = [(17408, 5120, 1), (17408, 5120, 4), (5120, 17408, 1), (5120, 17408, 4)]
@@ -153,19 +214,7 @@ def main():
         detail.append({"shape": f"{rows}x{k}", "m": m, "us_per_call": round(us, 2),
                        "gbps": round(cb / (us * 1e-6) / 1e9, 1), "frac_hbm": round(cb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 3)})
 
-    # ------------------------------------------------------------------ dominant kernel alone
-    rows, k, m = 17408, 5120, 1
-    x = torch.randn(m, k, device="cuda", dtype=torch.bfloat16)
-    q8 = C.lcpp_quantize_q8_1(x, IQ3_S, False, False)
-    ws = weights[(rows, k)]
-    kg = graph(torch, [lambda w=w: C.lcpp_mul_mat_vec_iq3_mma_packed(w, x, IQ3_S, rows, q8) for w in ws])
-    kernel_us = time_graphs(torch, [kg], max(5, args.steps)) * 1e3 / len(ws)
-    alg_bytes = ws[0].numel() + m * k * 2 + m * rows * 2
-    achieved = alg_bytes / (kernel_us * 1e-6) / 1e9
-    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": "gemv_iq3s_tile_kernel<1> (17408x5120, M=1, q8_1 precomputed)",
-                "us_per_launch": round(kernel_us, 3), "alg_bytes_per_launch": alg_bytes}
+    roofline = dominant_kernel(torch, C, weights[(17408, 5120)], args.steps)
     del weights
     torch.cuda.empty_cache()
 
