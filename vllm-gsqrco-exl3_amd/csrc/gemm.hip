@@ -1,8 +1,8 @@
 // int8-MFMA GEMM for 9+ activation rows on GGUF bytes: Y[c, r] = sum_k X[c, k] * W[r, k].
 //
-// Replaces the reference's MMQ-class products (vendored mul_mat_q via lcpp_shim.cu:626-671, the
-// owned mma_k kernel lcpp_owned_mma_k.cu:354-540 and the tiled IQ3 kernel
-// lcpp_owned_iq3_mma.cu:769-1020) with a gfx950 design on v_mfma_i32_16x16x32_i8:
+// Replaces the reference's MMQ-class products on plain GGUF rows (vendored mul_mat_q via
+// lcpp_shim.cu:626-671 and the owned mma_k kernel lcpp_owned_mma_k.cu:354-540) with a gfx950
+// design on v_mfma_i32_16x16x32_i8 (IQ3_S in the tile layout has its own GEMM, gemm_tile.hip):
 //  * X is quantised to q8_1 in the MMQ block layout (quantize.hip); one 32-value slice is one
 //    MFMA K step, so every MFMA result is exactly the reference's per-slice int32 dot;
 //  * a workgroup owns 16 weight rows and 16*NT columns of X; its 4 waves split the K slices;
@@ -13,30 +13,23 @@
 //    combined in int32 as the reference does; Q4_K's min term uses the integer q8 sum;
 //  * the 4 waves' partial sums are added in wave order through LDS (deterministic).
 #include "decode.h"
-#include "iq3_tile.h"
 
 namespace gguf {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
-
-__device__ const Iq3sSignedTable kIq3sSignedGemm = make_iq3s_signed_table();
 
 __device__ __forceinline__ v4i mfma16x16x32(long a, long b) {
   const v4i z = {0, 0, 0, 0};
   return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, z, 0, 0, 0);
 }
 
-template <int TYPE, int NT, bool TILE>
+template <int TYPE, int NT>
 __global__ void __launch_bounds__(256) gemm_mfma_kernel(const uint8_t* __restrict__ W, int64_t row_bytes, int nrows,
                                                         int k, const uint8_t* __restrict__ q8, int n,
                                                         void* __restrict__ y, int y_dtype) {
-  __shared__ uint32_t grid[TYPE == kIQ3_S ? (TILE ? 8192 : 512) : 1];
+  __shared__ uint32_t grid[TYPE == kIQ3_S ? 512 : 1];
   __shared__ float part[3][NT][4][64];
-  if constexpr (TILE) {
-    const uint4* src = (const uint4*)kIq3sSignedGemm.v;
-    for (int i = threadIdx.x; i < 2048; i += blockDim.x) ((uint4*)grid)[i] = src[i];
-    __syncthreads();
-  } else if constexpr (TYPE == kIQ3_S) {
+  if constexpr (TYPE == kIQ3_S) {
     for (int i = threadIdx.x; i < 512; i += blockDim.x) grid[i] = kIq3sGrid.v[i];
     __syncthreads();
   }
@@ -52,8 +45,6 @@ __global__ void __launch_bounds__(256) gemm_mfma_kernel(const uint8_t* __restric
   const int s_begin = wave * per, s_end = s_begin + per;
   const bool row_ok = row < nrows;
   const uint8_t* wrow = W + (int64_t)(row_ok ? row : 0) * row_bytes;
-  // tile layout: the workgroup's 16 rows are one tile; tile-block b at 1760*b
-  const uint8_t* wtile = W + (int64_t)blockIdx.x * kTileRows * row_bytes;
 
   float acc[NT][4];
 #pragma unroll
@@ -66,9 +57,7 @@ __global__ void __launch_bounds__(256) gemm_mfma_kernel(const uint8_t* __restric
     const int u = s & 7;
     int wa[2];
     SliceScale sc;
-    if constexpr (TILE) {
-      decode_iq3s_tile_q(wtile + (int64_t)(s >> 3) * kTileBlockBytes, li, u, q, grid, wa, sc.d, sc.ls);
-    } else if constexpr (TYPE == kIQ3_S) {
+    if constexpr (TYPE == kIQ3_S) {
       decode_iq3s_q(b, u, q, grid, wa, sc);
     }
     if constexpr (TYPE == kQ4_K) decode_q4k_q(b, u, q, wa, sc);
@@ -168,20 +157,20 @@ __global__ void __launch_bounds__(256) gemm_mfma_kernel(const uint8_t* __restric
   }
 }
 
-template <int TYPE, bool TILE = false>
+template <int TYPE>
 static void launch_gemm_t(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n, void* y,
                           int y_dtype, hipStream_t stream) {
   const unsigned gx = (unsigned)((nrows + 15) / 16);
   const int tiles = (n + 15) / 16;
   if (tiles <= 1) {
-    gemm_mfma_kernel<TYPE, 1, TILE><<<dim3(gx, 1), 256, 0, stream>>>(W, row_bytes, nrows, k, q8, n, y, y_dtype);
+    gemm_mfma_kernel<TYPE, 1><<<dim3(gx, 1), 256, 0, stream>>>(W, row_bytes, nrows, k, q8, n, y, y_dtype);
   } else if (tiles == 2) {
-    gemm_mfma_kernel<TYPE, 2, TILE><<<dim3(gx, 1), 256, 0, stream>>>(W, row_bytes, nrows, k, q8, n, y, y_dtype);
+    gemm_mfma_kernel<TYPE, 2><<<dim3(gx, 1), 256, 0, stream>>>(W, row_bytes, nrows, k, q8, n, y, y_dtype);
   } else if (tiles == 3) {
-    gemm_mfma_kernel<TYPE, 3, TILE><<<dim3(gx, 1), 256, 0, stream>>>(W, row_bytes, nrows, k, q8, n, y, y_dtype);
+    gemm_mfma_kernel<TYPE, 3><<<dim3(gx, 1), 256, 0, stream>>>(W, row_bytes, nrows, k, q8, n, y, y_dtype);
   } else {
     const unsigned gy = (unsigned)((tiles + 3) / 4);
-    gemm_mfma_kernel<TYPE, 4, TILE><<<dim3(gx, gy), 256, 0, stream>>>(W, row_bytes, nrows, k, q8, n, y, y_dtype);
+    gemm_mfma_kernel<TYPE, 4><<<dim3(gx, gy), 256, 0, stream>>>(W, row_bytes, nrows, k, q8, n, y, y_dtype);
   }
 }
 
@@ -195,13 +184,6 @@ hipError_t launch_gemm(int type, const uint8_t* W, int64_t row_bytes, int nrows,
     case kQ6_K: launch_gemm_t<kQ6_K>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream); break;
     default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
-}
-
-// IQ3_S in the tile layout (iq3_tile.h); nrows % 16 == 0.
-hipError_t launch_gemm_packed(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n,
-                              void* y, int y_dtype, hipStream_t stream) {
-  launch_gemm_t<kIQ3_S, true>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);
   return hipGetLastError();
 }
 

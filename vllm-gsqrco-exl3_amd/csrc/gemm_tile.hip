@@ -1,0 +1,290 @@
+// int8-MFMA GEMM for IQ3_S in the tile layout (iq3_tile.h) on activations in the xq layout (xq.h):
+// Y[c, r] = sum_k X[c, k] * W[r, k] for 9+ activation rows.
+//
+// Replaces the reference's tiled IQ3 products on packed weights (lcpp_owned_iq3_mma.cu:769-1020,
+// lcpp_mul_mat_iq3_packed / lcpp_mul_mat_vec_iq3_mma_packed above 8 rows) with a gfx950 design:
+//  * a workgroup owns RW 16-row tiles and NT column tiles of 16 activation rows; its KS waves
+//    split the K blocks;
+//  * per K block a wave loads each tile-block with the decode GEMV's contiguous loads (lane
+//    L = 8p + s: slice s of rows 2p, 2p+1), turns every 4-value group into one read of the 32 KB
+//    signed-grid table in LDS, and writes the int8 values to a per-wave LDS buffer from which
+//    lane 16q + j reads the MFMA A operand (values 8q..8q+7 of slice u of tile row j);
+//  * the B operands of the block come from the xq unit with four 16-byte loads per lane and
+//    serve all RW tiles; one v_mfma_i32_16x16x32_i8 per (tile, slice, column tile) gives the
+//    reference's integer slice dot for 16 x 16 (row, column) pairs;
+//  * each dot is scaled by its slice sub-scale (integer) and activation scale (fp32) and summed
+//    over the block's 8 slices, then multiplied by the block scale d of its row;
+//  * the next block's weight and activation loads are issued before the current block is
+//    computed (two named register sets); the waves' partial sums are added in wave order.
+#include "iq3_tile.h"
+#include "xq.h"
+
+namespace gguf {
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+__device__ const Iq3sSignedTable kIq3sSignedMma = make_iq3s_signed_table();
+
+// Per-wave transposition buffer: slice u at 528u (512 B + 16 B pad), tile row j at 32j, the
+// four 8-byte quarters q of the row in slots q ^ (j >> 2). Lane 16q + j reads its A operand of
+// slice u from slot q ^ (j >> 2) of row j; a writer lane stores a row's quarter pairs with
+// 16-byte stores.
+constexpr int kTrSlice = 528;
+constexpr int kTrBytes = 8 * kTrSlice;
+
+struct MmaFrag {
+  u32x4 qs;     // decode view: qs of slice s, rows 2p, 2p+1
+  uint32_t e8x, e8y, l2;
+  u32x4 sc;     // MFMA view: scale bytes of rows 4q .. 4q+3
+  uint32_t d01, d23;  // fp16 d of rows 4q .. 4q+3
+};
+
+__device__ __forceinline__ void load_mma_frag(__amdgpu_buffer_rsrc_t rs, int boff, int lane, int q, MmaFrag& f) {
+  f.qs = __builtin_amdgcn_raw_buffer_load_b128(rs, 16 * lane, boff, 0);
+  const auto e = __builtin_amdgcn_raw_buffer_load_b64(rs, kTe8 + 8 * lane, boff, 0);
+  f.e8x = e[0];
+  f.e8y = e[1];
+  f.l2 = __builtin_amdgcn_raw_buffer_load_b16(rs, kTl2 + 2 * lane, boff, 0);
+  f.sc = __builtin_amdgcn_raw_buffer_load_b128(rs, kTsc + 16 * q, boff, 0);
+  const auto d = __builtin_amdgcn_raw_buffer_load_b64(rs, kTd + 8 * q, boff, 0);
+  f.d01 = d[0];
+  f.d23 = d[1];
+}
+
+template <int NT>
+struct XqFrag {
+  u32x4 b[NT][4];  // B operands: slices 2i, 2i+1 in b[t][i]
+  u32x4 d[NT][2];  // fp32 activation scales of slices 0..7 (as bits)
+};
+
+// units[t] = (column tile) * nb of the workgroup's column tile t; block b
+template <int NT>
+__device__ __forceinline__ void load_xq_frag(__amdgpu_buffer_rsrc_t rs, const int (&units)[NT], int b, int sbase,
+                                             int lane, int j, XqFrag<NT>& x) {
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int unit = units[t] + b;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      x.b[t][i] = __builtin_amdgcn_raw_buffer_load_b128(rs, 64 * lane + 16 * i, unit * kXqUnit, 0);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      x.d[t][i] = __builtin_amdgcn_raw_buffer_load_b128(rs, 32 * j + 16 * i, sbase + unit * kXqScaleUnit, 0);
+  }
+}
+
+__device__ __forceinline__ long b_operand(const u32x4& v, int h) {
+  return h == 0 ? (long)(((uint64_t)v[1] << 32) | v[0]) : (long)(((uint64_t)v[3] << 32) | v[2]);
+}
+
+// decode one tile-block (decode view) into the wave's transposition buffer, then read the 8
+// A operands (MFMA view)
+__device__ __forceinline__ void tile_to_a(const uint8_t* tbl, uint8_t* tr, const MmaFrag& f, int p, int s, int q, int j,
+                                          long (&a)[8]) {
+  const int c = p >> 1;  // (row >> 2) of both rows of the lane
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const uint32_t q0 = r == 0 ? f.qs[0] : f.qs[2];
+    const uint32_t q1 = r == 0 ? f.qs[1] : f.qs[3];
+    uint32_t lo, hi;
+    iq3_tile_ex(r == 0 ? f.e8x : f.e8y, f.l2, r, lo, hi);
+    int w[8];
+    tile_lookup2(tbl, __builtin_amdgcn_perm(lo, q0, 0x05010400u), w[0], w[1]);
+    tile_lookup2(tbl, __builtin_amdgcn_perm(lo, q0, 0x07030602u), w[2], w[3]);
+    tile_lookup2(tbl, __builtin_amdgcn_perm(hi, q1, 0x05010400u), w[4], w[5]);
+    tile_lookup2(tbl, __builtin_amdgcn_perm(hi, q1, 0x07030602u), w[6], w[7]);
+    const int row = 2 * p + r;
+    uint8_t* dst = tr + s * kTrSlice + row * 32;
+#pragma unroll
+    for (int P = 0; P < 2; ++P) {
+      // quarters 2P, 2P+1 go to slots (2P) ^ c and (2P+1) ^ c: the pair P ^ (c >> 1), swapped if c is odd
+      const bool sw = c & 1;
+      uint4 v;
+      v.x = (uint32_t)(sw ? w[4 * P + 2] : w[4 * P + 0]);
+      v.y = (uint32_t)(sw ? w[4 * P + 3] : w[4 * P + 1]);
+      v.z = (uint32_t)(sw ? w[4 * P + 0] : w[4 * P + 2]);
+      v.w = (uint32_t)(sw ? w[4 * P + 1] : w[4 * P + 3]);
+      *(uint4*)(dst + 16 * (P ^ (c >> 1))) = v;
+    }
+  }
+  // a wave's LDS operations complete in issue order, so the reads below see the writes above;
+  // the compiler barriers keep the program order (and measured faster than free scheduling)
+  __asm__ volatile("" ::: "memory");
+  const int slot = (q ^ (j >> 2)) & 3;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) a[u] = *(const long*)(tr + u * kTrSlice + j * 32 + slot * 8);
+  __asm__ volatile("" ::: "memory");
+}
+
+// one K block of RW tiles: decode + MFMA + scale, added into acc
+template <int NT, int RW>
+__device__ __forceinline__ void mma_block(const uint8_t* tbl, uint8_t* tr, const MmaFrag (&f)[RW], const XqFrag<NT>& x,
+                                          int p, int s, int q, int j, float (&acc)[RW][NT][4]) {
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    long a[8];
+    tile_to_a(tbl, tr, f[r], p, s, q, j, a);
+    float accb[NT][4];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) accb[t][v] = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      // sub-scales ls = 1 + 2 * nibble of rows 4q + v: byte 8 (v >> 1) + 2 (u >> 1) + (v & 1), nibble u & 1
+      int ls[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const uint32_t word = f[r].sc[2 * (v >> 1) + (u >> 2)];
+        const int sh = 8 * (2 * ((u >> 1) & 1) + (v & 1)) + 4 * (u & 1);
+        ls[v] = 1 + 2 * (int)((word >> sh) & 0xFu);
+      }
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const long b = b_operand(x.b[t][u >> 1], u & 1);
+        const v4i zero = {0, 0, 0, 0};
+        const v4i c = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[u], b, zero, 0, 0, 0);
+        const float cd = __uint_as_float(x.d[t][u >> 2][u & 3]);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) accb[t][v] = fmaf((float)__mul24(c[v], ls[v]), cd, accb[t][v]);
+      }
+    }
+    const float d[4] = {half_bits_to_float(f[r].d01 & 0xFFFF), half_bits_to_float(f[r].d01 >> 16),
+                        half_bits_to_float(f[r].d23 & 0xFFFF), half_bits_to_float(f[r].d23 >> 16)};
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[r][t][v] = fmaf(accb[t][v], d[v], acc[r][t][v]);
+  }
+}
+
+template <int NT, int RW, int KS>
+__global__ void __launch_bounds__(64 * KS) gemm_iq3s_tile_kernel(const uint8_t* __restrict__ W, int64_t row_bytes,
+                                                                 int nrows, int k, const uint8_t* __restrict__ xq,
+                                                                 int nct, int n, void* __restrict__ y, int y_dtype) {
+  static_assert((KS - 1) * RW * NT * 4 * 64 * 4 <= 2048 * 16, "wave partials fit the table region");
+  __shared__ uint4 table[2048];  // signed-grid table; the waves' partial sums at the end
+  __shared__ uint4 trbuf[KS][kTrBytes / 16];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int p = lane >> 3, s = lane & 7;   // decode view
+  const int j = lane & 15, q = lane >> 4;  // MFMA view
+  const int ntiles = nrows / kTileRows;
+  const int tile0 = blockIdx.x * RW;
+  const int ct0 = blockIdx.y * NT;
+  const int nb = k / kQK;
+  const int b_begin = wave * nb / KS, b_end = (wave + 1) * nb / KS;
+  const int64_t tile_bytes = (int64_t)kTileRows * row_bytes;
+  const int tiles_here = ntiles - tile0 < RW ? ntiles - tile0 : RW;
+  // every load stays inside the workgroup's tiles and the xq buffer: a missing tile of the last
+  // workgroup re-reads its last tile (never stored), the prefetch past the wave's last block
+  // re-reads that block
+  const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(W + tile0 * tile_bytes, (uint32_t)(tiles_here * tile_bytes));
+  const int sbase = (int)xq_scale_base(nct, nb);
+  const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(xq, (uint32_t)xq_bytes((int64_t)nct * kXqCols, k));
+  const uint8_t* tbl = (const uint8_t*)table;
+  uint8_t* tr = (uint8_t*)trbuf[wave];
+
+  float acc[RW][NT][4];
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[r][t][v] = 0.0f;
+
+  MmaFrag fa[RW], fb[RW];
+  XqFrag<NT> xa, xb;
+  // column tiles past nct (last workgroup of the y grid) re-read column tile nct - 1 (never stored)
+  int units[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) units[t] = (ct0 + t < nct ? ct0 + t : nct - 1) * nb;
+  int toff[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) toff[r] = (int)((r < tiles_here ? r : tiles_here - 1) * tile_bytes);
+  const int b_last = b_end - 1;
+  if (b_begin < b_end) {
+    load_xq_frag<NT>(xrs, units, b_begin, sbase, lane, j, xa);
+#pragma unroll
+    for (int r = 0; r < RW; ++r) load_mma_frag(wrs, toff[r] + b_begin * kTileBlockBytes, lane, q, fa[r]);
+  }
+  iq3_table_to_lds<KS>(table, &kIq3sSignedMma, wave, lane);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int b = b_begin; b < b_end; b += 2) {
+    const int b1 = b + 1 < b_last ? b + 1 : b_last, b2 = b + 2 < b_last ? b + 2 : b_last;
+    load_xq_frag<NT>(xrs, units, b1, sbase, lane, j, xb);
+#pragma unroll
+    for (int r = 0; r < RW; ++r) load_mma_frag(wrs, toff[r] + b1 * kTileBlockBytes, lane, q, fb[r]);
+    mma_block<NT, RW>(tbl, tr, fa, xa, p, s, q, j, acc);
+    if (b + 1 >= b_end) break;
+    load_xq_frag<NT>(xrs, units, b2, sbase, lane, j, xa);
+#pragma unroll
+    for (int r = 0; r < RW; ++r) load_mma_frag(wrs, toff[r] + b2 * kTileBlockBytes, lane, q, fa[r]);
+    mma_block<NT, RW>(tbl, tr, fb, xb, p, s, q, j, acc);
+  }
+
+  // partial sums of waves 1.. through LDS (the table is no longer read), added in wave order
+  __syncthreads();
+  float* red = (float*)table;
+  if (wave > 0) {
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) red[((((wave - 1) * RW + r) * NT + t) * 4 + v) * 64 + lane] = acc[r][t][v];
+  }
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      if (r >= tiles_here) break;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const int col = (ct0 + t) * kXqCols + j;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          float sum = acc[r][t][v];
+          for (int w2 = 1; w2 < KS; ++w2) sum += red[((((w2 - 1) * RW + r) * NT + t) * 4 + v) * 64 + lane];
+          if (col < n) store_y(y, (int64_t)col * nrows + (int64_t)(tile0 + r) * kTileRows + 4 * q + v, sum, y_dtype);
+        }
+      }
+    }
+  }
+}
+
+template <int NT, int RW, int KS>
+void launch_tile_gemm(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n, void* y,
+                      int y_dtype, hipStream_t stream) {
+  const int nct = (int)xq_col_tiles(n);
+  const dim3 grid((unsigned)((nrows / kTileRows + RW - 1) / RW), (unsigned)((nct + NT - 1) / NT));
+  gemm_iq3s_tile_kernel<NT, RW, KS><<<grid, 64 * KS, 0, stream>>>(W, row_bytes, nrows, k, xq, nct, n, y, y_dtype);
+}
+
+}  // namespace
+
+// IQ3_S in the tile layout; nrows % 16 == 0; xq: X in the xq layout (launch_quantize_xq).
+// Launch shapes measured at 17408 x 5120, 5120 x 17408 and 5120 x 5120: four waves per tile,
+// eight for one column tile on matrices of fewer than 512 tiles (more waves per tile to fill
+// the GPU); above 64 activation rows the y grid walks groups of four column tiles.
+hipError_t launch_gemm_packed_xq(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n,
+                                 void* y, int y_dtype, hipStream_t stream) {
+  const int nct = (int)xq_col_tiles(n);
+  const bool few = nrows / kTileRows < 512;
+  if (nct == 1) {
+    if (few) launch_tile_gemm<1, 1, 8>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
+    else launch_tile_gemm<1, 1, 4>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
+  } else if (nct == 2) {
+    launch_tile_gemm<2, 1, 4>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
+  } else if (nct == 3) {
+    launch_tile_gemm<3, 1, 4>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
+  } else {
+    launch_tile_gemm<4, 1, 4>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace gguf

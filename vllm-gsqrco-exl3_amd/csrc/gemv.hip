@@ -168,14 +168,6 @@ struct TileFrag {
   uint32_t l2, sc, dd;
 };
 
-// Buffer-descriptor loads (raw buffer loads: SGPR descriptor + VGPR lane offset + SGPR offset +
-// immediate), so the K loop spends no vector instructions on addresses. gfx9 descriptor word 3.
-constexpr int kBufDword3 = 0x00020000;
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, kBufDword3);
-}
-
 // per-lane byte offsets of a lane's data inside a tile-block (constant over the K loop)
 struct TileOffs {
   uint32_t qs, e8, l2, sc, dd;
@@ -220,12 +212,6 @@ __device__ __forceinline__ void load_x_frag(__amdgpu_buffer_rsrc_t rs, uint32_t 
   }
 }
 
-// signed-grid words of the table entries for the two groups a byte permute pairs in P
-__device__ __forceinline__ void tile_lookup2(const uint8_t* tbl, uint32_t P, int& w0, int& w1) {
-  w0 = *(const int*)(tbl + ((P & 0xFFFFu) << 2));
-  w1 = *(const int*)(tbl + (P >> 14));  // bits 14, 15 of P are zero (ex has 5 bits)
-}
-
 template <int NC>
 __device__ __forceinline__ void tile_compute(const uint8_t* tbl, const TileFrag& f, const XFrag<NC>& x, int s,
                                              float (&acc)[2][NC]) {
@@ -250,17 +236,6 @@ __device__ __forceinline__ void tile_compute(const uint8_t* tbl, const TileFrag&
       acc[r][c] = fmaf((float)sumi, dl * x.d[c], acc[r][c]);
     }
   }
-}
-
-// the 32 KB signed-grid table, global -> LDS without VGPRs: 32 wave-wide 1 KB DMA loads shared
-// out over the workgroup's waves (global_load_lds_dwordx4)
-template <int WPT>
-__device__ __forceinline__ void table_to_lds(uint4* table, int wave, int lane) {
-  const uint4* src = (const uint4*)kIq3sSignedDev.v;
-#pragma unroll
-  for (int i = wave; i < 32; i += WPT)
-    __builtin_amdgcn_global_load_lds((const void*)(src + i * 64 + lane),
-                                     (__attribute__((address_space(3))) void*)(table + i * 64), 16, 0, 0);
 }
 
 template <int NC, int TPW, int WPT>
@@ -301,7 +276,7 @@ __global__ void __launch_bounds__(64 * TPW * WPT) gemv_iq3s_tile_kernel(const ui
   TileFrag fa, fb;
   if (b_begin < b_end) load_tile_frag(wrs, b_begin * kTileBlockBytes, off, fa);
   if (b_begin + 1 < b_end) load_tile_frag(wrs, (b_begin + 1) * kTileBlockBytes, off, fb);
-  table_to_lds<TPW * WPT>(table, wv, lane);
+  iq3_table_to_lds<TPW * WPT>(table, &kIq3sSignedDev, wv, lane);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   for (int b = b_begin; b < b_end; b += 2) {

@@ -99,6 +99,15 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t h) {
 
 __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
+// Buffer-descriptor loads (raw buffer loads: SGPR descriptor + VGPR lane offset + SGPR offset +
+// immediate), so K loops spend no vector instructions on addresses; a load past `bytes` returns
+// zero. gfx9 descriptor word 3.
+constexpr int kBufDword3 = 0x00020000;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, kBufDword3);
+}
+
 // fp32 -> storage dtype with round-to-nearest-even (as torch's casts)
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
   uint32_t u = __float_as_uint(f);

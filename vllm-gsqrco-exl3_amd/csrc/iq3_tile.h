@@ -126,22 +126,23 @@ __device__ __forceinline__ void iq3_tile_ex(uint32_t e8, uint32_t l2, int r, uin
   hi = ((e8 >> 5) & 0x07070707u) | (t2 << 3);
 }
 
-// Values 8q..8q+7 (groups 2q, 2q+1) of slice u of row li (0..15) from a tile-block, through the
-// signed-grid table (in LDS), for the MFMA kernel's lane mapping.
-__device__ __forceinline__ void decode_iq3s_tile_q(const uint8_t* t, int li, int u, int q, const uint32_t* table,
-                                                   int (&w)[2], float& d, int& ls) {
-  const int L = 8 * (li >> 1) + u, r = li & 1;
-  const uint32_t qs = *(const uint16_t*)(t + kTqs + 16 * L + 8 * r + 2 * q);
-  const uint32_t e8 = *(const uint32_t*)(t + kTe8 + 8 * L + 4 * r);
-  const uint32_t l2 = *(const uint16_t*)(t + kTl2 + 2 * L);
-  uint32_t lo, hi;
-  iq3_tile_ex(e8, l2, r, lo, hi);
-  const uint32_t ex = q < 2 ? lo : hi;
-  const int j = 2 * (q & 1);
-  w[0] = (int)table[(qs & 0xFF) | (((ex >> (8 * j)) & 0xFF) << 8)];
-  w[1] = (int)table[(qs >> 8) | (((ex >> (8 * j + 8)) & 0xFF) << 8)];
-  d = half_bits_to_float(*(const uint16_t*)(t + kTd + 4 * (li >> 1) + 2 * r));
-  ls = 1 + 2 * ((t[kTsc + 2 * (4 * (li >> 1) + (u >> 1)) + r] >> (4 * (u & 1))) & 0xF);
+// signed-grid words of the table entries for the two groups a byte permute pairs in P
+// (P = qs0 | ex0 << 8 | qs1 << 16 | ex1 << 24; tbl is the table in LDS)
+__device__ __forceinline__ void tile_lookup2(const uint8_t* tbl, uint32_t P, int& w0, int& w1) {
+  w0 = *(const int*)(tbl + ((P & 0xFFFFu) << 2));
+  w1 = *(const int*)(tbl + (P >> 14));  // bits 14, 15 of P are zero (ex has 5 bits)
+}
+
+// The 32 KB signed-grid table, global -> LDS without VGPRs: 32 wave-wide 1 KB DMA loads
+// (global_load_lds_dwordx4) shared out over the workgroup's NW waves. The caller waits
+// (vmcnt) and synchronises the workgroup before reading the table.
+template <int NW>
+__device__ __forceinline__ void iq3_table_to_lds(uint4* table, const Iq3sSignedTable* src_table, int wave, int lane) {
+  const uint4* src = (const uint4*)src_table->v;
+#pragma unroll
+  for (int i = wave; i < 32; i += NW)
+    __builtin_amdgcn_global_load_lds((const void*)(src + i * 64 + lane),
+                                     (__attribute__((address_space(3))) void*)(table + i * 64), 16, 0, 0);
 }
 
 }  // namespace gguf

@@ -1,6 +1,6 @@
 // q8_1 activation quantisation on gfx950.
 //
-// Two output layouts, both bit-exact with the reference's arithmetic:
+// Three output layouts; the first two are the reference's, bit-exact with its arithmetic:
 //  * block_q8_1 (decode GEMV input), lcpp_shim.cu:274-294: per 32 values d = amax/127 (IEEE
 //    division), q = amax == 0 ? 0 : roundf(x/d), sum by a 32-lane xor butterfly with offsets
 //    16, 8, 4, 2, 1, stored as half2(d, sum) followed by 32 int8; block (row, k/32) row-major.
@@ -8,10 +8,12 @@
 //    q = roundf(x*d_inv), d = 1/d_inv; 144-byte blocks of 128 values, block index
 //    (k/128)*n + row, 16 bytes of scales (4 x fp32 d, or 4 x half2(d, sum) for Q4_K) then 128
 //    int8. An all-zero 32-block stores q = 0, d = 0 (the reference's NaN -> 0 conversion).
+//  * the xq layout of the tile GEMM (xq.h): the MMQ arithmetic, values placed as MFMA B operands.
 //
 // Wave64 mapping: the MMVQ kernel gives each 32-lane half-wave one block (one value per lane);
 // the MMQ kernel gives each lane 4 consecutive values, 8 lanes per 32-block.
 #include "gguf_common.h"
+#include "xq.h"
 
 namespace gguf {
 
@@ -93,6 +95,68 @@ __global__ void __launch_bounds__(128) quantize_q8_1_mmq_kernel(const void* __re
       *(float*)(b + 4 * (iqs / 32)) = d;
     }
   }
+}
+
+// The MFMA GEMMs' layout (xq.h), with the MMQ arithmetic above. Thread i takes 8 consecutive
+// values (one quarter of a slice) of padded activation row c = i / (k/8); the 4 quarters of a
+// slice are 4 consecutive lanes. Rows c >= n (padding of the last column tile) write zeros.
+template <int DT>
+__global__ void __launch_bounds__(256) quantize_xq_kernel(const void* __restrict__ x, uint8_t* __restrict__ y,
+                                                          int64_t k, int64_t s01, int n, int64_t total) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;  // total % 4 == 0: whole slices exit together
+  const int64_t per_row = k / 8;
+  const int64_t c = i / per_row;
+  const int64_t kk = (i - c * per_row) * 8;
+  float v[8];
+  if (c < n) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = ldx<DT>(x, c * s01 + kk + e);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = 0.0f;
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+  amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+  uint32_t lo = 0, hi = 0;
+  float d = 0.0f;
+  if (amax != 0.0f) {
+    const float d_inv = 127.0f / amax;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      lo |= ((uint32_t)(int)roundf(v[e] * d_inv) & 0xFFu) << (8 * e);
+      hi |= ((uint32_t)(int)roundf(v[4 + e] * d_inv) & 0xFFu) << (8 * e);
+    }
+    d = 1.0f / d_inv;
+  }
+  const int64_t nb = k / kQK;
+  const int64_t b = kk / kQK;
+  const int u = (int)((kk / kQ81) & 7), q = (int)((kk / 8) & 3);
+  const int64_t t = c / kXqCols;
+  const int j = (int)(c % kXqCols);
+  const int64_t unit = t * nb + b;
+  *(uint2*)(y + unit * kXqUnit + (16 * q + j) * 64 + 8 * u) = make_uint2(lo, hi);
+  if (q == 0) {
+    const int64_t nct = total / per_row / kXqCols;
+    *(float*)(y + xq_scale_base(nct, nb) + (unit * kXqCols + j) * 32 + 4 * u) = d;
+  }
+}
+
+// X [n, k] -> the xq layout at y (xq_bytes(n, k) bytes).
+hipError_t launch_quantize_xq(const void* x, int dtype, int64_t n, int64_t k, int64_t s01, void* y,
+                              hipStream_t stream) {
+  if (n == 0) return hipSuccess;
+  const int64_t total = xq_col_tiles(n) * kXqCols * (k / 8);
+  const unsigned blocks = (unsigned)((total + 255) / 256);
+  switch (dtype) {
+    case kF32: quantize_xq_kernel<kF32><<<blocks, 256, 0, stream>>>(x, (uint8_t*)y, k, s01, (int)n, total); break;
+    case kF16: quantize_xq_kernel<kF16><<<blocks, 256, 0, stream>>>(x, (uint8_t*)y, k, s01, (int)n, total); break;
+    default: quantize_xq_kernel<kBF16><<<blocks, 256, 0, stream>>>(x, (uint8_t*)y, k, s01, (int)n, total); break;
+  }
+  return hipGetLastError();
 }
 
 // X [n, k] (row stride s01 elements, dtype DT) -> q8 bytes at y.

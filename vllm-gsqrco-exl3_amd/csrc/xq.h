@@ -1,0 +1,36 @@
+// The build's q8 activation layout for the int8-MFMA GEMMs ("xq"), an internal workspace format
+// (the reference's block_q8_1_mmq, mmq.cuh:27-56, serves its CUDA mma fragments; the values and
+// scales here are the same, only their placement differs).
+//
+// Activation rows are grouped in column tiles of 16 (the B-operand width of
+// v_mfma_i32_16x16x32_i8); rows past n in the last tile are zero. For column tile t and 256-value
+// K block b (nb = K / 256 blocks):
+//   values  4096 B at ((t * nb + b) * 4096): lane l = 16q + j of a wave owns, for the block's
+//           slices u = 0..7, the eight q8 values 32u + 8q .. 32u + 8q + 7 of activation row
+//           16t + j, 8 bytes at 64l + 8u. One wave reads a (t, b) unit with four contiguous
+//           16-byte loads per lane, and those bytes are the MFMA B operands of the 8 slices.
+//   scales  512 B at nct * nb * 4096 + ((t * nb + b) * 16 + j) * 32: fp32 d of slices u = 0..7
+//           of activation row 16t + j.
+// Quantisation per 32-value slice is the reference's MMQ arithmetic (lcpp_shim.cu:298-355):
+// d_inv = 127 / amax, q = roundf(x * d_inv), d = 1 / d_inv, and q = 0, d = 0 for an all-zero
+// slice.
+#pragma once
+
+#include "gguf_common.h"
+
+namespace gguf {
+
+constexpr int kXqCols = 16;         // activation rows per column tile
+constexpr int kXqUnit = 4096;       // value bytes per (column tile, K block)
+constexpr int kXqScaleUnit = 512;   // scale bytes per (column tile, K block)
+
+__host__ __device__ inline int64_t xq_col_tiles(int64_t n) { return (n + kXqCols - 1) / kXqCols; }
+
+__host__ __device__ inline int64_t xq_scale_base(int64_t nct, int64_t nb) { return nct * nb * kXqUnit; }
+
+__host__ __device__ inline size_t xq_bytes(int64_t n, int64_t k) {
+  const int64_t nct = xq_col_tiles(n), nb = k / kQK;
+  return (size_t)(nct * nb * (kXqUnit + kXqScaleUnit));
+}
+
+}  // namespace gguf
