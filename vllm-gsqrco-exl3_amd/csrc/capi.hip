@@ -26,8 +26,10 @@ hipError_t launch_gemm(int type, const uint8_t* W, int64_t row_bytes, int nrows,
                        void* y, int y_dtype, hipStream_t stream);
 hipError_t launch_gemv_packed(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n,
                               void* y, int y_dtype, hipStream_t stream);
-hipError_t launch_quantize_xq(const void* x, int dtype, int64_t n, int64_t k, int64_t s01, void* y,
+hipError_t launch_quantize_xq(const void* x, int dtype, int64_t n, int64_t k, int64_t s01, int type, void* y,
                               hipStream_t stream);
+hipError_t launch_gemm_xq(int type, const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n,
+                          void* y, int y_dtype, hipStream_t stream);
 hipError_t launch_gemm_packed_xq(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n,
                                  void* y, int y_dtype, hipStream_t stream);
 hipError_t launch_iq3_pack(uint8_t* w, int64_t rows, int64_t row_bytes, bool unpack, uint8_t* scratch,
@@ -196,11 +198,10 @@ size_t gguf_q8_1_bytes(int64_t n, int64_t k, int mmq) {
 }
 
 size_t gguf_op_workspace_bytes(int op, int64_t type, int64_t row, int64_t k, int64_t n, int has_x_q8) {
-  (void)type;
   (void)row;
   if (n <= 0) return 0;
   if (op_packed(op) && (op == GGUF_OP_MUL_MAT_IQ3_PACKED || n > 8)) return align256(gguf::xq_bytes(n, k));
-  if (op_gemm(op)) return align256(gguf_q8_1_bytes(n, k, 1));
+  if (op_gemm(op)) return align256(type == gguf::kIQ3_S ? gguf_q8_1_bytes(n, k, 1) : gguf::xq_bytes(n, k));
   return has_x_q8 ? 0 : align256(gguf_q8_1_bytes(n, k, 0));
 }
 
@@ -232,9 +233,16 @@ int gguf_mul_mat(int op, const gguf_view* W, const gguf_view* X, int64_t type, i
 
   if (gemm) {
     if (packed) {
-      e = gguf::launch_quantize_xq(X->data, X->dtype, n, k, s01, workspace, s);
+      e = gguf::launch_quantize_xq(X->data, X->dtype, n, k, s01, (int)type, workspace, s);
       if (e != hipSuccess) return hip_fail(e, name, "quantize");
       e = gguf::launch_gemm_packed_xq(w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace, (int)n, y, ydt, s);
+      if (e != hipSuccess) return hip_fail(e, name, "gemm");
+      return GGUF_OK;
+    }
+    if (type != gguf::kIQ3_S) {
+      e = gguf::launch_quantize_xq(X->data, X->dtype, n, k, s01, (int)type, workspace, s);
+      if (e != hipSuccess) return hip_fail(e, name, "quantize");
+      e = gguf::launch_gemm_xq((int)type, w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace, (int)n, y, ydt, s);
       if (e != hipSuccess) return hip_fail(e, name, "gemm");
       return GGUF_OK;
     }

@@ -13,6 +13,7 @@
 //    combined in int32 as the reference does; Q4_K's min term uses the integer q8 sum;
 //  * the 4 waves' partial sums are added in wave order through LDS (deterministic).
 #include "decode.h"
+#include "xq.h"
 
 namespace gguf {
 
@@ -182,6 +183,322 @@ hipError_t launch_gemm(int type, const uint8_t* W, int64_t row_bytes, int nrows,
     case kQ4_K: launch_gemm_t<kQ4_K>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream); break;
     case kIQ4_XS: launch_gemm_t<kIQ4_XS>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream); break;
     case kQ6_K: launch_gemm_t<kQ6_K>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+
+// ---------------------------------------------------------------------------------------------
+// Q4_K / IQ4_XS / Q6_K on plain GGUF rows, activations in the xq layout (xq.h).
+//  * a workgroup owns one 16-row tile and NT column tiles; its KS waves split the K blocks;
+//  * per K block lane 16q + j loads, from weight row j, the bytes of values 8q..8q+7 of every
+//    slice (Q4_K: four 8-byte loads, each holding two slices as low / high nibbles; IQ4_XS: one
+//    8-byte load per slice, codebook through byte permutes; Q6_K: four ql and two qh loads), so
+//    the decoded words are the MFMA A operands directly; the row headers of the four C rows
+//    4q..4q+3 it accumulates come with 8- or 16-byte loads;
+//  * one v_mfma_i32_16x16x32_i8 per (slice, column tile) is the reference's integer slice dot
+//    (Q6_K: two, one per 16-value sub-scale, combined in int32 as the reference does);
+//  * per slice the dot is scaled by the integer sub-scale and the fp32 activation scale, summed
+//    over the block, then multiplied by the row's block scale (Q4_K: minus dmin times the
+//    min-term sum of m * d8 * sum(q8), with d8 in fp16 as the reference's half2 MMQ layout);
+//  * next block's loads are issued before the current block is computed (two register sets);
+//    the waves' partial sums are added in wave order.
+namespace {
+
+constexpr int kRawRows = 16;  // weight rows per workgroup (the MFMA A rows)
+
+template <int TYPE>
+struct RawFrag;
+template <>
+struct RawFrag<kQ4_K> {
+  uint32_t qs[8];  // 8-byte quarter c = 0..3: slices 2c (low nibbles), 2c+1 (high)
+  u32x4 hdr[4];    // d | dmin << 16, scales[0..3], scales[4..7], scales[8..11] of C row 4q + v
+};
+template <>
+struct RawFrag<kIQ4_XS> {
+  uint32_t qs[16];    // slice u: bytes 8 (q & 1) .. of qs[16u..], nibble q >> 1
+  uint32_t hdr[4][2]; // d | scales_h << 16, scales_l of C row 4q + v
+};
+template <>
+struct RawFrag<kQ6_K> {
+  uint32_t ql[8];  // (n, h) = 2n + h: ql[64n + 32h + 8q ..], 8 bytes
+  uint32_t qh[4];  // n: qh[32n + 8q ..], 8 bytes
+  u32x4 sc[4];     // 16 int8 sub-scales of C row 4q + v
+  uint32_t d[4];   // fp16 d of C row 4q + v
+};
+
+__device__ __forceinline__ void ld64w(__amdgpu_buffer_rsrc_t rs, int voff, int soff, uint32_t* dst) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, voff, soff, 0);
+  dst[0] = v[0];
+  dst[1] = v[1];
+}
+
+// row_off: j * row_bytes; crow_off[v]: (4q + v) * row_bytes; soff: block offset
+template <int TYPE>
+__device__ __forceinline__ void load_raw_frag(__amdgpu_buffer_rsrc_t rs, int row_off, const int (&crow_off)[4],
+                                              int soff, int q, RawFrag<TYPE>& f) {
+  if constexpr (TYPE == kQ4_K) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) ld64w(rs, row_off + 16 + 32 * c + 8 * q, soff, &f.qs[2 * c]);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) f.hdr[v] = __builtin_amdgcn_raw_buffer_load_b128(rs, crow_off[v], soff, 0);
+  } else if constexpr (TYPE == kIQ4_XS) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) ld64w(rs, row_off + 8 + 16 * u + 8 * (q & 1), soff, &f.qs[2 * u]);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) ld64w(rs, crow_off[v], soff, f.hdr[v]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ld64w(rs, row_off + 64 * (i >> 1) + 32 * (i & 1) + 8 * q, soff, &f.ql[2 * i]);
+#pragma unroll
+    for (int n = 0; n < 2; ++n) ld64w(rs, row_off + 128 + 32 * n + 8 * q, soff, &f.qh[2 * n]);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      f.sc[v] = __builtin_amdgcn_raw_buffer_load_b128(rs, crow_off[v] + 192, soff, 0);
+      f.d[v] = __builtin_amdgcn_raw_buffer_load_b16(rs, crow_off[v] + 208, soff, 0);
+    }
+  }
+}
+
+__device__ __forceinline__ long pack_a(uint32_t lo, uint32_t hi) { return (long)(((uint64_t)hi << 32) | lo); }
+
+// A operand of slice u (values 8q..8q+7 of the lane's row)
+template <int TYPE>
+__device__ __forceinline__ long raw_a(const RawFrag<TYPE>& f, int u, int q) {
+  if constexpr (TYPE == kQ4_K) {
+    const int c = u >> 1, sh = 4 * (u & 1);
+    return pack_a((f.qs[2 * c] >> sh) & 0x0F0F0F0Fu, (f.qs[2 * c + 1] >> sh) & 0x0F0F0F0Fu);
+  } else if constexpr (TYPE == kIQ4_XS) {
+    const int sh = 4 * (q >> 1);
+    return pack_a((uint32_t)lut16((f.qs[2 * u] >> sh) & 0x0F0F0F0Fu),
+                  (uint32_t)lut16((f.qs[2 * u + 1] >> sh) & 0x0F0F0F0Fu));
+  } else {
+    const int n = u >> 2, sub = u & 3, i = 2 * n + (sub & 1);
+    const int lsh = 4 * (sub >> 1), hsh = 2 * sub;
+    const uint32_t w0 = (uint32_t)sub32_bytes(((f.ql[2 * i] >> lsh) & 0x0F0F0F0Fu) |
+                                              (((f.qh[2 * n] >> hsh) & 0x03030303u) << 4));
+    const uint32_t w1 = (uint32_t)sub32_bytes(((f.ql[2 * i + 1] >> lsh) & 0x0F0F0F0Fu) |
+                                              (((f.qh[2 * n + 1] >> hsh) & 0x03030303u) << 4));
+    return pack_a(w0, w1);
+  }
+}
+
+// Q4_K 6-bit scale and min of sub-block u from scales[0..11] (get_scale_min_k4,
+// csrc/gguf/dequantize.cuh:156-163)
+__device__ __forceinline__ void q4k_sm(const u32x4& h, int u, int& sc, int& m) {
+  const int jj = u & 3;
+  const uint32_t a = (h[1] >> (8 * jj)) & 0xFF, c = (h[2] >> (8 * jj)) & 0xFF, e = (h[3] >> (8 * jj)) & 0xFF;
+  if (u < 4) {
+    sc = (int)(a & 63);
+    m = (int)(c & 63);
+  } else {
+    sc = (int)((e & 0xF) | ((a >> 6) << 4));
+    m = (int)((e >> 4) | ((c >> 6) << 4));
+  }
+}
+
+template <int NT>
+struct XRawFrag {
+  u32x4 b[NT][4];  // B operands: slices 2i, 2i+1 in b[t][i]
+  u32x4 d[NT][2];  // scale words of slices 0..7
+};
+
+template <int NT>
+__device__ __forceinline__ void load_xraw(__amdgpu_buffer_rsrc_t rs, const int (&units)[NT], int b, int sbase, int lane,
+                                          int j, XRawFrag<NT>& x) {
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int unit = units[t] + b;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      x.b[t][i] = __builtin_amdgcn_raw_buffer_load_b128(rs, 64 * lane + 16 * i, unit * kXqUnit, 0);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      x.d[t][i] = __builtin_amdgcn_raw_buffer_load_b128(rs, 32 * j + 16 * i, sbase + unit * kXqScaleUnit, 0);
+  }
+}
+
+template <int TYPE, int NT>
+__device__ __forceinline__ void raw_block(const RawFrag<TYPE>& f, const XRawFrag<NT>& x, int q, float (&acc)[NT][4]) {
+  float accb[NT][4], accm[NT][4];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) accb[t][v] = accm[t][v] = 0.0f;
+  const v4i zero = {0, 0, 0, 0};
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const long a = raw_a<TYPE>(f, u, q);
+    int s1[4], s2[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      if constexpr (TYPE == kQ4_K) {
+        q4k_sm(f.hdr[v], u, s1[v], s2[v]);
+      } else if constexpr (TYPE == kIQ4_XS) {
+        const uint32_t sl = (f.hdr[v][1] >> (8 * (u >> 1) + 4 * (u & 1))) & 0xF;
+        const uint32_t shh = (f.hdr[v][0] >> (16 + 2 * u)) & 3u;
+        s1[v] = (int)(sl | (shh << 4)) - 32;
+      } else {
+        const uint32_t word = f.sc[v][u >> 1];
+        s1[v] = (int)(int8_t)((word >> (16 * (u & 1))) & 0xFF);
+        s2[v] = (int)(int8_t)((word >> (16 * (u & 1) + 8)) & 0xFF);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const long b = xq_b_operand(x.b[t][u >> 1], u & 1);
+      const uint32_t sw = x.d[t][u >> 2][u & 3];
+      // Q4_K: fp16 d | int16 sum(q) << 16; other types: fp32 d
+      const float cd = TYPE == kQ4_K ? half_bits_to_float(sw & 0xFFFF) : __uint_as_float(sw);
+      if constexpr (TYPE == kQ6_K) {
+        const v4i c0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(q < 2 ? a : 0, b, zero, 0, 0, 0);
+        const v4i c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(q < 2 ? 0 : a, b, zero, 0, 0, 0);
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          accb[t][v] = fmaf((float)(__mul24(c0[v], s1[v]) + __mul24(c1[v], s2[v])), cd, accb[t][v]);
+      } else {
+        const v4i c = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, zero, 0, 0, 0);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) accb[t][v] = fmaf((float)__mul24(c[v], s1[v]), cd, accb[t][v]);
+        if constexpr (TYPE == kQ4_K) {
+          const float cs = cd * (float)(int)(int16_t)(sw >> 16);
+#pragma unroll
+          for (int v = 0; v < 4; ++v) accm[t][v] = fmaf((float)s2[v], cs, accm[t][v]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    float d, dmin = 0.0f;
+    if constexpr (TYPE == kQ4_K) {
+      d = half_bits_to_float(f.hdr[v][0] & 0xFFFF);
+      dmin = half_bits_to_float(f.hdr[v][0] >> 16);
+    } else if constexpr (TYPE == kIQ4_XS) {
+      d = half_bits_to_float(f.hdr[v][0] & 0xFFFF);
+    } else {
+      d = half_bits_to_float(f.d[v] & 0xFFFF);
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      acc[t][v] = fmaf(accb[t][v], d, acc[t][v]);
+      if constexpr (TYPE == kQ4_K) acc[t][v] = fmaf(-accm[t][v], dmin, acc[t][v]);
+    }
+  }
+}
+
+template <int TYPE, int NT, int KS>
+__global__ void __launch_bounds__(64 * KS) gemm_raw_kernel(const uint8_t* __restrict__ W, int64_t row_bytes, int nrows,
+                                                           int k, const uint8_t* __restrict__ xq, int nct, int n,
+                                                           void* __restrict__ y, int y_dtype) {
+  constexpr int BS = block_bytes(TYPE);
+  __shared__ float red[KS > 1 ? KS - 1 : 1][NT][4][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 15, q = lane >> 4;
+  const int row0 = blockIdx.x * kRawRows;
+  const int rows_here = nrows - row0 < kRawRows ? nrows - row0 : kRawRows;
+  const int ct0 = blockIdx.y * NT;
+  const int nb = k / kQK;
+  const int b_begin = wave * nb / KS, b_end = (wave + 1) * nb / KS;
+  // rows past nrows lie past the descriptor's size and read zeros
+  const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(W + (int64_t)row0 * row_bytes, (uint32_t)(rows_here * row_bytes));
+  const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(xq, (uint32_t)xq_bytes((int64_t)nct * kXqCols, k));
+  const int sbase = (int)xq_scale_base(nct, nb);
+  const int row_off = j * (int)row_bytes;
+  int crow_off[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) crow_off[v] = (4 * q + v) * (int)row_bytes;
+  int units[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) units[t] = (ct0 + t < nct ? ct0 + t : nct - 1) * nb;
+
+  float acc[NT][4];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[t][v] = 0.0f;
+
+  // Two blocks per iteration (an odd last block after the loop); every load feeds a use that is
+  // not behind a branch of its own (a load whose only use is conditional is sunk to it); the
+  // scheduling barriers keep the next block's decode below the loads just issued. The prefetch
+  // past the wave's last block reads zeros through an empty descriptor and is never used.
+  const __amdgpu_buffer_rsrc_t nrs = buffer_rsrc(W, 0);
+  RawFrag<TYPE> fa, fb;
+  XRawFrag<NT> xa, xb;
+  const int b_last = b_end - 1;
+  if (b_begin < b_end) {
+    load_xraw<NT>(xrs, units, b_begin, sbase, lane, j, xa);
+    load_raw_frag<TYPE>(wrs, row_off, crow_off, b_begin * BS, q, fa);
+  }
+  const int nblk = b_end - b_begin;
+  int b = b_begin;
+  for (int it = 0; it < nblk / 2; ++it, b += 2) {
+    const int b2 = b + 2 < b_last ? b + 2 : b_last;
+    const __amdgpu_buffer_rsrc_t rs2 = b + 2 < b_end ? wrs : nrs;
+    load_xraw<NT>(xrs, units, b + 1, sbase, lane, j, xb);
+    load_raw_frag<TYPE>(wrs, row_off, crow_off, (b + 1) * BS, q, fb);
+    __builtin_amdgcn_sched_barrier(0);
+    raw_block<TYPE, NT>(fa, xa, q, acc);
+    load_xraw<NT>(xrs, units, b2, sbase, lane, j, xa);
+    load_raw_frag<TYPE>(rs2, row_off, crow_off, (b + 2) * BS, q, fa);
+    __builtin_amdgcn_sched_barrier(0);
+    raw_block<TYPE, NT>(fb, xb, q, acc);
+  }
+  if (nblk & 1) raw_block<TYPE, NT>(fa, xa, q, acc);
+
+  if constexpr (KS > 1) {
+    if (wave > 0) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) red[wave - 1][t][v][lane] = acc[t][v];
+    }
+    __syncthreads();
+  }
+  if (wave == 0) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int col = (ct0 + t) * kXqCols + j;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        float sum = acc[t][v];
+        for (int w2 = 1; w2 < KS; ++w2) sum += red[w2 - 1][t][v][lane];
+        const int row = 4 * q + v;
+        if (col < n && row < rows_here) store_y(y, (int64_t)col * nrows + row0 + row, sum, y_dtype);
+      }
+    }
+  }
+}
+
+template <int TYPE, int NT, int KS>
+void launch_raw_t(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n, void* y,
+                  int y_dtype, hipStream_t stream) {
+  const int nct = (int)xq_col_tiles(n);
+  const dim3 grid((unsigned)((nrows + kRawRows - 1) / kRawRows), (unsigned)((nct + NT - 1) / NT));
+  gemm_raw_kernel<TYPE, NT, KS><<<grid, 64 * KS, 0, stream>>>(W, row_bytes, nrows, k, xq, nct, n, y, y_dtype);
+}
+
+template <int TYPE>
+void launch_raw_type(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n, void* y,
+                     int y_dtype, hipStream_t stream) {
+  const int nct = (int)xq_col_tiles(n);
+  if (nct == 1) launch_raw_t<TYPE, 1, 4>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
+  else if (nct == 2) launch_raw_t<TYPE, 2, 4>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
+  else if (nct == 3) launch_raw_t<TYPE, 3, 4>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
+  else launch_raw_t<TYPE, 4, 4>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
+}
+
+}  // namespace
+
+// Q4_K / IQ4_XS / Q6_K rows; xq: X in the xq layout (launch_quantize_xq).
+hipError_t launch_gemm_xq(int type, const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n,
+                          void* y, int y_dtype, hipStream_t stream) {
+  switch (type) {
+    case kQ4_K: launch_raw_type<kQ4_K>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream); break;
+    case kIQ4_XS: launch_raw_type<kIQ4_XS>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream); break;
+    case kQ6_K: launch_raw_type<kQ6_K>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

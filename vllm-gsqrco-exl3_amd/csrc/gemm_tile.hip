@@ -75,10 +75,6 @@ __device__ __forceinline__ void load_xq_frag(__amdgpu_buffer_rsrc_t rs, const in
   }
 }
 
-__device__ __forceinline__ long b_operand(const u32x4& v, int h) {
-  return h == 0 ? (long)(((uint64_t)v[1] << 32) | v[0]) : (long)(((uint64_t)v[3] << 32) | v[2]);
-}
-
 // decode one tile-block (decode view) into the wave's transposition buffer, then read the 8
 // A operands (MFMA view)
 __device__ __forceinline__ void tile_to_a(const uint8_t* tbl, uint8_t* tr, const MmaFrag& f, int p, int s, int q, int j,
@@ -143,7 +139,7 @@ __device__ __forceinline__ void mma_block(const uint8_t* tbl, uint8_t* tr, const
       }
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        const long b = b_operand(x.b[t][u >> 1], u & 1);
+        const long b = xq_b_operand(x.b[t][u >> 1], u & 1);
         const v4i zero = {0, 0, 0, 0};
         const v4i c = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[u], b, zero, 0, 0, 0);
         const float cd = __uint_as_float(x.d[t][u >> 2][u & 3]);
@@ -204,6 +200,11 @@ __global__ void __launch_bounds__(64 * KS) gemm_iq3s_tile_kernel(const uint8_t* 
   int toff[RW];
 #pragma unroll
   for (int r = 0; r < RW; ++r) toff[r] = (int)((r < tiles_here ? r : tiles_here - 1) * tile_bytes);
+  // Two blocks per iteration (an odd last block after the loop); every load feeds a use that is
+  // not behind a branch of its own (the compiler sinks a load whose only use is conditional to
+  // that use, which would serialise the prefetch). The prefetch past the wave's last block reads
+  // zeros through an empty descriptor and is never used.
+  const __amdgpu_buffer_rsrc_t nrs = buffer_rsrc(W, 0);
   const int b_last = b_end - 1;
   if (b_begin < b_end) {
     load_xq_frag<NT>(xrs, units, b_begin, sbase, lane, j, xa);
@@ -213,18 +214,24 @@ __global__ void __launch_bounds__(64 * KS) gemm_iq3s_tile_kernel(const uint8_t* 
   iq3_table_to_lds<KS>(table, &kIq3sSignedMma, wave, lane);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  for (int b = b_begin; b < b_end; b += 2) {
-    const int b1 = b + 1 < b_last ? b + 1 : b_last, b2 = b + 2 < b_last ? b + 2 : b_last;
-    load_xq_frag<NT>(xrs, units, b1, sbase, lane, j, xb);
+  const int nblk = b_end - b_begin;
+  int b = b_begin;
+  for (int it = 0; it < nblk / 2; ++it, b += 2) {
+    const int b2 = b + 2 < b_last ? b + 2 : b_last;
+    const __amdgpu_buffer_rsrc_t rs2 = b + 2 < b_end ? wrs : nrs;
+    load_xq_frag<NT>(xrs, units, b + 1, sbase, lane, j, xb);
 #pragma unroll
-    for (int r = 0; r < RW; ++r) load_mma_frag(wrs, toff[r] + b1 * kTileBlockBytes, lane, q, fb[r]);
+    for (int r = 0; r < RW; ++r) load_mma_frag(wrs, toff[r] + (b + 1) * kTileBlockBytes, lane, q, fb[r]);
+    __builtin_amdgcn_sched_barrier(0);  // the scheduler hoists the next block's decode (and its
+                                        // wait) above these loads otherwise
     mma_block<NT, RW>(tbl, tr, fa, xa, p, s, q, j, acc);
-    if (b + 1 >= b_end) break;
     load_xq_frag<NT>(xrs, units, b2, sbase, lane, j, xa);
 #pragma unroll
-    for (int r = 0; r < RW; ++r) load_mma_frag(wrs, toff[r] + b2 * kTileBlockBytes, lane, q, fa[r]);
+    for (int r = 0; r < RW; ++r) load_mma_frag(rs2, toff[r] + (b + 2) * kTileBlockBytes, lane, q, fa[r]);
+    __builtin_amdgcn_sched_barrier(0);
     mma_block<NT, RW>(tbl, tr, fb, xb, p, s, q, j, acc);
   }
+  if (nblk & 1) mma_block<NT, RW>(tbl, tr, fa, xa, p, s, q, j, acc);
 
   // partial sums of waves 1.. through LDS (the table is no longer read), added in wave order
   __syncthreads();

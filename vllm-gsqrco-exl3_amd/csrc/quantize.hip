@@ -100,7 +100,7 @@ __global__ void __launch_bounds__(128) quantize_q8_1_mmq_kernel(const void* __re
 // The MFMA GEMMs' layout (xq.h), with the MMQ arithmetic above. Thread i takes 8 consecutive
 // values (one quarter of a slice) of padded activation row c = i / (k/8); the 4 quarters of a
 // slice are 4 consecutive lanes. Rows c >= n (padding of the last column tile) write zeros.
-template <int DT>
+template <int DT, bool DS4>
 __global__ void __launch_bounds__(256) quantize_xq_kernel(const void* __restrict__ x, uint8_t* __restrict__ y,
                                                           int64_t k, int64_t s01, int n, int64_t total) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -123,15 +123,20 @@ __global__ void __launch_bounds__(256) quantize_xq_kernel(const void* __restrict
   amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
   uint32_t lo = 0, hi = 0;
   float d = 0.0f;
+  int qsum = 0;
   if (amax != 0.0f) {
     const float d_inv = 127.0f / amax;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      lo |= ((uint32_t)(int)roundf(v[e] * d_inv) & 0xFFu) << (8 * e);
-      hi |= ((uint32_t)(int)roundf(v[4 + e] * d_inv) & 0xFFu) << (8 * e);
+      const int q0 = (int)roundf(v[e] * d_inv), q1 = (int)roundf(v[4 + e] * d_inv);
+      lo |= ((uint32_t)q0 & 0xFFu) << (8 * e);
+      hi |= ((uint32_t)q1 & 0xFFu) << (8 * e);
+      qsum += q0 + q1;
     }
     d = 1.0f / d_inv;
   }
+  qsum += __shfl_xor(qsum, 1, 64);
+  qsum += __shfl_xor(qsum, 2, 64);
   const int64_t nb = k / kQK;
   const int64_t b = kk / kQK;
   const int u = (int)((kk / kQ81) & 7), q = (int)((kk / 8) & 3);
@@ -141,21 +146,27 @@ __global__ void __launch_bounds__(256) quantize_xq_kernel(const void* __restrict
   *(uint2*)(y + unit * kXqUnit + (16 * q + j) * 64 + 8 * u) = make_uint2(lo, hi);
   if (q == 0) {
     const int64_t nct = total / per_row / kXqCols;
-    *(float*)(y + xq_scale_base(nct, nb) + (unit * kXqCols + j) * 32 + 4 * u) = d;
+    uint32_t word = __float_as_uint(d);
+    if constexpr (DS4) word = (uint32_t)__half_as_ushort(__float2half_rn(d)) | ((uint32_t)qsum << 16);
+    *(uint32_t*)(y + xq_scale_base(nct, nb) + (unit * kXqCols + j) * 32 + 4 * u) = word;
   }
 }
 
-// X [n, k] -> the xq layout at y (xq_bytes(n, k) bytes).
-hipError_t launch_quantize_xq(const void* x, int dtype, int64_t n, int64_t k, int64_t s01, void* y,
+// X [n, k] -> the xq layout at y (xq_bytes(n, k) bytes) for weights of ggml type `type`.
+hipError_t launch_quantize_xq(const void* x, int dtype, int64_t n, int64_t k, int64_t s01, int type, void* y,
                               hipStream_t stream) {
   if (n == 0) return hipSuccess;
   const int64_t total = xq_col_tiles(n) * kXqCols * (k / 8);
   const unsigned blocks = (unsigned)((total + 255) / 256);
+#define GGUF_QXQ(DT)                                                                                       \
+  if (type == kQ4_K) quantize_xq_kernel<DT, true><<<blocks, 256, 0, stream>>>(x, (uint8_t*)y, k, s01, (int)n, total); \
+  else quantize_xq_kernel<DT, false><<<blocks, 256, 0, stream>>>(x, (uint8_t*)y, k, s01, (int)n, total);
   switch (dtype) {
-    case kF32: quantize_xq_kernel<kF32><<<blocks, 256, 0, stream>>>(x, (uint8_t*)y, k, s01, (int)n, total); break;
-    case kF16: quantize_xq_kernel<kF16><<<blocks, 256, 0, stream>>>(x, (uint8_t*)y, k, s01, (int)n, total); break;
-    default: quantize_xq_kernel<kBF16><<<blocks, 256, 0, stream>>>(x, (uint8_t*)y, k, s01, (int)n, total); break;
+    case kF32: GGUF_QXQ(kF32) break;
+    case kF16: GGUF_QXQ(kF16) break;
+    default: GGUF_QXQ(kBF16) break;
   }
+#undef GGUF_QXQ
   return hipGetLastError();
 }
 

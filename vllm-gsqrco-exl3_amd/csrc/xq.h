@@ -9,11 +9,13 @@
 //           slices u = 0..7, the eight q8 values 32u + 8q .. 32u + 8q + 7 of activation row
 //           16t + j, 8 bytes at 64l + 8u. One wave reads a (t, b) unit with four contiguous
 //           16-byte loads per lane, and those bytes are the MFMA B operands of the 8 slices.
-//   scales  512 B at nct * nb * 4096 + ((t * nb + b) * 16 + j) * 32: fp32 d of slices u = 0..7
-//           of activation row 16t + j.
+//   scales  512 B at nct * nb * 4096 + ((t * nb + b) * 16 + j) * 32: one dword per slice
+//           u = 0..7 of activation row 16t + j: fp32 d, or for Q4_K weights fp16 d in the low half
+//           and the slice's int16 sum of q above it (d * sum is the activation side of Q4_K's
+//           min term; |sum| <= 4064, and fp16 d times it is exact in fp32).
 // Quantisation per 32-value slice is the reference's MMQ arithmetic (lcpp_shim.cu:298-355):
 // d_inv = 127 / amax, q = roundf(x * d_inv), d = 1 / d_inv, and q = 0, d = 0 for an all-zero
-// slice.
+// slice; for Q4_K d is stored as fp16 as in the reference's half2 (DS4) MMQ layout.
 #pragma once
 
 #include "gguf_common.h"
@@ -31,6 +33,11 @@ __host__ __device__ inline int64_t xq_scale_base(int64_t nct, int64_t nb) { retu
 __host__ __device__ inline size_t xq_bytes(int64_t n, int64_t k) {
   const int64_t nct = xq_col_tiles(n), nb = k / kQK;
   return (size_t)(nct * nb * (kXqUnit + kXqScaleUnit));
+}
+
+// MFMA B operand of slice 2i + h from the 16 bytes b[t][i] of a lane's xq unit
+__device__ __forceinline__ long xq_b_operand(const u32x4& v, int h) {
+  return h == 0 ? (long)(((uint64_t)v[1] << 32) | v[0]) : (long)(((uint64_t)v[3] << 32) | v[2]);
 }
 
 }  // namespace gguf
