@@ -271,19 +271,36 @@ def test_packed_ops_vs_q81(n, k):
     x = _x(n, k, seed=n + 500)
     op = "lcpp_mul_mat_vec_iq3_mma_packed" if n <= 32 else "lcpp_mul_mat_iq3_packed"
     y = getattr(C(), op)(w, x.cuda(), o.IQ3_S, rows).cpu().numpy()
-    ref = o.q81_model(raw, o.IQ3_S, x, layout="mmvq" if n <= 8 else "mmq")
+    # the decode op quantises X as block_q8_1 at every row count (lcpp_shim.cu:883-888)
+    ref = o.q81_model(raw, o.IQ3_S, x, layout="mmvq" if n <= 32 else "mmq")
     assert o.rel_l2(y, ref) <= 1e-3, o.rel_l2(y, ref)
 
 
 # ------------------------------------------------------------------------------------ x_q8, graphs
 @pytest.mark.parametrize("qt", TYPES, ids=lambda t: TN[t])
-def test_shared_x_q8_equals_own_quantize(qt):
-    rows, k, n = 64, 1024, 4
-    raw = _dev(_w(qt, rows, k, seed=80))
-    x = _x(n, k, seed=81, dtype=torch.bfloat16).cuda()
+@pytest.mark.parametrize("n", [2, 4, 8])
+def test_shared_x_q8_equals_own_quantize(qt, n):
+    """A caller's x_q8 gives the same bits as the op's own quantisation, on the GEMV and (from a
+    per-type row count on) on the MFMA GEMM, which converts x_q8 into its operand layout."""
+    rows, k = 64, 1024
+    raw = _dev(_w(qt, rows, k, seed=80 + n))
+    x = _x(n, k, seed=81 + n, dtype=torch.bfloat16).cuda()
     q8 = C().lcpp_quantize_q8_1(x, qt, False, False)
     a = getattr(C(), VEC_OP[qt])(raw, x, qt, rows)
     b = getattr(C(), VEC_OP[qt])(raw, x, qt, rows, q8)
+    assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("n", [4, 8, 24])
+def test_shared_x_q8_packed(n):
+    from vllm_gguf_plugin.quantization import iq3_pack
+
+    rows, k = 64, 1024
+    w = iq3_pack.pack(_dev(_w(o.IQ3_S, rows, k, seed=90 + n)), o.IQ3_S)
+    x = _x(n, k, seed=91 + n, dtype=torch.bfloat16).cuda()
+    q8 = C().lcpp_quantize_q8_1(x, o.IQ3_S, False, False)
+    a = C().lcpp_mul_mat_vec_iq3_mma_packed(w, x, o.IQ3_S, rows)
+    b = C().lcpp_mul_mat_vec_iq3_mma_packed(w, x, o.IQ3_S, rows, q8)
     assert torch.equal(a, b)
 
 

@@ -26,8 +26,9 @@ hipError_t launch_gemm(int type, const uint8_t* W, int64_t row_bytes, int nrows,
                        void* y, int y_dtype, hipStream_t stream);
 hipError_t launch_gemv_packed(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n,
                               void* y, int y_dtype, hipStream_t stream);
-hipError_t launch_quantize_xq(const void* x, int dtype, int64_t n, int64_t k, int64_t s01, int type, void* y,
-                              hipStream_t stream);
+hipError_t launch_quantize_xq(const void* x, int dtype, int64_t n, int64_t k, int64_t s01, int type, bool vec,
+                              void* y, hipStream_t stream);
+hipError_t launch_q8_1_to_xq(const void* q8, int64_t n, int64_t k, int type, void* y, hipStream_t stream);
 hipError_t launch_gemm_xq(int type, const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n,
                           void* y, int y_dtype, hipStream_t stream);
 hipError_t launch_gemm_packed_xq(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n,
@@ -197,11 +198,28 @@ size_t gguf_q8_1_bytes(int64_t n, int64_t k, int mmq) {
   return mmq ? (size_t)(n * k / 128 * 144) : (size_t)(n * k / gguf::kQ81 * 36);
 }
 
+namespace {
+
+// Decode ops (1..8 rows; the packed IQ3 op up to 32) go to the int8-MFMA GEMM from this many
+// activation rows on, measured against the dot4 GEMV at the 27B-layer shapes: the GEMV's time
+// grows with every row, the GEMM's is flat up to 16. IQ3_S on plain rows stays on the GEMV.
+int64_t vec_mma_from(int op, int64_t type) {
+  if (op_packed(op)) return 5;
+  if (type == gguf::kQ4_K || type == gguf::kQ6_K) return 3;
+  if (type == gguf::kIQ4_XS) return 5;
+  return INT64_MAX;
+}
+
+}  // namespace
+
 size_t gguf_op_workspace_bytes(int op, int64_t type, int64_t row, int64_t k, int64_t n, int has_x_q8) {
   (void)row;
   if (n <= 0) return 0;
-  if (op_packed(op) && (op == GGUF_OP_MUL_MAT_IQ3_PACKED || n > 8)) return align256(gguf::xq_bytes(n, k));
-  if (op_gemm(op)) return align256(type == gguf::kIQ3_S ? gguf_q8_1_bytes(n, k, 1) : gguf::xq_bytes(n, k));
+  if (op_gemm(op)) {
+    const bool mmq_layout = !op_packed(op) && type == gguf::kIQ3_S;
+    return align256(mmq_layout ? gguf_q8_1_bytes(n, k, 1) : gguf::xq_bytes(n, k));
+  }
+  if (n >= vec_mma_from(op, type)) return align256(gguf::xq_bytes(n, k));  // x_q8 is converted into it
   return has_x_q8 ? 0 : align256(gguf_q8_1_bytes(n, k, 0));
 }
 
@@ -216,8 +234,8 @@ int gguf_mul_mat(int op, const gguf_view* W, const gguf_view* X, int64_t type, i
   if (type == kIQ3_XXS) return fail("%s: unsupported ggml type %lld", name, (long long)type);
   if (y_bytes < (size_t)(n * row * elem_size(X->dtype))) return fail("%s: output buffer too small", name);
   const bool packed = op_packed(op);
-  const bool gemm = op_gemm(op) || (op == GGUF_OP_MUL_MAT_VEC_IQ3_MMA_PACKED && n > 8);
-  const size_t need = gguf_op_workspace_bytes(op, type, row, k, n, x_q8 != nullptr && !gemm);
+  const bool gemm = op_gemm(op);
+  const size_t need = gguf_op_workspace_bytes(op, type, row, k, n, x_q8 != nullptr);
   if (workspace_bytes < need || (need > 0 && !workspace))
     return fail("%s: workspace of %zu bytes needed, got %zu", name, need, workspace_bytes);
   if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0) return fail("%s: workspace must be 16-byte aligned", name);
@@ -231,21 +249,22 @@ int gguf_mul_mat(int op, const gguf_view* W, const gguf_view* X, int64_t type, i
   const int64_t row_bytes = W->size[1];
   const int ydt = X->dtype;
 
-  if (gemm) {
-    if (packed) {
-      e = gguf::launch_quantize_xq(X->data, X->dtype, n, k, s01, (int)type, workspace, s);
-      if (e != hipSuccess) return hip_fail(e, name, "quantize");
-      e = gguf::launch_gemm_packed_xq(w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace, (int)n, y, ydt, s);
-      if (e != hipSuccess) return hip_fail(e, name, "gemm");
-      return GGUF_OK;
-    }
-    if (type != gguf::kIQ3_S) {
-      e = gguf::launch_quantize_xq(X->data, X->dtype, n, k, s01, (int)type, workspace, s);
-      if (e != hipSuccess) return hip_fail(e, name, "quantize");
-      e = gguf::launch_gemm_xq((int)type, w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace, (int)n, y, ydt, s);
-      if (e != hipSuccess) return hip_fail(e, name, "gemm");
-      return GGUF_OK;
-    }
+  // int8-MFMA GEMMs on the xq layout: the product ops with the MMQ arithmetic, the decode ops
+  // (from vec_mma_from rows on) with the decode ops' q8_1 arithmetic or the caller's x_q8
+  if ((gemm && (packed || type != gguf::kIQ3_S)) || (!gemm && n >= vec_mma_from(op, type))) {
+    if (!gemm && x_q8)
+      e = gguf::launch_q8_1_to_xq(x_q8->data, n, k, (int)type, workspace, s);
+    else
+      e = gguf::launch_quantize_xq(X->data, X->dtype, n, k, s01, (int)type, !gemm, workspace, s);
+    if (e != hipSuccess) return hip_fail(e, name, "quantize");
+    e = packed ? gguf::launch_gemm_packed_xq(w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace, (int)n, y,
+                                             ydt, s)
+               : gguf::launch_gemm_xq((int)type, w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace, (int)n,
+                                      y, ydt, s);
+    if (e != hipSuccess) return hip_fail(e, name, "gemm");
+    return GGUF_OK;
+  }
+  if (gemm) {  // IQ3_S on plain rows: the MMQ layout and the per-slice MFMA GEMM
     e = gguf::launch_quantize(X->data, X->dtype, n, k, s01, (int)type, true, workspace, s);
     if (e != hipSuccess) return hip_fail(e, name, "quantize");
     e = gguf::launch_gemm((int)type, w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace, (int)n, y, ydt, s);

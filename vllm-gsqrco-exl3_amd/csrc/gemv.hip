@@ -193,7 +193,7 @@ __device__ __forceinline__ void load_tile_frag(__amdgpu_buffer_rsrc_t rs, uint32
 template <int NC>
 struct XFrag {
   int q[NC][8];
-  float d[NC];
+  uint32_t d[NC];  // fp16 bits (converted where used, so a prefetch does not wait for its load)
 };
 
 // q8_1 blocks of X at slice `slice0 + s` for every activation row c (row c starts nslices
@@ -204,7 +204,7 @@ __device__ __forceinline__ void load_x_frag(__amdgpu_buffer_rsrc_t rs, uint32_t 
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     const int so = (c * nslices + slice0) * 36;
-    x.d[c] = half_bits_to_float(__builtin_amdgcn_raw_buffer_load_b16(rs, (int)lane_off, so, 0));
+    x.d[c] = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)lane_off, so, 0);
     const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)lane_off, so + 4, 0);
     const u32x4 e = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)lane_off, so + 20, 0);
     x.q[c][0] = (int)a.x; x.q[c][1] = (int)a.y; x.q[c][2] = (int)a.z; x.q[c][3] = (int)a.w;
@@ -233,7 +233,7 @@ __device__ __forceinline__ void tile_compute(const uint8_t* tbl, const TileFrag&
       int sumi = 0;
 #pragma unroll
       for (int e = 0; e < 8; ++e) sumi = dot4(w[e], x.q[c][e], sumi);
-      acc[r][c] = fmaf((float)sumi, dl * x.d[c], acc[r][c]);
+      acc[r][c] = fmaf((float)sumi, dl * half_bits_to_float(x.d[c]), acc[r][c]);
     }
   }
 }
@@ -269,30 +269,40 @@ __global__ void __launch_bounds__(64 * TPW * WPT) gemv_iq3s_tile_kernel(const ui
 #pragma unroll
     for (int c = 0; c < NC; ++c) acc[i][c] = 0.0f;
 
-  // the first two weight blocks of the wave, then the table DMA; the wait before the barrier
-  // covers both. Two named weight buffers (A: blocks b, b+2, ...; B: b+1, b+3, ...) keep one
-  // block in flight while the other is computed, with no register copies; the q8_1 blocks of X
-  // (L1-resident) are loaded just before use.
+  // Two named register sets (A, B) for the weight tile-block and the q8_1 blocks of X; the next
+  // block's loads are issued before the current block is computed. Two blocks per iteration and
+  // an odd last block after the loop, so that no load is behind a branch: a load under a branch
+  // makes the compiler wait for it before the next compute (vmcnt(0) on the joined paths), and
+  // one whose only use is conditional is sunk to that use. The weight prefetch past the wave's
+  // last block reads zeros through an empty descriptor and is never used; the X prefetch is
+  // clamped to the last block. The scheduling barriers keep the next block's decode below the
+  // loads just issued.
+  const __amdgpu_buffer_rsrc_t nrs = buffer_rsrc(W, 0);
+  const int b_last = b_end - 1;
+  const int nblk = b_end - b_begin;
   TileFrag fa, fb;
-  if (b_begin < b_end) load_tile_frag(wrs, b_begin * kTileBlockBytes, off, fa);
-  if (b_begin + 1 < b_end) load_tile_frag(wrs, (b_begin + 1) * kTileBlockBytes, off, fb);
+  XFrag<NC> xa, xb;
+  if (nblk > 0) {
+    load_x_frag<NC>(xrs, xoff, nslices, b_begin * 8, xa);
+    load_tile_frag(wrs, b_begin * kTileBlockBytes, off, fa);
+  }
   iq3_table_to_lds<TPW * WPT>(table, &kIq3sSignedDev, wv, lane);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  for (int b = b_begin; b < b_end; b += 2) {
-    {
-      XFrag<NC> x;
-      load_x_frag<NC>(xrs, xoff, nslices, b * 8, x);
-      tile_compute<NC>(tbl, fa, x, s, acc);
-    }
-    if (b + 2 < b_end) load_tile_frag(wrs, (b + 2) * kTileBlockBytes, off, fa);
-    if (b + 1 < b_end) {
-      XFrag<NC> x;
-      load_x_frag<NC>(xrs, xoff, nslices, (b + 1) * 8, x);
-      tile_compute<NC>(tbl, fb, x, s, acc);
-      if (b + 3 < b_end) load_tile_frag(wrs, (b + 3) * kTileBlockBytes, off, fb);
-    }
+  int b = b_begin;
+  for (int it = 0; it < nblk / 2; ++it, b += 2) {
+    const int b2 = b + 2 < b_last ? b + 2 : b_last;
+    const __amdgpu_buffer_rsrc_t rs2 = b + 2 < b_end ? wrs : nrs;
+    load_x_frag<NC>(xrs, xoff, nslices, (b + 1) * 8, xb);
+    load_tile_frag(wrs, (b + 1) * kTileBlockBytes, off, fb);
+    __builtin_amdgcn_sched_barrier(0);
+    tile_compute<NC>(tbl, fa, xa, s, acc);
+    load_x_frag<NC>(xrs, xoff, nslices, b2 * 8, xa);
+    load_tile_frag(rs2, (b + 2) * kTileBlockBytes, off, fa);
+    __builtin_amdgcn_sched_barrier(0);
+    tile_compute<NC>(tbl, fb, xb, s, acc);
   }
+  if (nblk & 1) tile_compute<NC>(tbl, fa, xa, s, acc);
 
 #pragma unroll
   for (int i = 0; i < 2; ++i) {

@@ -8,7 +8,8 @@
 //    q = roundf(x*d_inv), d = 1/d_inv; 144-byte blocks of 128 values, block index
 //    (k/128)*n + row, 16 bytes of scales (4 x fp32 d, or 4 x half2(d, sum) for Q4_K) then 128
 //    int8. An all-zero 32-block stores q = 0, d = 0 (the reference's NaN -> 0 conversion).
-//  * the xq layout of the tile GEMM (xq.h): the MMQ arithmetic, values placed as MFMA B operands.
+//  * the xq layout of the MFMA GEMMs (xq.h): either arithmetic above, values placed as MFMA B
+//    operands (and a converter from block_q8_1 bytes).
 //
 // Wave64 mapping: the MMVQ kernel gives each 32-lane half-wave one block (one value per lane);
 // the MMQ kernel gives each lane 4 consecutive values, 8 lanes per 32-block.
@@ -97,10 +98,32 @@ __global__ void __launch_bounds__(128) quantize_q8_1_mmq_kernel(const void* __re
   }
 }
 
-// The MFMA GEMMs' layout (xq.h), with the MMQ arithmetic above. Thread i takes 8 consecutive
-// values (one quarter of a slice) of padded activation row c = i / (k/8); the 4 quarters of a
-// slice are 4 consecutive lanes. Rows c >= n (padding of the last column tile) write zeros.
-template <int DT, bool DS4>
+// The MFMA GEMMs' layout (xq.h). Thread i takes 8 consecutive values (one quarter of a slice) of
+// padded activation row c = i / (k/8); the 4 quarters of a slice are 4 consecutive lanes. Rows
+// c >= n (padding of the last column tile) write zeros. VEC selects the block_q8_1 arithmetic of
+// the reference's decode ops (d = amax/127, q = roundf(x/d), d kept as fp16) instead of the MMQ
+// arithmetic; DS4 (Q4_K weights) stores fp16 d with the slice's int16 sum of q.
+template <bool VEC, bool DS4>
+__device__ __forceinline__ void xq_store(uint8_t* y, int64_t k, int64_t c, int64_t kk, int64_t total, uint32_t lo,
+                                         uint32_t hi, float d, int qsum) {
+  const int64_t per_row = k / 8;
+  const int64_t nb = k / kQK;
+  const int64_t b = kk / kQK;
+  const int u = (int)((kk / kQ81) & 7), q = (int)((kk / 8) & 3);
+  const int64_t t = c / kXqCols;
+  const int j = (int)(c % kXqCols);
+  const int64_t unit = t * nb + b;
+  *(uint2*)(y + unit * kXqUnit + (16 * q + j) * 64 + 8 * u) = make_uint2(lo, hi);
+  if (q == 0) {
+    const int64_t nct = total / per_row / kXqCols;
+    const uint32_t dh = __half_as_ushort(__float2half_rn(d));
+    uint32_t word = VEC ? __float_as_uint(half_bits_to_float(dh)) : __float_as_uint(d);
+    if constexpr (DS4) word = dh | ((uint32_t)qsum << 16);
+    *(uint32_t*)(y + xq_scale_base(nct, nb) + (unit * kXqCols + j) * 32 + 4 * u) = word;
+  }
+}
+
+template <int DT, bool VEC, bool DS4>
 __global__ void __launch_bounds__(256) quantize_xq_kernel(const void* __restrict__ x, uint8_t* __restrict__ y,
                                                           int64_t k, int64_t s01, int n, int64_t total) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -124,49 +147,81 @@ __global__ void __launch_bounds__(256) quantize_xq_kernel(const void* __restrict
   uint32_t lo = 0, hi = 0;
   float d = 0.0f;
   int qsum = 0;
+  if (VEC) d = amax / 127.0f;
   if (amax != 0.0f) {
     const float d_inv = 127.0f / amax;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int q0 = (int)roundf(v[e] * d_inv), q1 = (int)roundf(v[4 + e] * d_inv);
-      lo |= ((uint32_t)q0 & 0xFFu) << (8 * e);
-      hi |= ((uint32_t)q1 & 0xFFu) << (8 * e);
-      qsum += q0 + q1;
+    for (int e = 0; e < 8; ++e) {
+      const int qe = VEC ? (int)roundf(v[e] / d) : (int)roundf(v[e] * d_inv);
+      if (e < 4) lo |= ((uint32_t)qe & 0xFFu) << (8 * e);
+      else hi |= ((uint32_t)qe & 0xFFu) << (8 * (e - 4));
+      qsum += qe;
     }
-    d = 1.0f / d_inv;
+    if (!VEC) d = 1.0f / d_inv;
   }
   qsum += __shfl_xor(qsum, 1, 64);
   qsum += __shfl_xor(qsum, 2, 64);
-  const int64_t nb = k / kQK;
-  const int64_t b = kk / kQK;
-  const int u = (int)((kk / kQ81) & 7), q = (int)((kk / 8) & 3);
-  const int64_t t = c / kXqCols;
-  const int j = (int)(c % kXqCols);
-  const int64_t unit = t * nb + b;
-  *(uint2*)(y + unit * kXqUnit + (16 * q + j) * 64 + 8 * u) = make_uint2(lo, hi);
-  if (q == 0) {
-    const int64_t nct = total / per_row / kXqCols;
-    uint32_t word = __float_as_uint(d);
-    if constexpr (DS4) word = (uint32_t)__half_as_ushort(__float2half_rn(d)) | ((uint32_t)qsum << 16);
-    *(uint32_t*)(y + xq_scale_base(nct, nb) + (unit * kXqCols + j) * 32 + 4 * u) = word;
-  }
+  xq_store<VEC, DS4>(y, k, c, kk, total, lo, hi, d, qsum);
 }
 
-// X [n, k] -> the xq layout at y (xq_bytes(n, k) bytes) for weights of ggml type `type`.
-hipError_t launch_quantize_xq(const void* x, int dtype, int64_t n, int64_t k, int64_t s01, int type, void* y,
-                              hipStream_t stream) {
+// block_q8_1 bytes of X (a caller's x_q8) -> the xq layout with the same values and fp16 scales.
+template <bool DS4>
+__global__ void __launch_bounds__(256) q8_1_to_xq_kernel(const uint8_t* __restrict__ q8, uint8_t* __restrict__ y,
+                                                         int64_t k, int n, int64_t total) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  const int64_t per_row = k / 8;
+  const int64_t c = i / per_row;
+  const int64_t kk = (i - c * per_row) * 8;
+  uint32_t lo = 0, hi = 0;
+  float d = 0.0f;
+  if (c < n) {
+    const uint8_t* blk = q8 + (c * (k / kQ81) + kk / kQ81) * 36;
+    const uint32_t* qv = (const uint32_t*)(blk + 4 + (kk % kQ81));
+    lo = qv[0];
+    hi = qv[1];
+    d = half_bits_to_float(*(const uint16_t*)blk);
+  }
+  int qsum = dot4((int)lo, 0x01010101, dot4((int)hi, 0x01010101, 0));
+  qsum += __shfl_xor(qsum, 1, 64);
+  qsum += __shfl_xor(qsum, 2, 64);
+  xq_store<true, DS4>(y, k, c, kk, total, lo, hi, d, qsum);
+}
+
+// X [n, k] -> the xq layout at y (xq_bytes(n, k) bytes) for weights of ggml type `type`; vec:
+// the decode ops' q8_1 arithmetic, else the MMQ arithmetic.
+hipError_t launch_quantize_xq(const void* x, int dtype, int64_t n, int64_t k, int64_t s01, int type, bool vec,
+                              void* y, hipStream_t stream) {
   if (n == 0) return hipSuccess;
   const int64_t total = xq_col_tiles(n) * kXqCols * (k / 8);
   const unsigned blocks = (unsigned)((total + 255) / 256);
-#define GGUF_QXQ(DT)                                                                                       \
-  if (type == kQ4_K) quantize_xq_kernel<DT, true><<<blocks, 256, 0, stream>>>(x, (uint8_t*)y, k, s01, (int)n, total); \
-  else quantize_xq_kernel<DT, false><<<blocks, 256, 0, stream>>>(x, (uint8_t*)y, k, s01, (int)n, total);
-  switch (dtype) {
-    case kF32: GGUF_QXQ(kF32) break;
-    case kF16: GGUF_QXQ(kF16) break;
-    default: GGUF_QXQ(kBF16) break;
+  const bool ds4 = type == kQ4_K;
+#define GGUF_QXQ(DT, V, D) quantize_xq_kernel<DT, V, D><<<blocks, 256, 0, stream>>>(x, (uint8_t*)y, k, s01, (int)n, total)
+#define GGUF_QXQ_DT(DT)                          \
+  if (vec) {                                     \
+    if (ds4) GGUF_QXQ(DT, true, true);           \
+    else GGUF_QXQ(DT, true, false);              \
+  } else {                                       \
+    if (ds4) GGUF_QXQ(DT, false, true);          \
+    else GGUF_QXQ(DT, false, false);             \
   }
+  switch (dtype) {
+    case kF32: GGUF_QXQ_DT(kF32) break;
+    case kF16: GGUF_QXQ_DT(kF16) break;
+    default: GGUF_QXQ_DT(kBF16) break;
+  }
+#undef GGUF_QXQ_DT
 #undef GGUF_QXQ
+  return hipGetLastError();
+}
+
+// block_q8_1 of X [n, k] -> the xq layout at y.
+hipError_t launch_q8_1_to_xq(const void* q8, int64_t n, int64_t k, int type, void* y, hipStream_t stream) {
+  if (n == 0) return hipSuccess;
+  const int64_t total = xq_col_tiles(n) * kXqCols * (k / 8);
+  const unsigned blocks = (unsigned)((total + 255) / 256);
+  if (type == kQ4_K) q8_1_to_xq_kernel<true><<<blocks, 256, 0, stream>>>((const uint8_t*)q8, (uint8_t*)y, k, (int)n, total);
+  else q8_1_to_xq_kernel<false><<<blocks, 256, 0, stream>>>((const uint8_t*)q8, (uint8_t*)y, k, (int)n, total);
   return hipGetLastError();
 }
 
