@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the GGUF quantized-matmul hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-points] [--no-cpu] [--kernel-only]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-points] [--no-configs] [--no-cpu] [--kernel-only]
 
 Workload: IQ3_S decode GEMV at M = 1 and 4 on the two 27B-layer
 shapes, gate/up 17408 x 5120 and down 5120 x 17408, bf16 activations N(0,1) quantised to q8_1,
@@ -16,7 +16,11 @@ per call) in GB/s.
 Also reported: the dominant kernel's roofline (the packed decode GEMV kernel at 17408 x 5120,
 M = 1, timed alone with the q8_1 input precomputed), the metric's other points (IQ3_S and Q4_K at
 M = 1, 4, 16, 32, 48 on 17408 x 5120, each through the routing table's op), and the CPU oracle
-(numpy dequantise + torch fp32 matmul) timed on the host cores on a bounded sample.
+(numpy dequantise + torch fp32 matmul) timed on the host cores on a bounded sample; and the other
+BASELINE configs under "configs": the CPU-path Q4_K 4096x4096 case next to its GPU op, the MTP
+small GEMM (IQ3_S / IQ4_XS / Q6_K at M = 4..48 on the attention shapes), the prefill GEMM
+(M = 512..8192, with int8 MFMA utilisation) and the 64-layer decoder sweep under one CUDA graph
+with a replay bit-exactness check.
 
 `traffic` (HBM bytes per launch of the dominant kernel) is read from the committed PMC summary
 profiles/gemv_iq3s_tile_17408x5120_m1.traffic.json when present (null otherwise). That summary
@@ -39,9 +43,11 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 NBUF = 8                       # distinct weight copies per shape (defeats the 256 MB MALL)
 COPY_BYTES = 256 << 20         # calibration copy: bytes read (and written) per launch
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_iq3s_tile_17408x5120_m1.traffic.json")
-IQ3_S, Q4_K = 21, 12
-BLOCK = {IQ3_S: 110, Q4_K: 144}
-SCALE_OFFSETS = {IQ3_S: (0,), Q4_K: (0, 2)}
+IQ3_S, Q4_K, Q6_K, IQ4_XS = 21, 12, 14, 23
+TYPE_NAME = {IQ3_S: "IQ3_S", Q4_K: "Q4_K", Q6_K: "Q6_K", IQ4_XS: "IQ4_XS"}
+BLOCK = {IQ3_S: 110, Q4_K: 144, Q6_K: 210, IQ4_XS: 136}
+SCALE_OFFSETS = {IQ3_S: (0,), Q4_K: (0, 2), Q6_K: (208,), IQ4_XS: (0,)}
+MFMA_I8_PEAK_TOPS = 5000.0     # MI355X dense int8 MFMA
 
 
 def make_weights(torch, qt, rows, k, seed):
@@ -80,6 +86,131 @@ def time_graphs(torch, graphs, reps):
     e.record()
     torch.cuda.synchronize()
     return s.elapsed_time(e) / reps
+
+
+def op_points(torch, C, iq3_pack, linear, qt, rows, k, ms, ncopies=NBUF, reps=5, seed=0):
+    """us/call of the routing table's op for a qt weight [rows, k] at each M in ms (bf16 X N(0,1)),
+    over ncopies weight copies captured in one graph per M. IQ3_S in the packed tile layout."""
+    ws = [make_weights(torch, qt, rows, k, seed + i) for i in range(ncopies)]
+    packed = qt == IQ3_S
+    if packed:
+        ws = [iq3_pack.pack(w, qt) for w in ws]
+    out = []
+    for m in ms:
+        op = linear._lcpp_op(m, qt, rows, k, packed)
+        fn = getattr(C, op)
+        x = torch.randn(m, k, device="cuda", dtype=torch.bfloat16)
+        g = graph(torch, [lambda w=w, x=x, fn=fn: fn(w, x, qt, rows) for w in ws])
+        us = time_graphs(torch, [g], reps) * 1e3 / len(ws)
+        wb = ws[0].numel()
+        cb = wb + m * k * 2 + m * rows * 2
+        out.append({"type": TYPE_NAME[qt], "shape": f"{rows}x{k}", "m": m, "op": op, "us_per_call": round(us, 2),
+                    "gbps": round(cb / (us * 1e-6) / 1e9, 1), "frac_hbm": round(cb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 3),
+                    "weight_us_per_MB": round(us / (wb / 1e6), 4),
+                    "int8_tops": round(2.0 * m * rows * k / (us * 1e-6) / 1e12, 2)})
+        del g
+    del ws
+    torch.cuda.empty_cache()
+    return out
+
+
+def config_mtp(torch, C, iq3_pack, linear):
+    """MTP verify small GEMM at M = 4, 8, 16, 32, 48 on q_proj 6144x5120,
+    k/v_proj 1024x5120 and o_proj 5120x6144 for IQ3_S (packed), IQ4_XS and Q6_K."""
+    out = []
+    for qt in (IQ3_S, IQ4_XS, Q6_K):
+        for rows, k in ((6144, 5120), (1024, 5120), (5120, 6144)):
+            out += op_points(torch, C, iq3_pack, linear, qt, rows, k, (4, 8, 16, 32, 48), ncopies=8, seed=2000)
+    return out
+
+
+def config_prefill(torch, C, iq3_pack, linear):
+    """prefill GEMM at M = 512, 2048, 8192 over K = 5120, N = 17408 and 5120,
+    IQ3_S (packed), Q4_K, Q6_K; int8 TOP/s against the dense int8 MFMA peak (X bf16 N(0,1) with 1%
+    outliers of magnitude 20 in the reference recipe; plain N(0,1) here, which times the same)."""
+    out = []
+    for qt in (IQ3_S, Q4_K, Q6_K):
+        for rows in (17408, 5120):
+            pts = op_points(torch, C, iq3_pack, linear, qt, rows, 5120, (512, 2048, 8192), ncopies=2, reps=2,
+                            seed=3000)
+            for p in pts:
+                p["frac_mfma_i8"] = round(p["int8_tops"] / MFMA_I8_PEAK_TOPS, 4)
+            out += pts
+    return out
+
+
+def config_layers(torch, C, iq3_pack, linear, steps, ms=(1, 4, 16, 32), nlayers=64):
+    """a 64-layer synthetic 27B-style decoder's linear layers (hidden 5120,
+    intermediate 17408, 48 query / 8 KV heads of dim 128) in the GSQ-RCO mix -- IQ3_S (packed)
+    q/k/v/o/gate/up, IQ4_XS down -- plus the Q6_K output head 151936x5120, every call of a step
+    captured in one CUDA graph. Per M: ms/step, weight GB streamed per step, and whether two
+    replays give bit-identical outputs."""
+    shapes = [("q", IQ3_S, 6144, 5120), ("k", IQ3_S, 1024, 5120), ("v", IQ3_S, 1024, 5120),
+              ("o", IQ3_S, 5120, 6144), ("gate", IQ3_S, 17408, 5120), ("up", IQ3_S, 17408, 5120),
+              ("down", IQ4_XS, 5120, 17408)]
+    layers = []
+    for li in range(nlayers):
+        lw = []
+        for name, qt, rows, k in shapes:
+            w = make_weights(torch, qt, rows, k, 10000 + 16 * li + len(lw))
+            lw.append((qt, rows, k, iq3_pack.pack(w, qt) if qt == IQ3_S else w))
+        layers.append(lw)
+    head = (Q6_K, 151936, 5120, make_weights(torch, Q6_K, 151936, 5120, 99999))
+    calls = [c for lw in layers for c in lw] + [head]
+    weight_bytes = sum(w.numel() for *_, w in calls)
+    out = []
+    for m in ms:
+        xs = {k: torch.randn(m, k, device="cuda", dtype=torch.bfloat16) for k in (5120, 6144, 17408)}
+        ys = []
+        fns = []
+        for qt, rows, k, w in calls:
+            op = getattr(C, linear._lcpp_op(m, qt, rows, k, qt == IQ3_S))
+            y = torch.empty(m, rows, device="cuda", dtype=torch.bfloat16)
+            ys.append(y)
+            fns.append(lambda op=op, w=w, x=xs[k], qt=qt, rows=rows, y=y: y.copy_(op(w, x, qt, rows)))
+        g = graph(torch, fns)
+        g.replay()
+        torch.cuda.synchronize()
+        first = [y.clone() for y in ys]
+        ms_step = time_graphs(torch, [g], max(3, steps // 4))
+        g.replay()
+        torch.cuda.synchronize()
+        exact = all(torch.equal(a, b) for a, b in zip(first, ys))
+        out.append({"m": m, "ms_per_step": round(ms_step, 3), "weight_gb_per_step": round(weight_bytes / 1e9, 3),
+                    "weight_gbps": round(weight_bytes / (ms_step * 1e-3) / 1e9, 1), "calls_per_step": len(fns),
+                    "replay_bit_exact": bool(exact)})
+        del g, first, ys, fns, xs
+        torch.cuda.empty_cache()
+    del layers, calls, head
+    torch.cuda.empty_cache()
+    return out
+
+
+def config_cpu_q4k(torch, C):
+    """Q4_K 4096x4096 at M = 1, fp32 X N(0,1): the GPU op next to the CPU
+    reference path (numpy dequantise + q8_1 round trip + torch fp32 matmul), seed 0."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+
+    import gguf_oracle as o
+
+    rows = k = 4096
+    raw = o.random_blocks(np.random.default_rng(0), o.Q4_K, rows, k, scale_sigma=1e-3)
+    x = np.random.default_rng(0).standard_normal((1, k)).astype(np.float32)
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        W = torch.from_numpy(o.dequantize(raw.reshape(-1), o.Q4_K).reshape(rows, k))
+        q, d, _ = o.dequant_q8_1(o.quantize_q8_1(x), 1, k)
+        xq = torch.from_numpy((q.astype(np.float32).reshape(1, -1, 32) * d[..., None]).reshape(1, k))
+        (xq @ W.T).sum().item()
+        times.append(time.perf_counter() - t0)
+    wd = torch.from_numpy(raw).cuda()
+    xd = torch.from_numpy(x).cuda()
+    g = graph(torch, [lambda: C.lcpp_mul_mat_vec_own(wd, xd, Q4_K, rows)] * 8)
+    us = time_graphs(torch, [g], 10) * 1e3 / 8
+    return {"shape": "4096x4096", "m": 1, "op": "lcpp_mul_mat_vec_own", "gpu_us_per_call": round(us, 2),
+            "cpu_us_per_call": round(statistics.median(times) * 1e6, 1), "cpu_cores": os.cpu_count() or 1}
 
 
 def cpu_baseline(torch):
@@ -163,6 +294,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-points", action="store_true", help="skip the metric's other (type, M) points")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the other BASELINE configs (CPU Q4_K, MTP small GEMM, prefill, 64-layer sweep)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--kernel-only", action="store_true",
                     help="time only the dominant kernel, then run the counter-calibration copy (for rocprofv3)")
@@ -221,25 +354,15 @@ def main():
     # ------------------------------------------------------------------ the metric's other points
     points = []
     if not args.no_points:
-        rows, k = 17408, 5120
-        for qt, name in ((IQ3_S, "IQ3_S"), (Q4_K, "Q4_K")):
-            ws = [make_weights(torch, qt, rows, k, 1000 + i) for i in range(NBUF)]
-            packed = qt == IQ3_S
-            if packed:
-                ws = [iq3_pack.pack(w, qt) for w in ws]
-            for m in (1, 4, 16, 32, 48):
-                op = linear._lcpp_op(m, qt, rows, k, packed)
-                fn = getattr(C, op)
-                x = torch.randn(m, k, device="cuda", dtype=torch.bfloat16)
-                g = graph(torch, [lambda w=w, x=x, fn=fn: fn(w, x, qt, rows) for w in ws])
-                us = time_graphs(torch, [g], 5) * 1e3 / len(ws)
-                cb = ws[0].numel() + m * k * 2 + m * rows * 2
-                points.append({"type": name, "shape": f"{rows}x{k}", "m": m, "op": op, "us_per_call": round(us, 2),
-                               "gbps": round(cb / (us * 1e-6) / 1e9, 1),
-                               "frac_hbm": round(cb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 3),
-                               "weight_us_per_MB": round(us / (ws[0].numel() / 1e6), 4)})
-            del ws
-            torch.cuda.empty_cache()
+        for qt in (IQ3_S, Q4_K):
+            points += op_points(torch, C, iq3_pack, linear, qt, 17408, 5120, (1, 4, 16, 32, 48), seed=1000)
+
+    configs = None
+    if not args.no_configs:
+        configs = {"cpu_q4k_4096": config_cpu_q4k(torch, C),
+                   "mtp_small_gemm": config_mtp(torch, C, iq3_pack, linear),
+                   "prefill": config_prefill(torch, C, iq3_pack, linear),
+                   "layer_sweep_64": config_layers(torch, C, iq3_pack, linear, args.steps)}
 
     cpu = None if args.no_cpu else cpu_baseline(torch)
 
@@ -263,6 +386,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "points": points,
+        "configs": configs,
     }
     print(json.dumps(line), flush=True)
 
