@@ -291,13 +291,17 @@ def test_shared_x_q8_equals_own_quantize(qt, n):
     assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("n", [4, 8, 24])
-def test_shared_x_q8_packed(n):
+@pytest.mark.parametrize("n,dtype", [(1, torch.bfloat16), (1, torch.float16), (1, torch.float32),
+                                     (4, torch.bfloat16), (8, torch.bfloat16), (24, torch.bfloat16)])
+def test_shared_x_q8_packed(n, dtype):
+    """n = 1 on these small weights takes the GEMV that quantises X itself: it must give the
+    bits of the q8_1 quantiser followed by the GEMV."""
     from vllm_gguf_plugin.quantization import iq3_pack
 
     rows, k = 64, 1024
     w = iq3_pack.pack(_dev(_w(o.IQ3_S, rows, k, seed=90 + n)), o.IQ3_S)
-    x = _x(n, k, seed=91 + n, dtype=torch.bfloat16).cuda()
+    x = _x(n, k, seed=91 + n, dtype=dtype).cuda()
+    x[:, 64:96] = 0  # an all-zero slice (d = 0, q = 0)
     q8 = C().lcpp_quantize_q8_1(x, o.IQ3_S, False, False)
     a = C().lcpp_mul_mat_vec_iq3_mma_packed(w, x, o.IQ3_S, rows)
     b = C().lcpp_mul_mat_vec_iq3_mma_packed(w, x, o.IQ3_S, rows, q8)

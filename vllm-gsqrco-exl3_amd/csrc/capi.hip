@@ -31,6 +31,8 @@ hipError_t launch_quantize_xq(const void* x, int dtype, int64_t n, int64_t k, in
 hipError_t launch_q8_1_to_xq(const void* q8, int64_t n, int64_t k, int type, void* y, hipStream_t stream);
 hipError_t launch_gemm_xq(int type, const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n,
                           void* y, int y_dtype, hipStream_t stream);
+hipError_t launch_gemv_packed_x(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x, int x_dtype,
+                                int64_t s01, int n, void* y, int y_dtype, hipStream_t stream);
 hipError_t launch_gemm_packed_xq(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n,
                                  void* y, int y_dtype, hipStream_t stream);
 hipError_t launch_iq3_pack(uint8_t* w, int64_t rows, int64_t row_bytes, bool unpack, uint8_t* scratch,
@@ -203,6 +205,12 @@ namespace {
 // Decode ops (1..8 rows; the packed IQ3 op up to 32) go to the int8-MFMA GEMM from this many
 // activation rows on, measured against the dot4 GEMV at the 27B-layer shapes: the GEMV's time
 // grows with every row, the GEMM's is flat up to 16. IQ3_S on plain rows stays on the GEMV.
+// The packed decode op at one activation row on weights of up to 32M values (the attention
+// projections) quantises X inside the GEMV instead of in a launch of its own.
+bool packed_fused(int op, int64_t row, int64_t k, int64_t n, bool has_x_q8) {
+  return op_packed(op) && !has_x_q8 && n == 1 && row * k <= ((int64_t)32 << 20);
+}
+
 int64_t vec_mma_from(int op, int64_t type) {
   if (op_packed(op)) return 5;
   if (type == gguf::kQ4_K || type == gguf::kQ6_K) return 3;
@@ -213,13 +221,13 @@ int64_t vec_mma_from(int op, int64_t type) {
 }  // namespace
 
 size_t gguf_op_workspace_bytes(int op, int64_t type, int64_t row, int64_t k, int64_t n, int has_x_q8) {
-  (void)row;
   if (n <= 0) return 0;
   if (op_gemm(op)) {
     const bool mmq_layout = !op_packed(op) && type == gguf::kIQ3_S;
     return align256(mmq_layout ? gguf_q8_1_bytes(n, k, 1) : gguf::xq_bytes(n, k));
   }
   if (n >= vec_mma_from(op, type)) return align256(gguf::xq_bytes(n, k));  // x_q8 is converted into it
+  if (packed_fused(op, row, k, n, has_x_q8 != 0)) return 0;
   return has_x_q8 ? 0 : align256(gguf_q8_1_bytes(n, k, 0));
 }
 
@@ -269,6 +277,11 @@ int gguf_mul_mat(int op, const gguf_view* W, const gguf_view* X, int64_t type, i
     if (e != hipSuccess) return hip_fail(e, name, "quantize");
     e = gguf::launch_gemm((int)type, w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace, (int)n, y, ydt, s);
     if (e != hipSuccess) return hip_fail(e, name, "gemm");
+    return GGUF_OK;
+  }
+  if (packed_fused(op, row, k, n, x_q8 != nullptr)) {  // quantisation inside the GEMV
+    e = gguf::launch_gemv_packed_x(w, row_bytes, (int)row, (int)k, X->data, X->dtype, s01, (int)n, y, ydt, s);
+    if (e != hipSuccess) return hip_fail(e, name, "gemv");
     return GGUF_OK;
   }
   const uint8_t* q8 = (const uint8_t*)workspace;

@@ -11,6 +11,8 @@
 //  * a 64-lane xor butterfly sums each (row, column) accumulator at the end.
 // The integer slice sums equal the reference's vec_dot sumi bit for bit; only the fp32 order in
 // which a row's slice terms are added differs (lane-strided, then the butterfly).
+#include <type_traits>
+
 #include "decode.h"
 #include "iq3_tile.h"
 
@@ -212,6 +214,69 @@ __device__ __forceinline__ void load_x_frag(__amdgpu_buffer_rsrc_t rs, uint32_t 
   }
 }
 
+// Fused quantisation of X (the decode ops' block_q8_1 arithmetic, done inside the GEMV): lane
+// L = 8p + s loads values 4p..4p+3 of slice s of a block of every activation row; the 8 lanes of a
+// slice exchange their partial amax and then their 4 q bytes through a 64-dword LDS area of the
+// wave, so each lane ends up with the slice's 32 q values as the q8_1 path would load them.
+template <int NC, int XDT>
+struct XRawFrag {
+  uint32_t v[NC][XDT == kF32 ? 4 : 2];
+};
+
+template <int NC, int XDT>
+__device__ __forceinline__ void load_xraw_frag(const void* x, int64_t s01, int block, int p, int s,
+                                               XRawFrag<NC, XDT>& r) {
+  const int64_t e0 = (int64_t)block * kQK + 32 * s + 4 * p;  // values 4p..4p+3 of slice s
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    if constexpr (XDT == kF32) {
+      const uint4 v = *(const uint4*)((const float*)x + c * s01 + e0);
+      r.v[c][0] = v.x; r.v[c][1] = v.y; r.v[c][2] = v.z; r.v[c][3] = v.w;
+    } else {
+      const uint2 v = *(const uint2*)((const uint16_t*)x + c * s01 + e0);
+      r.v[c][0] = v.x; r.v[c][1] = v.y;
+    }
+  }
+}
+
+template <int XDT>
+__device__ __forceinline__ float xraw_value(const uint32_t* v, int i) {
+  if constexpr (XDT == kF32) return __uint_as_float(v[i]);
+  const uint32_t h = (v[i >> 1] >> (16 * (i & 1))) & 0xFFFF;
+  if constexpr (XDT == kF16) return half_bits_to_float(h);
+  return __uint_as_float(h << 16);
+}
+
+// ex: the wave's 64-dword exchange area; the lane holds values 4p..4p+3 of slice s (the slice's
+// 8 lanes are s, s+8, ..., s+56)
+template <int NC, int XDT>
+__device__ __forceinline__ void quantize_xraw(const XRawFrag<NC, XDT>& r, uint32_t* ex, int p, int s,
+                                              XFrag<NC>& x) {
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = xraw_value<XDT>(r.v[c], i);
+    ex[8 * s + p] = __float_as_uint(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+    const uint4 a0 = *(const uint4*)(ex + 8 * s), a1 = *(const uint4*)(ex + 8 * s + 4);
+    const float amax = fmaxf(fmaxf(fmaxf(__uint_as_float(a0.x), __uint_as_float(a0.y)),
+                                   fmaxf(__uint_as_float(a0.z), __uint_as_float(a0.w))),
+                             fmaxf(fmaxf(__uint_as_float(a1.x), __uint_as_float(a1.y)),
+                                   fmaxf(__uint_as_float(a1.z), __uint_as_float(a1.w))));
+    const float d = amax / 127.0f;
+    // amax == 0 means every value is zero: dividing by 1 then gives q = 0 with no branch
+    const float dd = amax == 0.0f ? 1.0f : d;
+    uint32_t qw = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qw |= ((uint32_t)(int)roundf(v[i] / dd) & 0xFFu) << (8 * i);
+    ex[8 * s + p] = qw;  // after this wave's reads above: a wave's LDS operations complete in order
+    const uint4 q0 = *(const uint4*)(ex + 8 * s), q1 = *(const uint4*)(ex + 8 * s + 4);
+    x.q[c][0] = (int)q0.x; x.q[c][1] = (int)q0.y; x.q[c][2] = (int)q0.z; x.q[c][3] = (int)q0.w;
+    x.q[c][4] = (int)q1.x; x.q[c][5] = (int)q1.y; x.q[c][6] = (int)q1.z; x.q[c][7] = (int)q1.w;
+    x.d[c] = __half_as_ushort(__float2half_rn(d));
+  }
+}
+
 template <int NC>
 __device__ __forceinline__ void tile_compute(const uint8_t* tbl, const TileFrag& f, const XFrag<NC>& x, int s,
                                              float (&acc)[2][NC]) {
@@ -238,13 +303,19 @@ __device__ __forceinline__ void tile_compute(const uint8_t* tbl, const TileFrag&
   }
 }
 
-template <int NC, int TPW, int WPT>
+// XDT < 0: X given as block_q8_1 (q8); else X itself (dtype XDT, row stride s01), quantised in the
+// kernel with the same arithmetic.
+template <int NC, int TPW, int WPT, int XDT>
 __global__ void __launch_bounds__(64 * TPW * WPT) gemv_iq3s_tile_kernel(const uint8_t* __restrict__ W,
                                                                         int64_t row_bytes, int nrows, int k,
-                                                                        const uint8_t* __restrict__ q8,
-                                                                        void* __restrict__ y, int y_dtype) {
+                                                                        const void* __restrict__ xsrc,
+                                                                        int64_t s01, void* __restrict__ y,
+                                                                        int y_dtype) {
+  constexpr bool FUSED = XDT >= 0;
   __shared__ uint4 table[2048];  // the 8192-entry signed-grid table
   __shared__ float red[TPW][WPT][NC][kTileRows];
+  __shared__ uint32_t xex[FUSED ? TPW * WPT : 1][64];  // per-wave exchange of the fused quantisation
+  const uint8_t* q8 = (const uint8_t*)xsrc;
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave index, scalar
   const int wave = wv % WPT;   // K part of the tile
@@ -258,7 +329,7 @@ __global__ void __launch_bounds__(64 * TPW * WPT) gemv_iq3s_tile_kernel(const ui
   const int b_begin = active ? wave * nb / WPT : 0, b_end = active ? (wave + 1) * nb / WPT : 0;
   const uint8_t* tb = W + (int64_t)(active ? tile : 0) * kTileRows * row_bytes;  // scalar
   const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(tb, (uint32_t)(kTileRows * row_bytes));
-  const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(q8, (uint32_t)(NC * nslices * 36));
+  const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(q8, FUSED ? 0u : (uint32_t)(NC * nslices * 36));
   const uint8_t* tbl = (const uint8_t*)table;
   const TileOffs off = tile_offsets(lane, p, s);
   const uint32_t xoff = 36u * (uint32_t)s;
@@ -281,28 +352,62 @@ __global__ void __launch_bounds__(64 * TPW * WPT) gemv_iq3s_tile_kernel(const ui
   const int b_last = b_end - 1;
   const int nblk = b_end - b_begin;
   TileFrag fa, fb;
-  XFrag<NC> xa, xb;
-  if (nblk > 0) {
-    load_x_frag<NC>(xrs, xoff, nslices, b_begin * 8, xa);
-    load_tile_frag(wrs, b_begin * kTileBlockBytes, off, fa);
+  if constexpr (!FUSED) {
+    XFrag<NC> xa, xb;
+    if (nblk > 0) {
+      load_x_frag<NC>(xrs, xoff, nslices, b_begin * 8, xa);
+      load_tile_frag(wrs, b_begin * kTileBlockBytes, off, fa);
+    }
+    iq3_table_to_lds<TPW * WPT>(table, &kIq3sSignedDev, wv, lane);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    int b = b_begin;
+    for (int it = 0; it < nblk / 2; ++it, b += 2) {
+      const int b2 = b + 2 < b_last ? b + 2 : b_last;
+      const __amdgpu_buffer_rsrc_t rs2 = b + 2 < b_end ? wrs : nrs;
+      load_x_frag<NC>(xrs, xoff, nslices, (b + 1) * 8, xb);
+      load_tile_frag(wrs, (b + 1) * kTileBlockBytes, off, fb);
+      __builtin_amdgcn_sched_barrier(0);
+      tile_compute<NC>(tbl, fa, xa, s, acc);
+      load_x_frag<NC>(xrs, xoff, nslices, b2 * 8, xa);
+      load_tile_frag(rs2, (b + 2) * kTileBlockBytes, off, fa);
+      __builtin_amdgcn_sched_barrier(0);
+      tile_compute<NC>(tbl, fb, xb, s, acc);
+    }
+    if (nblk & 1) tile_compute<NC>(tbl, fa, xa, s, acc);
+  } else {
+    // Raw X runs two blocks ahead and is quantised one block ahead, so the slice exchange of
+    // the next block overlaps the current block's decode.
+    constexpr int XD = FUSED ? XDT : kBF16;
+    uint32_t* ex = xex[wv];
+    XRawFrag<NC, XD> ra, rb;
+    XFrag<NC> qa, qb;
+    auto clampb = [&](int bb) { return bb < b_last ? bb : b_last; };
+    if (nblk > 0) {
+      load_xraw_frag<NC, XD>(xsrc, s01, b_begin, p, s, ra);
+      load_xraw_frag<NC, XD>(xsrc, s01, clampb(b_begin + 1), p, s, rb);
+      load_tile_frag(wrs, b_begin * kTileBlockBytes, off, fa);
+    }
+    iq3_table_to_lds<TPW * WPT>(table, &kIq3sSignedDev, wv, lane);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    quantize_xraw<NC, XD>(ra, ex, p, s, qa);
+    int b = b_begin;
+    for (int it = 0; it < nblk / 2; ++it, b += 2) {
+      const __amdgpu_buffer_rsrc_t rs2 = b + 2 < b_end ? wrs : nrs;
+      load_xraw_frag<NC, XD>(xsrc, s01, clampb(b + 2), p, s, ra);
+      load_tile_frag(wrs, (b + 1) * kTileBlockBytes, off, fb);
+      __builtin_amdgcn_sched_barrier(0);
+      quantize_xraw<NC, XD>(rb, ex, p, s, qb);
+      tile_compute<NC>(tbl, fa, qa, s, acc);
+      load_xraw_frag<NC, XD>(xsrc, s01, clampb(b + 3), p, s, rb);
+      load_tile_frag(rs2, (b + 2) * kTileBlockBytes, off, fa);
+      __builtin_amdgcn_sched_barrier(0);
+      quantize_xraw<NC, XD>(ra, ex, p, s, qa);
+      tile_compute<NC>(tbl, fb, qb, s, acc);
+    }
+    if (nblk & 1) tile_compute<NC>(tbl, fa, qa, s, acc);
   }
-  iq3_table_to_lds<TPW * WPT>(table, &kIq3sSignedDev, wv, lane);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  int b = b_begin;
-  for (int it = 0; it < nblk / 2; ++it, b += 2) {
-    const int b2 = b + 2 < b_last ? b + 2 : b_last;
-    const __amdgpu_buffer_rsrc_t rs2 = b + 2 < b_end ? wrs : nrs;
-    load_x_frag<NC>(xrs, xoff, nslices, (b + 1) * 8, xb);
-    load_tile_frag(wrs, (b + 1) * kTileBlockBytes, off, fb);
-    __builtin_amdgcn_sched_barrier(0);
-    tile_compute<NC>(tbl, fa, xa, s, acc);
-    load_x_frag<NC>(xrs, xoff, nslices, b2 * 8, xa);
-    load_tile_frag(rs2, (b + 2) * kTileBlockBytes, off, fa);
-    __builtin_amdgcn_sched_barrier(0);
-    tile_compute<NC>(tbl, fb, xb, s, acc);
-  }
-  if (nblk & 1) tile_compute<NC>(tbl, fa, xa, s, acc);
 
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
@@ -329,33 +434,59 @@ __global__ void __launch_bounds__(64 * TPW * WPT) gemv_iq3s_tile_kernel(const ui
   }
 }
 
-template <int TPW, int WPT>
-static void launch_gemv_packed_w(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n,
-                                 void* y, int y_dtype, hipStream_t stream) {
+template <int TPW, int WPT, int XDT>
+static void launch_gemv_packed_w(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x, int64_t s01,
+                                 int n, void* y, int y_dtype, hipStream_t stream) {
   const int tiles = nrows / kTileRows;
   const unsigned blocks = (unsigned)((tiles + TPW - 1) / TPW);
-#define GGUF_GT(NC) \
-  gemv_iq3s_tile_kernel<NC, TPW, WPT><<<blocks, 64 * TPW * WPT, 0, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype)
-  switch (n) {
-    case 1: GGUF_GT(1); break;
-    case 2: GGUF_GT(2); break;
-    case 3: GGUF_GT(3); break;
-    case 4: GGUF_GT(4); break;
-    case 5: GGUF_GT(5); break;
-    case 6: GGUF_GT(6); break;
-    case 7: GGUF_GT(7); break;
-    default: GGUF_GT(8); break;
+#define GGUF_GT(NC)                                                                                             \
+  gemv_iq3s_tile_kernel<NC, TPW, WPT, XDT><<<blocks, 64 * TPW * WPT, 0, stream>>>(W, row_bytes, nrows, k, x, s01, y, \
+                                                                                  y_dtype)
+  if constexpr (XDT >= 0) {  // the fused path serves one row
+    GGUF_GT(1);
+  } else {
+    switch (n) {
+      case 1: GGUF_GT(1); break;
+      case 2: GGUF_GT(2); break;
+      case 3: GGUF_GT(3); break;
+      case 4: GGUF_GT(4); break;
+      case 5: GGUF_GT(5); break;
+      case 6: GGUF_GT(6); break;
+      case 7: GGUF_GT(7); break;
+      default: GGUF_GT(8); break;
+    }
   }
 #undef GGUF_GT
 }
 
-// nrows % 16 == 0, n in 1..8.
+// One tile per workgroup. Eight waves split K for one or two columns (measured best at
+// 17408 x 5120: 12.3 us at M=1); from three columns on, the register file allows four.
+template <int XDT>
+static void launch_gemv_packed_dt(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x, int64_t s01,
+                                  int n, void* y, int y_dtype, hipStream_t stream) {
+  if (n <= 2) launch_gemv_packed_w<1, 8, XDT>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream);
+  else launch_gemv_packed_w<1, 4, XDT>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream);
+}
+
+// nrows % 16 == 0, n in 1..8; q8: block_q8_1 of X.
 hipError_t launch_gemv_packed(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n,
                               void* y, int y_dtype, hipStream_t stream) {
-  // One tile per workgroup. Eight waves split K for one or two columns (measured best at
-  // 17408 x 5120: 12.3 us at M=1); from three columns on, the register file allows four.
-  if (n <= 2) launch_gemv_packed_w<1, 8>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);
-  else launch_gemv_packed_w<1, 4>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);
+  launch_gemv_packed_dt<-1>(W, row_bytes, nrows, k, q8, 0, n, y, y_dtype, stream);
+  return hipGetLastError();
+}
+
+// nrows % 16 == 0, n == 1; X [1, k] of dtype x_dtype, quantised in the kernel (bit-identical to the
+// q8_1 quantiser followed by the GEMV). Measured faster than the two launches for the attention
+// shapes (up to 6144 x 5120 weights), slower for the 17408 x 5120 FFN shapes, where the exact
+// divisions and the slice exchange lengthen the latency-bound GEMV by more than the launch costs.
+hipError_t launch_gemv_packed_x(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x, int x_dtype,
+                                int64_t s01, int n, void* y, int y_dtype, hipStream_t stream) {
+  if (n != 1) return hipErrorInvalidValue;
+  switch (x_dtype) {
+    case kF32: launch_gemv_packed_dt<kF32>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream); break;
+    case kF16: launch_gemv_packed_dt<kF16>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream); break;
+    default: launch_gemv_packed_dt<kBF16>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream); break;
+  }
   return hipGetLastError();
 }
 
