@@ -1,7 +1,8 @@
 #!/usr/bin/env python3
 """Benchmark of the GGUF quantized-matmul hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-points] [--no-configs] [--no-cpu] [--kernel-only]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-points] [--no-configs] [--no-cpu]
+                    [--kernel-only | --section {mtp,prefill,layers}]
 
 Workload: IQ3_S decode GEMV at M = 1 and 4 on the two 27B-layer
 shapes, gate/up 17408 x 5120 and down 5120 x 17408, bf16 activations N(0,1) quantised to q8_1,
@@ -296,6 +297,8 @@ def main():
     ap.add_argument("--no-points", action="store_true", help="skip the metric's other (type, M) points")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the other BASELINE configs (CPU Q4_K, MTP small GEMM, prefill, 64-layer sweep)")
+    ap.add_argument("--section", choices=["mtp", "prefill", "layers"],
+                    help="run only this BASELINE config and print its JSON (for rocprofv3 counter runs)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--kernel-only", action="store_true",
                     help="time only the dominant kernel, then run the counter-calibration copy (for rocprofv3)")
@@ -314,6 +317,12 @@ def main():
     torch.cuda.set_device(0)
     if args.kernel_only:
         kernel_only(torch, C, iq3_pack, args.steps)
+        return
+    if args.section:
+        fn = {"mtp": lambda: config_mtp(torch, C, iq3_pack, linear),
+              "prefill": lambda: config_prefill(torch, C, iq3_pack, linear),
+              "layers": lambda: config_layers(torch, C, iq3_pack, linear, args.steps)}[args.section]
+        print(json.dumps({"mode": "section", "section": args.section, "result": fn()}), flush=True)
         return
 
     # ------------------------------------------------------------------ headline workload
