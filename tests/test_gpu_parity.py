@@ -276,6 +276,73 @@ def test_packed_ops_vs_q81(n, k):
     assert o.rel_l2(y, ref) <= 1e-3, o.rel_l2(y, ref)
 
 
+# ------------------------------------------------------------------------------------ prefill
+# Product ops from 256 activation rows on run the 128 x 128-tile prefill GEMM.
+PREFILL_N = [256, 300, 600]
+
+
+@pytest.mark.parametrize("qt", TYPES, ids=lambda t: TN[t])
+@pytest.mark.parametrize("n", [256, 330])
+def test_prefill_exact_integer_dots(qt, n):
+    """Rows past the last full 128-row group and activation rows past the last 16-column tile."""
+    from vllm_gguf_plugin.quantization import iq3_pack
+
+    rows, k = 144 if qt == o.IQ3_S else 150, 512
+    raw = _exact_weights(qt, rows, k, seed=130 + n)
+    x = _exact_x(n, k, seed=140 + n, dtype=torch.float32)
+    want = _exact_ref(raw, qt, x)
+    if qt == o.IQ3_S:
+        w = iq3_pack.pack(_dev(raw), qt)
+        y = C().lcpp_mul_mat_iq3_packed(w, x.cuda(), qt, rows).cpu().numpy()
+    else:
+        y = C().lcpp_mul_mat_q(_dev(raw), x.cuda(), qt, rows).cpu().numpy()
+    np.testing.assert_array_equal(y.astype(np.int64), want)
+    assert (y == y.astype(np.int64)).all()
+
+
+@pytest.mark.parametrize("qt", [o.Q4_K, o.IQ4_XS, o.Q6_K], ids=lambda t: TN[t])
+@pytest.mark.parametrize("n", PREFILL_N)
+def test_prefill_vs_q81(qt, n):
+    rows, k = 272, 1024
+    raw = _w(qt, rows, k, seed=n * 17 + qt)
+    x = _x(n, k, seed=n + 600)
+    x[-1, 256:288] = 0  # an all-zero slice
+    y = C().lcpp_mul_mat_q(_dev(raw), x.cuda(), qt, rows).cpu().numpy()
+    ref = o.q81_model(raw, qt, x, layout="mmq")
+    assert o.rel_l2(y, ref) <= 1e-3, o.rel_l2(y, ref)
+
+
+@pytest.mark.parametrize("n", PREFILL_N)
+@pytest.mark.parametrize("k", [512, 5120])
+def test_prefill_packed_vs_q81(n, k):
+    from vllm_gguf_plugin.quantization import iq3_pack
+
+    rows = 272
+    raw = _w(o.IQ3_S, rows, k, seed=n + k + 7)
+    w = iq3_pack.pack(_dev(raw), o.IQ3_S)
+    x = _x(n, k, seed=n + 700)
+    y = C().lcpp_mul_mat_iq3_packed(w, x.cuda(), o.IQ3_S, rows).cpu().numpy()
+    ref = o.q81_model(raw, o.IQ3_S, x, layout="mmq")
+    assert o.rel_l2(y, ref) <= 1e-3, o.rel_l2(y, ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
+@pytest.mark.parametrize("qt", TYPES, ids=lambda t: TN[t])
+def test_prefill_16bit_x(qt, dtype):
+    from vllm_gguf_plugin.quantization import iq3_pack
+
+    rows, k, n = 128, 1024, 260
+    raw = _w(qt, rows, k, seed=qt + 800)
+    x = _x(n, k, seed=801, dtype=dtype)
+    if qt == o.IQ3_S:
+        y = C().lcpp_mul_mat_iq3_packed(iq3_pack.pack(_dev(raw), qt), x.cuda(), qt, rows)
+    else:
+        y = C().lcpp_mul_mat_q(_dev(raw), x.cuda(), qt, rows)
+    assert y.dtype == dtype and y.shape == (n, rows)
+    ref = o.q81_model(raw, qt, x, layout="mmq")
+    assert o.rel_l2(y.float().cpu().numpy(), ref) <= TIGHT[dtype]
+
+
 # ------------------------------------------------------------------------------------ x_q8, graphs
 @pytest.mark.parametrize("qt", TYPES, ids=lambda t: TN[t])
 @pytest.mark.parametrize("n", [2, 4, 8])
@@ -315,6 +382,8 @@ def test_shared_x_q8_packed(n, dtype):
     ("lcpp_mul_mat_mma_k", o.Q4_K, 16, False),
     ("lcpp_mul_mat_q", o.Q6_K, 48, False),
     ("lcpp_mul_mat_vec_q", o.IQ4_XS, 1, False),
+    ("lcpp_mul_mat_iq3_packed", o.IQ3_S, 300, True),
+    ("lcpp_mul_mat_q", o.Q4_K, 260, False),
 ])
 def test_graph_replay_bit_exact(op, qt, n, packed):
     from vllm_gguf_plugin.quantization import iq3_pack

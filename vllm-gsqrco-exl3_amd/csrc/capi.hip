@@ -35,6 +35,8 @@ hipError_t launch_gemv_packed_x(const uint8_t* W, int64_t row_bytes, int nrows, 
                                 int64_t s01, int n, void* y, int y_dtype, hipStream_t stream);
 hipError_t launch_gemm_packed_xq(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n,
                                  void* y, int y_dtype, hipStream_t stream);
+hipError_t launch_gemm_prefill(int type, bool packed, const uint8_t* W, int64_t row_bytes, int nrows, int k,
+                               const uint8_t* xq, int n, void* y, int y_dtype, hipStream_t stream);
 hipError_t launch_iq3_pack(uint8_t* w, int64_t rows, int64_t row_bytes, bool unpack, uint8_t* scratch,
                            size_t scratch_bytes, hipStream_t stream);
 size_t iq3_pack_scratch_bytes(int64_t rows, int64_t row_bytes);
@@ -211,6 +213,10 @@ bool packed_fused(int op, int64_t row, int64_t k, int64_t n, bool has_x_q8) {
   return op_packed(op) && !has_x_q8 && n == 1 && row * k <= ((int64_t)32 << 20);
 }
 
+// Product ops go to the 128 x 128-tile prefill GEMM from this many activation rows on (the small
+// GEMMs' one-column-tile-group plans re-decode the weights once per 16..64 activation rows).
+constexpr int64_t kPrefillFrom = 256;
+
 int64_t vec_mma_from(int op, int64_t type) {
   if (op_packed(op)) return 5;
   if (type == gguf::kQ4_K || type == gguf::kQ6_K) return 3;
@@ -265,10 +271,14 @@ int gguf_mul_mat(int op, const gguf_view* W, const gguf_view* X, int64_t type, i
     else
       e = gguf::launch_quantize_xq(X->data, X->dtype, n, k, s01, (int)type, !gemm, workspace, s);
     if (e != hipSuccess) return hip_fail(e, name, "quantize");
-    e = packed ? gguf::launch_gemm_packed_xq(w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace, (int)n, y,
-                                             ydt, s)
-               : gguf::launch_gemm_xq((int)type, w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace, (int)n,
-                                      y, ydt, s);
+    if (gemm && n >= kPrefillFrom)
+      e = gguf::launch_gemm_prefill((int)type, packed, w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace,
+                                    (int)n, y, ydt, s);
+    else if (packed)
+      e = gguf::launch_gemm_packed_xq(w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace, (int)n, y, ydt, s);
+    else
+      e = gguf::launch_gemm_xq((int)type, w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace, (int)n, y, ydt,
+                               s);
     if (e != hipSuccess) return hip_fail(e, name, "gemm");
     return GGUF_OK;
   }
