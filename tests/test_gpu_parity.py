@@ -300,6 +300,24 @@ def test_prefill_exact_integer_dots(qt, n):
     assert (y == y.astype(np.int64)).all()
 
 
+@pytest.mark.parametrize("qt", TYPES, ids=lambda t: TN[t])
+def test_prefill_wide_exact_integer_dots(qt):
+    """A grid of 256 workgroup tiles (the prefill GEMM's wide-workgroup plan for IQ3_S / Q4_K),
+    in the exact-integer mode; with every scale 1 the float64 q81 model is the exact integer."""
+    from vllm_gguf_plugin.quantization import iq3_pack
+
+    rows, k, n = 4096, 512, 2048
+    raw = _exact_weights(qt, rows, k, seed=150)
+    x = _exact_x(n, k, seed=151, dtype=torch.float32)
+    want = o.q81_model(raw, qt, x, layout="mmq")
+    assert np.abs(want).max() < 2 ** 24 and (want == np.round(want)).all()
+    if qt == o.IQ3_S:
+        y = C().lcpp_mul_mat_iq3_packed(iq3_pack.pack(_dev(raw), qt), x.cuda(), qt, rows)
+    else:
+        y = C().lcpp_mul_mat_q(_dev(raw), x.cuda(), qt, rows)
+    np.testing.assert_array_equal(y.cpu().numpy().astype(np.float64), want)
+
+
 @pytest.mark.parametrize("qt", [o.Q4_K, o.IQ4_XS, o.Q6_K], ids=lambda t: TN[t])
 @pytest.mark.parametrize("n", PREFILL_N)
 def test_prefill_vs_q81(qt, n):

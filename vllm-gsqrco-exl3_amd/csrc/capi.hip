@@ -35,6 +35,9 @@ hipError_t launch_gemv_packed_x(const uint8_t* W, int64_t row_bytes, int nrows, 
                                 int64_t s01, int n, void* y, int y_dtype, hipStream_t stream);
 hipError_t launch_gemm_packed_xq(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n,
                                  void* y, int y_dtype, hipStream_t stream);
+hipError_t launch_quantize_xh(const void* x, int dtype, int64_t n, int64_t k, int64_t s01, int type, void* y,
+                              hipStream_t stream);
+bool prefill_uses_xh(int type, bool packed);
 hipError_t launch_gemm_prefill(int type, bool packed, const uint8_t* W, int64_t row_bytes, int nrows, int k,
                                const uint8_t* xq, int n, void* y, int y_dtype, hipStream_t stream);
 hipError_t launch_iq3_pack(uint8_t* w, int64_t rows, int64_t row_bytes, bool unpack, uint8_t* scratch,
@@ -230,6 +233,8 @@ size_t gguf_op_workspace_bytes(int op, int64_t type, int64_t row, int64_t k, int
   if (n <= 0) return 0;
   if (op_gemm(op)) {
     const bool mmq_layout = !op_packed(op) && type == gguf::kIQ3_S;
+    if (!mmq_layout && n >= kPrefillFrom && gguf::prefill_uses_xh((int)type, op_packed(op)))
+      return align256(gguf::xh_bytes(n, k));
     return align256(mmq_layout ? gguf_q8_1_bytes(n, k, 1) : gguf::xq_bytes(n, k));
   }
   if (n >= vec_mma_from(op, type)) return align256(gguf::xq_bytes(n, k));  // x_q8 is converted into it
@@ -266,12 +271,15 @@ int gguf_mul_mat(int op, const gguf_view* W, const gguf_view* X, int64_t type, i
   // int8-MFMA GEMMs on the xq layout: the product ops with the MMQ arithmetic, the decode ops
   // (from vec_mma_from rows on) with the decode ops' q8_1 arithmetic or the caller's x_q8
   if ((gemm && (packed || type != gguf::kIQ3_S)) || (!gemm && n >= vec_mma_from(op, type))) {
+    const bool prefill = gemm && n >= kPrefillFrom;
     if (!gemm && x_q8)
       e = gguf::launch_q8_1_to_xq(x_q8->data, n, k, (int)type, workspace, s);
+    else if (prefill && gguf::prefill_uses_xh((int)type, packed))
+      e = gguf::launch_quantize_xh(X->data, X->dtype, n, k, s01, (int)type, workspace, s);
     else
       e = gguf::launch_quantize_xq(X->data, X->dtype, n, k, s01, (int)type, !gemm, workspace, s);
     if (e != hipSuccess) return hip_fail(e, name, "quantize");
-    if (gemm && n >= kPrefillFrom)
+    if (prefill)
       e = gguf::launch_gemm_prefill((int)type, packed, w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace,
                                     (int)n, y, ydt, s);
     else if (packed)

@@ -18,6 +18,8 @@
 //  * IQ3_S decodes through the 2 KB unsigned grid with the signs applied by VALU (the 32 KB
 //    signed table would leave room for one workgroup per CU).
 // Single-buffered: two workgroups per CU overlap one's staging with the other's MFMAs.
+#include <type_traits>
+
 #include "decode.h"
 #include "iq3_tile.h"
 #include "xq.h"
@@ -298,6 +300,383 @@ __global__ void __launch_bounds__(256, 2) gemm_prefill_kernel(const uint8_t* __r
   }
 }
 
+// ------------------------------------------------------------------------- fp16-operand variant
+// IQ3_S and Q4_K: the weight value times its slice sub-scale is an integer of at most 465 (IQ3_S)
+// or 945 (Q4_K), exact in fp16, and so are the activation's q8 values (the xh layout). One
+// v_mfma_f32_16x16x32_f16 with a zero accumulator then returns sub-scale x integer slice dot
+// exactly (every partial sum is an integer below 2^24), already in fp32, and the per-slice
+// epilogue is one FMA by the activation scale. The row's block scale d is not applied per
+// slice: each row's accumulator is held in units of the d of the block being summed (e, the last
+// nonzero d; a block with d = 0 decodes to zeros), and is multiplied by e_prev / e_cur when a new
+// block starts and by the last e at the end. The Q4_K min term, sum over slices of
+// (-dmin * m / e) x (d_x * sum q), is a K = 4 fp32 product per half block: one
+// v_mfma_f32_16x16x4f32 into the accumulator.
+//
+// Workgroup: NW waves over 128 weight rows x 32 NW activation rows. Wave w owns column tiles 2w,
+// 2w+1 against all 8 row tiles (16 accumulator tiles); its B operands (4 KB per column tile and
+// half block) come straight from global memory into registers one step ahead, so only the
+// decoded weights are shared through LDS, double-buffered, with one barrier per step (half
+// block). Each wave decodes 8 / NW row tiles per step from raw bytes it loaded two steps ahead.
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+constexpr int kHRegion = 1040;                     // A bytes per (row tile, slice): 16 rows x 64 B + pad
+constexpr int kHA = kPfRowTiles * 4 * kHRegion;    // 33,280 per buffer (half a K block)
+
+// fp16 bits of a small positive integer
+constexpr uint32_t small_int_half(uint32_t v) {
+  int e = 0;
+  while ((v >> (e + 1)) != 0) ++e;
+  return ((uint32_t)(e + 15) << 10) | ((v - (1u << e)) << (10 - e));
+}
+static_assert(small_int_half(1) == 0x3C00 && small_int_half(15) == 0x4B80, "fp16 bits");
+
+// The IQ3_S grid as fp16: entry i = the 4 grid values of index i, 2 per dword
+struct Iq3sGridHalf {
+  uint32_t v[1024];
+};
+constexpr Iq3sGridHalf make_iq3s_grid_half() {
+  Iq3sGridHalf g{};
+  for (int i = 0; i < 512; ++i) {
+    const uint32_t w = kIq3sGrid.v[i];
+    g.v[2 * i] = small_int_half(w & 0xFF) | (small_int_half((w >> 8) & 0xFF) << 16);
+    g.v[2 * i + 1] = small_int_half((w >> 16) & 0xFF) | (small_int_half(w >> 24) << 16);
+  }
+  return g;
+}
+__device__ const Iq3sGridHalf kIq3sGridHalf = make_iq3s_grid_half();
+
+// A slot of (row tile t, slice u of the half block, row j, quarter q): the quarter's 16 bytes sit
+// in slot q ^ g(j) of the row, g(j) = ((j >> 1) ^ (j >> 3)) & 3, which keeps the operand reads
+// (lane (j, q)) free of bank conflicts.
+__device__ __forceinline__ int h_off(int t, int u, int j, int q) {
+  return (t * 4 + u) * kHRegion + j * 64 + ((q ^ ((j >> 1) ^ (j >> 3))) & 3) * 16;
+}
+
+__device__ __forceinline__ uint32_t h2_bits(h2 v) { return __builtin_bit_cast(uint32_t, v); }
+__device__ __forceinline__ h2 bits_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
+
+// A decoding lane's raw weight bytes for one step, loaded two steps ahead.
+struct RawIq3 {
+  uint2 qs;     // qs of the lane's row and slice
+  uint32_t e8;  // E8 dword of the row
+  uint32_t l2;  // L2 halfword of the row pair
+  uint32_t sc;  // SC byte (two 4-bit sub-scales)
+  uint32_t d;   // fp16 d of the row
+};
+struct RawQ4k {
+  u32x4 hdr;    // d, dmin, scales[12]
+  uint2 v0, v1; // quarter q of the two 32-byte quant groups of the half block
+};
+
+// IQ3_S lane (row j, slice 4h + sp) of a tile-block in the tile layout
+__device__ __forceinline__ void load_step(RawIq3& w, const uint8_t* tb, int h, int j, int sp) {
+  const int p = j >> 1, r = j & 1, s = 4 * h + sp, L = 8 * p + s;
+  w.qs = *(const uint2*)(tb + kTqs + 16 * L + 8 * r);
+  w.e8 = *(const uint32_t*)(tb + kTe8 + 8 * L + 4 * r);
+  w.l2 = *(const uint16_t*)(tb + kTl2 + 2 * L);
+  w.sc = tb[kTsc + 2 * (4 * p + (s >> 1)) + r];
+  w.d = *(const uint16_t*)(tb + kTd + 4 * p + 2 * r);
+}
+
+// Q4_K lane (row j, quarter q) of the row's block
+__device__ __forceinline__ void load_step(RawQ4k& w, const uint8_t* blk, int h, int q) {
+  w.hdr = *(const u32x4*)blk;
+  w.v0 = *(const uint2*)(blk + 16 + 64 * h + 8 * q);
+  w.v1 = *(const uint2*)(blk + 48 + 64 * h + 8 * q);
+}
+
+// The row's running scale at a block start (h == 0): e_cur = d, or e_prev for d = 0; the ratio
+// and the final scale go to LDS (the lanes of a row store the same values).
+__device__ __forceinline__ float next_scale(float d, float& e, float* RT, float* EF, int row) {
+  const float en = d != 0.0f ? d : e;
+  RT[row] = e / en;
+  EF[row] = en;
+  e = en;
+  return en;
+}
+
+__device__ __forceinline__ void decode_step(const RawIq3& w, int h, const uint32_t* gh, const uint2* sm, uint8_t* A,
+                                            float* RT, float* EF, float& e, int t, int j, int sp) {
+  const int s = 4 * h + sp;
+  const float d = half_bits_to_float(w.d);
+  if (h == 0) next_scale(d, e, RT, EF, t * 16 + j);
+  uint32_t lo, hi;
+  iq3_tile_ex(w.e8, w.l2, j & 1, lo, hi);
+  const uint32_t nib = (w.sc >> (4 * (s & 1))) & 0xF;
+  const _Float16 ls = d != 0.0f ? (_Float16)(float)(1 + 2 * nib) : (_Float16)0.0f;
+  const h2 lsh = {ls, ls};
+  uint32_t v[16];
+#pragma unroll
+  for (int g = 0; g < 8; ++g) {
+    const uint32_t qb = ((g < 4 ? w.qs.x : w.qs.y) >> (8 * (g & 3))) & 0xFF;
+    const uint32_t ex = ((g < 4 ? lo : hi) >> (8 * (g & 3))) & 0xFF;
+    const uint2 gv = *(const uint2*)(gh + 2 * (qb | ((ex >> 4) << 8)));
+    const uint2 sg = sm[ex & 0xF];
+    v[2 * g] = h2_bits(bits_h2(gv.x ^ sg.x) * lsh);
+    v[2 * g + 1] = h2_bits(bits_h2(gv.y ^ sg.y) * lsh);
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    *(uint4*)(A + h_off(t, sp, j, q)) = make_uint4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+}
+
+// Q4_K: fp16 (1024 + nibble) by a byte permute, then one packed FMA gives nibble x sc exactly.
+__device__ __forceinline__ void decode_step(const RawQ4k& w, int h, float* AM, uint8_t* A, float* RT, float* EF,
+                                            float& e, int t, int j, int q) {
+  const float d = half_bits_to_float(w.hdr[0] & 0xFFFF);
+  const float dmin = half_bits_to_float(w.hdr[0] >> 16);
+  const float en = h == 0 ? next_scale(d, e, RT, EF, t * 16 + j) : e;
+  const float mf = -dmin / en;
+  const bool nz = d != 0.0f;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int us = 4 * h + u, jj = us & 3;
+    const uint32_t a = (w.hdr[1] >> (8 * jj)) & 0xFF, c = (w.hdr[2] >> (8 * jj)) & 0xFF;
+    uint32_t sc, m;
+    if (us < 4) {
+      sc = a & 63;
+      m = c & 63;
+    } else {
+      const uint32_t ee = (w.hdr[3] >> (8 * jj)) & 0xFF;
+      sc = (ee & 0xF) | ((a >> 6) << 4);
+      m = (ee >> 4) | ((c >> 6) << 4);
+    }
+    const _Float16 scf = nz ? (_Float16)(float)sc : (_Float16)0.0f;
+    const h2 mul = {scf, scf};
+    const h2 off = mul * (_Float16)(-1024.0f);
+    const uint2 vv = u < 2 ? w.v0 : w.v1;
+    const int sh = 4 * (u & 1);
+    const uint32_t x0 = (vv.x >> sh) & 0x0F0F0F0Fu, x1 = (vv.y >> sh) & 0x0F0F0F0Fu;
+    const uint32_t w0 = h2_bits(__builtin_elementwise_fma(bits_h2(__builtin_amdgcn_perm(0x64646464u, x0, 0x04010400u)), mul, off));
+    const uint32_t w1 = h2_bits(__builtin_elementwise_fma(bits_h2(__builtin_amdgcn_perm(0x64646464u, x0, 0x04030402u)), mul, off));
+    const uint32_t w2 = h2_bits(__builtin_elementwise_fma(bits_h2(__builtin_amdgcn_perm(0x64646464u, x1, 0x04010400u)), mul, off));
+    const uint32_t w3 = h2_bits(__builtin_elementwise_fma(bits_h2(__builtin_amdgcn_perm(0x64646464u, x1, 0x04030402u)), mul, off));
+    *(uint4*)(A + h_off(t, u, j, q)) = make_uint4(w0, w1, w2, w3);
+    AM[(t * 4 + u) * 16 + j] = mf * (float)m;  // the 4 lanes of row j store the same value
+  }
+}
+
+template <int TYPE, int NW>
+__global__ void __launch_bounds__(64 * NW, 8 / NW) gemm_prefill_h_kernel(const uint8_t* __restrict__ W,
+                                                                         int64_t row_bytes, int nrows, int k,
+                                                                         const uint8_t* __restrict__ xh, int nct,
+                                                                         int n, void* __restrict__ y, int y_dtype) {
+  constexpr bool IQ3 = TYPE == kIQ3_S;
+  constexpr int TPW = 8 / NW;  // row tiles a wave decodes per step
+  using Raw = typename std::conditional<IQ3, RawIq3, RawQ4k>::type;
+  __shared__ __attribute__((aligned(16))) uint8_t A[2 * kHA];
+  __shared__ __attribute__((aligned(16))) float RT[128];
+  __shared__ __attribute__((aligned(16))) float EF[128];
+  __shared__ __attribute__((aligned(16))) float AM[IQ3 ? 4 : 2 * 512];
+  __shared__ __attribute__((aligned(16))) uint32_t GH[IQ3 ? 1024 : 4];
+  __shared__ __attribute__((aligned(16))) uint2 SM[16];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 15, q = lane >> 4;
+  const int ntiles = (nrows + 15) / 16;
+  const int tile0 = blockIdx.x * kPfRowTiles;
+  const int nb = k / kQK;
+  if constexpr (IQ3) {
+    for (int i = threadIdx.x; i < 1024; i += 64 * NW) GH[i] = kIq3sGridHalf.v[i];
+    if (threadIdx.x < 16) {
+      const uint32_t nib = threadIdx.x;
+      SM[nib] = make_uint2(((nib & 1u) << 15) | ((nib & 2u) << 30), ((nib & 4u) << 13) | ((nib & 8u) << 28));
+    }
+  }
+
+  // this wave's column tiles (past nct: the last one again, never stored)
+  const uint8_t* xv[2];
+  const uint8_t* xs[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int ct = min((int)blockIdx.y * 2 * NW + 2 * wave + c, nct - 1);
+    xv[c] = xh + (int64_t)ct * nb * kXhUnit + 16 * lane;
+    xs[c] = xh + xh_scale_base(nct, nb) + (int64_t)ct * nb * kXhScaleUnit + 32 * j;
+  }
+  // B operands of the current step: slice u of column tile c, refilled with the next step's as
+  // soon as the slice's MFMAs are issued; its scales (and Q4_K's sums) in a second set
+  u32x4 bq[2][4];
+  float dx[2][4], dxn[2][4], sq[2], sqn[2];
+  auto load_bq = [&](int c, int u, int b, int h) {
+    bq[c][u] = *(const u32x4*)(xv[c] + (int64_t)b * kXhUnit + 4096 * h + 1024 * u);
+  };
+  auto load_scales = [&](int b, int h) {
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const f4 v = *(const f4*)(xs[c] + (int64_t)b * kXhScaleUnit + 16 * h);
+      dxn[c][0] = v[0];
+      dxn[c][1] = v[1];
+      dxn[c][2] = v[2];
+      dxn[c][3] = v[3];
+      if constexpr (!IQ3) sqn[c] = *(const float*)(xs[c] + (int64_t)b * kXhScaleUnit + 512 + 16 * h + 4 * q);
+    }
+  };
+  auto take_scales = [&]() {
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) dx[c][u] = dxn[c][u];
+      sq[c] = sqn[c];
+    }
+  };
+  // this wave's decode rows (tiles past the weight's end, rows past nrows: copies, never stored)
+  const uint8_t* wp[TPW];
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) {
+    const int t = wave * TPW + i;
+    if constexpr (IQ3) {
+      wp[i] = W + (int64_t)min(tile0 + t, ntiles - 1) * kTileRows * row_bytes;
+    } else {
+      wp[i] = W + (int64_t)min((tile0 + t) * 16 + j, nrows - 1) * row_bytes;
+    }
+  }
+  Raw raw[TPW];
+  float e[TPW];
+  auto load_w = [&](int b, int h) {
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+      if constexpr (IQ3) load_step(raw[i], wp[i] + (int64_t)b * kTileBlockBytes, h, j, q);
+      else load_step(raw[i], wp[i] + (int64_t)b * block_bytes(kQ4_K), h, q);
+    }
+  };
+  auto decode = [&](int h) {
+    uint8_t* Ab = A + h * kHA;
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+      const int t = wave * TPW + i;
+      if constexpr (IQ3) decode_step(raw[i], h, GH, SM, Ab, RT, EF, e[i], t, j, q);
+      else decode_step(raw[i], h, AM + h * 512, Ab, RT, EF, e[i], t, j, q);
+    }
+  };
+
+  f4 acc[8][2];
+#pragma unroll
+  for (int r = 0; r < 8; ++r) acc[r][0] = acc[r][1] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  // One step: 4 slices x 8 row tiles x 2 column tiles. Software-pipelined: the next A operand is
+  // read while the current pair of MFMAs runs, and a pair's results are folded into acc one
+  // row tile later. nb_, nh: the step whose B operands refill the registers.
+  auto compute = [&](int h, int bnext, int hnext) {
+    const uint8_t* Ab = A + h * kHA;
+    if (h == 0) {  // a new block: rescale every row to its e
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const f4 rt = *(const f4*)(RT + r * 16 + 4 * q);
+        acc[r][0] *= rt;
+        acc[r][1] *= rt;
+      }
+    }
+    h8 a = *(const h8*)(Ab + h_off(0, 0, j, q));
+    f4 p0 = zero, p1 = zero;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const int rn = r == 7 ? 0 : r + 1, un = r == 7 ? u + 1 : u;
+        h8 an = a;
+        if (un < 4) an = *(const h8*)(Ab + h_off(rn, un, j, q));
+        const f4 n0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(h8, bq[0][u]), zero, 0, 0, 0);
+        const f4 n1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(h8, bq[1][u]), zero, 0, 0, 0);
+        if (u > 0 || r > 0) {
+          const int rp = r == 0 ? 7 : r - 1, upv = r == 0 ? u - 1 : u;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            acc[rp][0][v] = fmaf(p0[v], dx[0][upv], acc[rp][0][v]);
+            acc[rp][1][v] = fmaf(p1[v], dx[1][upv], acc[rp][1][v]);
+          }
+        }
+        p0 = n0;
+        p1 = n1;
+        a = an;
+      }
+      load_bq(0, u, bnext, hnext);  // slice u's operands are consumed: the next step's
+      load_bq(1, u, bnext, hnext);
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      acc[7][0][v] = fmaf(p0[v], dx[0][3], acc[7][0][v]);
+      acc[7][1][v] = fmaf(p1[v], dx[1][3], acc[7][1][v]);
+    }
+    if constexpr (!IQ3) {  // the min term of the half block
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const float am = AM[h * 512 + (r * 4 + q) * 16 + j];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) acc[r][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(am, sq[c], acc[r][c], 0, 0, 0);
+      }
+    }
+  };
+
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) e[i] = 1.0f;
+  load_w(0, 0);
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    load_bq(0, u, 0, 0);
+    load_bq(1, u, 0, 0);
+  }
+  load_scales(0, 0);
+  if constexpr (IQ3) __syncthreads();  // the decode tables
+  decode(0);
+  load_w(0, 1);
+  take_scales();
+  __syncthreads();
+  for (int b = 0; b < nb; ++b) {
+    const int bn = min(b + 1, nb - 1);  // past the end: block nb - 1 again (never computed)
+    // sched_barrier: the decode's arithmetic on the raw bytes stays after the MFMAs (hoisted
+    // into them it makes the whole step wait for the raw loads of the step after)
+    load_scales(b, 1);
+    compute(0, b, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    decode(1);
+    load_w(bn, 0);
+    take_scales();
+    __syncthreads();
+    load_scales(bn, 0);
+    compute(1, bn, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    decode(0);  // at the last block a repeat of it, which leaves e and EF as they are
+    load_w(bn, 1);
+    take_scales();
+    __syncthreads();
+  }
+
+  const int col0 = ((int)blockIdx.y * 2 * NW + 2 * wave) * kXqCols + j;
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    const int t = tile0 + r;
+    const f4 ef = *(const f4*)(EF + r * 16 + 4 * q);
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int col = col0 + c * kXqCols;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = t * 16 + 4 * q + v;
+        if (col < n && t < ntiles && row < nrows) store_y(y, (int64_t)col * nrows + row, acc[r][c][v] * ef[v], y_dtype);
+      }
+    }
+  }
+}
+
+template <int TYPE, int NW>
+void launch_prefill_h_t(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xh, int n, void* y,
+                        int y_dtype, hipStream_t stream) {
+  const int nct = (int)xq_col_tiles(n);
+  const int ntiles = (nrows + 15) / 16;
+  const dim3 grid((unsigned)((ntiles + kPfRowTiles - 1) / kPfRowTiles), (unsigned)((nct + 2 * NW - 1) / (2 * NW)));
+  gemm_prefill_h_kernel<TYPE, NW><<<grid, 64 * NW, 0, stream>>>(W, row_bytes, nrows, k, xh, nct, n, y, y_dtype);
+}
+
+template <int TYPE>
+void launch_prefill_h(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xh, int n, void* y,
+                      int y_dtype, hipStream_t stream) {
+  const int64_t groups = (int64_t)((nrows + 127) / 128) * ((xq_col_tiles(n) + 15) / 16);
+  if (groups >= 256) launch_prefill_h_t<TYPE, 8>(W, row_bytes, nrows, k, xh, n, y, y_dtype, stream);
+  else launch_prefill_h_t<TYPE, 4>(W, row_bytes, nrows, k, xh, n, y, y_dtype, stream);
+}
+
 template <int TYPE, bool TILE>
 void launch_prefill_t(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n, void* y,
                       int y_dtype, hipStream_t stream) {
@@ -309,14 +688,18 @@ void launch_prefill_t(const uint8_t* W, int64_t row_bytes, int nrows, int k, con
 
 }  // namespace
 
-// Large-M products; xq: X in the xq layout. packed: IQ3_S in the tile layout (nrows % 16 == 0).
+// Whether the prefill GEMM of this type takes X in the xh layout (else xq).
+bool prefill_uses_xh(int type, bool packed) { return packed || type == kQ4_K; }
+
+// Large-M products; xq: X in the xq layout, or the xh layout where prefill_uses_xh. packed: IQ3_S
+// in the tile layout (nrows % 16 == 0).
 hipError_t launch_gemm_prefill(int type, bool packed, const uint8_t* W, int64_t row_bytes, int nrows, int k,
                                const uint8_t* xq, int n, void* y, int y_dtype, hipStream_t stream) {
   if (packed) {
-    launch_prefill_t<kIQ3_S, true>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
+    launch_prefill_h<kIQ3_S>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
   } else {
     switch (type) {
-      case kQ4_K: launch_prefill_t<kQ4_K, false>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream); break;
+      case kQ4_K: launch_prefill_h<kQ4_K>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream); break;
       case kIQ4_XS: launch_prefill_t<kIQ4_XS, false>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream); break;
       case kQ6_K: launch_prefill_t<kQ6_K, false>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream); break;
       default: return hipErrorInvalidValue;

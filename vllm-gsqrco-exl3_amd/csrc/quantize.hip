@@ -123,7 +123,36 @@ __device__ __forceinline__ void xq_store(uint8_t* y, int64_t k, int64_t c, int64
   }
 }
 
-template <int DT, bool VEC, bool DS4>
+// The prefill GEMM's fp16 layout (xq.h, "xh"); same thread mapping and values as xq_store.
+template <bool DS4>
+__device__ __forceinline__ void xh_store(uint8_t* y, int64_t k, int64_t c, int64_t kk, int64_t total, uint32_t lo,
+                                         uint32_t hi, float d, int qsum) {
+  const int64_t per_row = k / 8;
+  const int64_t nb = k / kQK;
+  const int64_t b = kk / kQK;
+  const int u = (int)((kk / kQ81) & 7), q = (int)((kk / 8) & 3);
+  const int64_t t = c / kXqCols;
+  const int j = (int)(c % kXqCols);
+  const int64_t unit = t * nb + b;
+  uint32_t h[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t w = e < 2 ? lo : hi;
+    const int sh = 16 * (e & 1);
+    const float f0 = (float)(int8_t)((w >> sh) & 0xFF), f1 = (float)(int8_t)((w >> (sh + 8)) & 0xFF);
+    h[e] = (uint32_t)__half_as_ushort(__float2half_rn(f0)) | ((uint32_t)__half_as_ushort(__float2half_rn(f1)) << 16);
+  }
+  *(uint4*)(y + unit * kXhUnit + 1024 * u + 16 * (16 * q + j)) = make_uint4(h[0], h[1], h[2], h[3]);
+  if (q == 0) {
+    const int64_t nct = total / per_row / kXqCols;
+    uint8_t* sc = y + xh_scale_base(nct, nb) + unit * kXhScaleUnit + 32 * j + 4 * u;
+    const float dd = DS4 ? half_bits_to_float(__half_as_ushort(__float2half_rn(d))) : d;
+    *(float*)sc = dd;
+    if constexpr (DS4) *(float*)(sc + 512) = dd * (float)qsum;
+  }
+}
+
+template <int DT, bool VEC, bool DS4, bool XH = false>
 __global__ void __launch_bounds__(256) quantize_xq_kernel(const void* __restrict__ x, uint8_t* __restrict__ y,
                                                           int64_t k, int64_t s01, int n, int64_t total) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -161,7 +190,8 @@ __global__ void __launch_bounds__(256) quantize_xq_kernel(const void* __restrict
   }
   qsum += __shfl_xor(qsum, 1, 64);
   qsum += __shfl_xor(qsum, 2, 64);
-  xq_store<VEC, DS4>(y, k, c, kk, total, lo, hi, d, qsum);
+  if constexpr (XH) xh_store<DS4>(y, k, c, kk, total, lo, hi, d, qsum);
+  else xq_store<VEC, DS4>(y, k, c, kk, total, lo, hi, d, qsum);
 }
 
 // block_q8_1 bytes of X (a caller's x_q8) -> the xq layout with the same values and fp16 scales.
@@ -212,6 +242,25 @@ hipError_t launch_quantize_xq(const void* x, int dtype, int64_t n, int64_t k, in
   }
 #undef GGUF_QXQ_DT
 #undef GGUF_QXQ
+  return hipGetLastError();
+}
+
+// X [n, k] -> the xh layout at y (xh_bytes(n, k) bytes), MMQ arithmetic, for weights of `type`.
+hipError_t launch_quantize_xh(const void* x, int dtype, int64_t n, int64_t k, int64_t s01, int type, void* y,
+                              hipStream_t stream) {
+  if (n == 0) return hipSuccess;
+  const int64_t total = xq_col_tiles(n) * kXqCols * (k / 8);
+  const unsigned blocks = (unsigned)((total + 255) / 256);
+  const bool ds4 = type == kQ4_K;
+#define GGUF_QXH(DT)                                                                                          \
+  if (ds4) quantize_xq_kernel<DT, false, true, true><<<blocks, 256, 0, stream>>>(x, (uint8_t*)y, k, s01, (int)n, total); \
+  else quantize_xq_kernel<DT, false, false, true><<<blocks, 256, 0, stream>>>(x, (uint8_t*)y, k, s01, (int)n, total);
+  switch (dtype) {
+    case kF32: GGUF_QXH(kF32) break;
+    case kF16: GGUF_QXH(kF16) break;
+    default: GGUF_QXH(kBF16) break;
+  }
+#undef GGUF_QXH
   return hipGetLastError();
 }
 

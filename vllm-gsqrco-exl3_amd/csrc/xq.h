@@ -35,6 +35,25 @@ __host__ __device__ inline size_t xq_bytes(int64_t n, int64_t k) {
   return (size_t)(nct * nb * (kXqUnit + kXqScaleUnit));
 }
 
+// The prefill GEMM's fp16 variant of the layout ("xh"): the same q8 values held as fp16 (exact),
+// the same column tiles and K blocks. For column tile t and block b:
+//   values  8192 B at ((t * nb + b) * 8192): slice u at 1024u, lane l = 16q + j of a wave owns 16
+//           bytes at 1024u + 16l: the fp16 values 32u + 8q .. 32u + 8q + 7 of activation row
+//           16t + j (the f16 MFMA B operand of the slice). Slices 4h..4h+3 are 4 KB contiguous.
+//   scales  1024 B at nct * nb * 8192 + (t * nb + b) * 1024: fp32 d of (row j, slice u) at 32j + 4u
+//           (a lane reads the 4 scales of its half block with one 16-byte load); for Q4_K
+//           weights, d is the fp16-rounded scale, and 512 + 32j + 4u holds d times the slice's sum
+//           of q (exact in fp32), the activation side of the min term.
+constexpr int kXhUnit = 8192;       // fp16 value bytes per (column tile, K block)
+constexpr int kXhScaleUnit = 1024;  // scale bytes per (column tile, K block)
+
+__host__ __device__ inline int64_t xh_scale_base(int64_t nct, int64_t nb) { return nct * nb * kXhUnit; }
+
+__host__ __device__ inline size_t xh_bytes(int64_t n, int64_t k) {
+  const int64_t nct = xq_col_tiles(n), nb = k / kQK;
+  return (size_t)(nct * nb * (kXhUnit + kXhScaleUnit));
+}
+
 // MFMA B operand of slice 2i + h from the 16 bytes b[t][i] of a lane's xq unit
 __device__ __forceinline__ long xq_b_operand(const u32x4& v, int h) {
   return h == 0 ? (long)(((uint64_t)v[1] << 32) | v[0]) : (long)(((uint64_t)v[3] << 32) | v[2]);
