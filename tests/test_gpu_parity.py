@@ -361,6 +361,36 @@ def test_prefill_16bit_x(qt, dtype):
     assert o.rel_l2(y.float().cpu().numpy(), ref) <= TIGHT[dtype]
 
 
+@pytest.mark.parametrize("n", [1, 2, 3, 4])  # the persistent kernel serves 1-2 rows
+def test_packed_gemv_many_tiles(n):
+    """More 16-row tiles than the GEMV's persistent grid (two workgroups per CU), so each
+    workgroup loops over several tiles; X given as q8_1 (x_q8), which keeps n = 1 off the fused
+    path: exact-integer dots, the q81 model, and bit-identical CUDA-graph replays."""
+    from vllm_gguf_plugin.quantization import iq3_pack
+
+    rows, k = 16 * 700, 2048  # 8 K blocks: one per wave at the most waves per tile
+    op = C().lcpp_mul_mat_vec_iq3_mma_packed
+    raw = _exact_weights(o.IQ3_S, rows, k, seed=160 + n)
+    w = iq3_pack.pack(_dev(raw), o.IQ3_S)
+    x = _exact_x(n, k, seed=161 + n, dtype=torch.float32).cuda()
+    q8 = C().lcpp_quantize_q8_1(x, o.IQ3_S, False, False)
+    y = op(w, x, o.IQ3_S, rows, q8).cpu().numpy()
+    np.testing.assert_array_equal(y.astype(np.int64), _exact_ref(raw, o.IQ3_S, x.cpu()))
+    raw = _w(o.IQ3_S, rows, k, seed=170 + n)
+    w = iq3_pack.pack(_dev(raw), o.IQ3_S)
+    x = _x(n, k, seed=171 + n, dtype=torch.bfloat16).cuda()
+    q8 = C().lcpp_quantize_q8_1(x, o.IQ3_S, False, False)
+    eager = op(w, x, o.IQ3_S, rows, q8)
+    assert o.rel_l2(eager.float().cpu().numpy(), o.q81_model(raw, o.IQ3_S, x.cpu())) <= TIGHT[torch.bfloat16]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = op(w, x, o.IQ3_S, rows, q8)
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+
+
 # ------------------------------------------------------------------------------------ x_q8, graphs
 @pytest.mark.parametrize("qt", TYPES, ids=lambda t: TN[t])
 @pytest.mark.parametrize("n", [2, 4, 8])
