@@ -423,6 +423,23 @@ def test_shared_x_q8_packed(n, dtype):
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("n,dtype", [(1, torch.bfloat16), (1, torch.float16), (1, torch.float32),
+                                     (2, torch.bfloat16), (2, torch.float32)])
+@pytest.mark.parametrize("rows,k", [(16 * 700, 2048), (6144, 5120), (5120, 17408)])
+def test_fused_quantisation_large_weights(rows, k, n, dtype):
+    """Without x_q8, the packed decode op quantises X itself on large weights (and at two rows):
+    all of X into LDS first. It must give the bits of the q8_1 quantiser followed by the GEMV."""
+    from vllm_gguf_plugin.quantization import iq3_pack
+
+    w = iq3_pack.pack(_dev(_w(o.IQ3_S, rows, k, seed=180 + n)), o.IQ3_S)
+    x = _x(n, k, seed=181 + n, dtype=dtype).cuda()
+    x[:, 96:128] = 0  # an all-zero slice (d = 0, q = 0)
+    q8 = C().lcpp_quantize_q8_1(x, o.IQ3_S, False, False)
+    a = C().lcpp_mul_mat_vec_iq3_mma_packed(w, x, o.IQ3_S, rows)
+    b = C().lcpp_mul_mat_vec_iq3_mma_packed(w, x, o.IQ3_S, rows, q8)
+    assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize("op,qt,n,packed", [
     ("lcpp_mul_mat_vec_iq3_mma_packed", o.IQ3_S, 4, True),
     ("lcpp_mul_mat_iq3_packed", o.IQ3_S, 32, True),

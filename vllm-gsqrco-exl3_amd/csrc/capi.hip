@@ -33,6 +33,7 @@ hipError_t launch_gemm_xq(int type, const uint8_t* W, int64_t row_bytes, int nro
                           void* y, int y_dtype, hipStream_t stream);
 hipError_t launch_gemv_packed_x(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x, int x_dtype,
                                 int64_t s01, int n, void* y, int y_dtype, hipStream_t stream);
+bool gemv_packed_x_supported(int64_t nrows, int64_t k, int64_t n);
 hipError_t launch_gemm_packed_xq(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n,
                                  void* y, int y_dtype, hipStream_t stream);
 hipError_t launch_quantize_xh(const void* x, int dtype, int64_t n, int64_t k, int64_t s01, int type, void* y,
@@ -210,10 +211,11 @@ namespace {
 // Decode ops (1..8 rows; the packed IQ3 op up to 32) go to the int8-MFMA GEMM from this many
 // activation rows on, measured against the dot4 GEMV at the 27B-layer shapes: the GEMV's time
 // grows with every row, the GEMM's is flat up to 16. IQ3_S on plain rows stays on the GEMV.
-// The packed decode op at one activation row on weights of up to 32M values (the attention
-// projections) quantises X inside the GEMV instead of in a launch of its own.
+// The packed decode op quantises X inside the GEMV when the caller gives no x_q8: at one
+// activation row on weights of up to 32M values (the attention projections) block by block, and
+// at one or two rows on larger weights by quantising all of X into LDS first.
 bool packed_fused(int op, int64_t row, int64_t k, int64_t n, bool has_x_q8) {
-  return op_packed(op) && !has_x_q8 && n == 1 && row * k <= ((int64_t)32 << 20);
+  return op_packed(op) && !has_x_q8 && gguf::gemv_packed_x_supported(row, k, n);
 }
 
 // Product ops go to the 128 x 128-tile prefill GEMM from this many activation rows on (the small

@@ -13,6 +13,8 @@
 // which a row's slice terms are added differs (lane-strided, then the butterfly).
 #include <type_traits>
 
+#include <algorithm>
+
 #include "decode.h"
 #include "iq3_tile.h"
 
@@ -438,14 +440,20 @@ __global__ void __launch_bounds__(64 * TPW * WPT) gemv_iq3s_tile_kernel(const ui
 // g loops over tiles g, g + G, ...; the 32 KB table is copied once per workgroup, and each wave's
 // prefetch runs on from its last block of one tile to its first block of the next (a one-tile
 // workgroup starts every tile with an exposed load). The per-wave K ranges, partial sums and
-// reduction order are those of gemv_iq3s_tile_kernel, so the results are bit-identical. q8 input;
-// every wave needs at least one K block (k / 256 >= WPT).
-template <int NC, int WPT>
+// reduction order are those of gemv_iq3s_tile_kernel, so the results are bit-identical. Every
+// wave needs at least one K block (k / 256 >= WPT).
+// XDT < 0: X given as block_q8_1. XDT >= 0: X itself (dtype XDT, row stride s01); each workgroup
+// first quantises all of X into LDS with the q8_1 quantiser's arithmetic (bit-identical bytes),
+// 8 lanes per 32-value slice, so the separate quantise launch goes and the per-block X reads
+// come from LDS. Dynamic LDS: NC * k / 32 * 36 bytes.
+template <int NC, int WPT, int XDT>
 __global__ void __launch_bounds__(64 * WPT) gemv_iq3s_persist_kernel(const uint8_t* __restrict__ W, int64_t row_bytes,
-                                                                     int nrows, int k, const uint8_t* __restrict__ q8,
-                                                                     void* __restrict__ y, int y_dtype) {
+                                                                     int nrows, int k, const void* __restrict__ xsrc,
+                                                                     int64_t s01, void* __restrict__ y, int y_dtype) {
+  constexpr bool FUSED = XDT >= 0;
   __shared__ uint4 table[2048];
   __shared__ float red[2][WPT][NC][kTileRows];  // by tile parity: one barrier per tile
+  extern __shared__ uint4 xdyn[];               // FUSED: q values [NC][slice][8 dwords], then d [NC][slice]
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int ntiles = nrows / kTileRows;
@@ -454,15 +462,31 @@ __global__ void __launch_bounds__(64 * WPT) gemv_iq3s_persist_kernel(const uint8
   const int b_begin = wave * nb / WPT, b_end = (wave + 1) * nb / WPT;
   const int nblk = b_end - b_begin;
   const int G = gridDim.x;
-  const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(q8, (uint32_t)(NC * nslices * 36));
+  const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(xsrc, FUSED ? 0u : (uint32_t)(NC * nslices * 36));
   const __amdgpu_buffer_rsrc_t nrs = buffer_rsrc(W, 0);
   const uint8_t* tbl = (const uint8_t*)table;
   const TileOffs off = tile_offsets(lane, p, s);
   const uint32_t xoff = 36u * (uint32_t)s;
+  uint32_t* xq = (uint32_t*)xdyn;
+  const uint32_t* xd = xq + NC * nslices * 8;
   iq3_table_to_lds<WPT>(table, &kIq3sSignedDev, wave, lane);
   // tile t's rows, or an empty descriptor past the last tile (prefetch beyond the stream)
   auto tile_rs = [&](int t) {
     return t < ntiles ? buffer_rsrc(W + (int64_t)t * kTileRows * row_bytes, (uint32_t)(kTileRows * row_bytes)) : nrs;
+  };
+  auto load_x = [&](int b, XFrag<NC>& x) {
+    if constexpr (FUSED) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int sl = c * nslices + b * 8 + s;
+        const uint4 a0 = *(const uint4*)(xq + sl * 8), a1 = *(const uint4*)(xq + sl * 8 + 4);
+        x.q[c][0] = (int)a0.x; x.q[c][1] = (int)a0.y; x.q[c][2] = (int)a0.z; x.q[c][3] = (int)a0.w;
+        x.q[c][4] = (int)a1.x; x.q[c][5] = (int)a1.y; x.q[c][6] = (int)a1.z; x.q[c][7] = (int)a1.w;
+        x.d[c] = xd[sl];
+      }
+    } else {
+      load_x_frag<NC>(xrs, xoff, nslices, b * 8, x);
+    }
   };
   // the wave's stream: (tile t, block b) for t = blockIdx.x, blockIdx.x + G, ..., b in [b_begin, b_end)
   int t = blockIdx.x, b = b_begin, it = 0;
@@ -470,9 +494,39 @@ __global__ void __launch_bounds__(64 * WPT) gemv_iq3s_persist_kernel(const uint8
   TileFrag fa, fb;
   XFrag<NC> xa, xb;
   load_tile_frag(tile_rs(t), b * kTileBlockBytes, off, fa);
-  load_x_frag<NC>(xrs, xoff, nslices, b * 8, xa);
+  if constexpr (FUSED) {
+    // quantise X: group g (4 values) of slice g / 8 of row c; the 8 lanes of a slice are
+    // consecutive (the stride is a multiple of 8), so they reduce amax by xor shuffles
+    constexpr int XD = FUSED ? XDT : kBF16;
+    for (int g = threadIdx.x; g < NC * nslices * 8; g += 64 * WPT) {
+      const int c = g / (nslices * 8), sl = (g >> 3) - c * nslices, part = g & 7;
+      const int64_t e0 = c * s01 + sl * kQ81 + 4 * part;
+      float v[4];
+      if constexpr (XD == kF32) {
+        const float4 f = *(const float4*)((const float*)xsrc + e0);
+        v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
+      } else {
+        const uint2 h = *(const uint2*)((const uint16_t*)xsrc + e0);
+        const uint32_t hv[4] = {h.x & 0xFFFF, h.x >> 16, h.y & 0xFFFF, h.y >> 16};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = XD == kF16 ? half_bits_to_float(hv[i]) : __uint_as_float(hv[i] << 16);
+      }
+      float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+      amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+      amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+      amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+      const float d = amax / 127.0f;
+      const float dd = amax == 0.0f ? 1.0f : d;  // all values zero: q = 0 without a branch
+      uint32_t qw = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) qw |= ((uint32_t)(int)roundf(v[i] / dd) & 0xFFu) << (8 * i);
+      xq[(c * nslices + sl) * 8 + part] = qw;
+      if (part == 0) ((uint32_t*)xd)[c * nslices + sl] = __half_as_ushort(__float2half_rn(d));
+    }
+  }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  load_x(b, xa);
   float acc[2][NC];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -485,7 +539,7 @@ __global__ void __launch_bounds__(64 * WPT) gemv_iq3s_persist_kernel(const uint8
       bn = b_begin;
     }
     load_tile_frag(tile_rs(tn), bn * kTileBlockBytes, off, fn);
-    load_x_frag<NC>(xrs, xoff, nslices, bn * 8, xn);
+    load_x(bn, xn);
     __builtin_amdgcn_sched_barrier(0);
     tile_compute<NC>(tbl, fc, xc, s, acc);
     if (b == b_end - 1) {  // the wave's last block of tile t: reduce and store the tile
@@ -561,17 +615,23 @@ static void launch_gemv_packed_w(const uint8_t* W, int64_t row_bytes, int nrows,
 
 // One tile per workgroup. Eight waves split K for one or two columns (measured best at
 // 17408 x 5120: 12.3 us at M=1); from three columns on, the register file allows four.
+// The persistent kernel: g workgroups (two per CU, at most one per tile), n <= 2 rows.
+template <int XDT>
+static void launch_gemv_persist(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x, int64_t s01, int n,
+                                void* y, int y_dtype, hipStream_t stream) {
+  const unsigned g = (unsigned)std::min(nrows / kTileRows, persist_grid());
+  const size_t lds = XDT >= 0 ? (size_t)n * (k / kQ81) * 36 : 0;
+  if (n == 1) gemv_iq3s_persist_kernel<1, 8, XDT><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, x, s01, y, y_dtype);
+  else gemv_iq3s_persist_kernel<2, 8, XDT><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, x, s01, y, y_dtype);
+}
+
 template <int XDT>
 static void launch_gemv_packed_dt(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x, int64_t s01,
                                   int n, void* y, int y_dtype, hipStream_t stream) {
   if constexpr (XDT < 0) {  // q8 input: the persistent kernel when the tiles outnumber its grid
-    // (and every wave has a K block: its per-tile barrier counts on all waves reducing)
-    const int tiles = nrows / kTileRows, g = persist_grid();
     // (measured: 17408 x 5120 M = 1 11.4 us against 12.8; no gain at 3-4 rows, 4 waves per tile)
-    if (tiles > g && n <= 2 && k / kQK >= 8) {
-      const uint8_t* q8 = (const uint8_t*)x;
-      if (n == 1) gemv_iq3s_persist_kernel<1, 8><<<g, 512, 0, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype);
-      else gemv_iq3s_persist_kernel<2, 8><<<g, 512, 0, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype);
+    if (nrows / kTileRows > persist_grid() && n <= 2 && k / kQK >= 8) {
+      launch_gemv_persist<XDT>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream);
       return;
     }
   }
@@ -586,17 +646,35 @@ hipError_t launch_gemv_packed(const uint8_t* W, int64_t row_bytes, int nrows, in
   return hipGetLastError();
 }
 
-// nrows % 16 == 0, n == 1; X [1, k] of dtype x_dtype, quantised in the kernel (bit-identical to the
-// q8_1 quantiser followed by the GEMV). Measured faster than the two launches for the attention
-// shapes (up to 6144 x 5120 weights), slower for the 17408 x 5120 FFN shapes, where the exact
-// divisions and the slice exchange lengthen the latency-bound GEMV by more than the launch costs.
+// nrows % 16 == 0; X [n, k] of dtype x_dtype, quantised in the kernel (bit-identical to the q8_1
+// quantiser followed by the GEMV). n == 1 on weights of up to 32M values: the one-tile kernel,
+// which quantises each block as it goes (measured faster than the two launches for the attention
+// shapes). Otherwise n <= 2 with k / 256 >= 8, X's q8_1 fitting in 48 KB of LDS and more tiles
+// than the persistent grid: the persistent kernel, which quantises all of X into LDS first
+// (17408 x 5120 M = 1: 12.8 us per op against 13.8; with one tile per workgroup, as at
+// 5120 x 17408, the per-workgroup quantisation costs more than the launch it saves).
+bool gemv_packed_x_supported(int64_t nrows, int64_t k, int64_t n) {
+  if (n == 1 && nrows * k <= ((int64_t)32 << 20)) return true;
+  return n >= 1 && n <= 2 && k / kQK >= 8 && n * (k / kQ81) * 36 <= 48 * 1024 && nrows / kTileRows > persist_grid();
+}
+
 hipError_t launch_gemv_packed_x(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x, int x_dtype,
                                 int64_t s01, int n, void* y, int y_dtype, hipStream_t stream) {
-  if (n != 1) return hipErrorInvalidValue;
+  if (!gemv_packed_x_supported(nrows, k, n)) return hipErrorInvalidValue;
+  const bool small = n == 1 && (int64_t)nrows * k <= ((int64_t)32 << 20);
   switch (x_dtype) {
-    case kF32: launch_gemv_packed_dt<kF32>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream); break;
-    case kF16: launch_gemv_packed_dt<kF16>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream); break;
-    default: launch_gemv_packed_dt<kBF16>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream); break;
+    case kF32:
+      if (small) launch_gemv_packed_dt<kF32>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream);
+      else launch_gemv_persist<kF32>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream);
+      break;
+    case kF16:
+      if (small) launch_gemv_packed_dt<kF16>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream);
+      else launch_gemv_persist<kF16>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream);
+      break;
+    default:
+      if (small) launch_gemv_packed_dt<kBF16>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream);
+      else launch_gemv_persist<kBF16>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream);
+      break;
   }
   return hipGetLastError();
 }
