@@ -423,6 +423,31 @@ def test_shared_x_q8_packed(n, dtype):
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("n", [1, 2])
+def test_q4k_gemv_tiles(n):
+    """The Q4_K decode GEMV's tile kernel (1-2 rows, K >= 2048): a row count that is not a
+    multiple of 16 and more tiles than the persistent grid; exact-integer dots, the q81 model and
+    bit-identical CUDA-graph replays."""
+    rows, k = 16 * 700 + 5, 2048
+    op = getattr(C(), VEC_OP[o.Q4_K])
+    raw = _exact_weights(o.Q4_K, rows, k, seed=190 + n)
+    x = _exact_x(n, k, seed=191 + n, dtype=torch.float32)
+    y = op(_dev(raw), x.cuda(), o.Q4_K, rows).cpu().numpy()
+    np.testing.assert_array_equal(y.astype(np.int64), _exact_ref(raw, o.Q4_K, x))
+    raw = _w(o.Q4_K, rows, k, seed=192 + n)
+    w = _dev(raw)
+    x = _x(n, k, seed=193 + n, dtype=torch.bfloat16).cuda()
+    eager = op(w, x, o.Q4_K, rows)
+    assert o.rel_l2(eager.float().cpu().numpy(), o.q81_model(raw, o.Q4_K, x.cpu())) <= TIGHT[torch.bfloat16]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = op(w, x, o.Q4_K, rows)
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+
+
 @pytest.mark.parametrize("n,dtype", [(1, torch.bfloat16), (1, torch.float16), (1, torch.float32),
                                      (2, torch.bfloat16), (2, torch.float32)])
 @pytest.mark.parametrize("rows,k", [(16 * 700, 2048), (6144, 5120), (5120, 17408)])

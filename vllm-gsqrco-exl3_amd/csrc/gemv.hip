@@ -22,6 +22,8 @@ namespace gguf {
 
 constexpr int kGemvWaves = 4;
 
+static int persist_grid();
+
 template <int TYPE, int NC, int RW>
 __global__ void __launch_bounds__(256) gemv_raw_kernel(const uint8_t* __restrict__ W, int64_t row_bytes, int nrows,
                                                        int k, const uint8_t* __restrict__ q8, void* __restrict__ y,
@@ -118,6 +120,140 @@ __global__ void __launch_bounds__(256) gemv_raw_kernel(const uint8_t* __restrict
       if (lane == r * NC + c && row0 + r < nrows) store_y(y, (int64_t)c * nrows + row0 + r, acc[r][c], y_dtype);
 }
 
+// Q4_K on GGUF rows, tile style: a 16-row tile at a time, lane (row j = lane & 15, slice pair
+// pc = lane >> 4) of each 144-byte block loads the block header (16 B: d, dmin, scales) and the
+// pair's 32 bytes of nibbles, so a wave's 3 loads cover the tile's 16 blocks; the next block is
+// loaded before the current one is computed. WPT waves split the K blocks; workgroups are
+// persistent over tiles (two per CU) and first copy the q8_1 of X into LDS with each slice's sum
+// of q. Per slice: d * sc * sum(q4 * q8) - dmin * m * sum(q8), times the slice's d8 (the reference
+// vec_dot_q4_K_q8_1 terms, vecdotq.cuh:508-530); partial sums over the 4 pair lanes of a row
+// (xor butterfly), then over the waves in wave order.
+struct Q4kFrag {
+  u32x4 hdr;      // d | dmin << 16, scales[0..11]
+  u32x4 lo, hi;   // the pair's 32 nibble bytes
+};
+
+template <int NC, int WPT>
+__global__ void __launch_bounds__(64 * WPT) gemv_q4k_tile_kernel(const uint8_t* __restrict__ W, int64_t row_bytes,
+                                                                 int nrows, int k, const uint8_t* __restrict__ q8,
+                                                                 void* __restrict__ y, int y_dtype) {
+  constexpr int BS = 144;
+  __shared__ float red[2][WPT][NC][kTileRows];
+  extern __shared__ uint4 xdyn[];  // q values [NC][slice][8 dwords], then (d8, sum q) [NC][slice]
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 15, pc = lane >> 4;
+  const int ntiles = (nrows + kTileRows - 1) / kTileRows;
+  const int nb = k / kQK, nslices = k / kQ81;
+  const int b_begin = wave * nb / WPT, b_end = (wave + 1) * nb / WPT;
+  const int nblk = b_end - b_begin;
+  const int G = gridDim.x;
+  uint32_t* xq = (uint32_t*)xdyn;
+  float2* xs = (float2*)(xq + NC * nslices * 8);
+  // X's q8_1 into LDS: 9 dwords per (row, slice)
+  for (int i = threadIdx.x; i < NC * nslices * 9; i += 64 * WPT) {
+    const int sl = i / 9, e = i - sl * 9;
+    const uint32_t v = *(const uint32_t*)(q8 + (int64_t)sl * 36 + 4 * e);
+    if (e == 0) xs[sl].x = half_bits_to_float(v & 0xFFFF);
+    else xq[sl * 8 + e - 1] = v;
+  }
+  __syncthreads();
+  for (int sl = threadIdx.x; sl < NC * nslices; sl += 64 * WPT) {
+    int t = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) t = dot4(0x01010101, (int)xq[sl * 8 + e], t);
+    xs[sl].y = (float)t;
+  }
+  const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(W, (uint32_t)((int64_t)nrows * row_bytes));
+  const __amdgpu_buffer_rsrc_t nrs = buffer_rsrc(W, 0);
+  auto roff = [&](int t) { return min(t * kTileRows + j, nrows - 1) * (int)row_bytes; };
+  auto load = [&](int t, int b, Q4kFrag& f) {
+    const __amdgpu_buffer_rsrc_t rs = t < ntiles ? wrs : nrs;
+    const int o = roff(t < ntiles ? t : 0), bo = b * BS;
+    f.hdr = __builtin_amdgcn_raw_buffer_load_b128(rs, o, bo, 0);
+    f.lo = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 16 + 32 * pc, bo, 0);
+    f.hi = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 32 + 32 * pc, bo, 0);
+  };
+  float acc[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) acc[c] = 0.0f;
+  auto compute = [&](const Q4kFrag& f, int b) {
+    const float d = half_bits_to_float(f.hdr[0] & 0xFFFF), dmin = half_bits_to_float(f.hdr[0] >> 16);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {  // slice u = 2pc + h: low (h = 0) or high nibbles of the pair
+      const int u = 2 * pc + h, jj = u & 3;
+      const uint32_t a = (f.hdr[1] >> (8 * jj)) & 0xFF, cb = (f.hdr[2] >> (8 * jj)) & 0xFF;
+      const uint32_t ee = (f.hdr[3] >> (8 * jj)) & 0xFF;
+      const uint32_t sc = u < 4 ? (a & 63) : ((ee & 0xF) | ((a >> 6) << 4));
+      const uint32_t m = u < 4 ? (cb & 63) : ((ee >> 4) | ((cb >> 6) << 4));
+      int w[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        w[e] = (int)((f.lo[e] >> (4 * h)) & 0x0F0F0F0Fu);
+        w[4 + e] = (int)((f.hi[e] >> (4 * h)) & 0x0F0F0F0Fu);
+      }
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int sl = c * nslices + b * 8 + u;
+        const uint4 x0 = *(const uint4*)(xq + sl * 8), x1 = *(const uint4*)(xq + sl * 8 + 4);
+        const float2 ds = xs[sl];
+        int sumi = dot4(w[0], (int)x0.x, 0);
+        sumi = dot4(w[1], (int)x0.y, sumi);
+        sumi = dot4(w[2], (int)x0.z, sumi);
+        sumi = dot4(w[3], (int)x0.w, sumi);
+        sumi = dot4(w[4], (int)x1.x, sumi);
+        sumi = dot4(w[5], (int)x1.y, sumi);
+        sumi = dot4(w[6], (int)x1.z, sumi);
+        sumi = dot4(w[7], (int)x1.w, sumi);
+        const float t = (d * (float)sc) * (float)sumi - (dmin * (float)m) * ds.y;
+        acc[c] = fmaf(t, ds.x, acc[c]);
+      }
+    }
+  };
+  // the wave's stream: (tile t, block b) for t = blockIdx.x, blockIdx.x + G, ..., b in [b_begin, b_end)
+  int t = blockIdx.x, b = b_begin, it = 0;
+  const int items = ((int)blockIdx.x < ntiles ? (ntiles - 1 - (int)blockIdx.x) / G + 1 : 0) * nblk;
+  Q4kFrag fa, fb;
+  load(t, b, fa);
+  auto step = [&](const Q4kFrag& fc, Q4kFrag& fn) {
+    int tn = t, bn = b + 1;
+    if (bn == b_end) {
+      tn = t + G;
+      bn = b_begin;
+    }
+    load(tn, bn, fn);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(fc, b);
+    if (b == b_end - 1) {  // the wave's last block of tile t: reduce and store the tile
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        float v = acc[c];
+        v += __shfl_xor(v, 16, 64);
+        v += __shfl_xor(v, 32, 64);
+        if (pc == 0) red[it & 1][wave][c][j] = v;
+        acc[c] = 0.0f;
+      }
+      __syncthreads();
+      if (threadIdx.x < NC * kTileRows) {
+        const int c = threadIdx.x / kTileRows, r = threadIdx.x % kTileRows;
+        const int row = t * kTileRows + r;
+        float v = red[it & 1][0][c][r];
+#pragma unroll
+        for (int w2 = 1; w2 < WPT; ++w2) v += red[it & 1][w2][c][r];
+        if (row < nrows) store_y(y, (int64_t)c * nrows + row, v, y_dtype);
+      }
+      ++it;
+    }
+    t = tn;
+    b = bn;
+  };
+  for (int i = 0; i + 1 < items; i += 2) {
+    step(fa, fb);
+    step(fb, fa);
+  }
+  if (items & 1) step(fa, fb);
+}
+
 template <int TYPE, int NC>
 static void launch_nc(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, void* y, int y_dtype,
                       hipStream_t stream) {
@@ -144,6 +280,17 @@ static void launch_type(const uint8_t* W, int64_t row_bytes, int nrows, int k, c
 // n in 1..8 activation rows; q8: block_q8_1 of X; y: [n, nrows] in y_dtype.
 hipError_t launch_gemv_raw(int type, const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n,
                            void* y, int y_dtype, hipStream_t stream) {
+  // Q4_K at 1-2 rows on weights of at least 8 K blocks (one per wave) below 4 GiB whose X q8_1
+  // fits in 48 KB of LDS: the tile kernel (17408 x 5120 M = 1 measured against the raw kernel)
+  if (type == kQ4_K && n <= 2 && k / kQK >= 8 && (int64_t)nrows * row_bytes < ((int64_t)1 << 32) &&
+      n * (k / kQ81) * 40 <= 48 * 1024) {
+    const int tiles = (nrows + kTileRows - 1) / kTileRows;
+    const unsigned g = (unsigned)std::min(tiles, persist_grid());
+    const size_t lds = (size_t)n * (k / kQ81) * 40;
+    if (n == 1) gemv_q4k_tile_kernel<1, 8><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype);
+    else gemv_q4k_tile_kernel<2, 8><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype);
+    return hipGetLastError();
+  }
   switch (type) {
     case kIQ3_S: launch_type<kIQ3_S>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream); break;
     case kQ4_K: launch_type<kQ4_K>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream); break;
