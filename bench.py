@@ -15,16 +15,16 @@ synchronize on each side. `value` is the whole-job algorithmic throughput (weigh
 per call) in GB/s.
 
 Also reported: the dominant kernel's roofline (the packed decode GEMV kernel at 17408 x 5120,
-M = 1, timed alone with the q8_1 input precomputed), the metric's other points (IQ3_S and Q4_K at
+M = 1, which quantises X itself, timed alone), the metric's other points (IQ3_S and Q4_K at
 M = 1, 4, 16, 32, 48 on 17408 x 5120, each through the routing table's op), and the CPU oracle
 (numpy dequantise + torch fp32 matmul) timed on the host cores on a bounded sample; and the other
 BASELINE configs under "configs": the CPU-path Q4_K 4096x4096 case next to its GPU op, the MTP
 small GEMM (IQ3_S / IQ4_XS / Q6_K at M = 4..48 on the attention shapes), the prefill GEMM
-(M = 512..8192, with int8 MFMA utilisation) and the 64-layer decoder sweep under one CUDA graph
+(M = 512..8192, with MFMA utilisation) and the 64-layer decoder sweep under one CUDA graph
 with a replay bit-exactness check.
 
 `traffic` (HBM bytes per launch of the dominant kernel) is read from the committed PMC summary
-profiles/gemv_iq3s_tile_17408x5120_m1.traffic.json when present (null otherwise). That summary
+profiles/gemv_iq3s_persist_17408x5120_m1.traffic.json when present (null otherwise). That summary
 comes from `rocprofv3 --pmc FETCH_SIZE` and `--pmc WRITE_SIZE` runs of `bench.py --kernel-only`,
 which times only the dominant kernel and then runs a plain elementwise copy of 256 MiB (read
 256 MiB, write 256 MiB) whose counter readings calibrate the counters' byte scale.
@@ -43,12 +43,13 @@ sys.path.insert(0, os.path.join(ROOT, "vllm-gsqrco-exl3_amd"))
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 NBUF = 8                       # distinct weight copies per shape (defeats the 256 MB MALL)
 COPY_BYTES = 256 << 20         # calibration copy: bytes read (and written) per launch
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_iq3s_tile_17408x5120_m1.traffic.json")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_iq3s_persist_17408x5120_m1.traffic.json")
 IQ3_S, Q4_K, Q6_K, IQ4_XS = 21, 12, 14, 23
 TYPE_NAME = {IQ3_S: "IQ3_S", Q4_K: "Q4_K", Q6_K: "Q6_K", IQ4_XS: "IQ4_XS"}
 BLOCK = {IQ3_S: 110, Q4_K: 144, Q6_K: 210, IQ4_XS: 136}
 SCALE_OFFSETS = {IQ3_S: (0,), Q4_K: (0, 2), Q6_K: (208,), IQ4_XS: (0,)}
 MFMA_I8_PEAK_TOPS = 5000.0     # MI355X dense int8 MFMA
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 
 
 def make_weights(torch, qt, rows, k, seed):
@@ -62,15 +63,19 @@ def make_weights(torch, qt, rows, k, seed):
     return w.view(rows, -1)
 
 
-def graph(torch, calls):
-    """One CUDA graph replaying `calls` (zero-arg launchers) back to back."""
+def graph(torch, calls, outputs=None):
+    """One CUDA graph replaying `calls` (zero-arg launchers) back to back. `outputs`, a list, receives
+    the tensors the captured calls return: they live in the graph's pool and every replay rewrites
+    them in place."""
     for c in calls[:2]:
         c()
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         for c in calls:
-            c()
+            r = c()
+            if outputs is not None:
+                outputs.append(r)
     g.replay()
     torch.cuda.synchronize()
     return g
@@ -135,7 +140,10 @@ def config_prefill(torch, C, iq3_pack, linear):
             pts = op_points(torch, C, iq3_pack, linear, qt, rows, 5120, (512, 2048, 8192), ncopies=2, reps=2,
                             seed=3000)
             for p in pts:
+                # IQ3_S and Q4_K run on fp16 MFMAs (exact sub-scaled integer operands), Q6_K on int8
+                p["mfma"] = "f16" if qt in (IQ3_S, Q4_K) else "i8"
                 p["frac_mfma_i8"] = round(p["int8_tops"] / MFMA_I8_PEAK_TOPS, 4)
+                p["frac_mfma_f16"] = round(p["int8_tops"] / MFMA_F16_PEAK_TFLOPS, 4)
             out += pts
     return out
 
@@ -162,14 +170,12 @@ def config_layers(torch, C, iq3_pack, linear, steps, ms=(1, 4, 16, 32), nlayers=
     out = []
     for m in ms:
         xs = {k: torch.randn(m, k, device="cuda", dtype=torch.bfloat16) for k in (5120, 6144, 17408)}
-        ys = []
+        ys = []  # the captured calls' outputs (graph-owned, rewritten by every replay)
         fns = []
         for qt, rows, k, w in calls:
             op = getattr(C, linear._lcpp_op(m, qt, rows, k, qt == IQ3_S))
-            y = torch.empty(m, rows, device="cuda", dtype=torch.bfloat16)
-            ys.append(y)
-            fns.append(lambda op=op, w=w, x=xs[k], qt=qt, rows=rows, y=y: y.copy_(op(w, x, qt, rows)))
-        g = graph(torch, fns)
+            fns.append(lambda op=op, w=w, x=xs[k], qt=qt, rows=rows: op(w, x, qt, rows))
+        g = graph(torch, fns, ys)
         g.replay()
         torch.cuda.synchronize()
         first = [y.clone() for y in ys]
@@ -251,18 +257,19 @@ def load_traffic():
 
 
 def dominant_kernel(torch, C, ws, steps):
-    """The packed decode GEMV kernel alone (17408 x 5120, M = 1, q8_1 input precomputed): one graph
-    of one launch per weight copy, timed with HIP events on the stream the op launches on."""
+    """The headline's dominant kernel alone: the packed decode op at 17408 x 5120, M = 1, bf16 X,
+    which is one launch of the persistent GEMV that quantises X itself
+    (gemv_iq3s_persist_kernel<1, 8, bf16>); one graph of one launch per weight copy, timed with
+    HIP events on the stream the op launches on."""
     rows, k, m = 17408, 5120, 1
     x = torch.randn(m, k, device="cuda", dtype=torch.bfloat16)
-    q8 = C.lcpp_quantize_q8_1(x, IQ3_S, False, False)
-    kg = graph(torch, [lambda w=w: C.lcpp_mul_mat_vec_iq3_mma_packed(w, x, IQ3_S, rows, q8) for w in ws])
+    kg = graph(torch, [lambda w=w: C.lcpp_mul_mat_vec_iq3_mma_packed(w, x, IQ3_S, rows) for w in ws])
     kernel_us = time_graphs(torch, [kg], max(5, steps)) * 1e3 / len(ws)
-    alg_bytes = ws[0].numel() + q8.numel() + m * rows * 2
+    alg_bytes = ws[0].numel() + m * k * 2 + m * rows * 2
     achieved = alg_bytes / (kernel_us * 1e-6) / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic(),
-            "kernel": "gemv_iq3s_tile_kernel<1,1,8> (17408x5120, M=1, q8_1 precomputed)",
+            "kernel": "gemv_iq3s_persist_kernel<1,8,bf16> (17408x5120, M=1, X quantised in the kernel)",
             "us_per_launch": round(kernel_us, 3), "alg_bytes_per_launch": alg_bytes}
 
 
