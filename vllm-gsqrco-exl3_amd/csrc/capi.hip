@@ -256,14 +256,14 @@ int gguf_mul_mat(int op, const gguf_view* W, const gguf_view* X, int64_t type, i
   if (y_bytes < (size_t)(n * row * elem_size(X->dtype))) return fail("%s: output buffer too small", name);
   const bool packed = op_packed(op);
   const bool gemm = op_gemm(op);
+  hipStream_t s = (hipStream_t)stream;
+  const DeviceScope scope(X->device);
+  if (scope.err != hipSuccess) return hip_fail(scope.err, name, "device select");
+  // sized on X's device, as the dispatch below decides (some plans depend on its CU count)
   const size_t need = gguf_op_workspace_bytes(op, type, row, k, n, x_q8 != nullptr);
   if (workspace_bytes < need || (need > 0 && !workspace))
     return fail("%s: workspace of %zu bytes needed, got %zu", name, need, workspace_bytes);
   if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0) return fail("%s: workspace must be 16-byte aligned", name);
-
-  hipStream_t s = (hipStream_t)stream;
-  const DeviceScope scope(X->device);
-  if (scope.err != hipSuccess) return hip_fail(scope.err, name, "device select");
   hipError_t e;
   const int64_t s01 = n == 1 ? k : X->stride[0];
   const uint8_t* w = (const uint8_t*)W->data;
