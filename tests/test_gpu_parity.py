@@ -423,25 +423,26 @@ def test_shared_x_q8_packed(n, dtype):
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("qt", [o.Q4_K, o.IQ4_XS, o.Q6_K], ids=lambda t: TN[t])
 @pytest.mark.parametrize("n", [1, 2])
-def test_q4k_gemv_tiles(n):
-    """The Q4_K decode GEMV's tile kernel (1-2 rows, K >= 2048): a row count that is not a
+def test_raw_gemv_tiles(qt, n):
+    """The GGUF-row decode GEMV's tile kernel (1-2 rows, K >= 2048): a row count that is not a
     multiple of 16 and more tiles than the persistent grid; exact-integer dots, the q81 model and
     bit-identical CUDA-graph replays."""
     rows, k = 16 * 700 + 5, 2048
-    op = getattr(C(), VEC_OP[o.Q4_K])
-    raw = _exact_weights(o.Q4_K, rows, k, seed=190 + n)
+    op = getattr(C(), VEC_OP[qt])
+    raw = _exact_weights(qt, rows, k, seed=190 + n)
     x = _exact_x(n, k, seed=191 + n, dtype=torch.float32)
-    y = op(_dev(raw), x.cuda(), o.Q4_K, rows).cpu().numpy()
-    np.testing.assert_array_equal(y.astype(np.int64), _exact_ref(raw, o.Q4_K, x))
-    raw = _w(o.Q4_K, rows, k, seed=192 + n)
+    y = op(_dev(raw), x.cuda(), qt, rows).cpu().numpy()
+    np.testing.assert_array_equal(y.astype(np.int64), _exact_ref(raw, qt, x))
+    raw = _w(qt, rows, k, seed=192 + n)
     w = _dev(raw)
     x = _x(n, k, seed=193 + n, dtype=torch.bfloat16).cuda()
-    eager = op(w, x, o.Q4_K, rows)
-    assert o.rel_l2(eager.float().cpu().numpy(), o.q81_model(raw, o.Q4_K, x.cpu())) <= TIGHT[torch.bfloat16]
+    eager = op(w, x, qt, rows)
+    assert o.rel_l2(eager.float().cpu().numpy(), o.q81_model(raw, qt, x.cpu())) <= TIGHT[torch.bfloat16]
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        out = op(w, x, o.Q4_K, rows)
+        out = op(w, x, qt, rows)
     for _ in range(3):
         g.replay()
         torch.cuda.synchronize()

@@ -120,24 +120,63 @@ __global__ void __launch_bounds__(256) gemv_raw_kernel(const uint8_t* __restrict
       if (lane == r * NC + c && row0 + r < nrows) store_y(y, (int64_t)c * nrows + row0 + r, acc[r][c], y_dtype);
 }
 
-// Q4_K on GGUF rows, tile style: a 16-row tile at a time, lane (row j = lane & 15, slice pair
-// pc = lane >> 4) of each 144-byte block loads the block header (16 B: d, dmin, scales) and the
-// pair's 32 bytes of nibbles, so a wave's 3 loads cover the tile's 16 blocks; the next block is
-// loaded before the current one is computed. WPT waves split the K blocks; workgroups are
-// persistent over tiles (two per CU) and first copy the q8_1 of X into LDS with each slice's sum
-// of q. Per slice: d * sc * sum(q4 * q8) - dmin * m * sum(q8), times the slice's d8 (the reference
-// vec_dot_q4_K_q8_1 terms, vecdotq.cuh:508-530); partial sums over the 4 pair lanes of a row
-// (xor butterfly), then over the waves in wave order.
-struct Q4kFrag {
-  u32x4 hdr;      // d | dmin << 16, scales[0..11]
-  u32x4 lo, hi;   // the pair's 32 nibble bytes
+// Q4_K, IQ4_XS and Q6_K on GGUF rows, tile style: a 16-row tile at a time, lane (row j = lane & 15,
+// slice pair pc = lane >> 4) of each block loads the row's header bytes and the 32 values-bytes of
+// its two slices (Q6_K: the ql and qh bytes the pair's values live in), so a wave's loads cover
+// the tile's 16 blocks; the next block is loaded before the current one is computed. WPT waves
+// split the K blocks; workgroups are persistent over tiles (two per CU) and first copy the q8_1
+// of X into LDS with each slice's sum of q. Per slice the reference vec_dot terms
+// (vecdotq.cuh: Q4_K 508-530, IQ4_XS 1357-1380, Q6_K 627-648) times the slice's d8; partial
+// sums over the 4 pair lanes of a row (xor butterfly), then over the waves in wave order.
+template <int TYPE>
+struct RawTileFrag;
+template <>
+struct RawTileFrag<kQ4_K> {
+  u32x4 hdr;     // d | dmin << 16, scales[0..11]
+  u32x4 lo, hi;  // the pair's 32 nibble bytes
+};
+template <>
+struct RawTileFrag<kIQ4_XS> {
+  uint32_t h0, h1;  // d | scales_h << 16, scales_l
+  u32x4 q0, q1;     // slice 2pc, 2pc + 1: 16 bytes each (low nibbles values 0..15, high 16..31)
+};
+template <>
+struct RawTileFrag<kQ6_K> {
+  u32x4 qa[2], qb[2];  // ql[64n .. 64n + 32), ql[64n + 32 .. 64n + 64), n = pc >> 1
+  u32x4 qh[2];         // qh[32n .. 32n + 32)
+  uint32_t sc, d;      // scales[4pc .. 4pc + 4), fp16 d
 };
 
-template <int NC, int WPT>
-__global__ void __launch_bounds__(64 * WPT) gemv_q4k_tile_kernel(const uint8_t* __restrict__ W, int64_t row_bytes,
-                                                                 int nrows, int k, const uint8_t* __restrict__ q8,
-                                                                 void* __restrict__ y, int y_dtype) {
-  constexpr int BS = 144;
+template <int TYPE>
+__device__ __forceinline__ void load_rawtile(__amdgpu_buffer_rsrc_t rs, int o, int bo, int pc, RawTileFrag<TYPE>& f) {
+  if constexpr (TYPE == kQ4_K) {
+    f.hdr = __builtin_amdgcn_raw_buffer_load_b128(rs, o, bo, 0);
+    f.lo = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 16 + 32 * pc, bo, 0);
+    f.hi = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 32 + 32 * pc, bo, 0);
+  } else if constexpr (TYPE == kIQ4_XS) {
+    const auto h = __builtin_amdgcn_raw_buffer_load_b64(rs, o, bo, 0);
+    f.h0 = h[0];
+    f.h1 = h[1];
+    f.q0 = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 8 + 32 * pc, bo, 0);
+    f.q1 = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 24 + 32 * pc, bo, 0);
+  } else {
+    const int n = pc >> 1;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      f.qa[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 64 * n + 16 * i, bo, 0);
+      f.qb[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 64 * n + 32 + 16 * i, bo, 0);
+      f.qh[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 128 + 32 * n + 16 * i, bo, 0);
+    }
+    f.sc = __builtin_amdgcn_raw_buffer_load_b32(rs, o + 192 + 4 * pc, bo, 0);
+    f.d = __builtin_amdgcn_raw_buffer_load_b16(rs, o + 208, bo, 0);
+  }
+}
+
+template <int TYPE, int NC, int WPT>
+__global__ void __launch_bounds__(64 * WPT) gemv_rawtile_kernel(const uint8_t* __restrict__ W, int64_t row_bytes,
+                                                                int nrows, int k, const uint8_t* __restrict__ q8,
+                                                                void* __restrict__ y, int y_dtype) {
+  constexpr int BS = block_bytes(TYPE);
   __shared__ float red[2][WPT][NC][kTileRows];
   extern __shared__ uint4 xdyn[];  // q values [NC][slice][8 dwords], then (d8, sum q) [NC][slice]
   const int lane = threadIdx.x & 63;
@@ -158,64 +197,89 @@ __global__ void __launch_bounds__(64 * WPT) gemv_q4k_tile_kernel(const uint8_t* 
     else xq[sl * 8 + e - 1] = v;
   }
   __syncthreads();
-  for (int sl = threadIdx.x; sl < NC * nslices; sl += 64 * WPT) {
-    int t = 0;
+  if constexpr (TYPE == kQ4_K) {
+    for (int sl = threadIdx.x; sl < NC * nslices; sl += 64 * WPT) {
+      int t = 0;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) t = dot4(0x01010101, (int)xq[sl * 8 + e], t);
-    xs[sl].y = (float)t;
+      for (int e = 0; e < 8; ++e) t = dot4(0x01010101, (int)xq[sl * 8 + e], t);
+      xs[sl].y = (float)t;
+    }
   }
   const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(W, (uint32_t)((int64_t)nrows * row_bytes));
   const __amdgpu_buffer_rsrc_t nrs = buffer_rsrc(W, 0);
-  auto roff = [&](int t) { return min(t * kTileRows + j, nrows - 1) * (int)row_bytes; };
-  auto load = [&](int t, int b, Q4kFrag& f) {
+  auto load = [&](int t, int b, RawTileFrag<TYPE>& f) {
     const __amdgpu_buffer_rsrc_t rs = t < ntiles ? wrs : nrs;
-    const int o = roff(t < ntiles ? t : 0), bo = b * BS;
-    f.hdr = __builtin_amdgcn_raw_buffer_load_b128(rs, o, bo, 0);
-    f.lo = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 16 + 32 * pc, bo, 0);
-    f.hi = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 32 + 32 * pc, bo, 0);
+    const int o = min((t < ntiles ? t : 0) * kTileRows + j, nrows - 1) * (int)row_bytes;
+    load_rawtile<TYPE>(rs, o, b * BS, pc, f);
   };
   float acc[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c) acc[c] = 0.0f;
-  auto compute = [&](const Q4kFrag& f, int b) {
-    const float d = half_bits_to_float(f.hdr[0] & 0xFFFF), dmin = half_bits_to_float(f.hdr[0] >> 16);
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {  // slice u = 2pc + h: low (h = 0) or high nibbles of the pair
-      const int u = 2 * pc + h, jj = u & 3;
-      const uint32_t a = (f.hdr[1] >> (8 * jj)) & 0xFF, cb = (f.hdr[2] >> (8 * jj)) & 0xFF;
-      const uint32_t ee = (f.hdr[3] >> (8 * jj)) & 0xFF;
-      const uint32_t sc = u < 4 ? (a & 63) : ((ee & 0xF) | ((a >> 6) << 4));
-      const uint32_t m = u < 4 ? (cb & 63) : ((ee >> 4) | ((cb >> 6) << 4));
-      int w[8];
+  // slice u = 2pc + h of the lane's row: the dot with X's slice, scaled by everything but d8
+  auto slice_term = [&](const RawTileFrag<TYPE>& f, int h, int c, int sl) -> float {
+    const uint4 x0 = *(const uint4*)(xq + sl * 8), x1 = *(const uint4*)(xq + sl * 8 + 4);
+    const int xv[8] = {(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+    const int u = 2 * pc + h;
+    int w[8];
+    if constexpr (TYPE == kQ4_K) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         w[e] = (int)((f.lo[e] >> (4 * h)) & 0x0F0F0F0Fu);
         w[4 + e] = (int)((f.hi[e] >> (4 * h)) & 0x0F0F0F0Fu);
       }
+      int sumi = 0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sumi = dot4(w[e], xv[e], sumi);
+      const int jj = u & 3;
+      const uint32_t a = (f.hdr[1] >> (8 * jj)) & 0xFF, cb = (f.hdr[2] >> (8 * jj)) & 0xFF;
+      const uint32_t ee = (f.hdr[3] >> (8 * jj)) & 0xFF;
+      const uint32_t sc = u < 4 ? (a & 63) : ((ee & 0xF) | ((a >> 6) << 4));
+      const uint32_t m = u < 4 ? (cb & 63) : ((ee >> 4) | ((cb >> 6) << 4));
+      const float d = half_bits_to_float(f.hdr[0] & 0xFFFF), dmin = half_bits_to_float(f.hdr[0] >> 16);
+      return (d * (float)sc) * (float)sumi - (dmin * (float)m) * xs[sl].y;
+    } else if constexpr (TYPE == kIQ4_XS) {
+      const u32x4 q = h == 0 ? f.q0 : f.q1;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        w[e] = lut16(q[e] & 0x0F0F0F0Fu);
+        w[4 + e] = lut16((q[e] >> 4) & 0x0F0F0F0Fu);
+      }
+      int sumi = 0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sumi = dot4(w[e], xv[e], sumi);
+      const int ls = (int)(((f.h1 >> (8 * pc + 4 * h)) & 0xF) | (((f.h0 >> (16 + 2 * u)) & 3u) << 4)) - 32;
+      return half_bits_to_float(f.h0 & 0xFFFF) * (float)(sumi * ls);
+    } else {
+      const int lsh = 4 * (pc & 1), hsh = 2 * (2 * (pc & 1) + h);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t l = h == 0 ? f.qa[e >> 2][e & 3] : f.qb[e >> 2][e & 3];
+        w[e] = sub32_bytes(((l >> lsh) & 0x0F0F0F0Fu) | (((f.qh[e >> 2][e & 3] >> hsh) & 0x03030303u) << 4));
+      }
+      int sa = 0, sb = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sa = dot4(w[e], xv[e], sa);
+#pragma unroll
+      for (int e = 4; e < 8; ++e) sb = dot4(w[e], xv[e], sb);
+      const int sca = (int)(int8_t)((f.sc >> (16 * h)) & 0xFF), scb = (int)(int8_t)((f.sc >> (16 * h + 8)) & 0xFF);
+      return half_bits_to_float(f.d) * (float)(sa * sca + sb * scb);
+    }
+  };
+  auto compute = [&](const RawTileFrag<TYPE>& f, int b) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        const int sl = c * nslices + b * 8 + u;
-        const uint4 x0 = *(const uint4*)(xq + sl * 8), x1 = *(const uint4*)(xq + sl * 8 + 4);
-        const float2 ds = xs[sl];
-        int sumi = dot4(w[0], (int)x0.x, 0);
-        sumi = dot4(w[1], (int)x0.y, sumi);
-        sumi = dot4(w[2], (int)x0.z, sumi);
-        sumi = dot4(w[3], (int)x0.w, sumi);
-        sumi = dot4(w[4], (int)x1.x, sumi);
-        sumi = dot4(w[5], (int)x1.y, sumi);
-        sumi = dot4(w[6], (int)x1.z, sumi);
-        sumi = dot4(w[7], (int)x1.w, sumi);
-        const float t = (d * (float)sc) * (float)sumi - (dmin * (float)m) * ds.y;
-        acc[c] = fmaf(t, ds.x, acc[c]);
+        const int sl = c * nslices + b * 8 + 2 * pc + h;
+        acc[c] = fmaf(slice_term(f, h, c, sl), xs[sl].x, acc[c]);
       }
-    }
   };
   // the wave's stream: (tile t, block b) for t = blockIdx.x, blockIdx.x + G, ..., b in [b_begin, b_end)
   int t = blockIdx.x, b = b_begin, it = 0;
   const int items = ((int)blockIdx.x < ntiles ? (ntiles - 1 - (int)blockIdx.x) / G + 1 : 0) * nblk;
-  Q4kFrag fa, fb;
+  RawTileFrag<TYPE> fa, fb;
   load(t, b, fa);
-  auto step = [&](const Q4kFrag& fc, Q4kFrag& fn) {
+  auto step = [&](const RawTileFrag<TYPE>& fc, RawTileFrag<TYPE>& fn) {
     int tn = t, bn = b + 1;
     if (bn == b_end) {
       tn = t + G;
@@ -254,6 +318,19 @@ __global__ void __launch_bounds__(64 * WPT) gemv_q4k_tile_kernel(const uint8_t* 
   if (items & 1) step(fa, fb);
 }
 
+template <int TYPE>
+static bool launch_rawtile(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n, void* y,
+                           int y_dtype, hipStream_t stream) {
+  if (n > 2 || k / kQK < 8 || (int64_t)nrows * row_bytes >= ((int64_t)1 << 31) || n * (k / kQ81) * 40 > 48 * 1024)
+    return false;
+  const int tiles = (nrows + kTileRows - 1) / kTileRows;
+  const unsigned g = (unsigned)std::min(tiles, persist_grid());
+  const size_t lds = (size_t)n * (k / kQ81) * 40;
+  if (n == 1) gemv_rawtile_kernel<TYPE, 1, 8><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype);
+  else gemv_rawtile_kernel<TYPE, 2, 8><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype);
+  return true;
+}
+
 template <int TYPE, int NC>
 static void launch_nc(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, void* y, int y_dtype,
                       hipStream_t stream) {
@@ -280,17 +357,13 @@ static void launch_type(const uint8_t* W, int64_t row_bytes, int nrows, int k, c
 // n in 1..8 activation rows; q8: block_q8_1 of X; y: [n, nrows] in y_dtype.
 hipError_t launch_gemv_raw(int type, const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n,
                            void* y, int y_dtype, hipStream_t stream) {
-  // Q4_K at 1-2 rows on weights of at least 8 K blocks (one per wave) below 4 GiB whose X q8_1
-  // fits in 48 KB of LDS: the tile kernel (17408 x 5120 M = 1 measured against the raw kernel)
-  if (type == kQ4_K && n <= 2 && k / kQK >= 8 && (int64_t)nrows * row_bytes < ((int64_t)1 << 32) &&
-      n * (k / kQ81) * 40 <= 48 * 1024) {
-    const int tiles = (nrows + kTileRows - 1) / kTileRows;
-    const unsigned g = (unsigned)std::min(tiles, persist_grid());
-    const size_t lds = (size_t)n * (k / kQ81) * 40;
-    if (n == 1) gemv_q4k_tile_kernel<1, 8><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype);
-    else gemv_q4k_tile_kernel<2, 8><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype);
-    return hipGetLastError();
-  }
+  // Q4_K / IQ4_XS / Q6_K at 1-2 rows on weights of at least 8 K blocks (one per wave) below 2 GiB
+  // whose X q8_1 fits in 48 KB of LDS: the tile kernel
+  bool done = false;
+  if (type == kQ4_K) done = launch_rawtile<kQ4_K>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);
+  if (type == kIQ4_XS) done = launch_rawtile<kIQ4_XS>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);
+  if (type == kQ6_K) done = launch_rawtile<kQ6_K>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);
+  if (done) return hipGetLastError();
   switch (type) {
     case kIQ3_S: launch_type<kIQ3_S>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream); break;
     case kQ4_K: launch_type<kQ4_K>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream); break;
