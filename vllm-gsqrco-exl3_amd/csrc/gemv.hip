@@ -389,7 +389,8 @@ __device__ const Iq3sSignedTable kIq3sSignedDev = make_iq3s_signed_table();
 struct TileFrag {
   uint4 qs;
   uint2 e8;
-  uint32_t l2, sc, dd;
+  uint16_t l2, sc;  // 16-bit loads kept 16-bit: widening them is left to their uses
+  uint32_t dd;
 };
 
 // per-lane byte offsets of a lane's data inside a tile-block (constant over the K loop)
@@ -656,24 +657,135 @@ __global__ void __launch_bounds__(64 * TPW * WPT) gemv_iq3s_tile_kernel(const ui
   }
 }
 
+// X of the persistent GEMV, staged in LDS: q8 values [NC][slice][8 dwords], then each slice's fp16 d
+// [NC][slice] (one dword, low half). Work unit: group g = 8 values, part g & 3 of slice row
+// g >> 2 (= c * nslices + slice of activation row c). The four lanes of a slice are consecutive.
+template <int XDT>
+struct XGroup {
+  uint32_t v[XDT == kF32 ? 8 : (XDT < 0 ? 3 : 4)];
+};
+
+template <int NC, int XDT>
+__device__ __forceinline__ void xgroup_load(const void* x, __amdgpu_buffer_rsrc_t xrs, int64_t s01, int nslices, int g,
+                                            XGroup<XDT>& r) {
+  const int sr = g >> 2, part = g & 3;
+  if constexpr (XDT < 0) {  // block_q8_1: d (fp16) and s, then 32 q bytes
+    const int o = sr * 36;
+    r.v[0] = __builtin_amdgcn_raw_buffer_load_b32(xrs, o, 0, 0);
+    r.v[1] = __builtin_amdgcn_raw_buffer_load_b32(xrs, o + 4 + 8 * part, 0, 0);
+    r.v[2] = __builtin_amdgcn_raw_buffer_load_b32(xrs, o + 8 + 8 * part, 0, 0);
+  } else {
+    int c = 0, sl = sr;
+#pragma unroll
+    for (int i = 1; i < NC; ++i)
+      if (sl >= nslices) sl -= nslices, ++c;
+    const int64_t e0 = c * s01 + (int64_t)sl * kQ81 + 8 * part;
+    if constexpr (XDT == kF32) {
+      const uint4 a = *(const uint4*)((const float*)x + e0), b = *(const uint4*)((const float*)x + e0 + 4);
+      r.v[0] = a.x; r.v[1] = a.y; r.v[2] = a.z; r.v[3] = a.w;
+      r.v[4] = b.x; r.v[5] = b.y; r.v[6] = b.z; r.v[7] = b.w;
+    } else {
+      const uint4 a = *(const uint4*)((const uint16_t*)x + e0);
+      r.v[0] = a.x; r.v[1] = a.y; r.v[2] = a.z; r.v[3] = a.w;
+    }
+  }
+}
+
+// q8_1 bytes of 8 values of one slice, given the slice's amax: d = amax / 127 and q = roundf(v / d)
+// (q = 0 when amax == 0), bit for bit as the q8_1 quantiser computes them. The quotient comes from
+// the product v * rcp(d): for |v| <= amax it lies within 2^-15 of v / d (rcp within 1 ulp), and
+// the fp32 rounding of v / d moves that by less than 2^-16, so when the product lies more than
+// 2^-12 from every half-integer, roundf(v / d) is the integer nearest to it. Adding 1.5 * 2^23
+// rounds to that integer and leaves it in the low mantissa bits. The largest distance is taken
+// over the bit patterns of |a - n|, where a NaN (a NaN or infinite value) ranks above every
+// number. A lane with a value near a tie, a non-finite product or a tiny amax (rcp of a
+// subnormal d) takes the IEEE division.
+__device__ __forceinline__ void quantize8_q81(const float (&v)[8], float amax, float d, uint32_t& lo, uint32_t& hi) {
+  constexpr float kMagic = 12582912.0f;
+  const float r = __builtin_amdgcn_rcpf(d);
+  uint32_t m[8], dev = 0;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float a = v[e] * r;
+    const float t = a + kMagic;
+    m[e] = __float_as_uint(t);
+    dev = max(dev, __float_as_uint(a - (t - kMagic)) & 0x7FFFFFFFu);
+  }
+  lo = __builtin_amdgcn_perm(__builtin_amdgcn_perm(m[3], m[2], 0x0c0c0400u), __builtin_amdgcn_perm(m[1], m[0], 0x0c0c0400u),
+                             0x05040100u);
+  hi = __builtin_amdgcn_perm(__builtin_amdgcn_perm(m[7], m[6], 0x0c0c0400u), __builtin_amdgcn_perm(m[5], m[4], 0x0c0c0400u),
+                             0x05040100u);
+  if (!(amax >= 0x1p-100f) || dev > __float_as_uint(0.5f - 0x1p-12f)) {
+    lo = hi = 0;
+    if (amax != 0.0f) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t q = (uint32_t)(int)roundf(v[e] / d) & 0xFFu;
+        if (e < 4) lo |= q << (8 * e);
+        else hi |= q << (8 * (e - 4));
+      }
+    }
+  }
+}
+
+// max over the four lanes of a quad, exchanged by DPP quad permutes (xor 1, then xor 2)
+__device__ __forceinline__ float quad_fmax(float v) {
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false)));
+  return v;
+}
+
+// group g of X into the LDS staging area (only when `live`; every lane of a slice takes part in
+// the amax exchange)
+template <int XDT>
+__device__ __forceinline__ void xgroup_store(const XGroup<XDT>& r, int g, bool live, uint32_t* xq, uint32_t* xd) {
+  const int sr = g >> 2, part = g & 3;
+  uint32_t lo, hi, dbits;
+  if constexpr (XDT < 0) {
+    lo = r.v[1];
+    hi = r.v[2];
+    dbits = r.v[0] & 0xFFFFu;
+  } else {
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if constexpr (XDT == kF32) v[e] = __uint_as_float(r.v[e]);
+      else {
+        const uint32_t h = (r.v[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+        v[e] = XDT == kF16 ? half_bits_to_float(h) : __uint_as_float(h << 16);
+      }
+    }
+    float amax = fmaxf(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))),
+                       fmaxf(fmaxf(fabsf(v[4]), fabsf(v[5])), fmaxf(fabsf(v[6]), fabsf(v[7]))));
+    amax = quad_fmax(amax);
+    const float d = amax / 127.0f;
+    quantize8_q81(v, amax, d, lo, hi);
+    dbits = __half_as_ushort(__float2half_rn(d));
+  }
+  if (live) {
+    *(uint2*)(xq + sr * 8 + 2 * part) = make_uint2(lo, hi);
+    if (part == 0) xd[sr] = dbits;
+  }
+}
+
 // Persistent variant for weights with more tiles than the grid (two workgroups per CU): workgroup
-// g loops over tiles g, g + G, ...; the 32 KB table is copied once per workgroup, and each wave's
-// prefetch runs on from its last block of one tile to its first block of the next (a one-tile
-// workgroup starts every tile with an exposed load). The per-wave K ranges, partial sums and
-// reduction order are those of gemv_iq3s_tile_kernel, so the results are bit-identical. Every
+// g loops over tiles g, g + G, ...; the 32 KB table is copied once per workgroup. Each wave keeps
+// two tile-blocks of its stream in flight while it computes a third, and its prefetch runs on from
+// its last block of one tile to its first block of the next. The per-wave K ranges, partial sums
+// and reduction order are those of gemv_iq3s_tile_kernel, so the results are bit-identical. Every
 // wave needs at least one K block (k / 256 >= WPT).
-// XDT < 0: X given as block_q8_1. XDT >= 0: X itself (dtype XDT, row stride s01); each workgroup
-// first quantises all of X into LDS with the q8_1 quantiser's arithmetic (bit-identical bytes),
-// 8 lanes per 32-value slice, so the separate quantise launch goes and the per-block X reads
-// come from LDS. Dynamic LDS: NC * k / 32 * 36 bytes.
+// X is staged in LDS first (dynamic LDS: NC * k / 32 * 36 bytes). XDT < 0: X given as block_q8_1,
+// copied. XDT >= 0: X itself (dtype XDT, row stride s01), quantised with the q8_1 quantiser's
+// arithmetic (bit-identical bytes), so the separate quantise launch goes. The first weight
+// blocks and the table copy are issued before the staging's arithmetic, which hides it.
 template <int NC, int WPT, int XDT>
 __global__ void __launch_bounds__(64 * WPT) gemv_iq3s_persist_kernel(const uint8_t* __restrict__ W, int64_t row_bytes,
                                                                      int nrows, int k, const void* __restrict__ xsrc,
                                                                      int64_t s01, void* __restrict__ y, int y_dtype) {
-  constexpr bool FUSED = XDT >= 0;
+  constexpr int NT = 64 * WPT;
   __shared__ uint4 table[2048];
   __shared__ float red[2][WPT][NC][kTileRows];  // by tile parity: one barrier per tile
-  extern __shared__ uint4 xdyn[];               // FUSED: q values [NC][slice][8 dwords], then d [NC][slice]
+  extern __shared__ uint4 xdyn[];               // X: q values [NC][slice][8 dwords], then d [NC][slice]
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int ntiles = nrows / kTileRows;
@@ -682,86 +794,79 @@ __global__ void __launch_bounds__(64 * WPT) gemv_iq3s_persist_kernel(const uint8
   const int b_begin = wave * nb / WPT, b_end = (wave + 1) * nb / WPT;
   const int nblk = b_end - b_begin;
   const int G = gridDim.x;
-  const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(xsrc, FUSED ? 0u : (uint32_t)(NC * nslices * 36));
+  const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(xsrc, XDT < 0 ? (uint32_t)(NC * nslices * 36) : 0u);
   const __amdgpu_buffer_rsrc_t nrs = buffer_rsrc(W, 0);
   const uint8_t* tbl = (const uint8_t*)table;
   const TileOffs off = tile_offsets(lane, p, s);
-  const uint32_t xoff = 36u * (uint32_t)s;
   uint32_t* xq = (uint32_t*)xdyn;
-  const uint32_t* xd = xq + NC * nslices * 8;
-  iq3_table_to_lds<WPT>(table, &kIq3sSignedDev, wave, lane);
+  uint32_t* xd = xq + NC * nslices * 8;
   // tile t's rows, or an empty descriptor past the last tile (prefetch beyond the stream)
   auto tile_rs = [&](int t) {
     return t < ntiles ? buffer_rsrc(W + (int64_t)t * kTileRows * row_bytes, (uint32_t)(kTileRows * row_bytes)) : nrs;
   };
-  auto load_x = [&](int b, XFrag<NC>& x) {
-    if constexpr (FUSED) {
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const int sl = c * nslices + b * 8 + s;
-        const uint4 a0 = *(const uint4*)(xq + sl * 8), a1 = *(const uint4*)(xq + sl * 8 + 4);
-        x.q[c][0] = (int)a0.x; x.q[c][1] = (int)a0.y; x.q[c][2] = (int)a0.z; x.q[c][3] = (int)a0.w;
-        x.q[c][4] = (int)a1.x; x.q[c][5] = (int)a1.y; x.q[c][6] = (int)a1.z; x.q[c][7] = (int)a1.w;
-        x.d[c] = xd[sl];
-      }
-    } else {
-      load_x_frag<NC>(xrs, xoff, nslices, b * 8, x);
+  // the wave's stream: (tile t, block b) for t = blockIdx.x, blockIdx.x + G, ..., b in [b_begin, b_end)
+  const int items = ((int)blockIdx.x < ntiles ? (ntiles - 1 - (int)blockIdx.x) / G + 1 : 0) * nblk;
+  auto next = [&](int& tt, int& bb) {
+    if (++bb == b_end) {
+      bb = b_begin;
+      tt += G;
     }
   };
-  // the wave's stream: (tile t, block b) for t = blockIdx.x, blockIdx.x + G, ..., b in [b_begin, b_end)
-  int t = blockIdx.x, b = b_begin, it = 0;
-  const int items = ((int)blockIdx.x < ntiles ? (ntiles - 1 - (int)blockIdx.x) / G + 1 : 0) * nblk;
-  TileFrag fa, fb;
-  XFrag<NC> xa, xb;
-  load_tile_frag(tile_rs(t), b * kTileBlockBytes, off, fa);
-  if constexpr (FUSED) {
-    // quantise X: group g (4 values) of slice g / 8 of row c; the 8 lanes of a slice are
-    // consecutive (the stride is a multiple of 8), so they reduce amax by xor shuffles
-    constexpr int XD = FUSED ? XDT : kBF16;
-    for (int g = threadIdx.x; g < NC * nslices * 8; g += 64 * WPT) {
-      const int c = g / (nslices * 8), sl = (g >> 3) - c * nslices, part = g & 7;
-      const int64_t e0 = c * s01 + sl * kQ81 + 4 * part;
-      float v[4];
-      if constexpr (XD == kF32) {
-        const float4 f = *(const float4*)((const float*)xsrc + e0);
-        v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
-      } else {
-        const uint2 h = *(const uint2*)((const uint16_t*)xsrc + e0);
-        const uint32_t hv[4] = {h.x & 0xFFFF, h.x >> 16, h.y & 0xFFFF, h.y >> 16};
+  // the table, X's first two groups per thread and the first two weight blocks are loaded in that
+  // order; the table and X are written to LDS while the weights are in flight
+  const int ngroups = NC * nslices * 4;
+  const int ga = threadIdx.x, gb = threadIdx.x + NT;
+  // the table through VGPRs (16 B x 2048 / NT per thread): plain loads only, so the compiler's
+  // count of outstanding loads stays in order (an LDS DMA among them makes it wait for all)
+  constexpr int TPT = 2048 / NT;
+  static_assert(2048 % NT == 0, "table copy assumes NT divides 2048");
+  const __amdgpu_buffer_rsrc_t trs = buffer_rsrc(&kIq3sSignedDev, 2048 * 16);
+  u32x4 tv[TPT];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = XD == kF16 ? half_bits_to_float(hv[i]) : __uint_as_float(hv[i] << 16);
-      }
-      float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-      amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-      amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-      amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
-      const float d = amax / 127.0f;
-      const float dd = amax == 0.0f ? 1.0f : d;  // all values zero: q = 0 without a branch
-      uint32_t qw = 0;
+  for (int j = 0; j < TPT; ++j) tv[j] = __builtin_amdgcn_raw_buffer_load_b128(trs, 16 * threadIdx.x, 16 * j * NT, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  XGroup<XDT> xa, xb;
+  xgroup_load<NC, XDT>(xsrc, xrs, s01, nslices, ga < ngroups ? ga : ngroups - 1, xa);
+  xgroup_load<NC, XDT>(xsrc, xrs, s01, nslices, gb < ngroups ? gb : ngroups - 1, xb);
+  __builtin_amdgcn_sched_barrier(0);
+  TileFrag f0, f1, f2;
+  int lt = blockIdx.x, lb = b_begin;  // next item to load
+  load_tile_frag(tile_rs(lt), lb * kTileBlockBytes, off, f0);
+  next(lt, lb);
+  load_tile_frag(tile_rs(lt), lb * kTileBlockBytes, off, f1);
+  next(lt, lb);
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) qw |= ((uint32_t)(int)roundf(v[i] / dd) & 0xFFu) << (8 * i);
-      xq[(c * nslices + sl) * 8 + part] = qw;
-      if (part == 0) ((uint32_t*)xd)[c * nslices + sl] = __half_as_ushort(__float2half_rn(d));
-    }
+  for (int j = 0; j < TPT; ++j) table[threadIdx.x + j * NT] = make_uint4(tv[j][0], tv[j][1], tv[j][2], tv[j][3]);
+  xgroup_store<XDT>(xa, ga, ga < ngroups, xq, xd);
+  xgroup_store<XDT>(xb, gb, gb < ngroups, xq, xd);
+  for (int g = threadIdx.x + 2 * NT; g < ngroups; g += NT) {  // K beyond 2 groups per thread
+    XGroup<XDT> xc;
+    xgroup_load<NC, XDT>(xsrc, xrs, s01, nslices, g, xc);
+    xgroup_store<XDT>(xc, g, true, xq, xd);
   }
-  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  load_x(b, xa);
   float acc[2][NC];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int c = 0; c < NC; ++c) acc[i][c] = 0.0f;
-  auto step = [&](const TileFrag& fc, const XFrag<NC>& xc, TileFrag& fn, XFrag<NC>& xn) {
-    int tn = t, bn = b + 1;
-    if (bn == b_end) {
-      tn = t + G;
-      bn = b_begin;
-    }
-    load_tile_frag(tile_rs(tn), bn * kTileBlockBytes, off, fn);
-    load_x(bn, xn);
+  int t = blockIdx.x, b = b_begin, it = 0;  // item being computed
+  // compute fc (item i) while item i + 2 loads into fl
+  auto step = [&](const TileFrag& fc, TileFrag& fl) {
+    load_tile_frag(tile_rs(lt), lb * kTileBlockBytes, off, fl);
+    next(lt, lb);
     __builtin_amdgcn_sched_barrier(0);
-    tile_compute<NC>(tbl, fc, xc, s, acc);
+    XFrag<NC> x;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int sl = c * nslices + b * 8 + s;
+      const uint4 a0 = *(const uint4*)(xq + sl * 8), a1 = *(const uint4*)(xq + sl * 8 + 4);
+      x.q[c][0] = (int)a0.x; x.q[c][1] = (int)a0.y; x.q[c][2] = (int)a0.z; x.q[c][3] = (int)a0.w;
+      x.q[c][4] = (int)a1.x; x.q[c][5] = (int)a1.y; x.q[c][6] = (int)a1.z; x.q[c][7] = (int)a1.w;
+      x.d[c] = xd[sl];
+    }
+    tile_compute<NC>(tbl, fc, x, s, acc);
     if (b == b_end - 1) {  // the wave's last block of tile t: reduce and store the tile
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
@@ -785,14 +890,16 @@ __global__ void __launch_bounds__(64 * WPT) gemv_iq3s_persist_kernel(const uint8
       }
       ++it;
     }
-    t = tn;
-    b = bn;
+    next(t, b);
   };
-  for (int i = 0; i + 1 < items; i += 2) {
-    step(fa, xa, fb, xb);
-    step(fb, xb, fa, xa);
+  int i = 0;
+  for (; i + 3 <= items; i += 3) {
+    step(f0, f2);
+    step(f1, f0);
+    step(f2, f1);
   }
-  if (items & 1) step(fa, xa, fb, xb);
+  if (i < items) step(f0, f2);
+  if (i + 1 < items) step(f1, f0);
 }
 
 // workgroups of the persistent GEMV: two per CU of the current device
@@ -840,7 +947,7 @@ template <int XDT>
 static void launch_gemv_persist(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x, int64_t s01, int n,
                                 void* y, int y_dtype, hipStream_t stream) {
   const unsigned g = (unsigned)std::min(nrows / kTileRows, persist_grid());
-  const size_t lds = XDT >= 0 ? (size_t)n * (k / kQ81) * 36 : 0;
+  const size_t lds = (size_t)n * (k / kQ81) * 36;  // X staged in LDS
   if (n == 1) gemv_iq3s_persist_kernel<1, 8, XDT><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, x, s01, y, y_dtype);
   else gemv_iq3s_persist_kernel<2, 8, XDT><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, x, s01, y, y_dtype);
 }
@@ -850,7 +957,7 @@ static void launch_gemv_packed_dt(const uint8_t* W, int64_t row_bytes, int nrows
                                   int n, void* y, int y_dtype, hipStream_t stream) {
   if constexpr (XDT < 0) {  // q8 input: the persistent kernel when the tiles outnumber its grid
     // (measured: 17408 x 5120 M = 1 11.4 us against 12.8; no gain at 3-4 rows, 4 waves per tile)
-    if (nrows / kTileRows > persist_grid() && n <= 2 && k / kQK >= 8) {
+    if (nrows / kTileRows > persist_grid() && n <= 2 && k / kQK >= 8 && n * (k / kQ81) * 36 <= 48 * 1024) {
       launch_gemv_persist<XDT>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream);
       return;
     }

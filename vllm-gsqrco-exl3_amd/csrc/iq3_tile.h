@@ -128,21 +128,37 @@ __device__ __forceinline__ void iq3_tile_ex(uint32_t e8, uint32_t l2, int r, uin
 
 // signed-grid words of the table entries for the two groups a byte permute pairs in P
 // (P = qs0 | ex0 << 8 | qs1 << 16 | ex1 << 24; tbl is the table in LDS)
+// The low index's byte offset (P & 0xFFFF) << 2 is one SDWA shift of P's low word (the compiler
+// otherwise emits a shift and a mask).
 __device__ __forceinline__ void tile_lookup2(const uint8_t* tbl, uint32_t P, int& w0, int& w1) {
-  w0 = *(const int*)(tbl + ((P & 0xFFFFu) << 2));
+  uint32_t o0;
+  asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:WORD_0"
+      : "=v"(o0)
+      : "v"(P));
+  w0 = *(const int*)(tbl + o0);
   w1 = *(const int*)(tbl + (P >> 14));  // bits 14, 15 of P are zero (ex has 5 bits)
 }
 
 // The 32 KB signed-grid table, global -> LDS without VGPRs: 32 wave-wide 1 KB DMA loads
-// (global_load_lds_dwordx4) shared out over the workgroup's NW waves. The caller waits
-// (vmcnt) and synchronises the workgroup before reading the table.
+// (global_load_lds_dwordx4) shared out over the workgroup's NW waves (wave < NW). The caller waits
+// (vmcnt) and synchronises the workgroup before reading the table. When NW divides 32 every wave
+// issues the same number of loads with no branch, so the compiler's count of outstanding loads
+// stays exact past the copy.
 template <int NW>
 __device__ __forceinline__ void iq3_table_to_lds(uint4* table, const Iq3sSignedTable* src_table, int wave, int lane) {
   const uint4* src = (const uint4*)src_table->v;
+  if constexpr (32 % NW == 0) {
 #pragma unroll
-  for (int i = wave; i < 32; i += NW)
-    __builtin_amdgcn_global_load_lds((const void*)(src + i * 64 + lane),
-                                     (__attribute__((address_space(3))) void*)(table + i * 64), 16, 0, 0);
+    for (int j = 0; j < 32 / NW; ++j)
+      __builtin_amdgcn_global_load_lds((const void*)(src + (wave + j * NW) * 64 + lane),
+                                       (__attribute__((address_space(3))) void*)(table + (wave + j * NW) * 64), 16, 0,
+                                       0);
+  } else {
+#pragma unroll
+    for (int i = wave; i < 32; i += NW)
+      __builtin_amdgcn_global_load_lds((const void*)(src + i * 64 + lane),
+                                       (__attribute__((address_space(3))) void*)(table + i * 64), 16, 0, 0);
+  }
 }
 
 }  // namespace gguf
