@@ -466,6 +466,58 @@ def test_fused_quantisation_large_weights(rows, k, n, dtype):
     assert torch.equal(a, b)
 
 
+def _tie_slices(k, dtype, seed):
+    """One activation row whose 32-value slices put x / d exactly on, or one fp32 ulp either side
+    of, a half-integer (d = amax / 127), with all-zero, tiny-amax, negative, infinite and NaN
+    slices among random ones: the cases where a quantiser that divides differs from one that
+    multiplies by a reciprocal."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(k, generator=g, dtype=torch.float64)
+    ks = torch.arange(32, dtype=torch.float64)
+    halves = (ks * 4 % 127) + 0.5                  # k + 0.5 for k in 0..126
+    for sl in range(k // 32):
+        v = x[32 * sl: 32 * sl + 32]
+        kind = sl % 9
+        scale = 2.0 ** float((sl // 9) % 7 - 3)
+        if kind == 0:    # exact ties, d = scale
+            v[:] = halves * scale
+            v[31] = 127 * scale
+        elif kind == 1:  # negative ties
+            v[:] = -halves * scale
+            v[31] = -127 * scale
+        elif kind == 2:  # one fp32 ulp above / below the tie
+            t = (halves * scale).to(torch.float32)
+            v[:] = torch.where(ks % 2 == 0, torch.nextafter(t, t + 1), torch.nextafter(t, t - 1)).double()
+            v[31] = 127 * scale
+        elif kind == 3:
+            v[:] = 0.0
+        elif kind == 4:  # tiny amax: fp32 subnormal d (bf16 / fp32 only)
+            v[:] = v * 1e-37
+        elif kind == 5 and sl % 4 == 1:
+            v[7] = float("inf")
+        elif kind == 6 and sl % 4 == 2:
+            v[3] = float("nan")
+    return x.to(dtype)
+
+
+@pytest.mark.parametrize("n,dtype", [(1, torch.bfloat16), (1, torch.float16), (1, torch.float32),
+                                     (2, torch.bfloat16), (2, torch.float32)])
+def test_fused_quantisation_ties(n, dtype):
+    """The persistent GEMV's in-kernel quantisation rounds x / d from a reciprocal product and
+    takes the IEEE division for values near a tie, non-finite values and tiny scales: its bytes,
+    and so the outputs, must equal those of the q8_1 quantiser bit for bit (NaN included)."""
+    from vllm_gguf_plugin.quantization import iq3_pack
+
+    rows, k = 16 * 700, 4096  # more tiles than the persistent grid, above the one-tile path's size
+    w = iq3_pack.pack(_dev(_w(o.IQ3_S, rows, k, seed=190 + n)), o.IQ3_S)
+    x = torch.stack([_tie_slices(k, dtype, seed=191 + c) for c in range(n)]).cuda()
+    q8 = C().lcpp_quantize_q8_1(x, o.IQ3_S, False, False)
+    a = C().lcpp_mul_mat_vec_iq3_mma_packed(w, x, o.IQ3_S, rows)
+    b = C().lcpp_mul_mat_vec_iq3_mma_packed(w, x, o.IQ3_S, rows, q8)
+    bits = torch.int32 if dtype == torch.float32 else torch.int16
+    assert torch.equal(a.view(bits), b.view(bits))
+
+
 @pytest.mark.parametrize("op,qt,n,packed", [
     ("lcpp_mul_mat_vec_iq3_mma_packed", o.IQ3_S, 4, True),
     ("lcpp_mul_mat_iq3_packed", o.IQ3_S, 32, True),
