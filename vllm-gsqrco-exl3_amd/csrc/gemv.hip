@@ -942,22 +942,29 @@ static void launch_gemv_packed_w(const uint8_t* W, int64_t row_bytes, int nrows,
 
 // One tile per workgroup. Eight waves split K for one or two columns (measured best at
 // 17408 x 5120: 12.3 us at M=1); from three columns on, the register file allows four.
-// The persistent kernel: g workgroups (two per CU, at most one per tile), n <= 2 rows.
+// The persistent kernel: g workgroups (two per CU, at most one per tile), n <= 4 rows (raw X:
+// n <= 2).
 template <int XDT>
 static void launch_gemv_persist(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x, int64_t s01, int n,
                                 void* y, int y_dtype, hipStream_t stream) {
   const unsigned g = (unsigned)std::min(nrows / kTileRows, persist_grid());
   const size_t lds = (size_t)n * (k / kQ81) * 36;  // X staged in LDS
   if (n == 1) gemv_iq3s_persist_kernel<1, 8, XDT><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, x, s01, y, y_dtype);
-  else gemv_iq3s_persist_kernel<2, 8, XDT><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, x, s01, y, y_dtype);
+  else if (n == 2) gemv_iq3s_persist_kernel<2, 8, XDT><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, x, s01, y, y_dtype);
+  else if constexpr (XDT < 0) {  // three or four rows: q8_1 input only
+    if (n == 3) gemv_iq3s_persist_kernel<3, 8, XDT><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, x, s01, y, y_dtype);
+    else gemv_iq3s_persist_kernel<4, 8, XDT><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, x, s01, y, y_dtype);
+  }
 }
 
 template <int XDT>
 static void launch_gemv_packed_dt(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x, int64_t s01,
                                   int n, void* y, int y_dtype, hipStream_t stream) {
   if constexpr (XDT < 0) {  // q8 input: the persistent kernel when the tiles outnumber its grid
-    // (measured: 17408 x 5120 M = 1 11.4 us against 12.8; no gain at 3-4 rows, 4 waves per tile)
-    if (nrows / kTileRows > persist_grid() && n <= 2 && k / kQK >= 8 && n * (k / kQ81) * 36 <= 48 * 1024) {
+    // (measured at 17408 x 5120: 1-2 rows level with or faster than one tile per workgroup, 3-4
+    // rows 15.3 / 17.1 us against 17.1 / 19.4; on weights with fewer tiles than the grid the
+    // one-tile kernel is faster at every row count)
+    if (nrows / kTileRows > persist_grid() && n <= 4 && k / kQK >= 8 && n * (k / kQ81) * 36 <= 48 * 1024) {
       launch_gemv_persist<XDT>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream);
       return;
     }
