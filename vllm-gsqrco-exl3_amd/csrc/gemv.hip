@@ -123,9 +123,10 @@ __global__ void __launch_bounds__(256) gemv_raw_kernel(const uint8_t* __restrict
 // Q4_K, IQ4_XS and Q6_K on GGUF rows, tile style: a 16-row tile at a time, lane (row j = lane & 15,
 // slice pair pc = lane >> 4) of each block loads the row's header bytes and the 32 values-bytes of
 // its two slices (Q6_K: the ql and qh bytes the pair's values live in), so a wave's loads cover
-// the tile's 16 blocks; the next block is loaded before the current one is computed. WPT waves
-// split the K blocks; workgroups are persistent over tiles (two per CU) and first copy the q8_1
-// of X into LDS with each slice's sum of q. Per slice the reference vec_dot terms
+// the tile's 16 blocks; each wave keeps the next two blocks of its stream in flight while it
+// computes one. WPT waves split the K blocks; workgroups are persistent over tiles (two per CU)
+// and first copy the q8_1 of X into LDS with each slice's sum of q (while their first weight
+// blocks load). Per slice the reference vec_dot terms
 // (vecdotq.cuh: Q4_K 508-530, IQ4_XS 1357-1380, Q6_K 627-648) times the slice's d8; partial
 // sums over the 4 pair lanes of a row (xor butterfly), then over the waves in wave order.
 template <int TYPE>
@@ -172,12 +173,46 @@ __device__ __forceinline__ void load_rawtile(__amdgpu_buffer_rsrc_t rs, int o, i
   }
 }
 
+// X of the raw tile GEMV, staged in LDS: q8 values [NC][slice][8 dwords], then (d8, sum of q)
+// [NC][slice]. Group g = part g & 3 (8 q bytes) of slice row g >> 2 of the block_q8_1 array; the
+// four lanes of a slice are consecutive, so the slice's sum of q is a quad sum (DPP).
+struct XGroupQ8 {
+  uint32_t d, q0, q1;
+};
+
+__device__ __forceinline__ void xgroup_q8_load(__amdgpu_buffer_rsrc_t xrs, int g, XGroupQ8& r) {
+  const int o = (g >> 2) * 36, part = g & 3;
+  r.d = __builtin_amdgcn_raw_buffer_load_b32(xrs, o, 0, 0);
+  r.q0 = __builtin_amdgcn_raw_buffer_load_b32(xrs, o + 4 + 8 * part, 0, 0);
+  r.q1 = __builtin_amdgcn_raw_buffer_load_b32(xrs, o + 8 + 8 * part, 0, 0);
+}
+
+// A group past the end (live false) is written to `sink`, not skipped: a load whose only use is a
+// conditional store is moved under the condition by the compiler, and a load under a branch is
+// waited for (vmcnt(0)) where the paths join.
+template <bool SUM>
+__device__ __forceinline__ void xgroup_q8_store(const XGroupQ8& r, int g, bool live, uint32_t* xq, float2* xs,
+                                                uint4* sink) {
+  const int sr = g >> 2, part = g & 3;
+  float sum = 0.0f;
+  if constexpr (SUM) {
+    int t = dot4(0x01010101, (int)r.q1, dot4(0x01010101, (int)r.q0, 0));
+    t += __builtin_amdgcn_mov_dpp(t, 0xB1, 0xF, 0xF, false);  // quad xor 1
+    t += __builtin_amdgcn_mov_dpp(t, 0x4E, 0xF, 0xF, false);  // quad xor 2
+    sum = (float)t;
+  }
+  *(live ? (uint2*)(xq + sr * 8 + 2 * part) : (uint2*)sink) = make_uint2(r.q0, r.q1);
+  *(live && part == 0 ? xs + sr : (float2*)sink) = make_float2(half_bits_to_float(r.d & 0xFFFF), sum);
+}
+
 template <int TYPE, int NC, int WPT>
 __global__ void __launch_bounds__(64 * WPT) gemv_rawtile_kernel(const uint8_t* __restrict__ W, int64_t row_bytes,
                                                                 int nrows, int k, const uint8_t* __restrict__ q8,
                                                                 void* __restrict__ y, int y_dtype) {
   constexpr int BS = block_bytes(TYPE);
+  constexpr int NT = 64 * WPT;
   __shared__ float red[2][WPT][NC][kTileRows];
+  __shared__ uint4 sink;           // staging writes of groups past the end of X
   extern __shared__ uint4 xdyn[];  // q values [NC][slice][8 dwords], then (d8, sum q) [NC][slice]
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -189,29 +224,45 @@ __global__ void __launch_bounds__(64 * WPT) gemv_rawtile_kernel(const uint8_t* _
   const int G = gridDim.x;
   uint32_t* xq = (uint32_t*)xdyn;
   float2* xs = (float2*)(xq + NC * nslices * 8);
-  // X's q8_1 into LDS: 9 dwords per (row, slice)
-  for (int i = threadIdx.x; i < NC * nslices * 9; i += 64 * WPT) {
-    const int sl = i / 9, e = i - sl * 9;
-    const uint32_t v = *(const uint32_t*)(q8 + (int64_t)sl * 36 + 4 * e);
-    if (e == 0) xs[sl].x = half_bits_to_float(v & 0xFFFF);
-    else xq[sl * 8 + e - 1] = v;
-  }
-  __syncthreads();
-  if constexpr (TYPE == kQ4_K) {
-    for (int sl = threadIdx.x; sl < NC * nslices; sl += 64 * WPT) {
-      int t = 0;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) t = dot4(0x01010101, (int)xq[sl * 8 + e], t);
-      xs[sl].y = (float)t;
-    }
-  }
   const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(W, (uint32_t)((int64_t)nrows * row_bytes));
   const __amdgpu_buffer_rsrc_t nrs = buffer_rsrc(W, 0);
+  const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(q8, (uint32_t)(NC * nslices * 36));
   auto load = [&](int t, int b, RawTileFrag<TYPE>& f) {
     const __amdgpu_buffer_rsrc_t rs = t < ntiles ? wrs : nrs;
     const int o = min((t < ntiles ? t : 0) * kTileRows + j, nrows - 1) * (int)row_bytes;
     load_rawtile<TYPE>(rs, o, b * BS, pc, f);
   };
+  // the wave's stream: (tile t, block b) for t = blockIdx.x, blockIdx.x + G, ..., b in [b_begin, b_end)
+  const int items = ((int)blockIdx.x < ntiles ? (ntiles - 1 - (int)blockIdx.x) / G + 1 : 0) * nblk;
+  auto next = [&](int& tt, int& bb) {
+    if (++bb == b_end) {
+      bb = b_begin;
+      tt += G;
+    }
+  };
+  // X's first two groups per thread, then the first two weight blocks; X goes to LDS while the
+  // weights are in flight
+  const int ngroups = NC * nslices * 4;
+  const int ga = threadIdx.x, gb = threadIdx.x + NT;
+  XGroupQ8 xa, xb;
+  xgroup_q8_load(xrs, ga < ngroups ? ga : ngroups - 1, xa);
+  xgroup_q8_load(xrs, gb < ngroups ? gb : ngroups - 1, xb);
+  __builtin_amdgcn_sched_barrier(0);
+  RawTileFrag<TYPE> f0, f1, f2;
+  int lt = blockIdx.x, lb = b_begin;  // next item to load
+  load(lt, lb, f0);
+  next(lt, lb);
+  load(lt, lb, f1);
+  next(lt, lb);
+  __builtin_amdgcn_sched_barrier(0);
+  xgroup_q8_store<TYPE == kQ4_K>(xa, ga, ga < ngroups, xq, xs, &sink);
+  xgroup_q8_store<TYPE == kQ4_K>(xb, gb, gb < ngroups, xq, xs, &sink);
+  for (int g = threadIdx.x + 2 * NT; g < ngroups; g += NT) {  // K beyond 2 groups per thread
+    XGroupQ8 xc;
+    xgroup_q8_load(xrs, g, xc);
+    xgroup_q8_store<TYPE == kQ4_K>(xc, g, true, xq, xs, &sink);
+  }
+  __syncthreads();
   float acc[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c) acc[c] = 0.0f;
@@ -274,18 +325,11 @@ __global__ void __launch_bounds__(64 * WPT) gemv_rawtile_kernel(const uint8_t* _
         acc[c] = fmaf(slice_term(f, h, c, sl), xs[sl].x, acc[c]);
       }
   };
-  // the wave's stream: (tile t, block b) for t = blockIdx.x, blockIdx.x + G, ..., b in [b_begin, b_end)
-  int t = blockIdx.x, b = b_begin, it = 0;
-  const int items = ((int)blockIdx.x < ntiles ? (ntiles - 1 - (int)blockIdx.x) / G + 1 : 0) * nblk;
-  RawTileFrag<TYPE> fa, fb;
-  load(t, b, fa);
-  auto step = [&](const RawTileFrag<TYPE>& fc, RawTileFrag<TYPE>& fn) {
-    int tn = t, bn = b + 1;
-    if (bn == b_end) {
-      tn = t + G;
-      bn = b_begin;
-    }
-    load(tn, bn, fn);
+  int t = blockIdx.x, b = b_begin, it = 0;  // item being computed
+  // compute fc (item i) while item i + 2 loads into fl
+  auto step = [&](const RawTileFrag<TYPE>& fc, RawTileFrag<TYPE>& fl) {
+    load(lt, lb, fl);
+    next(lt, lb);
     __builtin_amdgcn_sched_barrier(0);
     compute(fc, b);
     if (b == b_end - 1) {  // the wave's last block of tile t: reduce and store the tile
@@ -308,14 +352,16 @@ __global__ void __launch_bounds__(64 * WPT) gemv_rawtile_kernel(const uint8_t* _
       }
       ++it;
     }
-    t = tn;
-    b = bn;
+    next(t, b);
   };
-  for (int i = 0; i + 1 < items; i += 2) {
-    step(fa, fb);
-    step(fb, fa);
+  int i = 0;
+  for (; i + 3 <= items; i += 3) {
+    step(f0, f2);
+    step(f1, f0);
+    step(f2, f1);
   }
-  if (items & 1) step(fa, fb);
+  if (i < items) step(f0, f2);
+  if (i + 1 < items) step(f1, f0);
 }
 
 template <int TYPE>
@@ -735,10 +781,12 @@ __device__ __forceinline__ float quad_fmax(float v) {
   return v;
 }
 
-// group g of X into the LDS staging area (only when `live`; every lane of a slice takes part in
-// the amax exchange)
+// group g of X into the LDS staging area (every lane of a slice takes part in the amax exchange);
+// a group past the end (live false) is written to `sink`: a load whose only use is a conditional
+// store is moved under the condition by the compiler and then waited for (vmcnt(0)) at the join
 template <int XDT>
-__device__ __forceinline__ void xgroup_store(const XGroup<XDT>& r, int g, bool live, uint32_t* xq, uint32_t* xd) {
+__device__ __forceinline__ void xgroup_store(const XGroup<XDT>& r, int g, bool live, uint32_t* xq, uint32_t* xd,
+                                             uint4* sink) {
   const int sr = g >> 2, part = g & 3;
   uint32_t lo, hi, dbits;
   if constexpr (XDT < 0) {
@@ -762,10 +810,8 @@ __device__ __forceinline__ void xgroup_store(const XGroup<XDT>& r, int g, bool l
     quantize8_q81(v, amax, d, lo, hi);
     dbits = __half_as_ushort(__float2half_rn(d));
   }
-  if (live) {
-    *(uint2*)(xq + sr * 8 + 2 * part) = make_uint2(lo, hi);
-    if (part == 0) xd[sr] = dbits;
-  }
+  *(live ? (uint2*)(xq + sr * 8 + 2 * part) : (uint2*)sink) = make_uint2(lo, hi);
+  *(live && part == 0 ? xd + sr : (uint32_t*)sink) = dbits;
 }
 
 // Persistent variant for weights with more tiles than the grid (two workgroups per CU): workgroup
@@ -785,6 +831,7 @@ __global__ void __launch_bounds__(64 * WPT) gemv_iq3s_persist_kernel(const uint8
   constexpr int NT = 64 * WPT;
   __shared__ uint4 table[2048];
   __shared__ float red[2][WPT][NC][kTileRows];  // by tile parity: one barrier per tile
+  __shared__ uint4 sink;                        // staging writes of groups past the end of X
   extern __shared__ uint4 xdyn[];               // X: q values [NC][slice][8 dwords], then d [NC][slice]
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -838,12 +885,12 @@ __global__ void __launch_bounds__(64 * WPT) gemv_iq3s_persist_kernel(const uint8
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int j = 0; j < TPT; ++j) table[threadIdx.x + j * NT] = make_uint4(tv[j][0], tv[j][1], tv[j][2], tv[j][3]);
-  xgroup_store<XDT>(xa, ga, ga < ngroups, xq, xd);
-  xgroup_store<XDT>(xb, gb, gb < ngroups, xq, xd);
+  xgroup_store<XDT>(xa, ga, ga < ngroups, xq, xd, &sink);
+  xgroup_store<XDT>(xb, gb, gb < ngroups, xq, xd, &sink);
   for (int g = threadIdx.x + 2 * NT; g < ngroups; g += NT) {  // K beyond 2 groups per thread
     XGroup<XDT> xc;
     xgroup_load<NC, XDT>(xsrc, xrs, s01, nslices, g, xc);
-    xgroup_store<XDT>(xc, g, true, xq, xd);
+    xgroup_store<XDT>(xc, g, true, xq, xd, &sink);
   }
   __syncthreads();
   float acc[2][NC];
