@@ -187,19 +187,25 @@ __device__ __forceinline__ void xgroup_q8_load(__amdgpu_buffer_rsrc_t xrs, int g
   r.q1 = __builtin_amdgcn_raw_buffer_load_b32(xrs, o + 8 + 8 * part, 0, 0);
 }
 
-// A group past the end (live false) is written to `sink`, not skipped: a load whose only use is a
-// conditional store is moved under the condition by the compiler, and a load under a branch is
-// waited for (vmcnt(0)) where the paths join.
-template <bool SUM>
+// SUMS: what the second word of a slice's (d8, .) pair holds. kSumSlice: the slice's sum of q (as
+// float; Q4_K's min term). kSumHalves: the sums of q over values 0..15 and 16..31 as two int16 in
+// the word's bits (Q6_K folds its -32 offset into them). A group past the end (live false) is
+// written to `sink`, not skipped: a load whose only use is a conditional store is moved under the
+// condition by the compiler, and a load under a branch is waited for (vmcnt(0)) where the paths
+// join.
+constexpr int kSumNone = 0, kSumSlice = 1, kSumHalves = 2;
+
+template <int SUMS>
 __device__ __forceinline__ void xgroup_q8_store(const XGroupQ8& r, int g, bool live, uint32_t* xq, float2* xs,
                                                 uint4* sink) {
   const int sr = g >> 2, part = g & 3;
   float sum = 0.0f;
-  if constexpr (SUM) {
+  if constexpr (SUMS != kSumNone) {
     int t = dot4(0x01010101, (int)r.q1, dot4(0x01010101, (int)r.q0, 0));
-    t += __builtin_amdgcn_mov_dpp(t, 0xB1, 0xF, 0xF, false);  // quad xor 1
-    t += __builtin_amdgcn_mov_dpp(t, 0x4E, 0xF, 0xF, false);  // quad xor 2
-    sum = (float)t;
+    t += __builtin_amdgcn_mov_dpp(t, 0xB1, 0xF, 0xF, false);  // quad xor 1: this half's sum
+    const int o = __builtin_amdgcn_mov_dpp(t, 0x4E, 0xF, 0xF, false);  // quad xor 2: the other half's
+    if constexpr (SUMS == kSumSlice) sum = (float)(t + o);
+    else sum = __uint_as_float(((uint32_t)t & 0xFFFFu) | ((uint32_t)o << 16));
   }
   *(live ? (uint2*)(xq + sr * 8 + 2 * part) : (uint2*)sink) = make_uint2(r.q0, r.q1);
   *(live && part == 0 ? xs + sr : (float2*)sink) = make_float2(half_bits_to_float(r.d & 0xFFFF), sum);
@@ -255,12 +261,13 @@ __global__ void __launch_bounds__(64 * WPT) gemv_rawtile_kernel(const uint8_t* _
   load(lt, lb, f1);
   next(lt, lb);
   __builtin_amdgcn_sched_barrier(0);
-  xgroup_q8_store<TYPE == kQ4_K>(xa, ga, ga < ngroups, xq, xs, &sink);
-  xgroup_q8_store<TYPE == kQ4_K>(xb, gb, gb < ngroups, xq, xs, &sink);
+  constexpr int SUMS = TYPE == kQ4_K ? kSumSlice : (TYPE == kQ6_K ? kSumHalves : kSumNone);
+  xgroup_q8_store<SUMS>(xa, ga, ga < ngroups, xq, xs, &sink);
+  xgroup_q8_store<SUMS>(xb, gb, gb < ngroups, xq, xs, &sink);
   for (int g = threadIdx.x + 2 * NT; g < ngroups; g += NT) {  // K beyond 2 groups per thread
     XGroupQ8 xc;
     xgroup_q8_load(xrs, g, xc);
-    xgroup_q8_store<TYPE == kQ4_K>(xc, g, true, xq, xs, &sink);
+    xgroup_q8_store<SUMS>(xc, g, true, xq, xs, &sink);
   }
   __syncthreads();
   float acc[NC];
@@ -301,17 +308,24 @@ __global__ void __launch_bounds__(64 * WPT) gemv_rawtile_kernel(const uint8_t* _
       const int ls = (int)(((f.h1 >> (8 * pc + 4 * h)) & 0xF) | (((f.h0 >> (16 + 2 * u)) & 3u) << 4)) - 32;
       return half_bits_to_float(f.h0 & 0xFFFF) * (float)(sumi * ls);
     } else {
+      // the 6-bit values q (0..63) enter the dot as they are; the -32 offset is applied to the
+      // two 16-value sums as 32 times X's sum over the same values (an exact integer identity);
+      // the two qh bits of each byte reach bits 4-5 by one rotate
       const int lsh = 4 * (pc & 1), hsh = 2 * (2 * (pc & 1) + h);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const uint32_t l = h == 0 ? f.qa[e >> 2][e & 3] : f.qb[e >> 2][e & 3];
-        w[e] = sub32_bytes(((l >> lsh) & 0x0F0F0F0Fu) | (((f.qh[e >> 2][e & 3] >> hsh) & 0x03030303u) << 4));
+        const uint32_t q = f.qh[e >> 2][e & 3];
+        w[e] = (int)(((l >> lsh) & 0x0F0F0F0Fu) | (__builtin_amdgcn_alignbit(q, q, (hsh + 28) & 31) & 0x30303030u));
       }
       int sa = 0, sb = 0;
 #pragma unroll
       for (int e = 0; e < 4; ++e) sa = dot4(w[e], xv[e], sa);
 #pragma unroll
       for (int e = 4; e < 8; ++e) sb = dot4(w[e], xv[e], sb);
+      const uint32_t hs = __float_as_uint(xs[sl].y);
+      sa -= 32 * (int)(int16_t)(hs & 0xFFFFu);
+      sb -= 32 * ((int)hs >> 16);
       const int sca = (int)(int8_t)((f.sc >> (16 * h)) & 0xFF), scb = (int)(int8_t)((f.sc >> (16 * h + 8)) & 0xFF);
       return half_bits_to_float(f.d) * (float)(sa * sca + sb * scb);
     }
@@ -364,6 +378,174 @@ __global__ void __launch_bounds__(64 * WPT) gemv_rawtile_kernel(const uint8_t* _
   if (i + 1 < items) step(f1, f0);
 }
 
+// Q6_K on GGUF rows with loads that run along each row: lane L = 8 r + c (r = row in an 8-row
+// group, c = 16-byte chunk of the row's 128 ql bytes) loads ql[16c .. 16c + 16), the 16 qh bytes
+// that hold the same values' high bits, the row's 8 scales of the block half and d, for rows r
+// and 8 + r of the tile. One load instruction then covers 8 rows' bytes contiguously (128 B of ql
+// per row), where a lane per slice pair (gemv_rawtile_kernel) touches about three times as many
+// cache lines per block, the L1 tag rate being what bounds it. Chunk c = 4n + 2t + h holds, in
+// its low nibbles, values 16h..16h+15 of slice 4n + t of the block and, in its high nibbles, the
+// same half of slice 4n + t + 2 (ggml-common.h block_q6_K; the reference's MMVQ dot,
+// vecdotq.cuh:627-648). Each lane forms the scaled integer sums of its two half slices, with the
+// -32 offset applied as 32 times X's half-slice sum; lanes c and c ^ 1 (the two halves) exchange
+// them by DPP, so each lane finishes one slice: d * (sum_a * sc_a + sum_b * sc_b) * d8, the
+// reference's order. Partial sums over a row's 8 lanes by DPP, then over the waves in wave order.
+struct Q6Frag {
+  u32x4 ql[2], qh[2];  // rows r, 8 + r
+  uint2 sc[2];         // scales[8n .. 8n + 8)
+  uint32_t d;          // fp16 d of row r | of row 8 + r << 16
+};
+
+template <int NC, int WPT>
+__global__ void __launch_bounds__(64 * WPT) gemv_q6k_rows_kernel(const uint8_t* __restrict__ W, int64_t row_bytes,
+                                                                 int nrows, int k, const uint8_t* __restrict__ q8,
+                                                                 void* __restrict__ y, int y_dtype) {
+  constexpr int BS = 210;
+  constexpr int NT = 64 * WPT;
+  __shared__ float red[2][WPT][NC][kTileRows];
+  __shared__ uint4 sink;           // staging writes of groups past the end of X
+  extern __shared__ uint4 xdyn[];  // q values [NC][slice][8 dwords], then (d8, half sums) [NC][slice]
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane >> 3, c = lane & 7;
+  const int n = c >> 2, tp = (c >> 1) & 1, h = c & 1;
+  const int ntiles = (nrows + kTileRows - 1) / kTileRows;
+  const int nb = k / kQK, nslices = k / kQ81;
+  const int b_begin = wave * nb / WPT, b_end = (wave + 1) * nb / WPT;
+  const int nblk = b_end - b_begin;
+  const int G = gridDim.x;
+  uint32_t* xq = (uint32_t*)xdyn;
+  float2* xs = (float2*)(xq + NC * nslices * 8);
+  const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(W, (uint32_t)((int64_t)nrows * row_bytes));
+  const __amdgpu_buffer_rsrc_t nrs = buffer_rsrc(W, 0);
+  const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(q8, (uint32_t)(NC * nslices * 36));
+  const int oql = 16 * c, oqh = 128 + 16 * (2 * n + h), osc = 192 + 8 * n;
+  auto load = [&](int t, int b, Q6Frag& f) {
+    const __amdgpu_buffer_rsrc_t rs = t < ntiles ? wrs : nrs;
+    const int t0 = (t < ntiles ? t : 0) * kTileRows;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int o = min(t0 + 8 * i + r, nrows - 1) * (int)row_bytes;
+      f.ql[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, o + oql, b * BS, 0);
+      f.qh[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, o + oqh, b * BS, 0);
+      const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, o + osc, b * BS, 0);
+      f.sc[i] = make_uint2(v[0], v[1]);
+    }
+    const uint32_t d0 = __builtin_amdgcn_raw_buffer_load_b16(rs, min(t0 + r, nrows - 1) * (int)row_bytes + 208, b * BS, 0);
+    const uint32_t d1 =
+        __builtin_amdgcn_raw_buffer_load_b16(rs, min(t0 + 8 + r, nrows - 1) * (int)row_bytes + 208, b * BS, 0);
+    f.d = (d0 & 0xFFFFu) | (d1 << 16);
+  };
+  const int items = ((int)blockIdx.x < ntiles ? (ntiles - 1 - (int)blockIdx.x) / G + 1 : 0) * nblk;
+  auto next = [&](int& tt, int& bb) {
+    if (++bb == b_end) {
+      bb = b_begin;
+      tt += G;
+    }
+  };
+  const int ngroups = NC * nslices * 4;
+  const int ga = threadIdx.x, gb = threadIdx.x + NT;
+  XGroupQ8 xa, xb;
+  xgroup_q8_load(xrs, ga < ngroups ? ga : ngroups - 1, xa);
+  xgroup_q8_load(xrs, gb < ngroups ? gb : ngroups - 1, xb);
+  __builtin_amdgcn_sched_barrier(0);
+  Q6Frag f0, f1, f2;
+  int lt = blockIdx.x, lb = b_begin;  // next item to load
+  load(lt, lb, f0);
+  next(lt, lb);
+  load(lt, lb, f1);
+  next(lt, lb);
+  __builtin_amdgcn_sched_barrier(0);
+  xgroup_q8_store<kSumHalves>(xa, ga, ga < ngroups, xq, xs, &sink);
+  xgroup_q8_store<kSumHalves>(xb, gb, gb < ngroups, xq, xs, &sink);
+  for (int g = threadIdx.x + 2 * NT; g < ngroups; g += NT) {  // K beyond 2 groups per thread
+    XGroupQ8 xc;
+    xgroup_q8_load(xrs, g, xc);
+    xgroup_q8_store<kSumHalves>(xc, g, true, xq, xs, &sink);
+  }
+  __syncthreads();
+  float acc[2][NC];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int cc = 0; cc < NC; ++cc) acc[i][cc] = 0.0f;
+  const uint32_t hq0 = 2 * tp, hq1 = 2 * tp + 4;  // qh bit pairs of the two half slices
+  auto compute = [&](const Q6Frag& f, int b) {
+#pragma unroll
+    for (int cc = 0; cc < NC; ++cc) {
+      const int s1 = cc * nslices + b * 8 + 4 * n + tp, s2 = s1 + 2;  // the chunk's two slices
+      const uint4 x1 = *(const uint4*)(xq + s1 * 8 + 4 * h), x2 = *(const uint4*)(xq + s2 * 8 + 4 * h);
+      const int xv1[4] = {(int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+      const int xv2[4] = {(int)x2.x, (int)x2.y, (int)x2.z, (int)x2.w};
+      const uint32_t hs1 = __float_as_uint(xs[s1].y), hs2 = __float_as_uint(xs[s2].y);
+      const int sx1 = (int)(int16_t)((hs1 >> (16 * h)) & 0xFFFFu), sx2 = (int)(int16_t)((hs2 >> (16 * h)) & 0xFFFFu);
+      const float d8 = h == 0 ? xs[s1].x : xs[s2].x;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        int a1 = 0, a2 = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t l = f.ql[i][e], q = f.qh[i][e];
+          const int w1 = (int)((l & 0x0F0F0F0Fu) | (__builtin_amdgcn_alignbit(q, q, (hq0 + 28) & 31) & 0x30303030u));
+          const int w2 =
+              (int)(((l >> 4) & 0x0F0F0F0Fu) | (__builtin_amdgcn_alignbit(q, q, (hq1 + 28) & 31) & 0x30303030u));
+          a1 = dot4(w1, xv1[e], a1);
+          a2 = dot4(w2, xv2[e], a2);
+        }
+        const int sc1 = (int)(int8_t)((f.sc[i].x >> (8 * (2 * tp + h))) & 0xFF);  // scale 8n + 2tp + h
+        const int sc2 = (int)(int8_t)((f.sc[i].y >> (8 * (2 * tp + h))) & 0xFF);  // and 4 above
+        const int p1 = (a1 - 32 * sx1) * sc1, p2 = (a2 - 32 * sx2) * sc2;
+        // lane h = 0 finishes slice s1, lane h = 1 slice s2: each sends its partner the other one
+        const int mine = h == 0 ? p1 : p2, send = h == 0 ? p2 : p1;
+        const int got = __builtin_amdgcn_mov_dpp(send, 0xB1, 0xF, 0xF, false);  // quad xor 1
+        const int tot = h == 0 ? mine + got : got + mine;  // half 0's term first
+        const float dr = half_bits_to_float((f.d >> (16 * i)) & 0xFFFFu);
+        acc[i][cc] = fmaf(dr * (float)tot, d8, acc[i][cc]);
+      }
+    }
+  };
+  int t = blockIdx.x, b = b_begin, it = 0;  // item being computed
+  auto step = [&](const Q6Frag& fc, Q6Frag& fl) {
+    load(lt, lb, fl);
+    next(lt, lb);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(fc, b);
+    if (b == b_end - 1) {  // the wave's last block of tile t: reduce and store the tile
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int cc = 0; cc < NC; ++cc) {
+          float v = acc[i][cc];
+          v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));  // xor 1
+          v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));  // xor 2
+          v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false));  // 7 - lane
+          if (c == 0) red[it & 1][wave][cc][8 * i + r] = v;
+          acc[i][cc] = 0.0f;
+        }
+      }
+      __syncthreads();
+      if (threadIdx.x < NC * kTileRows) {
+        const int cc = threadIdx.x / kTileRows, rr = threadIdx.x % kTileRows;
+        const int row = t * kTileRows + rr;
+        float v = red[it & 1][0][cc][rr];
+#pragma unroll
+        for (int w2 = 1; w2 < WPT; ++w2) v += red[it & 1][w2][cc][rr];
+        if (row < nrows) store_y(y, (int64_t)cc * nrows + row, v, y_dtype);
+      }
+      ++it;
+    }
+    next(t, b);
+  };
+  int i = 0;
+  for (; i + 3 <= items; i += 3) {
+    step(f0, f2);
+    step(f1, f0);
+    step(f2, f1);
+  }
+  if (i < items) step(f0, f2);
+  if (i + 1 < items) step(f1, f0);
+}
+
 template <int TYPE>
 static bool launch_rawtile(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n, void* y,
                            int y_dtype, hipStream_t stream) {
@@ -374,6 +556,19 @@ static bool launch_rawtile(const uint8_t* W, int64_t row_bytes, int nrows, int k
   const size_t lds = (size_t)n * (k / kQ81) * 40;
   if (n == 1) gemv_rawtile_kernel<TYPE, 1, 8><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype);
   else gemv_rawtile_kernel<TYPE, 2, 8><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype);
+  return true;
+}
+
+// Q6_K at 1-2 rows: the row-chunk kernel, same conditions as the tile kernels of the other types
+static bool launch_q6k_rows(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n, void* y,
+                            int y_dtype, hipStream_t stream) {
+  if (n > 2 || k / kQK < 8 || (int64_t)nrows * row_bytes >= ((int64_t)1 << 31) || n * (k / kQ81) * 40 > 48 * 1024)
+    return false;
+  const int tiles = (nrows + kTileRows - 1) / kTileRows;
+  const unsigned g = (unsigned)std::min(tiles, persist_grid());
+  const size_t lds = (size_t)n * (k / kQ81) * 40;
+  if (n == 1) gemv_q6k_rows_kernel<1, 8><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype);
+  else gemv_q6k_rows_kernel<2, 8><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype);
   return true;
 }
 
@@ -408,7 +603,7 @@ hipError_t launch_gemv_raw(int type, const uint8_t* W, int64_t row_bytes, int nr
   bool done = false;
   if (type == kQ4_K) done = launch_rawtile<kQ4_K>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);
   if (type == kIQ4_XS) done = launch_rawtile<kIQ4_XS>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);
-  if (type == kQ6_K) done = launch_rawtile<kQ6_K>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);
+  if (type == kQ6_K) done = launch_q6k_rows(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);
   if (done) return hipGetLastError();
   switch (type) {
     case kIQ3_S: launch_type<kIQ3_S>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream); break;
