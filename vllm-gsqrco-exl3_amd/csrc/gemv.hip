@@ -120,15 +120,14 @@ __global__ void __launch_bounds__(256) gemv_raw_kernel(const uint8_t* __restrict
       if (lane == r * NC + c && row0 + r < nrows) store_y(y, (int64_t)c * nrows + row0 + r, acc[r][c], y_dtype);
 }
 
-// Q4_K, IQ4_XS and Q6_K on GGUF rows, tile style: a 16-row tile at a time, lane (row j = lane & 15,
-// slice pair pc = lane >> 4) of each block loads the row's header bytes and the 32 values-bytes of
-// its two slices (Q6_K: the ql and qh bytes the pair's values live in), so a wave's loads cover
-// the tile's 16 blocks; each wave keeps the next two blocks of its stream in flight while it
-// computes one. WPT waves split the K blocks; workgroups are persistent over tiles (two per CU)
-// and first copy the q8_1 of X into LDS with each slice's sum of q (while their first weight
-// blocks load). Per slice the reference vec_dot terms
-// (vecdotq.cuh: Q4_K 508-530, IQ4_XS 1357-1380, Q6_K 627-648) times the slice's d8; partial
-// sums over the 4 pair lanes of a row (xor butterfly), then over the waves in wave order.
+// Q4_K on GGUF rows, tile style: a 16-row tile at a time, lane (row j = lane & 15, slice pair
+// pc = lane >> 4) of each block loads the row's 16-byte header and the 32 value bytes of its two
+// slices, so a wave's loads cover the tile's 16 blocks; each wave keeps the next two blocks of its
+// stream in flight while it computes one. WPT waves split the K blocks; workgroups are persistent
+// over tiles (two per CU) and first copy the q8_1 of X into LDS with each slice's sum of q (while
+// their first weight blocks load). Per slice the reference vec_dot term (vecdotq.cuh:508-530)
+// times the slice's d8; partial sums over the 4 pair lanes of a row (xor butterfly), then over the
+// waves in wave order. (IQ4_XS and Q6_K use gemv_rows_kernel below.)
 template <int TYPE>
 struct RawTileFrag;
 template <>
@@ -136,41 +135,12 @@ struct RawTileFrag<kQ4_K> {
   u32x4 hdr;     // d | dmin << 16, scales[0..11]
   u32x4 lo, hi;  // the pair's 32 nibble bytes
 };
-template <>
-struct RawTileFrag<kIQ4_XS> {
-  uint32_t h0, h1;  // d | scales_h << 16, scales_l
-  u32x4 q0, q1;     // slice 2pc, 2pc + 1: 16 bytes each (low nibbles values 0..15, high 16..31)
-};
-template <>
-struct RawTileFrag<kQ6_K> {
-  u32x4 qa[2], qb[2];  // ql[64n .. 64n + 32), ql[64n + 32 .. 64n + 64), n = pc >> 1
-  u32x4 qh[2];         // qh[32n .. 32n + 32)
-  uint32_t sc, d;      // scales[4pc .. 4pc + 4), fp16 d
-};
 
 template <int TYPE>
 __device__ __forceinline__ void load_rawtile(__amdgpu_buffer_rsrc_t rs, int o, int bo, int pc, RawTileFrag<TYPE>& f) {
-  if constexpr (TYPE == kQ4_K) {
-    f.hdr = __builtin_amdgcn_raw_buffer_load_b128(rs, o, bo, 0);
-    f.lo = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 16 + 32 * pc, bo, 0);
-    f.hi = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 32 + 32 * pc, bo, 0);
-  } else if constexpr (TYPE == kIQ4_XS) {
-    const auto h = __builtin_amdgcn_raw_buffer_load_b64(rs, o, bo, 0);
-    f.h0 = h[0];
-    f.h1 = h[1];
-    f.q0 = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 8 + 32 * pc, bo, 0);
-    f.q1 = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 24 + 32 * pc, bo, 0);
-  } else {
-    const int n = pc >> 1;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      f.qa[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 64 * n + 16 * i, bo, 0);
-      f.qb[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 64 * n + 32 + 16 * i, bo, 0);
-      f.qh[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 128 + 32 * n + 16 * i, bo, 0);
-    }
-    f.sc = __builtin_amdgcn_raw_buffer_load_b32(rs, o + 192 + 4 * pc, bo, 0);
-    f.d = __builtin_amdgcn_raw_buffer_load_b16(rs, o + 208, bo, 0);
-  }
+  f.hdr = __builtin_amdgcn_raw_buffer_load_b128(rs, o, bo, 0);
+  f.lo = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 16 + 32 * pc, bo, 0);
+  f.hi = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 32 + 32 * pc, bo, 0);
 }
 
 // X of the raw tile GEMV, staged in LDS: q8 values [NC][slice][8 dwords], then (d8, sum of q)
@@ -215,6 +185,7 @@ template <int TYPE, int NC, int WPT>
 __global__ void __launch_bounds__(64 * WPT) gemv_rawtile_kernel(const uint8_t* __restrict__ W, int64_t row_bytes,
                                                                 int nrows, int k, const uint8_t* __restrict__ q8,
                                                                 void* __restrict__ y, int y_dtype) {
+  static_assert(TYPE == kQ4_K, "the tile kernel serves Q4_K; IQ4_XS and Q6_K use gemv_rows_kernel");
   constexpr int BS = block_bytes(TYPE);
   constexpr int NT = 64 * WPT;
   __shared__ float red[2][WPT][NC][kTileRows];
@@ -261,13 +232,12 @@ __global__ void __launch_bounds__(64 * WPT) gemv_rawtile_kernel(const uint8_t* _
   load(lt, lb, f1);
   next(lt, lb);
   __builtin_amdgcn_sched_barrier(0);
-  constexpr int SUMS = TYPE == kQ4_K ? kSumSlice : (TYPE == kQ6_K ? kSumHalves : kSumNone);
-  xgroup_q8_store<SUMS>(xa, ga, ga < ngroups, xq, xs, &sink);
-  xgroup_q8_store<SUMS>(xb, gb, gb < ngroups, xq, xs, &sink);
+  xgroup_q8_store<kSumSlice>(xa, ga, ga < ngroups, xq, xs, &sink);
+  xgroup_q8_store<kSumSlice>(xb, gb, gb < ngroups, xq, xs, &sink);
   for (int g = threadIdx.x + 2 * NT; g < ngroups; g += NT) {  // K beyond 2 groups per thread
     XGroupQ8 xc;
     xgroup_q8_load(xrs, g, xc);
-    xgroup_q8_store<SUMS>(xc, g, true, xq, xs, &sink);
+    xgroup_q8_store<kSumSlice>(xc, g, true, xq, xs, &sink);
   }
   __syncthreads();
   float acc[NC];
@@ -279,7 +249,7 @@ __global__ void __launch_bounds__(64 * WPT) gemv_rawtile_kernel(const uint8_t* _
     const int xv[8] = {(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
     const int u = 2 * pc + h;
     int w[8];
-    if constexpr (TYPE == kQ4_K) {
+    {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         w[e] = (int)((f.lo[e] >> (4 * h)) & 0x0F0F0F0Fu);
@@ -295,39 +265,6 @@ __global__ void __launch_bounds__(64 * WPT) gemv_rawtile_kernel(const uint8_t* _
       const uint32_t m = u < 4 ? (cb & 63) : ((ee >> 4) | ((cb >> 6) << 4));
       const float d = half_bits_to_float(f.hdr[0] & 0xFFFF), dmin = half_bits_to_float(f.hdr[0] >> 16);
       return (d * (float)sc) * (float)sumi - (dmin * (float)m) * xs[sl].y;
-    } else if constexpr (TYPE == kIQ4_XS) {
-      const u32x4 q = h == 0 ? f.q0 : f.q1;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        w[e] = lut16(q[e] & 0x0F0F0F0Fu);
-        w[4 + e] = lut16((q[e] >> 4) & 0x0F0F0F0Fu);
-      }
-      int sumi = 0;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) sumi = dot4(w[e], xv[e], sumi);
-      const int ls = (int)(((f.h1 >> (8 * pc + 4 * h)) & 0xF) | (((f.h0 >> (16 + 2 * u)) & 3u) << 4)) - 32;
-      return half_bits_to_float(f.h0 & 0xFFFF) * (float)(sumi * ls);
-    } else {
-      // the 6-bit values q (0..63) enter the dot as they are; the -32 offset is applied to the
-      // two 16-value sums as 32 times X's sum over the same values (an exact integer identity);
-      // the two qh bits of each byte reach bits 4-5 by one rotate
-      const int lsh = 4 * (pc & 1), hsh = 2 * (2 * (pc & 1) + h);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t l = h == 0 ? f.qa[e >> 2][e & 3] : f.qb[e >> 2][e & 3];
-        const uint32_t q = f.qh[e >> 2][e & 3];
-        w[e] = (int)(((l >> lsh) & 0x0F0F0F0Fu) | (__builtin_amdgcn_alignbit(q, q, (hsh + 28) & 31) & 0x30303030u));
-      }
-      int sa = 0, sb = 0;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) sa = dot4(w[e], xv[e], sa);
-#pragma unroll
-      for (int e = 4; e < 8; ++e) sb = dot4(w[e], xv[e], sb);
-      const uint32_t hs = __float_as_uint(xs[sl].y);
-      sa -= 32 * (int)(int16_t)(hs & 0xFFFFu);
-      sb -= 32 * ((int)hs >> 16);
-      const int sca = (int)(int8_t)((f.sc >> (16 * h)) & 0xFF), scb = (int)(int8_t)((f.sc >> (16 * h + 8)) & 0xFF);
-      return half_bits_to_float(f.d) * (float)(sa * sca + sb * scb);
     }
   };
   auto compute = [&](const RawTileFrag<TYPE>& f, int b) {
@@ -378,37 +315,54 @@ __global__ void __launch_bounds__(64 * WPT) gemv_rawtile_kernel(const uint8_t* _
   if (i + 1 < items) step(f1, f0);
 }
 
-// Q6_K on GGUF rows with loads that run along each row: lane L = 8 r + c (r = row in an 8-row
-// group, c = 16-byte chunk of the row's 128 ql bytes) loads ql[16c .. 16c + 16), the 16 qh bytes
-// that hold the same values' high bits, the row's 8 scales of the block half and d, for rows r
-// and 8 + r of the tile. One load instruction then covers 8 rows' bytes contiguously (128 B of ql
-// per row), where a lane per slice pair (gemv_rawtile_kernel) touches about three times as many
-// cache lines per block, the L1 tag rate being what bounds it. Chunk c = 4n + 2t + h holds, in
-// its low nibbles, values 16h..16h+15 of slice 4n + t of the block and, in its high nibbles, the
-// same half of slice 4n + t + 2 (ggml-common.h block_q6_K; the reference's MMVQ dot,
-// vecdotq.cuh:627-648). Each lane forms the scaled integer sums of its two half slices, with the
-// -32 offset applied as 32 times X's half-slice sum; lanes c and c ^ 1 (the two halves) exchange
-// them by DPP, so each lane finishes one slice: d * (sum_a * sc_a + sum_b * sc_b) * d8, the
-// reference's order. Partial sums over a row's 8 lanes by DPP, then over the waves in wave order.
-struct Q6Frag {
-  u32x4 ql[2], qh[2];  // rows r, 8 + r
-  uint2 sc[2];         // scales[8n .. 8n + 8)
-  uint32_t d;          // fp16 d of row r | of row 8 + r << 16
+// Q4_K, IQ4_XS and Q6_K on GGUF rows with loads that run along each row: lane L = 8 r + c (r = row
+// in an 8-row group, c = 16-byte chunk of the row's 128 quant bytes) loads quant bytes
+// [16c, 16c + 16) of the block of rows r and 8 + r of the tile, and what its values need of the
+// block header. One load instruction then covers 8 rows' bytes contiguously (128 B per row); a
+// lane per slice pair (gemv_rawtile_kernel) touches two to three times as many cache lines per
+// block, and the L1 tag rate is what bounds that kernel. The chunk's values (ggml-common.h block
+// layouts; the reference's MMVQ dots, vecdotq.cuh: Q4_K 508-530, IQ4_XS 1357-1380, Q6_K 627-648):
+//   IQ4_XS  slice c (low nibbles values 0..15, high nibbles 16..31).
+//   Q4_K    half h = c & 1 (values 16h..16h+15) of slice 2j (low nibbles) and of slice 2j + 1
+//           (high nibbles), j = c >> 1.
+//   Q6_K    half h = c & 1 of slice 4n + t (low nibbles) and of slice 4n + t + 2 (high nibbles),
+//           c = 4n + 2t + h, with the high bits from the 16 qh bytes of the same positions; the
+//           -32 offset is applied as 32 times X's half-slice sum.
+// For Q4_K and Q6_K, lanes c and c ^ 1 hold the two halves of the same two slices; they exchange
+// the integer sums by DPP and each finishes one slice. Every slice's term is the reference's
+// (and gemv_rawtile_kernel's) arithmetic; partial sums over a row's 8 lanes by DPP, then over the
+// waves in wave order.
+template <int TYPE>
+struct RowsFrag;
+template <>
+struct RowsFrag<kQ4_K> {
+  u32x4 hdr[2], qs[2];  // rows r, 8 + r: d | dmin << 16, scales[0..12); the chunk
+};
+template <>
+struct RowsFrag<kIQ4_XS> {
+  uint2 hdr[2];  // d | scales_h << 16, scales_l
+  u32x4 qs[2];
+};
+template <>
+struct RowsFrag<kQ6_K> {
+  u32x4 ql[2], qh[2];
+  uint2 sc[2];  // scales[8n .. 8n + 8)
+  uint32_t d;   // fp16 d of row r | of row 8 + r << 16
 };
 
-template <int NC, int WPT>
-__global__ void __launch_bounds__(64 * WPT) gemv_q6k_rows_kernel(const uint8_t* __restrict__ W, int64_t row_bytes,
-                                                                 int nrows, int k, const uint8_t* __restrict__ q8,
-                                                                 void* __restrict__ y, int y_dtype) {
-  constexpr int BS = 210;
+template <int TYPE, int NC, int WPT>
+__global__ void __launch_bounds__(64 * WPT) gemv_rows_kernel(const uint8_t* __restrict__ W, int64_t row_bytes,
+                                                             int nrows, int k, const uint8_t* __restrict__ q8,
+                                                             void* __restrict__ y, int y_dtype) {
+  constexpr int BS = block_bytes(TYPE);
   constexpr int NT = 64 * WPT;
+  constexpr int SUMS = TYPE == kQ4_K ? kSumSlice : (TYPE == kQ6_K ? kSumHalves : kSumNone);
   __shared__ float red[2][WPT][NC][kTileRows];
   __shared__ uint4 sink;           // staging writes of groups past the end of X
-  extern __shared__ uint4 xdyn[];  // q values [NC][slice][8 dwords], then (d8, half sums) [NC][slice]
+  extern __shared__ uint4 xdyn[];  // q values [NC][slice][8 dwords], then (d8, sums) [NC][slice]
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int r = lane >> 3, c = lane & 7;
-  const int n = c >> 2, tp = (c >> 1) & 1, h = c & 1;
+  const int r = lane >> 3, c = lane & 7, h = c & 1;
   const int ntiles = (nrows + kTileRows - 1) / kTileRows;
   const int nb = k / kQK, nslices = k / kQ81;
   const int b_begin = wave * nb / WPT, b_end = (wave + 1) * nb / WPT;
@@ -419,22 +373,31 @@ __global__ void __launch_bounds__(64 * WPT) gemv_q6k_rows_kernel(const uint8_t* 
   const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(W, (uint32_t)((int64_t)nrows * row_bytes));
   const __amdgpu_buffer_rsrc_t nrs = buffer_rsrc(W, 0);
   const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(q8, (uint32_t)(NC * nslices * 36));
-  const int oql = 16 * c, oqh = 128 + 16 * (2 * n + h), osc = 192 + 8 * n;
-  auto load = [&](int t, int b, Q6Frag& f) {
+  auto load = [&](int t, int b, RowsFrag<TYPE>& f) {
     const __amdgpu_buffer_rsrc_t rs = t < ntiles ? wrs : nrs;
     const int t0 = (t < ntiles ? t : 0) * kTileRows;
+    const int bo = b * BS;
+    uint32_t d16[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int o = min(t0 + 8 * i + r, nrows - 1) * (int)row_bytes;
-      f.ql[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, o + oql, b * BS, 0);
-      f.qh[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, o + oqh, b * BS, 0);
-      const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, o + osc, b * BS, 0);
-      f.sc[i] = make_uint2(v[0], v[1]);
+      if constexpr (TYPE == kQ4_K) {
+        f.hdr[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, o, bo, 0);
+        f.qs[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 16 + 16 * c, bo, 0);
+      } else if constexpr (TYPE == kIQ4_XS) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, o, bo, 0);
+        f.hdr[i] = make_uint2(v[0], v[1]);
+        f.qs[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 8 + 16 * c, bo, 0);
+      } else {
+        const int n = c >> 2;
+        f.ql[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 16 * c, bo, 0);
+        f.qh[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 128 + 16 * (2 * n + h), bo, 0);
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, o + 192 + 8 * n, bo, 0);
+        f.sc[i] = make_uint2(v[0], v[1]);
+        d16[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, o + 208, bo, 0);
+      }
     }
-    const uint32_t d0 = __builtin_amdgcn_raw_buffer_load_b16(rs, min(t0 + r, nrows - 1) * (int)row_bytes + 208, b * BS, 0);
-    const uint32_t d1 =
-        __builtin_amdgcn_raw_buffer_load_b16(rs, min(t0 + 8 + r, nrows - 1) * (int)row_bytes + 208, b * BS, 0);
-    f.d = (d0 & 0xFFFFu) | (d1 << 16);
+    if constexpr (TYPE == kQ6_K) f.d = (d16[0] & 0xFFFFu) | (d16[1] << 16);
   };
   const int items = ((int)blockIdx.x < ntiles ? (ntiles - 1 - (int)blockIdx.x) / G + 1 : 0) * nblk;
   auto next = [&](int& tt, int& bb) {
@@ -449,19 +412,19 @@ __global__ void __launch_bounds__(64 * WPT) gemv_q6k_rows_kernel(const uint8_t* 
   xgroup_q8_load(xrs, ga < ngroups ? ga : ngroups - 1, xa);
   xgroup_q8_load(xrs, gb < ngroups ? gb : ngroups - 1, xb);
   __builtin_amdgcn_sched_barrier(0);
-  Q6Frag f0, f1, f2;
+  RowsFrag<TYPE> f0, f1, f2;
   int lt = blockIdx.x, lb = b_begin;  // next item to load
   load(lt, lb, f0);
   next(lt, lb);
   load(lt, lb, f1);
   next(lt, lb);
   __builtin_amdgcn_sched_barrier(0);
-  xgroup_q8_store<kSumHalves>(xa, ga, ga < ngroups, xq, xs, &sink);
-  xgroup_q8_store<kSumHalves>(xb, gb, gb < ngroups, xq, xs, &sink);
+  xgroup_q8_store<SUMS>(xa, ga, ga < ngroups, xq, xs, &sink);
+  xgroup_q8_store<SUMS>(xb, gb, gb < ngroups, xq, xs, &sink);
   for (int g = threadIdx.x + 2 * NT; g < ngroups; g += NT) {  // K beyond 2 groups per thread
     XGroupQ8 xc;
     xgroup_q8_load(xrs, g, xc);
-    xgroup_q8_store<kSumHalves>(xc, g, true, xq, xs, &sink);
+    xgroup_q8_store<SUMS>(xc, g, true, xq, xs, &sink);
   }
   __syncthreads();
   float acc[2][NC];
@@ -469,43 +432,94 @@ __global__ void __launch_bounds__(64 * WPT) gemv_q6k_rows_kernel(const uint8_t* 
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int cc = 0; cc < NC; ++cc) acc[i][cc] = 0.0f;
-  const uint32_t hq0 = 2 * tp, hq1 = 2 * tp + 4;  // qh bit pairs of the two half slices
-  auto compute = [&](const Q6Frag& f, int b) {
+  // the lane's two (Q4_K, Q6_K) or one (IQ4_XS) slices of block b, for activation row cc
+  auto slices = [&](int cc, int b, int& s1, int& s2) {
+    const int base = cc * nslices + b * 8;
+    if constexpr (TYPE == kQ4_K) {
+      s1 = base + 2 * (c >> 1);
+      s2 = s1 + 1;
+    } else if constexpr (TYPE == kQ6_K) {
+      s1 = base + 4 * (c >> 2) + ((c >> 1) & 1);
+      s2 = s1 + 2;
+    } else {
+      s1 = s2 = base + c;
+    }
+  };
+  // lanes h = 0 / 1 hold halves 0 / 1 of slices s1, s2: each sends its partner the integer sum of
+  // the slice the partner finishes (h = 0 finishes s1, h = 1 s2); half 0's sum comes first
+  auto join = [&](int p1, int p2) {
+    const int mine = h == 0 ? p1 : p2, send = h == 0 ? p2 : p1;
+    const int got = __builtin_amdgcn_mov_dpp(send, 0xB1, 0xF, 0xF, false);  // quad xor 1
+    return h == 0 ? mine + got : got + mine;
+  };
+  auto compute = [&](const RowsFrag<TYPE>& f, int b) {
 #pragma unroll
     for (int cc = 0; cc < NC; ++cc) {
-      const int s1 = cc * nslices + b * 8 + 4 * n + tp, s2 = s1 + 2;  // the chunk's two slices
-      const uint4 x1 = *(const uint4*)(xq + s1 * 8 + 4 * h), x2 = *(const uint4*)(xq + s2 * 8 + 4 * h);
-      const int xv1[4] = {(int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
-      const int xv2[4] = {(int)x2.x, (int)x2.y, (int)x2.z, (int)x2.w};
-      const uint32_t hs1 = __float_as_uint(xs[s1].y), hs2 = __float_as_uint(xs[s2].y);
-      const int sx1 = (int)(int16_t)((hs1 >> (16 * h)) & 0xFFFFu), sx2 = (int)(int16_t)((hs2 >> (16 * h)) & 0xFFFFu);
-      const float d8 = h == 0 ? xs[s1].x : xs[s2].x;
+      int s1, s2;
+      slices(cc, b, s1, s2);
+      if constexpr (TYPE == kIQ4_XS) {
+        const uint4 x0 = *(const uint4*)(xq + s1 * 8), x1 = *(const uint4*)(xq + s1 * 8 + 4);
+        const int xv[8] = {(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+        const float d8 = xs[s1].x;
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        int a1 = 0, a2 = 0;
+        for (int i = 0; i < 2; ++i) {
+          int sumi = 0;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t l = f.ql[i][e], q = f.qh[i][e];
-          const int w1 = (int)((l & 0x0F0F0F0Fu) | (__builtin_amdgcn_alignbit(q, q, (hq0 + 28) & 31) & 0x30303030u));
-          const int w2 =
-              (int)(((l >> 4) & 0x0F0F0F0Fu) | (__builtin_amdgcn_alignbit(q, q, (hq1 + 28) & 31) & 0x30303030u));
-          a1 = dot4(w1, xv1[e], a1);
-          a2 = dot4(w2, xv2[e], a2);
+          for (int e = 0; e < 4; ++e) sumi = dot4(lut16(f.qs[i][e] & 0x0F0F0F0Fu), xv[e], sumi);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sumi = dot4(lut16((f.qs[i][e] >> 4) & 0x0F0F0F0Fu), xv[4 + e], sumi);
+          const int ls = (int)(((f.hdr[i].y >> (4 * c)) & 0xF) | (((f.hdr[i].x >> (16 + 2 * c)) & 3u) << 4)) - 32;
+          acc[i][cc] = fmaf(half_bits_to_float(f.hdr[i].x & 0xFFFF) * (float)(sumi * ls), d8, acc[i][cc]);
         }
-        const int sc1 = (int)(int8_t)((f.sc[i].x >> (8 * (2 * tp + h))) & 0xFF);  // scale 8n + 2tp + h
-        const int sc2 = (int)(int8_t)((f.sc[i].y >> (8 * (2 * tp + h))) & 0xFF);  // and 4 above
-        const int p1 = (a1 - 32 * sx1) * sc1, p2 = (a2 - 32 * sx2) * sc2;
-        // lane h = 0 finishes slice s1, lane h = 1 slice s2: each sends its partner the other one
-        const int mine = h == 0 ? p1 : p2, send = h == 0 ? p2 : p1;
-        const int got = __builtin_amdgcn_mov_dpp(send, 0xB1, 0xF, 0xF, false);  // quad xor 1
-        const int tot = h == 0 ? mine + got : got + mine;  // half 0's term first
-        const float dr = half_bits_to_float((f.d >> (16 * i)) & 0xFFFFu);
-        acc[i][cc] = fmaf(dr * (float)tot, d8, acc[i][cc]);
+      } else {
+        const uint4 x1 = *(const uint4*)(xq + s1 * 8 + 4 * h), x2 = *(const uint4*)(xq + s2 * 8 + 4 * h);
+        const int xv1[4] = {(int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+        const int xv2[4] = {(int)x2.x, (int)x2.y, (int)x2.z, (int)x2.w};
+        const int sf = h == 0 ? s1 : s2;  // the slice this lane finishes
+        const float d8 = xs[sf].x;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          int a1 = 0, a2 = 0;
+          if constexpr (TYPE == kQ4_K) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              a1 = dot4((int)(f.qs[i][e] & 0x0F0F0F0Fu), xv1[e], a1);
+              a2 = dot4((int)((f.qs[i][e] >> 4) & 0x0F0F0F0Fu), xv2[e], a2);
+            }
+            const int sumi = join(a1, a2);
+            const int u = sf & 7;  // slice within the block
+            const int jj = u & 3;
+            const uint32_t sa = (f.hdr[i][1] >> (8 * jj)) & 0xFF, sb = (f.hdr[i][2] >> (8 * jj)) & 0xFF;
+            const uint32_t se = (f.hdr[i][3] >> (8 * jj)) & 0xFF;
+            const uint32_t sc = u < 4 ? (sa & 63) : ((se & 0xF) | ((sa >> 6) << 4));
+            const uint32_t m = u < 4 ? (sb & 63) : ((se >> 4) | ((sb >> 6) << 4));
+            const float d = half_bits_to_float(f.hdr[i][0] & 0xFFFF), dmin = half_bits_to_float(f.hdr[i][0] >> 16);
+            const float term = (d * (float)sc) * (float)sumi - (dmin * (float)m) * xs[sf].y;
+            acc[i][cc] = fmaf(term, d8, acc[i][cc]);
+          } else {
+            const uint32_t t2 = 2 * ((c >> 1) & 1);  // qh bit pair of the low-nibble half slice
+            const uint32_t hs1 = __float_as_uint(xs[s1].y), hs2 = __float_as_uint(xs[s2].y);
+            const int sx1 = (int)(int16_t)((hs1 >> (16 * h)) & 0xFFFFu), sx2 = (int)(int16_t)((hs2 >> (16 * h)) & 0xFFFFu);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const uint32_t l = f.ql[i][e], q = f.qh[i][e];
+              const int w1 = (int)((l & 0x0F0F0F0Fu) | (__builtin_amdgcn_alignbit(q, q, (t2 + 28) & 31) & 0x30303030u));
+              const int w2 = (int)(((l >> 4) & 0x0F0F0F0Fu) | (__builtin_amdgcn_alignbit(q, q, t2 & 31) & 0x30303030u));
+              a1 = dot4(w1, xv1[e], a1);
+              a2 = dot4(w2, xv2[e], a2);
+            }
+            const int sc1 = (int)(int8_t)((f.sc[i].x >> (8 * ((c >> 1 & 1) * 2 + h))) & 0xFF);  // 8n + 2t + h
+            const int sc2 = (int)(int8_t)((f.sc[i].y >> (8 * ((c >> 1 & 1) * 2 + h))) & 0xFF);  // and 4 above
+            const int tot = join((a1 - 32 * sx1) * sc1, (a2 - 32 * sx2) * sc2);
+            const float dr = half_bits_to_float((f.d >> (16 * i)) & 0xFFFFu);
+            acc[i][cc] = fmaf(dr * (float)tot, d8, acc[i][cc]);
+          }
+        }
       }
     }
   };
   int t = blockIdx.x, b = b_begin, it = 0;  // item being computed
-  auto step = [&](const Q6Frag& fc, Q6Frag& fl) {
+  auto step = [&](const RowsFrag<TYPE>& fc, RowsFrag<TYPE>& fl) {
     load(lt, lb, fl);
     next(lt, lb);
     __builtin_amdgcn_sched_barrier(0);
@@ -516,8 +530,8 @@ __global__ void __launch_bounds__(64 * WPT) gemv_q6k_rows_kernel(const uint8_t* 
 #pragma unroll
         for (int cc = 0; cc < NC; ++cc) {
           float v = acc[i][cc];
-          v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));  // xor 1
-          v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));  // xor 2
+          v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));   // xor 1
+          v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));   // xor 2
           v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false));  // 7 - lane
           if (c == 0) red[it & 1][wave][cc][8 * i + r] = v;
           acc[i][cc] = 0.0f;
@@ -559,16 +573,17 @@ static bool launch_rawtile(const uint8_t* W, int64_t row_bytes, int nrows, int k
   return true;
 }
 
-// Q6_K at 1-2 rows: the row-chunk kernel, same conditions as the tile kernels of the other types
-static bool launch_q6k_rows(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n, void* y,
-                            int y_dtype, hipStream_t stream) {
+// Q4_K / IQ4_XS / Q6_K at 1-2 rows: the row-chunk kernel (same conditions as the tile kernel)
+template <int TYPE>
+static bool launch_rows(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n, void* y,
+                        int y_dtype, hipStream_t stream) {
   if (n > 2 || k / kQK < 8 || (int64_t)nrows * row_bytes >= ((int64_t)1 << 31) || n * (k / kQ81) * 40 > 48 * 1024)
     return false;
   const int tiles = (nrows + kTileRows - 1) / kTileRows;
   const unsigned g = (unsigned)std::min(tiles, persist_grid());
   const size_t lds = (size_t)n * (k / kQ81) * 40;
-  if (n == 1) gemv_q6k_rows_kernel<1, 8><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype);
-  else gemv_q6k_rows_kernel<2, 8><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype);
+  if (n == 1) gemv_rows_kernel<TYPE, 1, 8><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype);
+  else gemv_rows_kernel<TYPE, 2, 8><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype);
   return true;
 }
 
@@ -599,11 +614,13 @@ static void launch_type(const uint8_t* W, int64_t row_bytes, int nrows, int k, c
 hipError_t launch_gemv_raw(int type, const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n,
                            void* y, int y_dtype, hipStream_t stream) {
   // Q4_K / IQ4_XS / Q6_K at 1-2 rows on weights of at least 8 K blocks (one per wave) below 2 GiB
-  // whose X q8_1 fits in 48 KB of LDS: the tile kernel
+  // whose X q8_1 fits in 48 KB of LDS: the tile kernel (Q4_K) or the row-chunk kernel (IQ4_XS,
+  // Q6_K; measured 17408 x 5120 M = 1: IQ4_XS 14.1 us against 14.3, Q6_K 21.0 against 37.2; for
+  // Q4_K the two are level)
   bool done = false;
   if (type == kQ4_K) done = launch_rawtile<kQ4_K>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);
-  if (type == kIQ4_XS) done = launch_rawtile<kIQ4_XS>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);
-  if (type == kQ6_K) done = launch_q6k_rows(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);
+  if (type == kIQ4_XS) done = launch_rows<kIQ4_XS>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);
+  if (type == kQ6_K) done = launch_rows<kQ6_K>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);
   if (done) return hipGetLastError();
   switch (type) {
     case kIQ3_S: launch_type<kIQ3_S>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream); break;
