@@ -33,6 +33,7 @@ hipError_t launch_gemm_xq(int type, const uint8_t* W, int64_t row_bytes, int nro
                           void* y, int y_dtype, hipStream_t stream);
 hipError_t launch_gemv_packed_x(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x, int x_dtype,
                                 int64_t s01, int n, void* y, int y_dtype, hipStream_t stream);
+bool gemv_rows_supported(int type, int64_t nrows, int64_t row_bytes, int64_t k, int64_t n);
 bool gemv_packed_x_supported(int64_t nrows, int64_t k, int64_t n);
 hipError_t launch_gemm_packed_xq(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n,
                                  void* y, int y_dtype, hipStream_t stream);
@@ -229,6 +230,14 @@ int64_t vec_mma_from(int op, int64_t type) {
   return INT64_MAX;
 }
 
+// A decode op runs the int8-MFMA small GEMM from vec_mma_from rows on, except at up to four rows
+// of Q4_K / IQ4_XS / Q6_K where the row-chunk GEMV takes the shape (X's q8_1 in LDS).
+bool decode_mma(int op, int64_t type, int64_t row, int64_t k, int64_t n) {
+  if (n < vec_mma_from(op, type)) return false;
+  const int64_t bb = type == gguf::kQ4_K ? 144 : type == gguf::kQ6_K ? 210 : type == gguf::kIQ4_XS ? 136 : 0;
+  return !(op_packed(op) == false && bb > 0 && gguf::gemv_rows_supported((int)type, row, k / 256 * bb, k, n));
+}
+
 }  // namespace
 
 size_t gguf_op_workspace_bytes(int op, int64_t type, int64_t row, int64_t k, int64_t n, int has_x_q8) {
@@ -239,7 +248,7 @@ size_t gguf_op_workspace_bytes(int op, int64_t type, int64_t row, int64_t k, int
       return align256(gguf::xh_bytes(n, k));
     return align256(mmq_layout ? gguf_q8_1_bytes(n, k, 1) : gguf::xq_bytes(n, k));
   }
-  if (n >= vec_mma_from(op, type)) return align256(gguf::xq_bytes(n, k));  // x_q8 is converted into it
+  if (decode_mma(op, type, row, k, n)) return align256(gguf::xq_bytes(n, k));  // x_q8 is converted into it
   if (packed_fused(op, row, k, n, has_x_q8 != 0)) return 0;
   return has_x_q8 ? 0 : align256(gguf_q8_1_bytes(n, k, 0));
 }
@@ -271,8 +280,9 @@ int gguf_mul_mat(int op, const gguf_view* W, const gguf_view* X, int64_t type, i
   const int ydt = X->dtype;
 
   // int8-MFMA GEMMs on the xq layout: the product ops with the MMQ arithmetic, the decode ops
-  // (from vec_mma_from rows on) with the decode ops' q8_1 arithmetic or the caller's x_q8
-  if ((gemm && (packed || type != gguf::kIQ3_S)) || (!gemm && n >= vec_mma_from(op, type))) {
+  // (from vec_mma_from rows on, see decode_mma) with the decode ops' q8_1 arithmetic or the
+  // caller's x_q8
+  if ((gemm && (packed || type != gguf::kIQ3_S)) || (!gemm && decode_mma(op, type, row, k, n))) {
     const bool prefill = gemm && n >= kPrefillFrom;
     if (!gemm && x_q8)
       e = gguf::launch_q8_1_to_xq(x_q8->data, n, k, (int)type, workspace, s);

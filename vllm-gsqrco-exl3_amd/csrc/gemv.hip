@@ -573,17 +573,26 @@ static bool launch_rawtile(const uint8_t* W, int64_t row_bytes, int nrows, int k
   return true;
 }
 
-// Q4_K / IQ4_XS / Q6_K at 1-2 rows: the row-chunk kernel (same conditions as the tile kernel)
+// Q4_K / IQ4_XS / Q6_K at 1-4 rows on weights of at least 8 K blocks (one per wave) below 2 GiB
+// whose X q8_1 (40 bytes per slice and row) fits in 48 KB of LDS: the row-chunk kernel
+bool gemv_rows_supported(int type, int64_t nrows, int64_t row_bytes, int64_t k, int64_t n) {
+  return (type == kQ4_K || type == kIQ4_XS || type == kQ6_K) && n >= 1 && n <= 4 && k / kQK >= 8 &&
+         nrows * row_bytes < ((int64_t)1 << 31) && n * (k / kQ81) * 40 <= 48 * 1024;
+}
+
 template <int TYPE>
 static bool launch_rows(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n, void* y,
                         int y_dtype, hipStream_t stream) {
-  if (n > 2 || k / kQK < 8 || (int64_t)nrows * row_bytes >= ((int64_t)1 << 31) || n * (k / kQ81) * 40 > 48 * 1024)
-    return false;
+  if (!gemv_rows_supported(TYPE, nrows, row_bytes, k, n)) return false;
   const int tiles = (nrows + kTileRows - 1) / kTileRows;
   const unsigned g = (unsigned)std::min(tiles, persist_grid());
   const size_t lds = (size_t)n * (k / kQ81) * 40;
-  if (n == 1) gemv_rows_kernel<TYPE, 1, 8><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype);
-  else gemv_rows_kernel<TYPE, 2, 8><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype);
+  switch (n) {
+    case 1: gemv_rows_kernel<TYPE, 1, 8><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype); break;
+    case 2: gemv_rows_kernel<TYPE, 2, 8><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype); break;
+    case 3: gemv_rows_kernel<TYPE, 3, 8><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype); break;
+    default: gemv_rows_kernel<TYPE, 4, 8><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype); break;
+  }
   return true;
 }
 
@@ -613,12 +622,16 @@ static void launch_type(const uint8_t* W, int64_t row_bytes, int nrows, int k, c
 // n in 1..8 activation rows; q8: block_q8_1 of X; y: [n, nrows] in y_dtype.
 hipError_t launch_gemv_raw(int type, const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n,
                            void* y, int y_dtype, hipStream_t stream) {
-  // Q4_K / IQ4_XS / Q6_K at 1-2 rows on weights of at least 8 K blocks (one per wave) below 2 GiB
-  // whose X q8_1 fits in 48 KB of LDS: the tile kernel (Q4_K) or the row-chunk kernel (IQ4_XS,
-  // Q6_K; measured 17408 x 5120 M = 1: IQ4_XS 14.1 us against 14.3, Q6_K 21.0 against 37.2; for
-  // Q4_K the two are level)
+  // Q4_K / IQ4_XS / Q6_K at 1-4 rows on weights of at least 8 K blocks (one per wave) below 2 GiB
+  // whose X q8_1 fits in 48 KB of LDS: the tile kernel (Q4_K at 1-2 rows) or the row-chunk kernel
+  // (measured 17408 x 5120 M = 1: IQ4_XS 14.1 us against 14.3, Q6_K 21.0 against 37.2; for Q4_K
+  // the two are level; at 3-4 rows it replaces the generic GEMV and the MMA small GEMM: IQ4_XS
+  // M = 4 18.8 us against 25.6, Q6_K 26.2 against 37.1 + quantise)
   bool done = false;
-  if (type == kQ4_K) done = launch_rawtile<kQ4_K>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);
+  if (type == kQ4_K) {
+    done = launch_rawtile<kQ4_K>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);
+    if (!done) done = launch_rows<kQ4_K>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);  // 3-4 rows
+  }
   if (type == kIQ4_XS) done = launch_rows<kIQ4_XS>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);
   if (type == kQ6_K) done = launch_rows<kQ6_K>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);
   if (done) return hipGetLastError();
