@@ -361,14 +361,16 @@ def test_prefill_16bit_x(qt, dtype):
     assert o.rel_l2(y.float().cpu().numpy(), ref) <= TIGHT[dtype]
 
 
-@pytest.mark.parametrize("n", [1, 2, 3, 4])  # the persistent kernel serves 1-2 rows
-def test_packed_gemv_many_tiles(n):
-    """More 16-row tiles than the GEMV's persistent grid (two workgroups per CU), so each
-    workgroup loops over several tiles; X given as q8_1 (x_q8), which keeps n = 1 off the fused
-    path: exact-integer dots, the q81 model, and bit-identical CUDA-graph replays."""
+@pytest.mark.parametrize("n,rows,k", [(1, 16 * 700, 2048), (2, 16 * 700, 2048), (3, 16 * 700, 2048),
+                                      (4, 16 * 700, 2048), (2, 16 * 200, 21504)])
+def test_packed_gemv_many_tiles(n, rows, k):
+    """The persistent GEMV on q8_1 input: 11200 rows have more 16-row tiles than its grid (two
+    workgroups per CU), so each workgroup loops over several tiles (1-4 activation rows; K = 2048
+    is 8 blocks, one per wave); 3200 x 21504 at two rows is a large weight with fewer tiles than
+    the grid. X given as q8_1 (x_q8), which keeps n = 1 off the fused path: exact-integer dots,
+    the q81 model, and bit-identical CUDA-graph replays."""
     from vllm_gguf_plugin.quantization import iq3_pack
 
-    rows, k = 16 * 700, 2048  # 8 K blocks: one per wave at the most waves per tile
     op = C().lcpp_mul_mat_vec_iq3_mma_packed
     raw = _exact_weights(o.IQ3_S, rows, k, seed=160 + n)
     w = iq3_pack.pack(_dev(raw), o.IQ3_S)
@@ -500,15 +502,18 @@ def _tie_slices(k, dtype, seed):
     return x.to(dtype)
 
 
-@pytest.mark.parametrize("n,dtype", [(1, torch.bfloat16), (1, torch.float16), (1, torch.float32),
-                                     (2, torch.bfloat16), (2, torch.float32)])
-def test_fused_quantisation_ties(n, dtype):
-    """The persistent GEMV's in-kernel quantisation rounds x / d from a reciprocal product and
-    takes the IEEE division for values near a tie, non-finite values and tiny scales: its bytes,
-    and so the outputs, must equal those of the q8_1 quantiser bit for bit (NaN included)."""
+@pytest.mark.parametrize("n,dtype,rows", [(1, torch.bfloat16, 16 * 700), (1, torch.float16, 16 * 700),
+                                          (1, torch.float32, 16 * 700), (2, torch.bfloat16, 16 * 700),
+                                          (2, torch.float32, 16 * 700), (1, torch.bfloat16, 1024),
+                                          (1, torch.float16, 1024), (1, torch.float32, 1024)])
+def test_fused_quantisation_ties(n, dtype, rows):
+    """The packed GEMV's in-kernel quantisation (all of X into LDS on the persistent kernel, 11200
+    rows; block by block on the one-tile kernel, 1024 rows) rounds x / d from a reciprocal product
+    and takes the IEEE division for values near a tie, non-finite values and tiny scales: its
+    bytes, and so the outputs, must equal those of the q8_1 quantiser bit for bit (NaN included)."""
     from vllm_gguf_plugin.quantization import iq3_pack
 
-    rows, k = 16 * 700, 4096  # more tiles than the persistent grid, above the one-tile path's size
+    k = 4096  # 11200 x 4096: more tiles than the persistent grid, above the one-tile path's size
     w = iq3_pack.pack(_dev(_w(o.IQ3_S, rows, k, seed=190 + n)), o.IQ3_S)
     x = torch.stack([_tie_slices(k, dtype, seed=191 + c) for c in range(n)]).cuda()
     q8 = C().lcpp_quantize_q8_1(x, o.IQ3_S, False, False)

@@ -741,6 +741,41 @@ __device__ __forceinline__ float xraw_value(const uint32_t* v, int i) {
   return __uint_as_float(h << 16);
 }
 
+// q8_1 bytes of N (4 or 8) values of one slice, given the slice's amax and d = amax / 127: q =
+// roundf(v / d) (q = 0 when amax == 0), bit for bit as the q8_1 quantiser computes them. The
+// quotient comes from the product v * rcp(d): for |v| <= amax it lies within 2^-15 of v / d (rcp
+// within 1 ulp), and the fp32 rounding of v / d moves that by less than 2^-16, so when the product
+// lies more than 2^-12 from every half-integer, roundf(v / d) is the integer nearest to it. Adding
+// 1.5 * 2^23 rounds to that integer and leaves it in the low mantissa bits. The largest distance
+// is taken over the bit patterns of |a - n|, where a NaN (a NaN or infinite value) ranks above
+// every number. A lane with a value near a tie, a non-finite product or a tiny amax (rcp of a
+// subnormal d) takes the IEEE division. out[j] holds the bytes of values 4j..4j+3.
+template <int N>
+__device__ __forceinline__ void quantize_q81(const float (&v)[N], float amax, float d, uint32_t (&out)[N / 4]) {
+  constexpr float kMagic = 12582912.0f;
+  const float r = __builtin_amdgcn_rcpf(d);
+  uint32_t m[N], dev = 0;
+#pragma unroll
+  for (int e = 0; e < N; ++e) {
+    const float a = v[e] * r;
+    const float t = a + kMagic;
+    m[e] = __float_as_uint(t);
+    dev = max(dev, __float_as_uint(a - (t - kMagic)) & 0x7FFFFFFFu);
+  }
+#pragma unroll
+  for (int j = 0; j < N / 4; ++j)
+    out[j] = __builtin_amdgcn_perm(__builtin_amdgcn_perm(m[4 * j + 3], m[4 * j + 2], 0x0c0c0400u),
+                                   __builtin_amdgcn_perm(m[4 * j + 1], m[4 * j], 0x0c0c0400u), 0x05040100u);
+  if (!(amax >= 0x1p-100f) || dev > __float_as_uint(0.5f - 0x1p-12f)) {
+#pragma unroll
+    for (int j = 0; j < N / 4; ++j) out[j] = 0;
+    if (amax != 0.0f) {
+#pragma unroll
+      for (int e = 0; e < N; ++e) out[e >> 2] |= ((uint32_t)(int)roundf(v[e] / d) & 0xFFu) << (8 * (e & 3));
+    }
+  }
+}
+
 // ex: the wave's 64-dword exchange area; the lane holds values 4p..4p+3 of slice s (the slice's
 // 8 lanes are s, s+8, ..., s+56)
 template <int NC, int XDT>
@@ -758,12 +793,9 @@ __device__ __forceinline__ void quantize_xraw(const XRawFrag<NC, XDT>& r, uint32
                              fmaxf(fmaxf(__uint_as_float(a1.x), __uint_as_float(a1.y)),
                                    fmaxf(__uint_as_float(a1.z), __uint_as_float(a1.w))));
     const float d = amax / 127.0f;
-    // amax == 0 means every value is zero: dividing by 1 then gives q = 0 with no branch
-    const float dd = amax == 0.0f ? 1.0f : d;
-    uint32_t qw = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) qw |= ((uint32_t)(int)roundf(v[i] / dd) & 0xFFu) << (8 * i);
-    ex[8 * s + p] = qw;  // after this wave's reads above: a wave's LDS operations complete in order
+    uint32_t qw[1];
+    quantize_q81<4>(v, amax, d, qw);
+    ex[8 * s + p] = qw[0];  // after this wave's reads above: a wave's LDS operations complete in order
     const uint4 q0 = *(const uint4*)(ex + 8 * s), q1 = *(const uint4*)(ex + 8 * s + 4);
     x.q[c][0] = (int)q0.x; x.q[c][1] = (int)q0.y; x.q[c][2] = (int)q0.z; x.q[c][3] = (int)q0.w;
     x.q[c][4] = (int)q1.x; x.q[c][5] = (int)q1.y; x.q[c][6] = (int)q1.z; x.q[c][7] = (int)q1.w;
@@ -962,43 +994,6 @@ __device__ __forceinline__ void xgroup_load(const void* x, __amdgpu_buffer_rsrc_
   }
 }
 
-// q8_1 bytes of 8 values of one slice, given the slice's amax: d = amax / 127 and q = roundf(v / d)
-// (q = 0 when amax == 0), bit for bit as the q8_1 quantiser computes them. The quotient comes from
-// the product v * rcp(d): for |v| <= amax it lies within 2^-15 of v / d (rcp within 1 ulp), and
-// the fp32 rounding of v / d moves that by less than 2^-16, so when the product lies more than
-// 2^-12 from every half-integer, roundf(v / d) is the integer nearest to it. Adding 1.5 * 2^23
-// rounds to that integer and leaves it in the low mantissa bits. The largest distance is taken
-// over the bit patterns of |a - n|, where a NaN (a NaN or infinite value) ranks above every
-// number. A lane with a value near a tie, a non-finite product or a tiny amax (rcp of a
-// subnormal d) takes the IEEE division.
-__device__ __forceinline__ void quantize8_q81(const float (&v)[8], float amax, float d, uint32_t& lo, uint32_t& hi) {
-  constexpr float kMagic = 12582912.0f;
-  const float r = __builtin_amdgcn_rcpf(d);
-  uint32_t m[8], dev = 0;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float a = v[e] * r;
-    const float t = a + kMagic;
-    m[e] = __float_as_uint(t);
-    dev = max(dev, __float_as_uint(a - (t - kMagic)) & 0x7FFFFFFFu);
-  }
-  lo = __builtin_amdgcn_perm(__builtin_amdgcn_perm(m[3], m[2], 0x0c0c0400u), __builtin_amdgcn_perm(m[1], m[0], 0x0c0c0400u),
-                             0x05040100u);
-  hi = __builtin_amdgcn_perm(__builtin_amdgcn_perm(m[7], m[6], 0x0c0c0400u), __builtin_amdgcn_perm(m[5], m[4], 0x0c0c0400u),
-                             0x05040100u);
-  if (!(amax >= 0x1p-100f) || dev > __float_as_uint(0.5f - 0x1p-12f)) {
-    lo = hi = 0;
-    if (amax != 0.0f) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t q = (uint32_t)(int)roundf(v[e] / d) & 0xFFu;
-        if (e < 4) lo |= q << (8 * e);
-        else hi |= q << (8 * (e - 4));
-      }
-    }
-  }
-}
-
 // max over the four lanes of a quad, exchanged by DPP quad permutes (xor 1, then xor 2)
 __device__ __forceinline__ float quad_fmax(float v) {
   v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false)));
@@ -1032,7 +1027,10 @@ __device__ __forceinline__ void xgroup_store(const XGroup<XDT>& r, int g, bool l
                        fmaxf(fmaxf(fabsf(v[4]), fabsf(v[5])), fmaxf(fabsf(v[6]), fabsf(v[7]))));
     amax = quad_fmax(amax);
     const float d = amax / 127.0f;
-    quantize8_q81(v, amax, d, lo, hi);
+    uint32_t qw[2];
+    quantize_q81<8>(v, amax, d, qw);
+    lo = qw[0];
+    hi = qw[1];
     dbits = __half_as_ushort(__float2half_rn(d));
   }
   *(live ? (uint2*)(xq + sr * 8 + 2 * part) : (uint2*)sink) = make_uint2(lo, hi);
@@ -1236,7 +1234,9 @@ static void launch_gemv_packed_dt(const uint8_t* W, int64_t row_bytes, int nrows
     // (measured at 17408 x 5120: 1-2 rows level with or faster than one tile per workgroup, 3-4
     // rows 15.3 / 17.1 us against 17.1 / 19.4; on weights with fewer tiles than the grid the
     // one-tile kernel is faster at every row count)
-    if (nrows / kTileRows > persist_grid() && n <= 4 && k / kQK >= 8 && n * (k / kQ81) * 36 <= 48 * 1024) {
+    // and at two rows on large weights (5120 x 17408: 15.2 us against 16.9)
+    const bool fits = k / kQK >= 8 && n * (k / kQ81) * 36 <= 48 * 1024;
+    if (fits && ((nrows / kTileRows > persist_grid() && n <= 4) || (n == 2 && (int64_t)nrows * k >= ((int64_t)64 << 20)))) {
       launch_gemv_persist<XDT>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream);
       return;
     }
