@@ -451,6 +451,34 @@ def test_raw_gemv_tiles(qt, n):
         assert torch.equal(out, eager)
 
 
+@pytest.mark.parametrize("qt", [o.Q4_K, o.IQ4_XS, o.Q6_K], ids=lambda t: TN[t])
+@pytest.mark.parametrize("n,k", [(3, 17408), (4, 17408), (1, 40960)])
+def test_rows_gemv_k_phases(qt, n, k):
+    """The row-chunk GEMV when X's q8_1 exceeds its LDS budget: K runs in two phases of blocks
+    with X staged per phase between barriers (21 tiles, the last one partial, one per workgroup):
+    exact-integer dots (at K = 17408; at K = 40960 the exact sums pass 2^24), the q81 model and
+    bit-identical CUDA-graph replays."""
+    rows = 16 * 20 + 5
+    op = getattr(C(), VEC_OP[qt])
+    if k <= 17408:
+        raw = _exact_weights(qt, rows, k, seed=200 + n)
+        x = _exact_x(n, k, seed=201 + n, dtype=torch.float32)
+        y = op(_dev(raw), x.cuda(), qt, rows).cpu().numpy()
+        np.testing.assert_array_equal(y.astype(np.int64), _exact_ref(raw, qt, x))
+    raw = _w(qt, rows, k, seed=202 + n)
+    w = _dev(raw)
+    x = _x(n, k, seed=203 + n, dtype=torch.bfloat16).cuda()
+    eager = op(w, x, qt, rows)
+    assert o.rel_l2(eager.float().cpu().numpy(), o.q81_model(raw, qt, x.cpu())) <= TIGHT[torch.bfloat16]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = op(w, x, qt, rows)
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+
+
 @pytest.mark.parametrize("n,dtype", [(1, torch.bfloat16), (1, torch.float16), (1, torch.float32),
                                      (2, torch.bfloat16), (2, torch.float32)])
 @pytest.mark.parametrize("rows,k", [(16 * 700, 2048), (6144, 5120), (5120, 17408)])

@@ -350,10 +350,13 @@ struct RowsFrag<kQ6_K> {
   uint32_t d;   // fp16 d of row r | of row 8 + r << 16
 };
 
+// kp > 1: X's q8_1 does not fit the LDS budget, so K runs in kp phases of whole blocks; in each
+// phase the 8 waves split its blocks, and the workgroup stages that phase's part of X (between
+// two barriers) when its waves reach it. Every wave has at least one block in every phase.
 template <int TYPE, int NC, int WPT>
 __global__ void __launch_bounds__(64 * WPT) gemv_rows_kernel(const uint8_t* __restrict__ W, int64_t row_bytes,
                                                              int nrows, int k, const uint8_t* __restrict__ q8,
-                                                             void* __restrict__ y, int y_dtype) {
+                                                             void* __restrict__ y, int y_dtype, int kp) {
   constexpr int BS = block_bytes(TYPE);
   constexpr int NT = 64 * WPT;
   constexpr int SUMS = TYPE == kQ4_K ? kSumSlice : (TYPE == kQ6_K ? kSumHalves : kSumNone);
@@ -365,11 +368,10 @@ __global__ void __launch_bounds__(64 * WPT) gemv_rows_kernel(const uint8_t* __re
   const int r = lane >> 3, c = lane & 7, h = c & 1;
   const int ntiles = (nrows + kTileRows - 1) / kTileRows;
   const int nb = k / kQK, nslices = k / kQ81;
-  const int b_begin = wave * nb / WPT, b_end = (wave + 1) * nb / WPT;
-  const int nblk = b_end - b_begin;
+  const int nsl = (nb + kp - 1) / kp * 8;  // LDS slices per activation row (the longest phase)
   const int G = gridDim.x;
   uint32_t* xq = (uint32_t*)xdyn;
-  float2* xs = (float2*)(xq + NC * nslices * 8);
+  float2* xs = (float2*)(xq + NC * nsl * 8);
   const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(W, (uint32_t)((int64_t)nrows * row_bytes));
   const __amdgpu_buffer_rsrc_t nrs = buffer_rsrc(W, 0);
   const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(q8, (uint32_t)(NC * nslices * 36));
@@ -399,32 +401,69 @@ __global__ void __launch_bounds__(64 * WPT) gemv_rows_kernel(const uint8_t* __re
     }
     if constexpr (TYPE == kQ6_K) f.d = (d16[0] & 0xFFFFu) | (d16[1] << 16);
   };
-  const int items = ((int)blockIdx.x < ntiles ? (ntiles - 1 - (int)blockIdx.x) / G + 1 : 0) * nblk;
-  auto next = [&](int& tt, int& bb) {
-    if (++bb == b_end) {
-      bb = b_begin;
-      tt += G;
+  // phase p: blocks [ph0(p), ph0(p + 1)); this wave's part of it: [wb(p), we(p))
+  auto ph0 = [&](int pp) { return pp * nb / kp; };
+  auto wb = [&](int pp) { return ph0(pp) + wave * (ph0(pp + 1) - ph0(pp)) / WPT; };
+  auto we = [&](int pp) { return ph0(pp) + (wave + 1) * (ph0(pp + 1) - ph0(pp)) / WPT; };
+  int per_tile = 0;
+  for (int pp = 0; pp < kp; ++pp) per_tile += we(pp) - wb(pp);
+  const int items = ((int)blockIdx.x < ntiles ? (ntiles - 1 - (int)blockIdx.x) / G + 1 : 0) * per_tile;
+  auto next = [&](int& tt, int& pp, int& bb) {
+    if (++bb == we(pp)) {
+      if (++pp == kp) {
+        pp = 0;
+        tt += G;
+      }
+      bb = wb(pp);
     }
   };
-  const int ngroups = NC * nslices * 4;
+  // X staging of phase pp: local group gl (8 values; 4 per slice) of activation row cc -> global
+  // group of the block_q8_1 array, and the group index of the LDS layout (row stride nsl)
+  auto groups = [&](int pp) { return NC * (ph0(pp + 1) - ph0(pp)) * 32; };
+  auto gmap = [&](int pp, int gl, int& gg, int& gL) {
+    const int per_row = (ph0(pp + 1) - ph0(pp)) * 32;
+    int cc = 0, rem = gl;
+#pragma unroll
+    for (int i = 1; i < NC; ++i)
+      if (rem >= per_row) rem -= per_row, ++cc;
+    gg = (cc * nslices + ph0(pp) * 8) * 4 + rem;
+    gL = cc * nsl * 4 + rem;
+  };
+  auto stage = [&](int pp) {  // the in-loop staging of a later phase (between barriers)
+    const int ng = groups(pp);
+    for (int gl = threadIdx.x; gl < ng; gl += NT) {
+      int gg, gL;
+      gmap(pp, gl, gg, gL);
+      XGroupQ8 xc;
+      xgroup_q8_load(xrs, gg, xc);
+      xgroup_q8_store<SUMS>(xc, gL, true, xq, xs, &sink);
+    }
+  };
+  // phase 0: X's first two groups per thread, then the first two weight blocks, then X to LDS
+  const int ng0 = groups(0);
   const int ga = threadIdx.x, gb = threadIdx.x + NT;
+  int gga, gLa, ggb, gLb;
+  gmap(0, ga < ng0 ? ga : ng0 - 1, gga, gLa);
+  gmap(0, gb < ng0 ? gb : ng0 - 1, ggb, gLb);
   XGroupQ8 xa, xb;
-  xgroup_q8_load(xrs, ga < ngroups ? ga : ngroups - 1, xa);
-  xgroup_q8_load(xrs, gb < ngroups ? gb : ngroups - 1, xb);
+  xgroup_q8_load(xrs, gga, xa);
+  xgroup_q8_load(xrs, ggb, xb);
   __builtin_amdgcn_sched_barrier(0);
   RowsFrag<TYPE> f0, f1, f2;
-  int lt = blockIdx.x, lb = b_begin;  // next item to load
+  int lt = blockIdx.x, lp = 0, lb = wb(0);  // next item to load
   load(lt, lb, f0);
-  next(lt, lb);
+  next(lt, lp, lb);
   load(lt, lb, f1);
-  next(lt, lb);
+  next(lt, lp, lb);
   __builtin_amdgcn_sched_barrier(0);
-  xgroup_q8_store<SUMS>(xa, ga, ga < ngroups, xq, xs, &sink);
-  xgroup_q8_store<SUMS>(xb, gb, gb < ngroups, xq, xs, &sink);
-  for (int g = threadIdx.x + 2 * NT; g < ngroups; g += NT) {  // K beyond 2 groups per thread
+  xgroup_q8_store<SUMS>(xa, gLa, ga < ng0, xq, xs, &sink);
+  xgroup_q8_store<SUMS>(xb, gLb, gb < ng0, xq, xs, &sink);
+  for (int gl = threadIdx.x + 2 * NT; gl < ng0; gl += NT) {  // phase 0 beyond 2 groups per thread
+    int gg, gL;
+    gmap(0, gl, gg, gL);
     XGroupQ8 xc;
-    xgroup_q8_load(xrs, g, xc);
-    xgroup_q8_store<SUMS>(xc, g, true, xq, xs, &sink);
+    xgroup_q8_load(xrs, gg, xc);
+    xgroup_q8_store<SUMS>(xc, gL, true, xq, xs, &sink);
   }
   __syncthreads();
   float acc[2][NC];
@@ -433,8 +472,8 @@ __global__ void __launch_bounds__(64 * WPT) gemv_rows_kernel(const uint8_t* __re
 #pragma unroll
     for (int cc = 0; cc < NC; ++cc) acc[i][cc] = 0.0f;
   // the lane's two (Q4_K, Q6_K) or one (IQ4_XS) slices of block b, for activation row cc
-  auto slices = [&](int cc, int b, int& s1, int& s2) {
-    const int base = cc * nslices + b * 8;
+  auto slices = [&](int cc, int b, int& s1, int& s2) {  // b: block index within the staged phase
+    const int base = cc * nsl + b * 8;
     if constexpr (TYPE == kQ4_K) {
       s1 = base + 2 * (c >> 1);
       s2 = s1 + 1;
@@ -518,13 +557,19 @@ __global__ void __launch_bounds__(64 * WPT) gemv_rows_kernel(const uint8_t* __re
       }
     }
   };
-  int t = blockIdx.x, b = b_begin, it = 0;  // item being computed
+  int t = blockIdx.x, p = 0, b = wb(0), it = 0, staged = 0;  // item being computed
   auto step = [&](const RowsFrag<TYPE>& fc, RowsFrag<TYPE>& fl) {
     load(lt, lb, fl);
-    next(lt, lb);
+    next(lt, lp, lb);
     __builtin_amdgcn_sched_barrier(0);
-    compute(fc, b);
-    if (b == b_end - 1) {  // the wave's last block of tile t: reduce and store the tile
+    if (p != staged) {  // the first block of a later phase (or of phase 0 of the next tile)
+      __syncthreads();
+      stage(p);
+      __syncthreads();
+      staged = p;
+    }
+    compute(fc, b - ph0(p));
+    if (p == kp - 1 && b == we(kp - 1) - 1) {  // the wave's last block of tile t: reduce and store
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
 #pragma unroll
@@ -548,7 +593,7 @@ __global__ void __launch_bounds__(64 * WPT) gemv_rows_kernel(const uint8_t* __re
       }
       ++it;
     }
-    next(t, b);
+    next(t, p, b);
   };
   int i = 0;
   for (; i + 3 <= items; i += 3) {
@@ -573,25 +618,34 @@ static bool launch_rawtile(const uint8_t* W, int64_t row_bytes, int nrows, int k
   return true;
 }
 
-// Q4_K / IQ4_XS / Q6_K at 1-4 rows on weights of at least 8 K blocks (one per wave) below 2 GiB
-// whose X q8_1 (40 bytes per slice and row) fits in 48 KB of LDS: the row-chunk kernel
+// Q4_K / IQ4_XS / Q6_K at 1-4 rows on weights below 2 GiB: the row-chunk kernel. X's q8_1 takes
+// 40 bytes of LDS per slice and row; kp: the fewest K phases that bring a phase within 48 KB
+// with at least one block per wave and phase (0 if none does).
+static int rows_phases(int64_t k, int64_t n) {
+  const int64_t nb = k / kQK;
+  for (int64_t kp = 1; nb / kp >= 8; ++kp)
+    if (n * ((nb + kp - 1) / kp) * 8 * 40 <= 48 * 1024) return (int)kp;
+  return 0;
+}
+
 bool gemv_rows_supported(int type, int64_t nrows, int64_t row_bytes, int64_t k, int64_t n) {
-  return (type == kQ4_K || type == kIQ4_XS || type == kQ6_K) && n >= 1 && n <= 4 && k / kQK >= 8 &&
-         nrows * row_bytes < ((int64_t)1 << 31) && n * (k / kQ81) * 40 <= 48 * 1024;
+  return (type == kQ4_K || type == kIQ4_XS || type == kQ6_K) && n >= 1 && n <= 4 &&
+         nrows * row_bytes < ((int64_t)1 << 31) && rows_phases(k, n) > 0;
 }
 
 template <int TYPE>
 static bool launch_rows(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n, void* y,
                         int y_dtype, hipStream_t stream) {
   if (!gemv_rows_supported(TYPE, nrows, row_bytes, k, n)) return false;
+  const int kp = rows_phases(k, n);
   const int tiles = (nrows + kTileRows - 1) / kTileRows;
   const unsigned g = (unsigned)std::min(tiles, persist_grid());
-  const size_t lds = (size_t)n * (k / kQ81) * 40;
+  const size_t lds = (size_t)n * ((k / kQK + kp - 1) / kp) * 8 * 40;
   switch (n) {
-    case 1: gemv_rows_kernel<TYPE, 1, 8><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype); break;
-    case 2: gemv_rows_kernel<TYPE, 2, 8><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype); break;
-    case 3: gemv_rows_kernel<TYPE, 3, 8><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype); break;
-    default: gemv_rows_kernel<TYPE, 4, 8><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype); break;
+    case 1: gemv_rows_kernel<TYPE, 1, 8><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype, kp); break;
+    case 2: gemv_rows_kernel<TYPE, 2, 8><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype, kp); break;
+    case 3: gemv_rows_kernel<TYPE, 3, 8><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype, kp); break;
+    default: gemv_rows_kernel<TYPE, 4, 8><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype, kp); break;
   }
   return true;
 }
