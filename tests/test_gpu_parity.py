@@ -234,6 +234,68 @@ def test_golden_rows(qt, n):
         assert o.rel_l2(y, ref) <= 1e-3, (k, o.rel_l2(y, ref))
 
 
+# ------------------------------------------------------------------------------------ fp16 small GEMM
+# Product ops of 64..255 activation rows with K <= 8192 on packed IQ3_S and Q4_K run the fp16
+# small GEMM: one 16-row tile per workgroup below 1024 tiles, two from 1024 tiles on.
+SMALL_H_ROWS = {o.IQ3_S: (64, 16 * 1025), o.Q4_K: (100, 16 * 1024 + 9)}
+
+
+def _small_h_op(qt, raw, rows):
+    from vllm_gguf_plugin.quantization import iq3_pack
+
+    if qt == o.IQ3_S:
+        return lambda x: C().lcpp_mul_mat_iq3_packed(iq3_pack.pack(_dev(raw), qt), x, qt, rows)
+    return lambda x: C().lcpp_mul_mat_q(_dev(raw), x, qt, rows)
+
+
+@pytest.mark.parametrize("qt", [o.IQ3_S, o.Q4_K], ids=lambda t: TN[t])
+@pytest.mark.parametrize("tiles", [0, 1], ids=["one_tile", "two_tiles"])
+@pytest.mark.parametrize("n", [64, 100, 255])
+def test_small_fp16_exact_integer_dots(qt, tiles, n):
+    """Exact-integer mode through the fp16 small GEMM: weight x sub-scale and the q8 values are exact
+    fp16 integers, so every output is the oracle's int64 sum of slice dots (rows past the last full
+    tile or tile pair, activation rows past the last column tile)."""
+    rows, k = SMALL_H_ROWS[qt][tiles], 512
+    raw = _exact_weights(qt, rows, k, seed=160 + n)
+    x = _exact_x(n, k, seed=170 + n, dtype=torch.float32)
+    y = _small_h_op(qt, raw, rows)(x.cuda()).cpu().numpy()
+    np.testing.assert_array_equal(y.astype(np.int64), _exact_ref(raw, qt, x))
+
+
+@pytest.mark.parametrize("qt", [o.IQ3_S, o.Q4_K], ids=lambda t: TN[t])
+@pytest.mark.parametrize("tiles", [0, 1], ids=["one_tile", "two_tiles"])
+@pytest.mark.parametrize("n", [64, 200])
+def test_small_fp16_vs_q81_with_zero_blocks(qt, tiles, n):
+    """The running block scale: blocks with d = 0 (a row's first block, blocks inside a row, and a
+    row with every block zero; Q4_K keeps its dmin term) against the q81 model."""
+    rows, k = SMALL_H_ROWS[qt][tiles], 2048
+    raw = _w(qt, rows, k, seed=180 + n + tiles)
+    b = raw.reshape(rows, k // 256, o.BLOCK_BYTES[qt])
+    rng = np.random.default_rng(190 + n)
+    zero = rng.random((rows, k // 256)) < 0.2
+    zero[:, 0] |= rng.random(rows) < 0.5
+    zero[3] = True
+    b[zero, 0:2] = 0
+    x = _x(n, k, seed=n + 800)
+    y = _small_h_op(qt, raw, rows)(x.cuda()).cpu().numpy()
+    ref = o.q81_model(raw, qt, x, layout="mmq")
+    assert o.rel_l2(y, ref) <= 1e-3, o.rel_l2(y, ref)
+    if qt == o.IQ3_S:
+        assert (y[:, 3] == 0).all()
+
+
+@pytest.mark.parametrize("qt", [o.IQ3_S, o.Q4_K], ids=lambda t: TN[t])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
+def test_small_fp16_16bit_x(qt, dtype):
+    rows, k, n = SMALL_H_ROWS[qt][0], 5120, 96
+    raw = _w(qt, rows, k, seed=210)
+    x = _x(n, k, seed=211, dtype=dtype)
+    y = _small_h_op(qt, raw, rows)(x.cuda())
+    assert y.dtype == dtype and y.shape == (n, rows)
+    ref = o.q81_model(raw, qt, x, layout="mmq")
+    assert o.rel_l2(y.float().cpu().numpy(), ref) <= TIGHT[dtype]
+
+
 # ------------------------------------------------------------------------------------ packed
 def test_pack_is_the_tile_layout_and_roundtrips():
     from vllm_gguf_plugin.quantization import iq3_pack
@@ -560,6 +622,8 @@ def test_fused_quantisation_ties(n, dtype, rows):
     ("lcpp_mul_mat_vec_q", o.IQ4_XS, 1, False),
     ("lcpp_mul_mat_iq3_packed", o.IQ3_S, 300, True),
     ("lcpp_mul_mat_q", o.Q4_K, 260, False),
+    ("lcpp_mul_mat_iq3_packed", o.IQ3_S, 64, True),
+    ("lcpp_mul_mat_q", o.Q4_K, 100, False),
 ])
 def test_graph_replay_bit_exact(op, qt, n, packed):
     from vllm_gguf_plugin.quantization import iq3_pack

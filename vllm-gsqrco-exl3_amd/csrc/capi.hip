@@ -40,6 +40,9 @@ hipError_t launch_gemm_packed_xq(const uint8_t* W, int64_t row_bytes, int nrows,
 hipError_t launch_quantize_xh(const void* x, int dtype, int64_t n, int64_t k, int64_t s01, int type, void* y,
                               hipStream_t stream);
 bool prefill_uses_xh(int type, bool packed);
+bool small_h_supported(int type, bool packed);
+hipError_t launch_gemm_small_h(int type, bool packed, const uint8_t* W, int64_t row_bytes, int nrows, int k,
+                               const uint8_t* xh, int n, void* y, int y_dtype, hipStream_t stream);
 hipError_t launch_gemm_prefill(int type, bool packed, const uint8_t* W, int64_t row_bytes, int nrows, int k,
                                const uint8_t* xq, int n, void* y, int y_dtype, hipStream_t stream);
 hipError_t launch_iq3_pack(uint8_t* w, int64_t rows, int64_t row_bytes, bool unpack, uint8_t* scratch,
@@ -238,13 +241,24 @@ bool decode_mma(int op, int64_t type, int64_t row, int64_t k, int64_t n) {
   return !(op_packed(op) == false && bb > 0 && gguf::gemv_rows_supported((int)type, row, k / 256 * bb, k, n));
 }
 
+// The MFMA products of 64 to 255 activation rows with K <= 8192 run the fp16 small GEMM (X in the
+// xh layout) for packed IQ3_S and Q4_K; the rest below the prefill rows the int8 small GEMM (xq
+// layout). Measured at the 27B-layer shapes: from 64 rows the fp16 GEMM's shared decode beats
+// re-decoding the weights per group of 4 column tiles (17408 x 5120 IQ3_S, 128 rows: 84 against
+// 134 us); below 64 rows, and over K = 17408 (68 blocks in one workgroup's loop, 320
+// workgroups), the int8 GEMM's K split across waves is faster.
+bool small_fp16(int op, int64_t type, int64_t k, int64_t n) {
+  return op_gemm(op) && n >= 64 && n < kPrefillFrom && k <= 8192 && gguf::small_h_supported((int)type, op_packed(op));
+}
+
 }  // namespace
 
 size_t gguf_op_workspace_bytes(int op, int64_t type, int64_t row, int64_t k, int64_t n, int has_x_q8) {
   if (n <= 0) return 0;
   if (op_gemm(op)) {
     const bool mmq_layout = !op_packed(op) && type == gguf::kIQ3_S;
-    if (!mmq_layout && n >= kPrefillFrom && gguf::prefill_uses_xh((int)type, op_packed(op)))
+    if (!mmq_layout && ((n >= kPrefillFrom && gguf::prefill_uses_xh((int)type, op_packed(op))) ||
+                        small_fp16(op, type, k, n)))
       return align256(gguf::xh_bytes(n, k));
     return align256(mmq_layout ? gguf_q8_1_bytes(n, k, 1) : gguf::xq_bytes(n, k));
   }
@@ -284,15 +298,20 @@ int gguf_mul_mat(int op, const gguf_view* W, const gguf_view* X, int64_t type, i
   // caller's x_q8
   if ((gemm && (packed || type != gguf::kIQ3_S)) || (!gemm && decode_mma(op, type, row, k, n))) {
     const bool prefill = gemm && n >= kPrefillFrom;
+    const bool fp16 = small_fp16(op, type, k, n);
+    const bool xh = fp16 || (prefill && gguf::prefill_uses_xh((int)type, packed));
     if (!gemm && x_q8)
       e = gguf::launch_q8_1_to_xq(x_q8->data, n, k, (int)type, workspace, s);
-    else if (prefill && gguf::prefill_uses_xh((int)type, packed))
+    else if (xh)
       e = gguf::launch_quantize_xh(X->data, X->dtype, n, k, s01, (int)type, workspace, s);
     else
       e = gguf::launch_quantize_xq(X->data, X->dtype, n, k, s01, (int)type, !gemm, workspace, s);
     if (e != hipSuccess) return hip_fail(e, name, "quantize");
     if (prefill)
       e = gguf::launch_gemm_prefill((int)type, packed, w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace,
+                                    (int)n, y, ydt, s);
+    else if (fp16)
+      e = gguf::launch_gemm_small_h((int)type, packed, w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace,
                                     (int)n, y, ydt, s);
     else if (packed)
       e = gguf::launch_gemm_packed_xq(w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace, (int)n, y, ydt, s);

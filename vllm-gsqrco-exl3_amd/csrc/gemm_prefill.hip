@@ -22,6 +22,7 @@
 
 #include "decode.h"
 #include "iq3_tile.h"
+#include "xh_decode.h"
 #include "xq.h"
 
 namespace gguf {
@@ -317,146 +318,7 @@ __global__ void __launch_bounds__(256, 2) gemm_prefill_kernel(const uint8_t* __r
 // half block) come straight from global memory into registers one step ahead, so only the
 // decoded weights are shared through LDS, double-buffered, with one barrier per step (half
 // block). Each wave decodes 8 / NW row tiles per step from raw bytes it loaded two steps ahead.
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-typedef float f4 __attribute__((ext_vector_type(4)));
-
-constexpr int kHRegion = 1040;                     // A bytes per (row tile, slice): 16 rows x 64 B + pad
 constexpr int kHA = kPfRowTiles * 4 * kHRegion;    // 33,280 per buffer (half a K block)
-
-// fp16 bits of a small positive integer
-constexpr uint32_t small_int_half(uint32_t v) {
-  int e = 0;
-  while ((v >> (e + 1)) != 0) ++e;
-  return ((uint32_t)(e + 15) << 10) | ((v - (1u << e)) << (10 - e));
-}
-static_assert(small_int_half(1) == 0x3C00 && small_int_half(15) == 0x4B80, "fp16 bits");
-
-// The IQ3_S grid as fp16: entry i = the 4 grid values of index i, 2 per dword
-struct Iq3sGridHalf {
-  uint32_t v[1024];
-};
-constexpr Iq3sGridHalf make_iq3s_grid_half() {
-  Iq3sGridHalf g{};
-  for (int i = 0; i < 512; ++i) {
-    const uint32_t w = kIq3sGrid.v[i];
-    g.v[2 * i] = small_int_half(w & 0xFF) | (small_int_half((w >> 8) & 0xFF) << 16);
-    g.v[2 * i + 1] = small_int_half((w >> 16) & 0xFF) | (small_int_half(w >> 24) << 16);
-  }
-  return g;
-}
-__device__ const Iq3sGridHalf kIq3sGridHalf = make_iq3s_grid_half();
-
-// A slot of (row tile t, slice u of the half block, row j, quarter q): the quarter's 16 bytes sit
-// in slot q ^ g(j) of the row, g(j) = ((j >> 1) ^ (j >> 3)) & 3, which keeps the operand reads
-// (lane (j, q)) free of bank conflicts.
-__device__ __forceinline__ int h_off(int t, int u, int j, int q) {
-  return (t * 4 + u) * kHRegion + j * 64 + ((q ^ ((j >> 1) ^ (j >> 3))) & 3) * 16;
-}
-
-__device__ __forceinline__ uint32_t h2_bits(h2 v) { return __builtin_bit_cast(uint32_t, v); }
-__device__ __forceinline__ h2 bits_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
-
-// A decoding lane's raw weight bytes for one step, loaded two steps ahead.
-struct RawIq3 {
-  uint2 qs;     // qs of the lane's row and slice
-  uint32_t e8;  // E8 dword of the row
-  uint32_t l2;  // L2 halfword of the row pair
-  uint32_t sc;  // SC byte (two 4-bit sub-scales)
-  uint32_t d;   // fp16 d of the row
-};
-struct RawQ4k {
-  u32x4 hdr;    // d, dmin, scales[12]
-  uint2 v0, v1; // quarter q of the two 32-byte quant groups of the half block
-};
-
-// IQ3_S lane (row j, slice 4h + sp) of a tile-block in the tile layout
-__device__ __forceinline__ void load_step(RawIq3& w, const uint8_t* tb, int h, int j, int sp) {
-  const int p = j >> 1, r = j & 1, s = 4 * h + sp, L = 8 * p + s;
-  w.qs = *(const uint2*)(tb + kTqs + 16 * L + 8 * r);
-  w.e8 = *(const uint32_t*)(tb + kTe8 + 8 * L + 4 * r);
-  w.l2 = *(const uint16_t*)(tb + kTl2 + 2 * L);
-  w.sc = tb[kTsc + 2 * (4 * p + (s >> 1)) + r];
-  w.d = *(const uint16_t*)(tb + kTd + 4 * p + 2 * r);
-}
-
-// Q4_K lane (row j, quarter q) of the row's block
-__device__ __forceinline__ void load_step(RawQ4k& w, const uint8_t* blk, int h, int q) {
-  w.hdr = *(const u32x4*)blk;
-  w.v0 = *(const uint2*)(blk + 16 + 64 * h + 8 * q);
-  w.v1 = *(const uint2*)(blk + 48 + 64 * h + 8 * q);
-}
-
-// The row's running scale at a block start (h == 0): e_cur = d, or e_prev for d = 0; the ratio
-// and the final scale go to LDS (the lanes of a row store the same values).
-__device__ __forceinline__ float next_scale(float d, float& e, float* RT, float* EF, int row) {
-  const float en = d != 0.0f ? d : e;
-  RT[row] = e / en;
-  EF[row] = en;
-  e = en;
-  return en;
-}
-
-__device__ __forceinline__ void decode_step(const RawIq3& w, int h, const uint32_t* gh, const uint2* sm, uint8_t* A,
-                                            float* RT, float* EF, float& e, int t, int j, int sp) {
-  const int s = 4 * h + sp;
-  const float d = half_bits_to_float(w.d);
-  if (h == 0) next_scale(d, e, RT, EF, t * 16 + j);
-  uint32_t lo, hi;
-  iq3_tile_ex(w.e8, w.l2, j & 1, lo, hi);
-  const uint32_t nib = (w.sc >> (4 * (s & 1))) & 0xF;
-  const _Float16 ls = d != 0.0f ? (_Float16)(float)(1 + 2 * nib) : (_Float16)0.0f;
-  const h2 lsh = {ls, ls};
-  uint32_t v[16];
-#pragma unroll
-  for (int g = 0; g < 8; ++g) {
-    const uint32_t qb = ((g < 4 ? w.qs.x : w.qs.y) >> (8 * (g & 3))) & 0xFF;
-    const uint32_t ex = ((g < 4 ? lo : hi) >> (8 * (g & 3))) & 0xFF;
-    const uint2 gv = *(const uint2*)(gh + 2 * (qb | ((ex >> 4) << 8)));
-    const uint2 sg = sm[ex & 0xF];
-    v[2 * g] = h2_bits(bits_h2(gv.x ^ sg.x) * lsh);
-    v[2 * g + 1] = h2_bits(bits_h2(gv.y ^ sg.y) * lsh);
-  }
-#pragma unroll
-  for (int q = 0; q < 4; ++q)
-    *(uint4*)(A + h_off(t, sp, j, q)) = make_uint4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
-}
-
-// Q4_K: fp16 (1024 + nibble) by a byte permute, then one packed FMA gives nibble x sc exactly.
-__device__ __forceinline__ void decode_step(const RawQ4k& w, int h, float* AM, uint8_t* A, float* RT, float* EF,
-                                            float& e, int t, int j, int q) {
-  const float d = half_bits_to_float(w.hdr[0] & 0xFFFF);
-  const float dmin = half_bits_to_float(w.hdr[0] >> 16);
-  const float en = h == 0 ? next_scale(d, e, RT, EF, t * 16 + j) : e;
-  const float mf = -dmin / en;
-  const bool nz = d != 0.0f;
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int us = 4 * h + u, jj = us & 3;
-    const uint32_t a = (w.hdr[1] >> (8 * jj)) & 0xFF, c = (w.hdr[2] >> (8 * jj)) & 0xFF;
-    uint32_t sc, m;
-    if (us < 4) {
-      sc = a & 63;
-      m = c & 63;
-    } else {
-      const uint32_t ee = (w.hdr[3] >> (8 * jj)) & 0xFF;
-      sc = (ee & 0xF) | ((a >> 6) << 4);
-      m = (ee >> 4) | ((c >> 6) << 4);
-    }
-    const _Float16 scf = nz ? (_Float16)(float)sc : (_Float16)0.0f;
-    const h2 mul = {scf, scf};
-    const h2 off = mul * (_Float16)(-1024.0f);
-    const uint2 vv = u < 2 ? w.v0 : w.v1;
-    const int sh = 4 * (u & 1);
-    const uint32_t x0 = (vv.x >> sh) & 0x0F0F0F0Fu, x1 = (vv.y >> sh) & 0x0F0F0F0Fu;
-    const uint32_t w0 = h2_bits(__builtin_elementwise_fma(bits_h2(__builtin_amdgcn_perm(0x64646464u, x0, 0x04010400u)), mul, off));
-    const uint32_t w1 = h2_bits(__builtin_elementwise_fma(bits_h2(__builtin_amdgcn_perm(0x64646464u, x0, 0x04030402u)), mul, off));
-    const uint32_t w2 = h2_bits(__builtin_elementwise_fma(bits_h2(__builtin_amdgcn_perm(0x64646464u, x1, 0x04010400u)), mul, off));
-    const uint32_t w3 = h2_bits(__builtin_elementwise_fma(bits_h2(__builtin_amdgcn_perm(0x64646464u, x1, 0x04030402u)), mul, off));
-    *(uint4*)(A + h_off(t, u, j, q)) = make_uint4(w0, w1, w2, w3);
-    AM[(t * 4 + u) * 16 + j] = mf * (float)m;  // the 4 lanes of row j store the same value
-  }
-}
 
 template <int TYPE, int NW>
 __global__ void __launch_bounds__(64 * NW, 8 / NW) gemm_prefill_h_kernel(const uint8_t* __restrict__ W,
@@ -479,11 +341,7 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW) gemm_prefill_h_kernel(const u
   const int tile0 = blockIdx.x * kPfRowTiles;
   const int nb = k / kQK;
   if constexpr (IQ3) {
-    for (int i = threadIdx.x; i < 1024; i += 64 * NW) GH[i] = kIq3sGridHalf.v[i];
-    if (threadIdx.x < 16) {
-      const uint32_t nib = threadIdx.x;
-      SM[nib] = make_uint2(((nib & 1u) << 15) | ((nib & 2u) << 30), ((nib & 4u) << 13) | ((nib & 8u) << 28));
-    }
+    iq3_half_tables_to_lds(GH, SM, threadIdx.x, 64 * NW);
   }
 
   // this wave's column tiles (past nct: the last one again, never stored)
