@@ -102,12 +102,6 @@ __global__ void __launch_bounds__(64 * (2 * RT + NM), 4) gemm_small_h_kernel(con
   const int ntiles = (nrows + 15) / 16;
   const int tile0 = blockIdx.x * RT;
   const int nb = k / kQK;
-  // Step i works on K block (i + rot) mod nb: with every workgroup on the same block at the same
-  // time, their reads of X's block (and of the table, at the start) meet in one L2 channel, which
-  // then bounds the kernel; a rotation by workgroup spreads them over the blocks. The running block
-  // scale is independent of the order, and each workgroup's order is fixed (deterministic output).
-  const int rot = (int)(blockIdx.x % (unsigned)nb);
-  auto kblock = [&](int i) { return i + rot < nb ? i + rot : i + rot - nb; };
   if constexpr (IQ3) {
     // all loads first, then the stores (indices past the table repeat its last entry)
     constexpr int TPT = (2048 + NT - 1) / NT;
@@ -131,9 +125,8 @@ __global__ void __launch_bounds__(64 * (2 * RT + NM), 4) gemm_small_h_kernel(con
     // the raw bytes of a block: two named sets, each refilled right after its decode and used
     // two steps later
     auto load_w = [&](int b, Raw& raw) {
-      const int kb = kblock(b);
-      if constexpr (IQ3) load_step(raw, wp + (int64_t)kb * kTileBlockBytes, dh, j, q);
-      else load_step(raw, wp + (int64_t)kb * block_bytes(kQ4_K), dh, q);
+      if constexpr (IQ3) load_step(raw, wp + (int64_t)b * kTileBlockBytes, dh, j, q);
+      else load_step(raw, wp + (int64_t)b * block_bytes(kQ4_K), dh, q);
     };
     auto decode = [&](int par, const Raw& raw) {
       uint8_t* Ab = A[par][dh];
@@ -176,12 +169,11 @@ __global__ void __launch_bounds__(64 * (2 * RT + NM), 4) gemm_small_h_kernel(con
     u32x4 bq[8];
     float dq[8], sqv[2];
   };
-  auto load_b = [&](BSet& o, int s, int i) {
-    const int64_t b = kblock(i);
-    o.bq[s] = *(const u32x4*)(xv + b * kXhUnit + 1024 * s);
-    o.dq[s] = *(const float*)(xs + b * kXhScaleUnit + 4 * s);
+  auto load_b = [&](BSet& o, int s, int b) {
+    o.bq[s] = *(const u32x4*)(xv + (int64_t)b * kXhUnit + 1024 * s);
+    o.dq[s] = *(const float*)(xs + (int64_t)b * kXhScaleUnit + 4 * s);
     if constexpr (!IQ3)
-      if ((s & 3) == 0) o.sqv[s >> 2] = *(const float*)(xs + b * kXhScaleUnit + 512 + 4 * (s + q));
+      if ((s & 3) == 0) o.sqv[s >> 2] = *(const float*)(xs + (int64_t)b * kXhScaleUnit + 512 + 4 * (s + q));
   };
   f4 acc[RT];
 #pragma unroll
