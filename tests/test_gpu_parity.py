@@ -519,7 +519,7 @@ def test_rows_gemv_k_phases(qt, n, k):
     """The row-chunk GEMV when X's q8_1 exceeds its LDS budget: K runs in two phases of blocks
     with X staged per phase between barriers (21 tiles, the last one partial, one per workgroup):
     exact-integer dots (at K = 17408; at K = 40960 the exact sums pass 2^24), the q81 model and
-    bit-identical CUDA-graph replays."""
+    bit-identical CUDA-graph replays. (Q4_K at 4 rows over K phases runs the int8 small GEMM.)"""
     rows = 16 * 20 + 5
     op = getattr(C(), VEC_OP[qt])
     if k <= 17408:

@@ -350,13 +350,16 @@ struct RowsFrag<kQ6_K> {
   uint32_t d;   // fp16 d of row r | of row 8 + r << 16
 };
 
-// kp > 1: X's q8_1 does not fit the LDS budget, so K runs in kp phases of whole blocks; in each
-// phase the 8 waves split its blocks, and the workgroup stages that phase's part of X (between
-// two barriers) when its waves reach it. Every wave has at least one block in every phase.
-template <int TYPE, int NC, int WPT>
+// PH (kp_arg > 1): X's q8_1 does not fit the LDS budget, so K runs in kp phases of whole blocks;
+// in each phase the 8 waves split its blocks, and the workgroup stages that phase's part of X
+// (between two barriers) when its waves reach it. Every wave has at least one block in every
+// phase. Without PH (one phase) the staging branch is compiled out: inside the K loop, a branch
+// with loads makes the compiler wait for every load in flight at its join.
+template <int TYPE, int NC, int WPT, bool PH>
 __global__ void __launch_bounds__(64 * WPT) gemv_rows_kernel(const uint8_t* __restrict__ W, int64_t row_bytes,
                                                              int nrows, int k, const uint8_t* __restrict__ q8,
-                                                             void* __restrict__ y, int y_dtype, int kp) {
+                                                             void* __restrict__ y, int y_dtype, int kp_arg) {
+  const int kp = PH ? kp_arg : 1;
   constexpr int BS = block_bytes(TYPE);
   constexpr int NT = 64 * WPT;
   constexpr int SUMS = TYPE == kQ4_K ? kSumSlice : (TYPE == kQ6_K ? kSumHalves : kSumNone);
@@ -562,7 +565,7 @@ __global__ void __launch_bounds__(64 * WPT) gemv_rows_kernel(const uint8_t* __re
     load(lt, lb, fl);
     next(lt, lp, lb);
     __builtin_amdgcn_sched_barrier(0);
-    if (p != staged) {  // the first block of a later phase (or of phase 0 of the next tile)
+    if (PH && p != staged) {  // the first block of a later phase (or of phase 0 of the next tile)
       __syncthreads();
       stage(p);
       __syncthreads();
@@ -628,9 +631,12 @@ static int rows_phases(int64_t k, int64_t n) {
   return 0;
 }
 
+// Q4_K at 4 rows in K phases stays on the int8-MFMA small GEMM (5120 x 17408: 34 against 51 us;
+// at 3 rows the phased GEMV is the faster, 32 against 34 us).
 bool gemv_rows_supported(int type, int64_t nrows, int64_t row_bytes, int64_t k, int64_t n) {
+  const int kp = rows_phases(k, n);
   return (type == kQ4_K || type == kIQ4_XS || type == kQ6_K) && n >= 1 && n <= 4 &&
-         nrows * row_bytes < ((int64_t)1 << 31) && rows_phases(k, n) > 0;
+         nrows * row_bytes < ((int64_t)1 << 31) && kp > 0 && !(type == kQ4_K && n == 4 && kp > 1);
 }
 
 template <int TYPE>
@@ -641,12 +647,16 @@ static bool launch_rows(const uint8_t* W, int64_t row_bytes, int nrows, int k, c
   const int tiles = (nrows + kTileRows - 1) / kTileRows;
   const unsigned g = (unsigned)std::min(tiles, persist_grid());
   const size_t lds = (size_t)n * ((k / kQK + kp - 1) / kp) * 8 * 40;
+#define GGUF_ROWS(NC)                                                                                            \
+  (kp > 1 ? gemv_rows_kernel<TYPE, NC, 8, true><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype, kp) \
+          : gemv_rows_kernel<TYPE, NC, 8, false><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype, 1))
   switch (n) {
-    case 1: gemv_rows_kernel<TYPE, 1, 8><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype, kp); break;
-    case 2: gemv_rows_kernel<TYPE, 2, 8><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype, kp); break;
-    case 3: gemv_rows_kernel<TYPE, 3, 8><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype, kp); break;
-    default: gemv_rows_kernel<TYPE, 4, 8><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype, kp); break;
+    case 1: GGUF_ROWS(1); break;
+    case 2: GGUF_ROWS(2); break;
+    case 3: GGUF_ROWS(3); break;
+    default: GGUF_ROWS(4); break;
   }
+#undef GGUF_ROWS
   return true;
 }
 
