@@ -41,7 +41,9 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "vllm-gsqrco-exl3_amd"))
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
-NBUF = 8                       # distinct weight copies per shape (defeats the 256 MB MALL)
+NBUF = 8                       # the fewest distinct weight copies a timed graph rotates through
+ROTATE_BYTES = 512 << 20       # ... and at least this many weight bytes: twice the 256 MB MALL,
+                               # so that no copy is still cached when its turn comes again
 COPY_BYTES = 256 << 20         # calibration copy: bytes read (and written) per launch
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_iq3s_persist_17408x5120_m1.traffic.json")
 IQ3_S, Q4_K, Q6_K, IQ4_XS = 21, 12, 14, 23
@@ -50,6 +52,11 @@ BLOCK = {IQ3_S: 110, Q4_K: 144, Q6_K: 210, IQ4_XS: 136}
 SCALE_OFFSETS = {IQ3_S: (0,), Q4_K: (0, 2), Q6_K: (208,), IQ4_XS: (0,)}
 MFMA_I8_PEAK_TOPS = 5000.0     # MI355X dense int8 MFMA
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
+
+
+def rotation_copies(weight_bytes):
+    """Weight copies for a timed graph: NBUF, or more where NBUF copies fit twice in the MALL."""
+    return max(NBUF, -(-ROTATE_BYTES // weight_bytes))
 
 
 def make_weights(torch, qt, rows, k, seed):
@@ -94,9 +101,12 @@ def time_graphs(torch, graphs, reps):
     return s.elapsed_time(e) / reps
 
 
-def op_points(torch, C, iq3_pack, linear, qt, rows, k, ms, ncopies=NBUF, reps=5, seed=0):
+def op_points(torch, C, iq3_pack, linear, qt, rows, k, ms, ncopies=None, reps=5, seed=0):
     """us/call of the routing table's op for a qt weight [rows, k] at each M in ms (bf16 X N(0,1)),
-    over ncopies weight copies captured in one graph per M. IQ3_S in the packed tile layout."""
+    over ncopies weight copies (default: rotation_copies) captured in one graph per M. IQ3_S in the
+    packed tile layout."""
+    if ncopies is None:
+        ncopies = rotation_copies(rows * (k // 256) * BLOCK[qt])
     ws = [make_weights(torch, qt, rows, k, seed + i) for i in range(ncopies)]
     packed = qt == IQ3_S
     if packed:
@@ -126,7 +136,7 @@ def config_mtp(torch, C, iq3_pack, linear):
     out = []
     for qt in (IQ3_S, IQ4_XS, Q6_K):
         for rows, k in ((6144, 5120), (1024, 5120), (5120, 6144)):
-            out += op_points(torch, C, iq3_pack, linear, qt, rows, k, (4, 8, 16, 32, 48), ncopies=8, seed=2000)
+            out += op_points(torch, C, iq3_pack, linear, qt, rows, k, (4, 8, 16, 32, 48), seed=2000)
     return out
 
 
@@ -288,7 +298,8 @@ def copy_calibration(torch):
 def kernel_only(torch, C, iq3_pack, steps):
     """--kernel-only: the dominant kernel (as in the full run) and the calibration copy; prints one
     JSON line with the roofline object."""
-    ws = [iq3_pack.pack(make_weights(torch, IQ3_S, 17408, 5120, i), IQ3_S) for i in range(NBUF)]
+    ws = [iq3_pack.pack(make_weights(torch, IQ3_S, 17408, 5120, i), IQ3_S)
+          for i in range(rotation_copies(17408 * 20 * BLOCK[IQ3_S]))]
     roofline = dominant_kernel(torch, C, ws, steps)
     del ws
     torch.cuda.empty_cache()
@@ -338,7 +349,7 @@ def main():
     weights = {}
     for si, (rows, k) in enumerate(shapes):
         weights[(rows, k)] = [iq3_pack.pack(make_weights(torch, IQ3_S, rows, k, 100 * si + i), IQ3_S)
-                              for i in range(NBUF)]
+                              for i in range(rotation_copies(rows * (k // 256) * BLOCK[IQ3_S]))]
     step_graphs, per_case, step_bytes = [], [], 0
     for rows, k, m in cases:
         x = torch.randn(m, k, device="cuda", dtype=torch.bfloat16)
