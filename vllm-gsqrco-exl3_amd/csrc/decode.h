@@ -117,8 +117,8 @@ __device__ __forceinline__ void decode_iq4xs(const uint8_t* b, int u, int (&w)[8
   const uint32_t q[4] = {(uint32_t)a, (uint32_t)(a >> 32), (uint32_t)c, (uint32_t)(c >> 32)};
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    w[j] = lut16(q[j] & 0x0F0F0F0Fu);
-    w[4 + j] = lut16((q[j] >> 4) & 0x0F0F0F0Fu);
+    w[j] = iq4nl(q[j], 0);
+    w[4 + j] = iq4nl(q[j], 4);
   }
   s.d = half_bits_to_float(ld16(b));
   s.ls = iq4xs_ls(b, u);
@@ -127,8 +127,8 @@ __device__ __forceinline__ void decode_iq4xs(const uint8_t* b, int u, int (&w)[8
 __device__ __forceinline__ void decode_iq4xs_q(const uint8_t* b, int u, int q, int (&w)[2], SliceScale& s) {
   const uint64_t a = ld64(b + 8 + 16 * u + 8 * (q & 1));
   const int sh = 4 * (q >> 1);
-  w[0] = lut16(((uint32_t)a >> sh) & 0x0F0F0F0Fu);
-  w[1] = lut16(((uint32_t)(a >> 32) >> sh) & 0x0F0F0F0Fu);
+  w[0] = iq4nl((uint32_t)a, sh);
+  w[1] = iq4nl((uint32_t)(a >> 32), sh);
   s.d = half_bits_to_float(ld16(b));
   s.ls = iq4xs_ls(b, u);
 }

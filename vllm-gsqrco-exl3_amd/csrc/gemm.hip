@@ -271,8 +271,8 @@ __device__ __forceinline__ long raw_a(const RawFrag<TYPE>& f, int u, int q) {
     return pack_a((f.qs[2 * c] >> sh) & 0x0F0F0F0Fu, (f.qs[2 * c + 1] >> sh) & 0x0F0F0F0Fu);
   } else if constexpr (TYPE == kIQ4_XS) {
     const int sh = 4 * (q >> 1);
-    return pack_a((uint32_t)lut16((f.qs[2 * u] >> sh) & 0x0F0F0F0Fu),
-                  (uint32_t)lut16((f.qs[2 * u + 1] >> sh) & 0x0F0F0F0Fu));
+    return pack_a((uint32_t)iq4nl(f.qs[2 * u], sh),
+                  (uint32_t)iq4nl(f.qs[2 * u + 1], sh));
   } else {
     const int n = u >> 2, sub = u & 3, i = 2 * n + (sub & 1);
     const int lsh = 4 * (sub >> 1), hsh = 2 * sub;

@@ -113,8 +113,8 @@ __device__ __forceinline__ void stage_raw_tile(const uint8_t* blk, bool valid, u
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         const uint2 v = *(const uint2*)(blk + 8 + 16 * u + 8 * (q & 1));
-        w0[u] = (uint32_t)lut16((v.x >> sh) & 0x0F0F0F0Fu);
-        w1[u] = (uint32_t)lut16((v.y >> sh) & 0x0F0F0F0Fu);
+        w0[u] = (uint32_t)iq4nl(v.x, sh);
+        w1[u] = (uint32_t)iq4nl(v.y, sh);
         s1[u] = iq4xs_ls(blk, u);
         s2[u] = 0;
       }

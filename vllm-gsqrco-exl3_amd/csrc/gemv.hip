@@ -507,9 +507,9 @@ __global__ void __launch_bounds__(64 * WPT) gemv_rows_kernel(const uint8_t* __re
         for (int i = 0; i < 2; ++i) {
           int sumi = 0;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) sumi = dot4(lut16(f.qs[i][e] & 0x0F0F0F0Fu), xv[e], sumi);
+          for (int e = 0; e < 4; ++e) sumi = dot4(iq4nl(f.qs[i][e], 0), xv[e], sumi);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) sumi = dot4(lut16((f.qs[i][e] >> 4) & 0x0F0F0F0Fu), xv[4 + e], sumi);
+          for (int e = 0; e < 4; ++e) sumi = dot4(iq4nl(f.qs[i][e], 4), xv[4 + e], sumi);
           const int ls = (int)(((f.hdr[i].y >> (4 * c)) & 0xF) | (((f.hdr[i].x >> (16 + 2 * c)) & 3u) << 4)) - 32;
           acc[i][cc] = fmaf(half_bits_to_float(f.hdr[i].x & 0xFFFF) * (float)(sumi * ls), d8, acc[i][cc]);
         }

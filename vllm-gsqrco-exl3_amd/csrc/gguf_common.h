@@ -141,12 +141,16 @@ __device__ __forceinline__ int apply_signs(uint32_t g, uint32_t s) {
   return (int)((g ^ mask) + one);
 }
 
-// 16-entry signed-byte table lookup for 4 nibble indices (one per byte, values 0..15): two byte
-// permutes over entries 0-7 and 8-15, then a per-byte select on index bit 3.
-__device__ __forceinline__ int lut16(uint32_t idx) {
-  const uint32_t lo = __builtin_amdgcn_perm(kIq4nl[1], kIq4nl[0], idx & 0x07070707u);
-  const uint32_t hi = __builtin_amdgcn_perm(kIq4nl[3], kIq4nl[2], idx & 0x07070707u);
-  const uint32_t sel = ((idx >> 3) & 0x01010101u) * 0xFFu;
+// IQ4_NL codebook values of the 4 nibbles q >> sh (sh = 0: the low nibble of each byte, 4: the
+// high one), one per byte: two byte permutes over entries 0-7 and 8-15, then the per-byte choice
+// on the nibble's bit 3, as a third permute: with that bit moved to bit 7 of its byte (t), the
+// selectors 8-11 of v_perm_b32 replicate the sign bits of bytes 1, 3 of t and of t << 8.
+__device__ __forceinline__ int iq4nl(uint32_t q, int sh) {
+  const uint32_t i = (q >> sh) & 0x07070707u;
+  const uint32_t lo = __builtin_amdgcn_perm(kIq4nl[1], kIq4nl[0], i);
+  const uint32_t hi = __builtin_amdgcn_perm(kIq4nl[3], kIq4nl[2], i);
+  const uint32_t t = q << (4 - sh);
+  const uint32_t sel = __builtin_amdgcn_perm(t << 8, t, 0x090B080Au);  // 0xFF where bit 3 is set
   return (int)((hi & sel) | (lo & ~sel));
 }
 
