@@ -18,7 +18,7 @@ Also reported: the dominant kernel's roofline (the packed decode GEMV kernel at 
 M = 1, which quantises X itself, timed alone), the metric's other points (IQ3_S and Q4_K at
 M = 1, 4, 16, 32, 48 on 17408 x 5120, each through the routing table's op), and the CPU oracle
 (numpy dequantise + torch fp32 matmul) timed on the host cores on a bounded sample; and the other
-BASELINE configs under "configs": the CPU-path Q4_K 4096x4096 case next to its GPU op, the MTP
+benchmark configs under "configs": the CPU-path Q4_K 4096x4096 case next to its GPU op, the MTP
 small GEMM (IQ3_S / IQ4_XS / Q6_K at M = 4..48 on the attention shapes), the prefill GEMM
 (M = 512..8192, with MFMA utilisation) and the 64-layer decoder sweep under one CUDA graph
 with a replay bit-exactness check.
@@ -60,7 +60,7 @@ def rotation_copies(weight_bytes):
 
 
 def make_weights(torch, qt, rows, k, seed):
-    """Uniform random code bytes, every fp16 block scale |N(0, 2e-3)|."""
+    """Uniform random code bytes, every fp16 block scale |N(0, 2e-3)| (benchmark configs)."""
     g = torch.Generator(device="cuda").manual_seed(seed)
     nb = rows * k // 256
     w = torch.randint(0, 256, (nb, BLOCK[qt]), dtype=torch.uint8, device="cuda", generator=g)
@@ -131,7 +131,7 @@ def op_points(torch, C, iq3_pack, linear, qt, rows, k, ms, ncopies=None, reps=5,
 
 
 def config_mtp(torch, C, iq3_pack, linear):
-    """MTP verify small GEMM at M = 4, 8, 16, 32, 48 on q_proj 6144x5120,
+    """benchmark configs[2]: MTP verify small GEMM at M = 4, 8, 16, 32, 48 on q_proj 6144x5120,
     k/v_proj 1024x5120 and o_proj 5120x6144 for IQ3_S (packed), IQ4_XS and Q6_K."""
     out = []
     for qt in (IQ3_S, IQ4_XS, Q6_K):
@@ -141,7 +141,7 @@ def config_mtp(torch, C, iq3_pack, linear):
 
 
 def config_prefill(torch, C, iq3_pack, linear):
-    """prefill GEMM at M = 512, 2048, 8192 over K = 5120, N = 17408 and 5120,
+    """benchmark configs[3]: prefill GEMM at M = 512, 2048, 8192 over K = 5120, N = 17408 and 5120,
     IQ3_S (packed), Q4_K, Q6_K; int8 TOP/s against the dense int8 MFMA peak (X bf16 N(0,1) with 1%
     outliers of magnitude 20 in the reference recipe; plain N(0,1) here, which times the same)."""
     out = []
@@ -159,7 +159,7 @@ def config_prefill(torch, C, iq3_pack, linear):
 
 
 def config_layers(torch, C, iq3_pack, linear, steps, ms=(1, 4, 16, 32), nlayers=64):
-    """a 64-layer synthetic 27B-style decoder's linear layers (hidden 5120,
+    """benchmark configs[4]: a 64-layer synthetic 27B-style decoder's linear layers (hidden 5120,
     intermediate 17408, 48 query / 8 KV heads of dim 128) in the GSQ-RCO mix -- IQ3_S (packed)
     q/k/v/o/gate/up, IQ4_XS down -- plus the Q6_K output head 151936x5120, every call of a step
     captured in one CUDA graph. Per M: ms/step, weight GB streamed per step, and whether two
@@ -204,7 +204,7 @@ def config_layers(torch, C, iq3_pack, linear, steps, ms=(1, 4, 16, 32), nlayers=
 
 
 def config_cpu_q4k(torch, C):
-    """Q4_K 4096x4096 at M = 1, fp32 X N(0,1): the GPU op next to the CPU
+    """benchmark configs[0]: Q4_K 4096x4096 at M = 1, fp32 X N(0,1): the GPU op next to the CPU
     reference path (numpy dequantise + q8_1 round trip + torch fp32 matmul), seed 0."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
@@ -314,9 +314,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-points", action="store_true", help="skip the metric's other (type, M) points")
     ap.add_argument("--no-configs", action="store_true",
-                    help="skip the other BASELINE configs (CPU Q4_K, MTP small GEMM, prefill, 64-layer sweep)")
+                    help="skip the other benchmark configs (CPU Q4_K, MTP small GEMM, prefill, 64-layer sweep)")
     ap.add_argument("--section", choices=["mtp", "prefill", "layers"],
-                    help="run only this BASELINE config and print its JSON (for rocprofv3 counter runs)")
+                    help="run only this benchmark config and print its JSON (for rocprofv3 counter runs)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--kernel-only", action="store_true",
                     help="time only the dominant kernel, then run the counter-calibration copy (for rocprofv3)")
@@ -407,7 +407,7 @@ def main():
         "dtype": "int8",
         "data": "synthetic (uniform random IQ3_S codes, d ~ |N(0,2e-3)|; X bf16 N(0,1))",
         "config": {"workload": "IQ3_S decode GEMV (packed tile layout) at M=1,4 on 17408x5120 and 5120x17408, "
-                               "BASELINE configs[1]; 8 weight copies per shape per step",
+                               "benchmark configs[1]; per shape, weight copies of at least 512 MiB in all",
                    "calls_per_step": sum(n for *_, n, _ in per_case), "bytes_per_step": step_bytes},
         "detail": detail,
         "roofline": roofline,

@@ -377,7 +377,7 @@ def rel_l2(y, ref) -> float:
 def random_blocks(rng: np.random.Generator, qt: int, rows: int, k: int,
                   scale_sigma: float = 2e-3) -> np.ndarray:
     """Seeded synthetic GGUF rows [rows, k/256*bytes]: uniform random code bytes with every fp16
-    scale replaced by |N(0, scale_sigma)| (the BASELINE configs; the reference's recipe is
+    scale replaced by |N(0, scale_sigma)| (the benchmark configs; the reference's recipe is
     kit/synth.py:70-87, uniform bytes with valid fp16 scales)."""
     bs = BLOCK_BYTES[qt]
     nb = rows * (k // QK_K)

@@ -1,7 +1,7 @@
 """Parity of the gfx950 kernels with the CPU oracle, through the C ABI (torch.ops._C_gguf ->
 libgguf_mi355x.so). Needs an MI355X.
 
-Bars (BASELINE north star):
+Bars:
   * q8_1 bytes (both layouts): bit-exact with the oracle;
   * int32 slice dots: bit-exact, checked through the real product kernels in an exact-integer
     mode (block scales d = dmin = 1, X integer-valued with one 127 per slice so every q8_1 scale
@@ -652,7 +652,7 @@ def test_graph_replay_bit_exact(op, qt, n, packed):
 # ------------------------------------------------------------------------------------ full sizes
 @pytest.mark.parametrize("n", [1, 4])
 def test_full_size_iq3s_gate_packed(n):
-    """BASELINE config 2 at its real shape (17408 x 5120), M = 1 and 4, through the packed path."""
+    """The decode benchmark's gate shape at its real size (17408 x 5120), M = 1 and 4, through the packed path."""
     from vllm_gguf_plugin.quantization import iq3_pack
 
     rows, k = 17408, 5120
@@ -664,7 +664,7 @@ def test_full_size_iq3s_gate_packed(n):
 
 
 def test_full_size_q4k_cpu_config():
-    """Q4_K 4096 x 4096, X 1 x 4096 fp32 N(0,1), seed 0."""
+    """The CPU-path benchmark case: Q4_K 4096 x 4096, X 1 x 4096 fp32 N(0,1), seed 0."""
     rows = k = 4096
     raw = _w(o.Q4_K, rows, k, seed=0)
     x = torch.from_numpy(np.random.default_rng(0).standard_normal((1, k)).astype(np.float32))
