@@ -53,6 +53,23 @@ def test_host_helpers(lib):
     assert lib.gguf_iq3_pack_scratch_bytes(65536, 2200) == (64 << 20) // (16 * 2200) * 16 * 2200
 
 
+def test_workspace_follows_the_product_plan(lib):
+    """Product ops size their workspace for the activation layout of the GEMM they run: the int8
+    layout (4,608 B per 16 rows x 256 values) below 64 rows, the fp16 one (9,216 B) for packed
+    IQ3_S and Q4_K from 64 rows at K <= 8192 and for the prefill from 256 rows; IQ4_XS and
+    K = 17408 stay on the int8 layout below the prefill."""
+    xq = lambda n, k: -(-n // 16) * (k // 256) * 4608
+    xh = lambda n, k: -(-n // 16) * (k // 256) * 9216
+    packed, mmq = 7, 1
+    assert lib.gguf_op_workspace_bytes(packed, 21, 17408, 5120, 48, 0) == xq(48, 5120)
+    assert lib.gguf_op_workspace_bytes(packed, 21, 17408, 5120, 64, 0) == xh(64, 5120)
+    assert lib.gguf_op_workspace_bytes(packed, 21, 17408, 5120, 255, 0) == xh(255, 5120)
+    assert lib.gguf_op_workspace_bytes(packed, 21, 17408, 5120, 256, 0) == xh(256, 5120)
+    assert lib.gguf_op_workspace_bytes(packed, 21, 5120, 17408, 64, 0) == xq(64, 17408)
+    assert lib.gguf_op_workspace_bytes(mmq, 12, 17408, 5120, 64, 0) == xh(64, 5120)
+    assert lib.gguf_op_workspace_bytes(mmq, 23, 17408, 5120, 64, 0) == xq(64, 5120)
+
+
 def test_guard_call_does_not_need_a_gpu(lib):
     import torch
 
