@@ -158,15 +158,21 @@ def config_prefill(torch, C, iq3_pack, linear):
     return out
 
 
-def config_layers(torch, C, iq3_pack, linear, steps, ms=(1, 4, 16, 32), nlayers=64):
+def config_layers(torch, C, iq3_pack, linear, steps, ms=(1, 4, 16, 32), nlayers=64, merged=False):
     """benchmark configs[4]: a 64-layer synthetic 27B-style decoder's linear layers (hidden 5120,
     intermediate 17408, 48 query / 8 KV heads of dim 128) in the GSQ-RCO mix -- IQ3_S (packed)
     q/k/v/o/gate/up, IQ4_XS down -- plus the Q6_K output head 151936x5120, every call of a step
     captured in one CUDA graph. Per M: ms/step, weight GB streamed per step, and whether two
-    replays give bit-identical outputs."""
-    shapes = [("q", IQ3_S, 6144, 5120), ("k", IQ3_S, 1024, 5120), ("v", IQ3_S, 1024, 5120),
-              ("o", IQ3_S, 5120, 6144), ("gate", IQ3_S, 17408, 5120), ("up", IQ3_S, 17408, 5120),
-              ("down", IQ4_XS, 5120, 17408)]
+    replays give bit-identical outputs. merged: one product per same-type run of a fused layer,
+    as the reference's glue issues them (linear.py:166-218: the q/k/v shards as one 8192-row
+    weight, gate/up as one 34816-row weight; the same bytes in 4 calls per layer instead of 7)."""
+    if merged:
+        shapes = [("qkv", IQ3_S, 8192, 5120), ("o", IQ3_S, 5120, 6144), ("gate_up", IQ3_S, 34816, 5120),
+                  ("down", IQ4_XS, 5120, 17408)]
+    else:
+        shapes = [("q", IQ3_S, 6144, 5120), ("k", IQ3_S, 1024, 5120), ("v", IQ3_S, 1024, 5120),
+                  ("o", IQ3_S, 5120, 6144), ("gate", IQ3_S, 17408, 5120), ("up", IQ3_S, 17408, 5120),
+                  ("down", IQ4_XS, 5120, 17408)]
     layers = []
     for li in range(nlayers):
         lw = []
@@ -339,7 +345,9 @@ def main():
     if args.section:
         fn = {"mtp": lambda: config_mtp(torch, C, iq3_pack, linear),
               "prefill": lambda: config_prefill(torch, C, iq3_pack, linear),
-              "layers": lambda: config_layers(torch, C, iq3_pack, linear, args.steps)}[args.section]
+              "layers": lambda: {"layer_sweep_64": config_layers(torch, C, iq3_pack, linear, args.steps),
+                                 "layer_sweep_64_runs": config_layers(torch, C, iq3_pack, linear, args.steps,
+                                                                      merged=True)}}[args.section]
         print(json.dumps({"mode": "section", "section": args.section, "result": fn()}), flush=True)
         return
 
@@ -389,7 +397,8 @@ def main():
         configs = {"cpu_q4k_4096": config_cpu_q4k(torch, C),
                    "mtp_small_gemm": config_mtp(torch, C, iq3_pack, linear),
                    "prefill": config_prefill(torch, C, iq3_pack, linear),
-                   "layer_sweep_64": config_layers(torch, C, iq3_pack, linear, args.steps)}
+                   "layer_sweep_64": config_layers(torch, C, iq3_pack, linear, args.steps),
+                   "layer_sweep_64_runs": config_layers(torch, C, iq3_pack, linear, args.steps, merged=True)}
 
     cpu = None if args.no_cpu else cpu_baseline(torch)
 
