@@ -355,21 +355,22 @@ struct RowsFrag<kQ6_K> {
 // (between two barriers) when its waves reach it. Every wave has at least one block in every
 // phase. Without PH (one phase) the staging branch is compiled out: inside the K loop, a branch
 // with loads makes the compiler wait for every load in flight at its join.
-template <int TYPE, int NC, int WPT, bool PH>
+template <int TYPE, int NC, int WPT, bool PH, int RPL>
 __global__ void __launch_bounds__(64 * WPT) gemv_rows_kernel(const uint8_t* __restrict__ W, int64_t row_bytes,
                                                              int nrows, int k, const uint8_t* __restrict__ q8,
                                                              void* __restrict__ y, int y_dtype, int kp_arg) {
   const int kp = PH ? kp_arg : 1;
+  constexpr int TR = 8 * RPL;  // rows per tile: lane 8r + c takes rows r (and 8 + r)
   constexpr int BS = block_bytes(TYPE);
   constexpr int NT = 64 * WPT;
   constexpr int SUMS = TYPE == kQ4_K ? kSumSlice : (TYPE == kQ6_K ? kSumHalves : kSumNone);
-  __shared__ float red[2][WPT][NC][kTileRows];
+  __shared__ float red[2][WPT][NC][TR];
   __shared__ uint4 sink;           // staging writes of groups past the end of X
   extern __shared__ uint4 xdyn[];  // q values [NC][slice][8 dwords], then (d8, sums) [NC][slice]
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane >> 3, c = lane & 7, h = c & 1;
-  const int ntiles = (nrows + kTileRows - 1) / kTileRows;
+  const int ntiles = (nrows + TR - 1) / TR;
   const int nb = k / kQK, nslices = k / kQ81;
   const int nsl = (nb + kp - 1) / kp * 8;  // LDS slices per activation row (the longest phase)
   const int G = gridDim.x;
@@ -380,11 +381,11 @@ __global__ void __launch_bounds__(64 * WPT) gemv_rows_kernel(const uint8_t* __re
   const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(q8, (uint32_t)(NC * nslices * 36));
   auto load = [&](int t, int b, RowsFrag<TYPE>& f) {
     const __amdgpu_buffer_rsrc_t rs = t < ntiles ? wrs : nrs;
-    const int t0 = (t < ntiles ? t : 0) * kTileRows;
+    const int t0 = (t < ntiles ? t : 0) * TR;
     const int bo = b * BS;
-    uint32_t d16[2];
+    uint32_t d16[2] = {0u, 0u};
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < RPL; ++i) {
       const int o = min(t0 + 8 * i + r, nrows - 1) * (int)row_bytes;
       if constexpr (TYPE == kQ4_K) {
         f.hdr[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, o, bo, 0);
@@ -471,7 +472,7 @@ __global__ void __launch_bounds__(64 * WPT) gemv_rows_kernel(const uint8_t* __re
   __syncthreads();
   float acc[2][NC];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < RPL; ++i)
 #pragma unroll
     for (int cc = 0; cc < NC; ++cc) acc[i][cc] = 0.0f;
   // the lane's two (Q4_K, Q6_K) or one (IQ4_XS) slices of block b, for activation row cc
@@ -504,7 +505,7 @@ __global__ void __launch_bounds__(64 * WPT) gemv_rows_kernel(const uint8_t* __re
         const int xv[8] = {(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
         const float d8 = xs[s1].x;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < RPL; ++i) {
           int sumi = 0;
 #pragma unroll
           for (int e = 0; e < 4; ++e) sumi = dot4(iq4nl(f.qs[i][e], 0), xv[e], sumi);
@@ -520,7 +521,7 @@ __global__ void __launch_bounds__(64 * WPT) gemv_rows_kernel(const uint8_t* __re
         const int sf = h == 0 ? s1 : s2;  // the slice this lane finishes
         const float d8 = xs[sf].x;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < RPL; ++i) {
           int a1 = 0, a2 = 0;
           if constexpr (TYPE == kQ4_K) {
 #pragma unroll
@@ -574,7 +575,7 @@ __global__ void __launch_bounds__(64 * WPT) gemv_rows_kernel(const uint8_t* __re
     compute(fc, b - ph0(p));
     if (p == kp - 1 && b == we(kp - 1) - 1) {  // the wave's last block of tile t: reduce and store
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
+      for (int i = 0; i < RPL; ++i) {
 #pragma unroll
         for (int cc = 0; cc < NC; ++cc) {
           float v = acc[i][cc];
@@ -586,9 +587,9 @@ __global__ void __launch_bounds__(64 * WPT) gemv_rows_kernel(const uint8_t* __re
         }
       }
       __syncthreads();
-      if (threadIdx.x < NC * kTileRows) {
-        const int cc = threadIdx.x / kTileRows, rr = threadIdx.x % kTileRows;
-        const int row = t * kTileRows + rr;
+      if (threadIdx.x < NC * TR) {
+        const int cc = threadIdx.x / TR, rr = threadIdx.x % TR;
+        const int row = t * TR + rr;
         float v = red[it & 1][0][cc][rr];
 #pragma unroll
         for (int w2 = 1; w2 < WPT; ++w2) v += red[it & 1][w2][cc][rr];
@@ -639,17 +640,16 @@ bool gemv_rows_supported(int type, int64_t nrows, int64_t row_bytes, int64_t k, 
          nrows * row_bytes < ((int64_t)1 << 31) && kp > 0 && !(type == kQ4_K && n == 4 && kp > 1);
 }
 
-template <int TYPE>
-static bool launch_rows(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n, void* y,
-                        int y_dtype, hipStream_t stream) {
-  if (!gemv_rows_supported(TYPE, nrows, row_bytes, k, n)) return false;
+template <int TYPE, int RPL>
+static void launch_rows_rpl(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n, void* y,
+                            int y_dtype, hipStream_t stream) {
   const int kp = rows_phases(k, n);
-  const int tiles = (nrows + kTileRows - 1) / kTileRows;
+  const int tiles = (nrows + 8 * RPL - 1) / (8 * RPL);
   const unsigned g = (unsigned)std::min(tiles, persist_grid());
   const size_t lds = (size_t)n * ((k / kQK + kp - 1) / kp) * 8 * 40;
 #define GGUF_ROWS(NC)                                                                                            \
-  (kp > 1 ? gemv_rows_kernel<TYPE, NC, 8, true><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype, kp) \
-          : gemv_rows_kernel<TYPE, NC, 8, false><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype, 1))
+  (kp > 1 ? gemv_rows_kernel<TYPE, NC, 8, true, RPL><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype, kp) \
+          : gemv_rows_kernel<TYPE, NC, 8, false, RPL><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype, 1))
   switch (n) {
     case 1: GGUF_ROWS(1); break;
     case 2: GGUF_ROWS(2); break;
@@ -657,6 +657,18 @@ static bool launch_rows(const uint8_t* W, int64_t row_bytes, int nrows, int k, c
     default: GGUF_ROWS(4); break;
   }
 #undef GGUF_ROWS
+}
+
+template <int TYPE>
+static bool launch_rows(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n, void* y,
+                        int y_dtype, hipStream_t stream) {
+  if (!gemv_rows_supported(TYPE, nrows, row_bytes, k, n)) return false;
+  // 8-row tiles (one row per lane): twice the work items, shared out more evenly over the CUs
+  // (measured at M = 1: 5120 x 17408 IQ4_XS 19.8 -> 16.3 us, Q6_K 31.1 -> 25.7; 17408 x 5120
+  // IQ4_XS 18.3 -> 15.5). Over K phases X is staged once per phase and tile, and there IQ4_XS
+  // keeps 16-row tiles (5120 x 17408 M = 4: 33.2 against 36.0 us; Q6_K 41.5 against 43.8).
+  if (rows_phases(k, n) == 1 || TYPE == kQ6_K) launch_rows_rpl<TYPE, 1>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);
+  else launch_rows_rpl<TYPE, 2>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);
   return true;
 }
 
