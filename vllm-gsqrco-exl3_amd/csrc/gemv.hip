@@ -120,30 +120,7 @@ __global__ void __launch_bounds__(256) gemv_raw_kernel(const uint8_t* __restrict
       if (lane == r * NC + c && row0 + r < nrows) store_y(y, (int64_t)c * nrows + row0 + r, acc[r][c], y_dtype);
 }
 
-// Q4_K on GGUF rows, tile style: a 16-row tile at a time, lane (row j = lane & 15, slice pair
-// pc = lane >> 4) of each block loads the row's 16-byte header and the 32 value bytes of its two
-// slices, so a wave's loads cover the tile's 16 blocks; each wave keeps the next two blocks of its
-// stream in flight while it computes one. WPT waves split the K blocks; workgroups are persistent
-// over tiles (two per CU) and first copy the q8_1 of X into LDS with each slice's sum of q (while
-// their first weight blocks load). Per slice the reference vec_dot term (vecdotq.cuh:508-530)
-// times the slice's d8; partial sums over the 4 pair lanes of a row (xor butterfly), then over the
-// waves in wave order. (IQ4_XS and Q6_K use gemv_rows_kernel below.)
-template <int TYPE>
-struct RawTileFrag;
-template <>
-struct RawTileFrag<kQ4_K> {
-  u32x4 hdr;     // d | dmin << 16, scales[0..11]
-  u32x4 lo, hi;  // the pair's 32 nibble bytes
-};
-
-template <int TYPE>
-__device__ __forceinline__ void load_rawtile(__amdgpu_buffer_rsrc_t rs, int o, int bo, int pc, RawTileFrag<TYPE>& f) {
-  f.hdr = __builtin_amdgcn_raw_buffer_load_b128(rs, o, bo, 0);
-  f.lo = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 16 + 32 * pc, bo, 0);
-  f.hi = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 32 + 32 * pc, bo, 0);
-}
-
-// X of the raw tile GEMV, staged in LDS: q8 values [NC][slice][8 dwords], then (d8, sum of q)
+// X of the row-chunk GEMV, staged in LDS: q8 values [NC][slice][8 dwords], then (d8, sum of q)
 // [NC][slice]. Group g = part g & 3 (8 q bytes) of slice row g >> 2 of the block_q8_1 array; the
 // four lanes of a slice are consecutive, so the slice's sum of q is a quad sum (DPP).
 struct XGroupQ8 {
@@ -181,146 +158,12 @@ __device__ __forceinline__ void xgroup_q8_store(const XGroupQ8& r, int g, bool l
   *(live && part == 0 ? xs + sr : (float2*)sink) = make_float2(half_bits_to_float(r.d & 0xFFFF), sum);
 }
 
-template <int TYPE, int NC, int WPT>
-__global__ void __launch_bounds__(64 * WPT) gemv_rawtile_kernel(const uint8_t* __restrict__ W, int64_t row_bytes,
-                                                                int nrows, int k, const uint8_t* __restrict__ q8,
-                                                                void* __restrict__ y, int y_dtype) {
-  static_assert(TYPE == kQ4_K, "the tile kernel serves Q4_K; IQ4_XS and Q6_K use gemv_rows_kernel");
-  constexpr int BS = block_bytes(TYPE);
-  constexpr int NT = 64 * WPT;
-  __shared__ float red[2][WPT][NC][kTileRows];
-  __shared__ uint4 sink;           // staging writes of groups past the end of X
-  extern __shared__ uint4 xdyn[];  // q values [NC][slice][8 dwords], then (d8, sum q) [NC][slice]
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int j = lane & 15, pc = lane >> 4;
-  const int ntiles = (nrows + kTileRows - 1) / kTileRows;
-  const int nb = k / kQK, nslices = k / kQ81;
-  const int b_begin = wave * nb / WPT, b_end = (wave + 1) * nb / WPT;
-  const int nblk = b_end - b_begin;
-  const int G = gridDim.x;
-  uint32_t* xq = (uint32_t*)xdyn;
-  float2* xs = (float2*)(xq + NC * nslices * 8);
-  const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(W, (uint32_t)((int64_t)nrows * row_bytes));
-  const __amdgpu_buffer_rsrc_t nrs = buffer_rsrc(W, 0);
-  const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(q8, (uint32_t)(NC * nslices * 36));
-  auto load = [&](int t, int b, RawTileFrag<TYPE>& f) {
-    const __amdgpu_buffer_rsrc_t rs = t < ntiles ? wrs : nrs;
-    const int o = min((t < ntiles ? t : 0) * kTileRows + j, nrows - 1) * (int)row_bytes;
-    load_rawtile<TYPE>(rs, o, b * BS, pc, f);
-  };
-  // the wave's stream: (tile t, block b) for t = blockIdx.x, blockIdx.x + G, ..., b in [b_begin, b_end)
-  const int items = ((int)blockIdx.x < ntiles ? (ntiles - 1 - (int)blockIdx.x) / G + 1 : 0) * nblk;
-  auto next = [&](int& tt, int& bb) {
-    if (++bb == b_end) {
-      bb = b_begin;
-      tt += G;
-    }
-  };
-  // X's first two groups per thread, then the first two weight blocks; X goes to LDS while the
-  // weights are in flight
-  const int ngroups = NC * nslices * 4;
-  const int ga = threadIdx.x, gb = threadIdx.x + NT;
-  XGroupQ8 xa, xb;
-  xgroup_q8_load(xrs, ga < ngroups ? ga : ngroups - 1, xa);
-  xgroup_q8_load(xrs, gb < ngroups ? gb : ngroups - 1, xb);
-  __builtin_amdgcn_sched_barrier(0);
-  RawTileFrag<TYPE> f0, f1, f2;
-  int lt = blockIdx.x, lb = b_begin;  // next item to load
-  load(lt, lb, f0);
-  next(lt, lb);
-  load(lt, lb, f1);
-  next(lt, lb);
-  __builtin_amdgcn_sched_barrier(0);
-  xgroup_q8_store<kSumSlice>(xa, ga, ga < ngroups, xq, xs, &sink);
-  xgroup_q8_store<kSumSlice>(xb, gb, gb < ngroups, xq, xs, &sink);
-  for (int g = threadIdx.x + 2 * NT; g < ngroups; g += NT) {  // K beyond 2 groups per thread
-    XGroupQ8 xc;
-    xgroup_q8_load(xrs, g, xc);
-    xgroup_q8_store<kSumSlice>(xc, g, true, xq, xs, &sink);
-  }
-  __syncthreads();
-  float acc[NC];
-#pragma unroll
-  for (int c = 0; c < NC; ++c) acc[c] = 0.0f;
-  // slice u = 2pc + h of the lane's row: the dot with X's slice, scaled by everything but d8
-  auto slice_term = [&](const RawTileFrag<TYPE>& f, int h, int c, int sl) -> float {
-    const uint4 x0 = *(const uint4*)(xq + sl * 8), x1 = *(const uint4*)(xq + sl * 8 + 4);
-    const int xv[8] = {(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
-    const int u = 2 * pc + h;
-    int w[8];
-    {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        w[e] = (int)((f.lo[e] >> (4 * h)) & 0x0F0F0F0Fu);
-        w[4 + e] = (int)((f.hi[e] >> (4 * h)) & 0x0F0F0F0Fu);
-      }
-      int sumi = 0;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) sumi = dot4(w[e], xv[e], sumi);
-      const int jj = u & 3;
-      const uint32_t a = (f.hdr[1] >> (8 * jj)) & 0xFF, cb = (f.hdr[2] >> (8 * jj)) & 0xFF;
-      const uint32_t ee = (f.hdr[3] >> (8 * jj)) & 0xFF;
-      const uint32_t sc = u < 4 ? (a & 63) : ((ee & 0xF) | ((a >> 6) << 4));
-      const uint32_t m = u < 4 ? (cb & 63) : ((ee >> 4) | ((cb >> 6) << 4));
-      const float d = half_bits_to_float(f.hdr[0] & 0xFFFF), dmin = half_bits_to_float(f.hdr[0] >> 16);
-      return (d * (float)sc) * (float)sumi - (dmin * (float)m) * xs[sl].y;
-    }
-  };
-  auto compute = [&](const RawTileFrag<TYPE>& f, int b) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const int sl = c * nslices + b * 8 + 2 * pc + h;
-        acc[c] = fmaf(slice_term(f, h, c, sl), xs[sl].x, acc[c]);
-      }
-  };
-  int t = blockIdx.x, b = b_begin, it = 0;  // item being computed
-  // compute fc (item i) while item i + 2 loads into fl
-  auto step = [&](const RawTileFrag<TYPE>& fc, RawTileFrag<TYPE>& fl) {
-    load(lt, lb, fl);
-    next(lt, lb);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(fc, b);
-    if (b == b_end - 1) {  // the wave's last block of tile t: reduce and store the tile
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        float v = acc[c];
-        v += __shfl_xor(v, 16, 64);
-        v += __shfl_xor(v, 32, 64);
-        if (pc == 0) red[it & 1][wave][c][j] = v;
-        acc[c] = 0.0f;
-      }
-      __syncthreads();
-      if (threadIdx.x < NC * kTileRows) {
-        const int c = threadIdx.x / kTileRows, r = threadIdx.x % kTileRows;
-        const int row = t * kTileRows + r;
-        float v = red[it & 1][0][c][r];
-#pragma unroll
-        for (int w2 = 1; w2 < WPT; ++w2) v += red[it & 1][w2][c][r];
-        if (row < nrows) store_y(y, (int64_t)c * nrows + row, v, y_dtype);
-      }
-      ++it;
-    }
-    next(t, b);
-  };
-  int i = 0;
-  for (; i + 3 <= items; i += 3) {
-    step(f0, f2);
-    step(f1, f0);
-    step(f2, f1);
-  }
-  if (i < items) step(f0, f2);
-  if (i + 1 < items) step(f1, f0);
-}
-
 // Q4_K, IQ4_XS and Q6_K on GGUF rows with loads that run along each row: lane L = 8 r + c (r = row
 // in an 8-row group, c = 16-byte chunk of the row's 128 quant bytes) loads quant bytes
 // [16c, 16c + 16) of the block of rows r and 8 + r of the tile, and what its values need of the
 // block header. One load instruction then covers 8 rows' bytes contiguously (128 B per row); a
-// lane per slice pair (gemv_rawtile_kernel) touches two to three times as many cache lines per
-// block, and the L1 tag rate is what bounds that kernel. The chunk's values (ggml-common.h block
+// lane per slice pair of a 16-row tile touches two to three times as many cache lines per block,
+// and the L1 tag rate is what bounds such a layout. The chunk's values (ggml-common.h block
 // layouts; the reference's MMVQ dots, vecdotq.cuh: Q4_K 508-530, IQ4_XS 1357-1380, Q6_K 627-648):
 //   IQ4_XS  slice c (low nibbles values 0..15, high nibbles 16..31).
 //   Q4_K    half h = c & 1 (values 16h..16h+15) of slice 2j (low nibbles) and of slice 2j + 1
@@ -330,8 +173,7 @@ __global__ void __launch_bounds__(64 * WPT) gemv_rawtile_kernel(const uint8_t* _
 //           -32 offset is applied as 32 times X's half-slice sum.
 // For Q4_K and Q6_K, lanes c and c ^ 1 hold the two halves of the same two slices; they exchange
 // the integer sums by DPP and each finishes one slice. Every slice's term is the reference's
-// (and gemv_rawtile_kernel's) arithmetic; partial sums over a row's 8 lanes by DPP, then over the
-// waves in wave order.
+// arithmetic; partial sums over a row's 8 lanes by DPP, then over the waves in wave order.
 template <int TYPE>
 struct RowsFrag;
 template <>
@@ -609,19 +451,6 @@ __global__ void __launch_bounds__(64 * WPT) gemv_rows_kernel(const uint8_t* __re
   if (i + 1 < items) step(f1, f0);
 }
 
-template <int TYPE>
-static bool launch_rawtile(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n, void* y,
-                           int y_dtype, hipStream_t stream) {
-  if (n > 2 || k / kQK < 8 || (int64_t)nrows * row_bytes >= ((int64_t)1 << 31) || n * (k / kQ81) * 40 > 48 * 1024)
-    return false;
-  const int tiles = (nrows + kTileRows - 1) / kTileRows;
-  const unsigned g = (unsigned)std::min(tiles, persist_grid());
-  const size_t lds = (size_t)n * (k / kQ81) * 40;
-  if (n == 1) gemv_rawtile_kernel<TYPE, 1, 8><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype);
-  else gemv_rawtile_kernel<TYPE, 2, 8><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype);
-  return true;
-}
-
 // Q4_K / IQ4_XS / Q6_K at 1-4 rows on weights below 2 GiB: the row-chunk kernel. X's q8_1 takes
 // 40 bytes of LDS per slice and row; kp: the fewest K phases that bring a phase within 48 KB
 // with at least one block per wave and phase (0 if none does).
@@ -698,16 +527,13 @@ static void launch_type(const uint8_t* W, int64_t row_bytes, int nrows, int k, c
 // n in 1..8 activation rows; q8: block_q8_1 of X; y: [n, nrows] in y_dtype.
 hipError_t launch_gemv_raw(int type, const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n,
                            void* y, int y_dtype, hipStream_t stream) {
-  // Q4_K / IQ4_XS / Q6_K at 1-4 rows on weights of at least 8 K blocks (one per wave) below 2 GiB
-  // whose X q8_1 fits in 48 KB of LDS: the tile kernel (Q4_K at 1-2 rows) or the row-chunk kernel
-  // (measured 17408 x 5120 M = 1: IQ4_XS 14.1 us against 14.3, Q6_K 21.0 against 37.2; for Q4_K
-  // the two are level; at 3-4 rows it replaces the generic GEMV and the MMA small GEMM: IQ4_XS
-  // M = 4 18.8 us against 25.6, Q6_K 26.2 against 37.1 + quantise)
+  // Q4_K / IQ4_XS / Q6_K at 1-4 rows on weights of at least 8 K blocks (one per wave) below 2 GiB:
+  // the row-chunk kernel (measured 17408 x 5120 M = 1 against a 16-row tile kernel with a lane per
+  // slice pair: Q4_K 13.8 us against 16.0, and 16.9 against 20.5 on 5120 x 17408; at 3-4 rows it
+  // replaces the generic GEMV and the MMA small GEMM: IQ4_XS M = 4 18.8 us against 25.6, Q6_K
+  // 26.2 against 37.1 + quantise)
   bool done = false;
-  if (type == kQ4_K) {
-    done = launch_rawtile<kQ4_K>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);
-    if (!done) done = launch_rows<kQ4_K>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);  // 3-4 rows
-  }
+  if (type == kQ4_K) done = launch_rows<kQ4_K>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);
   if (type == kIQ4_XS) done = launch_rows<kIQ4_XS>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);
   if (type == kQ6_K) done = launch_rows<kQ6_K>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);
   if (done) return hipGetLastError();
