@@ -296,6 +296,13 @@ def quantize_q8_1_mmq(x, qt: int) -> np.ndarray:
     return out.reshape(-1)
 
 
+def mmq_ds4_sums(q8: np.ndarray, n: int, k: int) -> np.ndarray:
+    """The half2 sum field of DS4 block_q8_1_mmq bytes (Q4_K), widened: float32 [n, K/32]."""
+    blk = np.ascontiguousarray(q8, dtype=np.uint8).reshape(k // 128, n, 144)
+    s = blk[..., :16].copy().view(np.float16).reshape(k // 128, n, 4, 2)[..., 1].astype(np.float32)
+    return np.ascontiguousarray(s.transpose(1, 0, 2).reshape(n, k // 32))
+
+
 def dequant_q8_1_mmq(q8: np.ndarray, n: int, k: int, qt: int) -> tuple[np.ndarray, np.ndarray]:
     """block_q8_1_mmq bytes -> (q int8 [n, K], d float32 [n, K/32]) (d from half for DS4)."""
     blk = np.ascontiguousarray(q8, dtype=np.uint8).reshape(k // 128, n, 144)
@@ -343,17 +350,28 @@ def slice_dots(raw: np.ndarray, qt: int, q: np.ndarray) -> dict:
 def q81_model(raw: np.ndarray, qt: int, x, layout: str = "mmvq") -> np.ndarray:
     """float64 y[n, rows] = dequant(q8_1(x)) @ dequant(W).T (tests/gpu/_refs.py:40-54,83).
     layout 'mmvq': x' = q * half(d) (block_q8_1, lcpp_shim.cu:274-294); 'mmq': x' = q * d
-    with the MMQ layout's rounding and fp32 d (half d for DS4 types, lcpp_shim.cu:298-355)."""
+    with the MMQ layout's rounding and fp32 d (half d for DS4 types, lcpp_shim.cu:298-355).
+    Q4_K's min term follows the layout's vec_dot: with 'mmvq' it is dmin * m * d8 * sum(q8) per
+    slice (vec_dot_q4_K_q8_1_impl_vmmq, vecdotq.cuh:508-530), which is what dequant(q8_1(x)) .
+    dequant(W) gives; with 'mmq' it is dmin * m * half(sum(x)) per slice, the DS4 sum of the
+    block_q8_1_mmq bytes (vec_dot_q4_K_q8_1_impl_mmq, vecdotq.cuh:533-557)."""
     xf = _as_f32(x)
     n, k = xf.shape
     rows = raw.shape[0]
-    W = dequantize(raw.reshape(-1), qt).astype(np.float64).reshape(rows, k)
     if layout == "mmvq":
         q, d, _ = dequant_q8_1(quantize_q8_1(xf), n, k)
     else:
-        q, d = dequant_q8_1_mmq(quantize_q8_1_mmq(xf, qt), n, k, qt)
-    xq = q.astype(np.float64).reshape(n, k // 32, 32) * d.astype(np.float64)[..., None]
-    return xq.reshape(n, k) @ W.T
+        q8 = quantize_q8_1_mmq(xf, qt)
+        q, d = dequant_q8_1_mmq(q8, n, k, qt)
+    xq = (q.astype(np.float64).reshape(n, k // 32, 32) * d.astype(np.float64)[..., None]).reshape(n, k)
+    if qt == Q4_K and layout == "mmq":
+        t = decode_int(raw.reshape(-1), qt)
+        dd = (t["d"][:, None] * t["sc"].astype(np.float32)).astype(np.float64)        # [nb, 8]
+        main = (np.repeat(dd, 32, axis=1) * t["w"].astype(np.float64)).reshape(rows, k)
+        mins = (t["dmin"][:, None] * t["m"].astype(np.float32)).astype(np.float64).reshape(rows, k // 32)
+        return xq @ main.T - mmq_ds4_sums(q8, n, k).astype(np.float64) @ mins.T
+    W = dequantize(raw.reshape(-1), qt).astype(np.float64).reshape(rows, k)
+    return xq @ W.T
 
 
 def full_model(raw: np.ndarray, qt: int, x) -> np.ndarray:

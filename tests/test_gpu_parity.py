@@ -11,6 +11,7 @@ Bars:
     dequant(W) @ dequant(q8_1(X)) in float64; 16-bit X/Y: within the reference's tight bars
     (5e-3 bf16, 2.5e-3 fp16, tests/gpu/test_kernel_parity.py:40) since Y is rounded to X's dtype;
   * bit-identical outputs across hipGraph replays.
+Every op call first poisons torch's caching allocator (tests/_gpu.py).
 """
 
 import glob
@@ -23,6 +24,13 @@ from conftest import GOLDEN
 
 import _tile
 import gguf_oracle as o
+from _gpu import TIGHT, C
+from _gpu import dev as _dev
+from _gpu import exact_ref as _exact_ref
+from _gpu import exact_weights as _exact_weights
+from _gpu import exact_x as _exact_x
+from _gpu import w_rand as _w
+from _gpu import x_rand as _x
 
 pytestmark = pytest.mark.gpu
 
@@ -32,7 +40,6 @@ VEC_OP = {o.IQ3_S: "lcpp_mul_mat_vec_iq3", o.Q4_K: "lcpp_mul_mat_vec_own", o.IQ4
           o.Q6_K: "lcpp_mul_mat_vec_q"}
 GEMM_OP = {o.IQ3_S: "lcpp_mul_mat_q", o.Q4_K: "lcpp_mul_mat_mma_k", o.IQ4_XS: "lcpp_mul_mat_mma_k",
            o.Q6_K: "lcpp_mul_mat_q"}
-TIGHT = {torch.float32: 1e-3, torch.bfloat16: 5e-3, torch.float16: 2.5e-3}
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -41,61 +48,6 @@ def _ops():
     from vllm_gguf_plugin import ops  # noqa: F401  registers torch.ops._C_gguf (fails if not built)
 
     return torch.ops._C_gguf
-
-
-def C():
-    return torch.ops._C_gguf
-
-
-def _x(n, k, seed, dtype=torch.float32):
-    g = torch.Generator().manual_seed(seed)
-    x = torch.randn(n, k, generator=g)
-    x[:, torch.randperm(k, generator=g)[: max(1, k // 256)]] *= 20
-    return x.to(dtype)
-
-
-def _w(qt, rows, k, seed):
-    return o.random_blocks(np.random.default_rng(seed), qt, rows, k)
-
-
-def _dev(a):
-    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
-
-
-def _exact_weights(qt, rows, k, seed):
-    """Random codes with every block scale 1.0 (Q6_K sub-scales kept within +-31)."""
-    w = _w(qt, rows, k, seed)
-    b = w.reshape(-1, o.BLOCK_BYTES[qt])
-    one = np.array([0x00, 0x3C], dtype=np.uint8)  # fp16 1.0
-    if qt == o.Q6_K:
-        b[:, 208:210] = one
-        sc = np.random.default_rng(seed + 1).integers(-31, 32, size=(b.shape[0], 16)).astype(np.int8)
-        b[:, 192:208] = sc.view(np.uint8)
-    else:
-        b[:, 0:2] = one
-        if qt == o.Q4_K:
-            b[:, 2:4] = one
-    return w
-
-
-def _exact_x(n, k, seed, dtype=torch.bfloat16):
-    """Integers in [-2, 2] with one +-127 per 32-slice: every q8_1 scale is exactly 1."""
-    rng = np.random.default_rng(seed)
-    x = rng.integers(-2, 3, size=(n, k)).astype(np.float32)
-    pos = rng.integers(0, 32, size=(n, k // 32)) + 32 * np.arange(k // 32)
-    x[np.arange(n)[:, None], pos] = 127 * rng.choice([-1.0, 1.0], size=(n, k // 32))
-    return torch.from_numpy(x).to(dtype)
-
-
-def _exact_ref(raw, qt, x):
-    q, d, _ = o.dequant_q8_1(o.quantize_q8_1(x), x.shape[0], x.shape[1])
-    assert (d == 1).all()
-    dots = o.slice_dots(raw, qt, q)
-    y = dots["dot"].sum(-1)
-    if qt == o.Q4_K:
-        y = y - dots["m"].sum(-1)
-    assert np.abs(y).max() < 2 ** 24
-    return y
 
 
 # ------------------------------------------------------------------------------------ q8_1
@@ -541,14 +493,21 @@ def test_rows_gemv_k_phases(qt, n, k):
         assert torch.equal(out, eager)
 
 
-@pytest.mark.parametrize("n,dtype", [(1, torch.bfloat16), (1, torch.float16), (1, torch.float32),
-                                     (2, torch.bfloat16), (2, torch.float32)])
-@pytest.mark.parametrize("rows,k", [(16 * 700, 2048), (6144, 5120), (5120, 17408)])
-def test_fused_quantisation_large_weights(rows, k, n, dtype):
-    """Without x_q8, the packed decode op quantises X itself on large weights (and at two rows):
-    all of X into LDS first. It must give the bits of the q8_1 quantiser followed by the GEMV."""
+@pytest.mark.parametrize("rows,k,n,dtype", [
+    (16 * 700, 2048, 1, torch.bfloat16), (16 * 700, 2048, 1, torch.float16), (16 * 700, 2048, 1, torch.float32),
+    (16 * 700, 2048, 2, torch.bfloat16), (16 * 700, 2048, 2, torch.float32),
+    (17408, 5120, 1, torch.bfloat16), (17408, 5120, 2, torch.bfloat16),
+    (6144, 5120, 1, torch.bfloat16), (6144, 5120, 1, torch.float16), (6144, 5120, 1, torch.float32)])
+def test_fused_quantisation_large_weights(lib, rows, k, n, dtype):
+    """Without x_q8, the packed decode op quantises X itself: all of X into LDS first on weights
+    with more 16-row tiles than the persistent grid (11200 and 17408 rows, one or two activation
+    rows), block by block at one row on weights of up to 32M values (6144 x 5120). It must give
+    the bits of the q8_1 quantiser followed by the GEMV. That these shapes take the fused path
+    is asserted from the op's workspace size (none: no q8_1 copy of X)."""
     from vllm_gguf_plugin.quantization import iq3_pack
 
+    assert lib.gguf_op_workspace_bytes(6, o.IQ3_S, rows, k, n, 0) == 0  # the fused GEMV
+    assert lib.gguf_op_workspace_bytes(6, o.IQ3_S, rows, k, n, 1) == 0
     w = iq3_pack.pack(_dev(_w(o.IQ3_S, rows, k, seed=180 + n)), o.IQ3_S)
     x = _x(n, k, seed=181 + n, dtype=dtype).cuda()
     x[:, 96:128] = 0  # an all-zero slice (d = 0, q = 0)

@@ -225,6 +225,84 @@ def test_q8_1_mmq_layout_and_rounding():
     assert (qa2 != qb2).any() and np.abs(qa2.astype(int) - qb2.astype(int)).max() == 1
 
 
+
+def _ds4_absorbing_slices(nslices, seed):
+    """Slices whose DS4 sum depends on the summation order: value 0 is 2^26 and value 16 is
+    -2^26; values 1-3 are 1, 2, 3 and values 17-19 are -1 (each below half an fp32 ulp of the
+    +-2^26 they meet, 8, so added to it first they vanish); the other 24 values are small
+    integers (exact in any order)."""
+    rng = np.random.default_rng(seed)
+    x = rng.integers(-9, 10, size=(nslices, 32)).astype(np.float32)
+    x[:, 0], x[:, 16] = 2.0 ** 26, -(2.0 ** 26)
+    x[:, 1:4] = [1.0, 2.0, 3.0]
+    x[:, 17:20] = -1.0
+    return x
+
+
+def test_q8_1_mmq_ds4_sum_pinned():
+    """The DS4 sum field (lcpp_shim.cu:320-326): the sum of the 32 raw x values, lane sums
+    ((x0 + x1) + x2) + x3 over 8 lanes of 4, then an xor butterfly with offsets 4, 2, 1, as
+    half. Pinned by (a) integer inputs, where every order is exact, against the exact sum (a sum
+    of q, or of q * d, fails); (b) absorbing inputs, where the 4-value lanes 0 and 4 each reduce
+    to +-2^26 before they meet, so exactly the other six lanes survive: the 32-lane butterfly of
+    the block_q8_1 quantiser (x0 + x16 first, then the rest exactly) keeps the 1 + 2 + 3 - 3 of
+    lanes 0 and 4, and a serial sum drops other values, so both fail."""
+    # (a) exact
+    rng = np.random.default_rng(21)
+    xi = rng.integers(-20, 21, size=(3, 1024)).astype(np.float32)
+    s = o.mmq_ds4_sums(o.quantize_q8_1_mmq(xi, o.Q4_K), 3, 1024)
+    np.testing.assert_array_equal(s, xi.reshape(3, -1, 32).sum(-1))
+    q, d = o.dequant_q8_1_mmq(o.quantize_q8_1_mmq(xi, o.Q4_K), 3, 1024, o.Q4_K)
+    qsum = q.astype(np.float64).reshape(3, -1, 32).sum(-1)
+    assert (qsum != s).mean() > 0.9 and (np.abs(qsum * d - s) > 0.01).mean() > 0.5
+    # (b) order
+    xa = _ds4_absorbing_slices(16, seed=22)
+    s = o.mmq_ds4_sums(o.quantize_q8_1_mmq(xa.reshape(1, -1), o.Q4_K), 1, 512)[0]
+    lanes = xa.reshape(16, 8, 4)
+    want = lanes[:, [1, 2, 3, 5, 6, 7]].sum((1, 2))
+    np.testing.assert_array_equal(s, want)
+    np.testing.assert_array_equal(xa.astype(np.float64).sum(-1) - want, 3.0)  # the exact sum
+    bf32 = xa.copy()                                  # block_q8_1's 32-lane order
+    for off in (16, 8, 4, 2, 1):
+        bf32 = (bf32 + bf32[:, np.arange(32) ^ off]).astype(np.float32)
+    np.testing.assert_array_equal(bf32[:, 0] - want, 3.0)
+    serial = xa[:, 0].copy()
+    for i in range(1, 32):
+        serial = (serial + xa[:, i]).astype(np.float32)
+    assert (serial != want).any()
+
+
+def _residual_heavy_x(n, k, seed):
+    """Per 32-value slice one value of magnitude a and 31 of magnitude 0.49 * a / 127, all of one
+    sign: every small value rounds to q = 0, so sum(x) exceeds d * sum(q) by about 15 d."""
+    rng = np.random.default_rng(seed)
+    a = np.exp2(rng.uniform(-2, 2, (n, k // 32, 1))).astype(np.float32)
+    sign = rng.choice([-1.0, 1.0], size=(n, k // 32, 1)).astype(np.float32)
+    x = np.broadcast_to(a * np.float32(0.49 / 127), (n, k // 32, 32)).copy()
+    x[..., rng.integers(0, 32)] = a[..., 0]
+    return (x * sign).reshape(n, k).astype(np.float32)
+
+
+def test_q81_model_q4k_min_term_forms():
+    """Q4_K's two min-term forms: equal (and equal to the full model) where q * d8 == x exactly;
+    apart on residual-heavy inputs, where the 'mmq' form's min term is dmin * m * half(sum x)
+    and the 'mmvq' form's dmin * m * d8 * sum(q) (vecdotq.cuh:533-557 against :508-530)."""
+    rng = np.random.default_rng(23)
+    raw = o.random_blocks(rng, o.Q4_K, 24, 1024)
+    xi = rng.integers(-2, 3, size=(3, 1024)).astype(np.float32)
+    xi.reshape(3, -1, 32)[..., 5] = 127.0                  # d8 = 1 in both layouts
+    a, b, f = (o.q81_model(raw, o.Q4_K, xi, "mmq"), o.q81_model(raw, o.Q4_K, xi, "mmvq"),
+               o.full_model(raw, o.Q4_K, xi))
+    # equal up to the fp32 rounding of gguf-py's dequantised weight (d*sc*q - dmin*m)
+    np.testing.assert_allclose(a, f, rtol=1e-8)
+    np.testing.assert_allclose(b, f, rtol=1e-8)
+    xr = _residual_heavy_x(3, 1024, seed=24)
+    a, b = o.q81_model(raw, o.Q4_K, xr, "mmq"), o.q81_model(raw, o.Q4_K, xr, "mmvq")
+    assert o.rel_l2(a, b) > 1e-2                      # ten times the kernels' 1e-3 bar
+    # the 'mmq' form keeps the exact slice sums (up to half rounding): it is closer to x . W
+    f = o.full_model(raw, o.Q4_K, xr)
+    assert o.rel_l2(a, f) < o.rel_l2(b, f)
+
 # ------------------------------------------------------------------------------------ dots
 def _brute_dots(raw, qt, q):
     """Pure-Python loops over a tiny case: decode every value from the block bytes directly

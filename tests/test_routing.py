@@ -1,124 +1,96 @@
-"""The Route L op choice per (activation rows n, type, weight rows[, K]) at every boundary of the
-reference's routing table (golden cases of tests/cpu/test_lcpp_routing.py:14-67), and the shared
-q8_1 quantisation decision of apply() (:70-127), on this build's linear.py."""
+"""The routing decisions of the linear method, driven by the case table
+tests/golden/routing_cases.json (the reference's routing cases, cited in the file):
+  * op_cases: the Route L op name _lcpp_op gives per (type, activation rows, weight rows, K,
+    packed), at every boundary of the table;
+  * shared_q8_1_cases: which run's type apply()'s single q8_1 quantisation of X is made for, or
+    none when every run's op quantises X itself.
+Plus the rules around them: the empty product, an unserved type, and the fp32-dst chunk size.
+"""
+
+import json
+import os
 
 import pytest
 import torch
+from conftest import GOLDEN
 
 from vllm_gguf_plugin.quantization import linear
-from vllm_gguf_plugin.quantization.utils import WeightType as T
+from vllm_gguf_plugin.quantization.utils import WeightType
 
-IQ3, MMA, OWN = "lcpp_mul_mat_vec_iq3", "lcpp_mul_mat_vec_iq3_mma", "lcpp_mul_mat_vec_own"
-MMVQ, MMQ, MMA_K = "lcpp_mul_mat_vec_q", "lcpp_mul_mat_q", "lcpp_mul_mat_mma_k"
-PACKED_VEC, PACKED_TILED = "lcpp_mul_mat_vec_iq3_mma_packed", "lcpp_mul_mat_iq3_packed"
-BIG = 17408
-K = 5120
-
-CASES = [
-    *[(t, n, rows, want) for t in (T.IQ3_S, T.IQ3_XXS) for rows in (1024, BIG)
-      for n, want in ((1, IQ3), (5, IQ3), (6, MMA), (8, MMA), (9, MMQ))],
-    (T.Q4_K, 1, BIG, MMVQ), (T.Q4_K, 2, BIG, MMVQ), (T.Q4_K, 3, BIG, OWN), (T.Q4_K, 8, BIG, OWN),
-    (T.Q4_K, 9, BIG, MMA_K), (T.Q4_K, 32, BIG, MMA_K), (T.Q4_K, 33, BIG, MMQ),
-    (T.Q4_K, 3, 2049, OWN), (T.Q4_K, 9, 2049, MMA_K),
-    (T.IQ2_S, 1, BIG, OWN), (T.IQ2_S, 8, BIG, OWN), (T.IQ2_S, 9, BIG, MMA_K), (T.IQ2_S, 32, BIG, MMA_K),
-    (T.IQ2_S, 33, BIG, MMQ), (T.IQ2_S, 1, 2049, OWN), (T.IQ2_S, 32, 2049, MMA_K),
-    (T.IQ4_XS, 7, BIG, MMVQ), (T.IQ4_XS, 8, BIG, MMQ), (T.IQ4_XS, 9, 2049, MMA_K),
-    (T.IQ4_XS, 16, 2049, MMA_K), (T.IQ4_XS, 17, 2049, MMQ), (T.IQ4_XS, 17, BIG, MMA_K),
-    (T.IQ4_XS, 32, BIG, MMA_K), (T.IQ4_XS, 33, BIG, MMQ),
-    (T.IQ4_XS, 17, 12288, MMA_K), (T.IQ4_XS, 17, 12032, MMQ), (T.IQ4_XS, 17, (6144, 2 * K), MMA_K),
-    (T.Q4_K, 4, 2048, MMVQ), (T.Q4_K, 8, 2048, MMQ), (T.IQ2_S, 1, 2048, MMVQ), (T.IQ2_S, 8, 2048, MMQ),
-    (T.Q4_K, 9, 2048, MMQ), (T.IQ2_S, 32, 2048, MMQ), (T.IQ4_XS, 9, 2048, MMQ),
-    *[(t, n, BIG, want) for t in (T.Q2_K, T.Q6_K, T.IQ2_XXS, T.IQ2_XS)
-      for n, want in ((1, MMVQ), (7, MMVQ), (8, MMQ), (9, MMQ), (32, MMQ))],
-    *[(T.IQ1_M, n, rows, want) for rows in (1024, BIG)
-      for n, want in ((1, MMVQ), (8, MMVQ), (9, MMVQ), (32, MMVQ), (33, None))],
-]
+with open(os.path.join(GOLDEN, "routing_cases.json")) as _f:
+    _DOC = json.load(_f)
+OP_CASES = _DOC["op_cases"]
+SHARED = _DOC["shared_q8_1_cases"]
 
 
-@pytest.mark.parametrize("qt,n,rows,want", CASES, ids=lambda v: getattr(v, "name", str(v)))
-def test_lcpp_op(qt, n, rows, want):
-    rows, k = rows if isinstance(rows, tuple) else (rows, K)
-    assert linear._lcpp_op(n, int(qt), rows, k) == want
-    assert linear._lcpp_op(n, int(qt), rows, k, False) == want
+def _tid(c):
+    return f"{c['type']}-n{c['n']}-r{c['rows']}-k{c['k']}{'-packed' if c['packed'] else ''}"
 
 
-PACKED_CASES = [
-    *[(t, n, rows, want) for t in (T.IQ3_S, T.IQ3_XXS) for rows in (1024, BIG)
-      for n, want in ((1, PACKED_VEC), (5, PACKED_VEC), (6, PACKED_VEC), (8, PACKED_VEC),
-                      (9, PACKED_TILED), (32, PACKED_TILED), (128, PACKED_TILED), (2048, PACKED_TILED))],
-    (T.Q4_K, 3, BIG, OWN), (T.Q4_K, 9, BIG, MMA_K), (T.IQ4_XS, 8, BIG, MMQ), (T.IQ1_M, 9, BIG, MMVQ),
-]
+@pytest.mark.parametrize("case", OP_CASES, ids=_tid)
+def test_op_case(case):
+    t = int(WeightType[case["type"]])
+    got = linear._lcpp_op(case["n"], t, case["rows"], case["k"], case["packed"])
+    assert got == case["op"]
+    if not case["packed"]:  # the default argument is the unpacked table
+        assert linear._lcpp_op(case["n"], t, case["rows"], case["k"]) == got
 
 
-@pytest.mark.parametrize("qt,n,rows,want", PACKED_CASES, ids=lambda v: getattr(v, "name", str(v)))
-def test_lcpp_op_packed(qt, n, rows, want):
-    assert linear._lcpp_op(n, int(qt), rows, K, True) == want
+def test_op_table_size_and_reach():
+    """84 unpacked and 36 packed cases, and every op name of the table appears in them."""
+    packed = [c for c in OP_CASES if c["packed"]]
+    assert (len(OP_CASES) - len(packed), len(packed)) == (84, 36)
+    assert {c["op"] for c in OP_CASES} == {
+        "lcpp_mul_mat_vec_q", "lcpp_mul_mat_q", "lcpp_mul_mat_vec_iq3", "lcpp_mul_mat_vec_iq3_mma",
+        "lcpp_mul_mat_vec_own", "lcpp_mul_mat_mma_k", "lcpp_mul_mat_vec_iq3_mma_packed", "lcpp_mul_mat_iq3_packed",
+        None}
 
 
-def test_case_count():
-    # the reference's 84 unpacked and 36 packed (type, n, rows) cases, all kept
-    assert (len(CASES), len(PACKED_CASES)) == (84, 36)
+@pytest.mark.parametrize("case", SHARED, ids=lambda c: f"n{c['n']}-{'+'.join(c['types'])}-{c['packed']}")
+def test_shared_q8_1_type(case):
+    from vllm_gguf_plugin import ops
+
+    types = [int(WeightType[t]) for t in case["types"]]
+    unserved = [t for t in case["types"] if int(WeightType[t]) not in ops.LCPP_QUANT_TYPES]
+    if unserved:
+        pytest.skip(f"{unserved} not served by this build's kernels")
+    want = case["quantize_as"]
+    got = linear._q8_1_type(case["n"], 512, types, case["rows"], case["packed"])
+    assert got == (None if want is None else int(WeightType[want]))
 
 
-class _Quantizer:
-    """Stands in for torch.ops._C_gguf: records which type the shared quantize runs with."""
-
-    def __init__(self):
-        self.calls = []
-
-    def lcpp_quantize_q8_1(self, x, qt, mmq, vendored):
-        self.calls.append((qt, mmq, vendored))
-        return "filled"
+def test_unquantized_shared_buffer_has_q8_1_size():
+    """When no run's op reads q8_1, _quantize_x_q8_1 returns an unfilled buffer of the q8_1 size
+    (n * K / 32 blocks of 36 bytes) and launches nothing (host x: no kernel can run)."""
+    for n, types, rows in ((9, ["IQ3_S", "Q4_K"], [17408, 17408]), (0, ["IQ3_S"], [17408])):
+        x = torch.zeros(n, 1024, dtype=torch.bfloat16)
+        out = linear._quantize_x_q8_1(x, [int(WeightType[t]) for t in types], rows)
+        assert out.dtype == torch.uint8 and out.shape == (n * 1024 // 32 * 36,)
 
 
-# The reference's cases (tests/cpu/test_lcpp_routing.py:81-92), restricted to runs of the types
-# this build serves (Route L here serves Q4_K, Q6_K, IQ3_S and IQ4_XS): runs of IQ2_XS / IQ1_M
-# route to no op in this build, so they never ask for the shared q8_1.
-@pytest.mark.parametrize("n,types,rows,want", [
-    (4, [T.Q4_K, T.IQ4_XS], [2048, BIG], T.Q4_K),      # first run that reads q8_1
-    (8, [T.Q4_K], [BIG], T.Q4_K),                      # the Q4_K decode op reads it at 8 rows
-    (8, [T.Q4_K], [2048], None),                       # MMQ quantizes for itself
-    (8, [T.IQ4_XS, T.Q4_K], [BIG, BIG], T.Q4_K),       # MMQ beside the Q4_K decode op
-    (8, [T.Q4_K, T.IQ3_S], [2048, BIG], T.IQ3_S),      # MMQ beside the IQ3 decode op
-    (9, [T.IQ3_S, T.Q4_K], [BIG, BIG], None),          # MMQ and mma_k quantize for themselves
-    (4, [T.Q6_K], [BIG], T.Q6_K),                      # Q6_K on the decode op
-    (0, [T.IQ3_S], [BIG], None),                       # no rows: nothing to quantize
-    (4, [T.IQ2_XS, T.Q4_K], [BIG, BIG], T.Q4_K),       # a type with no op here is skipped
-], ids=lambda v: str(v) if not isinstance(v, list) else "+".join(getattr(t, "name", str(t)) for t in v))
-def test_quantize_x_q8_1_fills(monkeypatch, n, types, rows, want, packed=False):
-    q = _Quantizer()
-    monkeypatch.setattr(torch.ops, "_C_gguf", q, raising=False)
-    x = torch.zeros(n, 512, dtype=torch.bfloat16)
-    out = linear._quantize_x_q8_1(x, [int(t) for t in types], rows, packed)
-    if want is None:
-        assert q.calls == [] and out.dtype == torch.uint8 and out.numel() == n * 512 // 32 * 36
-    else:
-        assert q.calls == [(int(want), False, False)] and out == "filled"
+def test_empty_product_launches_nothing():
+    """No activation rows: an empty [0, weight rows] result in X's dtype before any routing (host
+    tensors, so any launch would fail)."""
+    w = torch.zeros(17408, 2 * 110, dtype=torch.uint8)
+    for packed in (False, True):
+        y = linear._fused_mul_mat_gguf(torch.zeros(0, 512, dtype=torch.float16), w, int(WeightType.IQ3_S), None,
+                                       packed)
+        assert y.shape == (0, 17408) and y.dtype == torch.float16
 
 
-@pytest.mark.parametrize("n,types,rows,want", [
-    (4, [T.IQ3_S, T.Q4_K], [BIG, BIG], T.IQ3_S),       # the packed decode op reads it
-    (9, [T.IQ3_S, T.Q4_K], [BIG, BIG], None),          # tiled + mma_k
-], ids=lambda v: str(v) if not isinstance(v, list) else "+".join(getattr(t, "name", str(t)) for t in v))
-def test_quantize_x_q8_1_fills_packed(monkeypatch, n, types, rows, want):
-    test_quantize_x_q8_1_fills(monkeypatch, n, types, rows, want, packed=True)
+def test_unserved_type_is_refused():
+    """A quantized type this build has no kernel for raises NotImplementedError naming it."""
+    x = torch.zeros(2, 512, dtype=torch.bfloat16)
+    with pytest.raises(NotImplementedError, match="IQ1_S"):
+        linear._fused_mul_mat_gguf(x, torch.zeros(64, 2 * 50, dtype=torch.uint8), int(WeightType.IQ1_S))
 
 
-def test_fused_mul_mat_gguf_zero_rows():
-    """0 activation rows return an empty [0, rows] result before any routing or launch."""
-    y = linear._fused_mul_mat_gguf(torch.zeros(0, 512, dtype=torch.bfloat16),
-                                   torch.zeros(BIG, 512 // 256 * 110, dtype=torch.uint8), int(T.IQ3_S))
-    assert y.shape == (0, BIG) and y.dtype == torch.bfloat16
-
-
-def test_unserved_type_raises():
-    with pytest.raises(NotImplementedError):
-        linear._fused_mul_mat_gguf(torch.zeros(2, 512, dtype=torch.bfloat16),
-                                   torch.zeros(64, 512 // 256 * 82, dtype=torch.uint8), int(T.IQ2_S))
-
-
-def test_chunk_rule_matches_reference_budget():
-    """Products whose fp32 dst would pass 256 MiB run in 128-row multiples (linear.py:117-130)."""
+def test_fp32_dst_chunk_rows():
+    """A product whose fp32 dst would pass _FP32_DST_BUDGET (256 MiB) runs in activation-row chunks
+    of the largest multiple of 128 that fits (reference linear.py:117-130): 384 for a 151936-row
+    vocab head, and whole below 442 rows."""
     rows = 151936
-    step = max(1, linear._FP32_DST_BUDGET // (rows * 4))
-    assert step == 441 and step - step % 128 == 384
+    assert linear._FP32_DST_BUDGET == 256 << 20
+    fits = linear._FP32_DST_BUDGET // (rows * 4)
+    assert fits == 441 and fits - fits % 128 == 384
+    assert 441 * rows * 4 <= linear._FP32_DST_BUDGET < 442 * rows * 4

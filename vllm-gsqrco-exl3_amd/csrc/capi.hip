@@ -30,7 +30,7 @@ hipError_t launch_quantize_xq(const void* x, int dtype, int64_t n, int64_t k, in
                               void* y, hipStream_t stream);
 hipError_t launch_q8_1_to_xq(const void* q8, int64_t n, int64_t k, int type, void* y, hipStream_t stream);
 hipError_t launch_gemm_xq(int type, const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n,
-                          void* y, int y_dtype, hipStream_t stream);
+                          void* y, int y_dtype, bool mmq, hipStream_t stream);
 hipError_t launch_gemv_packed_x(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x, int x_dtype,
                                 int64_t s01, int n, void* y, int y_dtype, hipStream_t stream);
 bool gemv_rows_supported(int type, int64_t nrows, int64_t row_bytes, int64_t k, int64_t n);
@@ -317,7 +317,7 @@ int gguf_mul_mat(int op, const gguf_view* W, const gguf_view* X, int64_t type, i
       e = gguf::launch_gemm_packed_xq(w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace, (int)n, y, ydt, s);
     else
       e = gguf::launch_gemm_xq((int)type, w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace, (int)n, y, ydt,
-                               s);
+                               gemm, s);
     if (e != hipSuccess) return hip_fail(e, name, "gemm");
     return GGUF_OK;
   }

@@ -201,7 +201,8 @@ hipError_t launch_gemm(int type, const uint8_t* W, int64_t row_bytes, int nrows,
 //    (Q6_K: two, one per 16-value sub-scale, combined in int32 as the reference does);
 //  * per slice the dot is scaled by the integer sub-scale and the fp32 activation scale, summed
 //    over the block, then multiplied by the row's block scale (Q4_K: minus dmin times the
-//    min-term sum of m * d8 * sum(q8), with d8 in fp16 as the reference's half2 MMQ layout);
+//    min-term sum over slices of m times the activation side: d8 * sum(q8) for the decode ops'
+//    MMVQ arithmetic, the fp16 sum of x for the product ops' MMQ arithmetic, SX);
 //  * next block's loads are issued before the current block is computed (two register sets);
 //    the waves' partial sums are added in wave order.
 namespace {
@@ -319,7 +320,7 @@ __device__ __forceinline__ void load_xraw(__amdgpu_buffer_rsrc_t rs, const int (
   }
 }
 
-template <int TYPE, int NT>
+template <int TYPE, int NT, bool SX>
 __device__ __forceinline__ void raw_block(const RawFrag<TYPE>& f, const XRawFrag<NT>& x, int q, float (&acc)[NT][4]) {
   float accb[NT][4], accm[NT][4];
 #pragma unroll
@@ -349,7 +350,7 @@ __device__ __forceinline__ void raw_block(const RawFrag<TYPE>& f, const XRawFrag
     for (int t = 0; t < NT; ++t) {
       const long b = xq_b_operand(x.b[t][u >> 1], u & 1);
       const uint32_t sw = x.d[t][u >> 2][u & 3];
-      // Q4_K: fp16 d | int16 sum(q) << 16; other types: fp32 d
+      // Q4_K: fp16 d | (SX ? fp16 sum(x) : int16 sum(q)) << 16; other types: fp32 d
       const float cd = TYPE == kQ4_K ? half_bits_to_float(sw & 0xFFFF) : __uint_as_float(sw);
       if constexpr (TYPE == kQ6_K) {
         const v4i c0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(q < 2 ? a : 0, b, zero, 0, 0, 0);
@@ -362,7 +363,7 @@ __device__ __forceinline__ void raw_block(const RawFrag<TYPE>& f, const XRawFrag
 #pragma unroll
         for (int v = 0; v < 4; ++v) accb[t][v] = fmaf((float)__mul24(c[v], s1[v]), cd, accb[t][v]);
         if constexpr (TYPE == kQ4_K) {
-          const float cs = cd * (float)(int)(int16_t)(sw >> 16);
+          const float cs = SX ? half_bits_to_float(sw >> 16) : cd * (float)(int)(int16_t)(sw >> 16);
 #pragma unroll
           for (int v = 0; v < 4; ++v) accm[t][v] = fmaf((float)s2[v], cs, accm[t][v]);
         }
@@ -388,7 +389,7 @@ __device__ __forceinline__ void raw_block(const RawFrag<TYPE>& f, const XRawFrag
   }
 }
 
-template <int TYPE, int NT, int KS>
+template <int TYPE, int NT, int KS, bool SX>
 __global__ void __launch_bounds__(64 * KS) gemm_raw_kernel(const uint8_t* __restrict__ W, int64_t row_bytes, int nrows,
                                                            int k, const uint8_t* __restrict__ xq, int nct, int n,
                                                            void* __restrict__ y, int y_dtype) {
@@ -440,13 +441,13 @@ __global__ void __launch_bounds__(64 * KS) gemm_raw_kernel(const uint8_t* __rest
     load_xraw<NT>(xrs, units, b + 1, sbase, lane, j, xb);
     load_raw_frag<TYPE>(wrs, row_off, crow_off, (b + 1) * BS, q, fb);
     __builtin_amdgcn_sched_barrier(0);
-    raw_block<TYPE, NT>(fa, xa, q, acc);
+    raw_block<TYPE, NT, SX>(fa, xa, q, acc);
     load_xraw<NT>(xrs, units, b2, sbase, lane, j, xa);
     load_raw_frag<TYPE>(rs2, row_off, crow_off, (b + 2) * BS, q, fa);
     __builtin_amdgcn_sched_barrier(0);
-    raw_block<TYPE, NT>(fb, xb, q, acc);
+    raw_block<TYPE, NT, SX>(fb, xb, q, acc);
   }
-  if (nblk & 1) raw_block<TYPE, NT>(fa, xa, q, acc);
+  if (nblk & 1) raw_block<TYPE, NT, SX>(fa, xa, q, acc);
 
   if constexpr (KS > 1) {
     if (wave > 0) {
@@ -472,31 +473,35 @@ __global__ void __launch_bounds__(64 * KS) gemm_raw_kernel(const uint8_t* __rest
   }
 }
 
-template <int TYPE, int NT, int KS>
+template <int TYPE, int NT, int KS, bool SX>
 void launch_raw_t(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n, void* y,
                   int y_dtype, hipStream_t stream) {
   const int nct = (int)xq_col_tiles(n);
   const dim3 grid((unsigned)((nrows + kRawRows - 1) / kRawRows), (unsigned)((nct + NT - 1) / NT));
-  gemm_raw_kernel<TYPE, NT, KS><<<grid, 64 * KS, 0, stream>>>(W, row_bytes, nrows, k, xq, nct, n, y, y_dtype);
+  gemm_raw_kernel<TYPE, NT, KS, SX><<<grid, 64 * KS, 0, stream>>>(W, row_bytes, nrows, k, xq, nct, n, y, y_dtype);
 }
 
-template <int TYPE>
+template <int TYPE, bool SX = false>
 void launch_raw_type(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n, void* y,
                      int y_dtype, hipStream_t stream) {
   const int nct = (int)xq_col_tiles(n);
-  if (nct == 1) launch_raw_t<TYPE, 1, 4>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
-  else if (nct == 2) launch_raw_t<TYPE, 2, 4>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
-  else if (nct == 3) launch_raw_t<TYPE, 3, 4>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
-  else launch_raw_t<TYPE, 4, 4>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
+  if (nct == 1) launch_raw_t<TYPE, 1, 4, SX>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
+  else if (nct == 2) launch_raw_t<TYPE, 2, 4, SX>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
+  else if (nct == 3) launch_raw_t<TYPE, 3, 4, SX>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
+  else launch_raw_t<TYPE, 4, 4, SX>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
 }
 
 }  // namespace
 
-// Q4_K / IQ4_XS / Q6_K rows; xq: X in the xq layout (launch_quantize_xq).
+// Q4_K / IQ4_XS / Q6_K rows; xq: X in the xq layout (launch_quantize_xq). mmq: X quantised with
+// the product ops' MMQ arithmetic (for Q4_K the scale words then carry the fp16 sum of x).
 hipError_t launch_gemm_xq(int type, const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n,
-                          void* y, int y_dtype, hipStream_t stream) {
+                          void* y, int y_dtype, bool mmq, hipStream_t stream) {
   switch (type) {
-    case kQ4_K: launch_raw_type<kQ4_K>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream); break;
+    case kQ4_K:
+      if (mmq) launch_raw_type<kQ4_K, true>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
+      else launch_raw_type<kQ4_K, false>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
+      break;
     case kIQ4_XS: launch_raw_type<kIQ4_XS>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream); break;
     case kQ6_K: launch_raw_type<kQ6_K>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream); break;
     default: return hipErrorInvalidValue;

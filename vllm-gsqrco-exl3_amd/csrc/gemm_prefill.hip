@@ -310,8 +310,8 @@ __global__ void __launch_bounds__(256, 2) gemm_prefill_kernel(const uint8_t* __r
 // slice: each row's accumulator is held in units of the d of the block being summed (e, the last
 // nonzero d; a block with d = 0 decodes to zeros), and is multiplied by e_prev / e_cur when a new
 // block starts and by the last e at the end. The Q4_K min term, sum over slices of
-// (-dmin * m / e) x (d_x * sum q), is a K = 4 fp32 product per half block: one
-// v_mfma_f32_16x16x4f32 into the accumulator.
+// (-dmin * m / e) x (the fp16 sum of the slice's x, the MMQ form), is a K = 4 fp32 product per
+// half block: one v_mfma_f32_16x16x4f32 into the accumulator.
 //
 // Workgroup: NW waves over 128 weight rows x 32 NW activation rows. Wave w owns column tiles 2w,
 // 2w+1 against all 8 row tiles (16 accumulator tiles); its B operands (4 KB per column tile and

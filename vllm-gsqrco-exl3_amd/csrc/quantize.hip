@@ -102,10 +102,13 @@ __global__ void __launch_bounds__(128) quantize_q8_1_mmq_kernel(const void* __re
 // padded activation row c = i / (k/8); the 4 quarters of a slice are 4 consecutive lanes. Rows
 // c >= n (padding of the last column tile) write zeros. VEC selects the block_q8_1 arithmetic of
 // the reference's decode ops (d = amax/127, q = roundf(x/d), d kept as fp16) instead of the MMQ
-// arithmetic; DS4 (Q4_K weights) stores fp16 d with the slice's int16 sum of q.
+// arithmetic. DS4 (Q4_K weights) stores fp16 d in the low half of the scale word and, above it,
+// the activation side of the min term: with VEC the slice's int16 sum of q (the decode ops' MMVQ
+// form, vecdotq.cuh:525: d8 * sum(q8)), else the fp16 of the slice's sum of x, the half2 sum of
+// block_q8_1_mmq's DS4 layout (the product ops' MMQ form, vecdotq.cuh:549-552).
 template <bool VEC, bool DS4>
 __device__ __forceinline__ void xq_store(uint8_t* y, int64_t k, int64_t c, int64_t kk, int64_t total, uint32_t lo,
-                                         uint32_t hi, float d, int qsum) {
+                                         uint32_t hi, float d, int qsum, float xsum) {
   const int64_t per_row = k / 8;
   const int64_t nb = k / kQK;
   const int64_t b = kk / kQK;
@@ -118,15 +121,17 @@ __device__ __forceinline__ void xq_store(uint8_t* y, int64_t k, int64_t c, int64
     const int64_t nct = total / per_row / kXqCols;
     const uint32_t dh = __half_as_ushort(__float2half_rn(d));
     uint32_t word = VEC ? __float_as_uint(half_bits_to_float(dh)) : __float_as_uint(d);
-    if constexpr (DS4) word = dh | ((uint32_t)qsum << 16);
+    if constexpr (DS4)
+      word = dh | (VEC ? (uint32_t)qsum << 16 : (uint32_t)__half_as_ushort(__float2half_rn(xsum)) << 16);
     *(uint32_t*)(y + xq_scale_base(nct, nb) + (unit * kXqCols + j) * 32 + 4 * u) = word;
   }
 }
 
-// The prefill GEMM's fp16 layout (xq.h, "xh"); same thread mapping and values as xq_store.
+// The prefill GEMM's fp16 layout (xq.h, "xh"); same thread mapping and values as xq_store (MMQ
+// arithmetic: for DS4 the min term's activation side is the fp16 sum of x, widened to fp32).
 template <bool DS4>
 __device__ __forceinline__ void xh_store(uint8_t* y, int64_t k, int64_t c, int64_t kk, int64_t total, uint32_t lo,
-                                         uint32_t hi, float d, int qsum) {
+                                         uint32_t hi, float d, float xsum) {
   const int64_t per_row = k / 8;
   const int64_t nb = k / kQK;
   const int64_t b = kk / kQK;
@@ -148,7 +153,7 @@ __device__ __forceinline__ void xh_store(uint8_t* y, int64_t k, int64_t c, int64
     uint8_t* sc = y + xh_scale_base(nct, nb) + unit * kXhScaleUnit + 32 * j + 4 * u;
     const float dd = DS4 ? half_bits_to_float(__half_as_ushort(__float2half_rn(d))) : d;
     *(float*)sc = dd;
-    if constexpr (DS4) *(float*)(sc + 512) = dd * (float)qsum;
+    if constexpr (DS4) *(float*)(sc + 512) = half_bits_to_float(__half_as_ushort(__float2half_rn(xsum)));
   }
 }
 
@@ -190,8 +195,21 @@ __global__ void __launch_bounds__(256) quantize_xq_kernel(const void* __restrict
   }
   qsum += __shfl_xor(qsum, 1, 64);
   qsum += __shfl_xor(qsum, 2, 64);
-  if constexpr (XH) xh_store<DS4>(y, k, c, kk, total, lo, hi, d, qsum);
-  else xq_store<VEC, DS4>(y, k, c, kk, total, lo, hi, d, qsum);
+  // the MMQ quantiser's DS4 sum in its order (lcpp_shim.cu:320-326): 4-value lane sums
+  // ((x0 + x1) + x2) + x3, then xor-butterfly offsets 4, 2, 1 over the slice's 8 lanes; this
+  // lane holds the reference's lanes 2q, 2q + 1, so that is xor 2 then xor 1 here, then one add
+  float xsum = 0.0f;
+  if constexpr (DS4 && !VEC) {
+    float a = ((v[0] + v[1]) + v[2]) + v[3];
+    float b = ((v[4] + v[5]) + v[6]) + v[7];
+    a += __shfl_xor(a, 2, 64);
+    b += __shfl_xor(b, 2, 64);
+    a += __shfl_xor(a, 1, 64);
+    b += __shfl_xor(b, 1, 64);
+    xsum = a + b;
+  }
+  if constexpr (XH) xh_store<DS4>(y, k, c, kk, total, lo, hi, d, xsum);
+  else xq_store<VEC, DS4>(y, k, c, kk, total, lo, hi, d, qsum, xsum);
 }
 
 // block_q8_1 bytes of X (a caller's x_q8) -> the xq layout with the same values and fp16 scales.
@@ -215,7 +233,7 @@ __global__ void __launch_bounds__(256) q8_1_to_xq_kernel(const uint8_t* __restri
   int qsum = dot4((int)lo, 0x01010101, dot4((int)hi, 0x01010101, 0));
   qsum += __shfl_xor(qsum, 1, 64);
   qsum += __shfl_xor(qsum, 2, 64);
-  xq_store<true, DS4>(y, k, c, kk, total, lo, hi, d, qsum);
+  xq_store<true, DS4>(y, k, c, kk, total, lo, hi, d, qsum, 0.0f);
 }
 
 // X [n, k] -> the xq layout at y (xq_bytes(n, k) bytes) for weights of ggml type `type`; vec:

@@ -11,8 +11,10 @@
 //           16-byte loads per lane, and those bytes are the MFMA B operands of the 8 slices.
 //   scales  512 B at nct * nb * 4096 + ((t * nb + b) * 16 + j) * 32: one dword per slice
 //           u = 0..7 of activation row 16t + j: fp32 d, or for Q4_K weights fp16 d in the low half
-//           and the slice's int16 sum of q above it (d * sum is the activation side of Q4_K's
-//           min term; |sum| <= 4064, and fp16 d times it is exact in fp32).
+//           and, above it, the activation side of Q4_K's min term: with the decode ops' q8_1
+//           arithmetic the slice's int16 sum of q (times d: the MMVQ form, |sum| <= 4064, exact
+//           in fp32), with the MMQ arithmetic the fp16 of the slice's sum of x (the half2 sum of
+//           block_q8_1_mmq's DS4 layout, the MMQ form, vecdotq.cuh:549-552).
 // Quantisation per 32-value slice is the reference's MMQ arithmetic (lcpp_shim.cu:298-355):
 // d_inv = 127 / amax, q = roundf(x * d_inv), d = 1 / d_inv, and q = 0, d = 0 for an all-zero
 // slice; for Q4_K d is stored as fp16 as in the reference's half2 (DS4) MMQ layout.
@@ -42,8 +44,9 @@ __host__ __device__ inline size_t xq_bytes(int64_t n, int64_t k) {
 //           16t + j (the f16 MFMA B operand of the slice). Slices 4h..4h+3 are 4 KB contiguous.
 //   scales  1024 B at nct * nb * 8192 + (t * nb + b) * 1024: fp32 d of (row j, slice u) at 32j + 4u
 //           (a lane reads the 4 scales of its half block with one 16-byte load); for Q4_K
-//           weights, d is the fp16-rounded scale, and 512 + 32j + 4u holds d times the slice's sum
-//           of q (exact in fp32), the activation side of the min term.
+//           weights, d is the fp16-rounded scale, and 512 + 32j + 4u holds the fp16 sum of the
+//           slice's x values widened to fp32 (DS4's half2 sum), the activation side of the min
+//           term.
 constexpr int kXhUnit = 8192;       // fp16 value bytes per (column tile, K block)
 constexpr int kXhScaleUnit = 1024;  // scale bytes per (column tile, K block)
 

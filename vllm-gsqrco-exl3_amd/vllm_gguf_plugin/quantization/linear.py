@@ -154,15 +154,21 @@ def _shard_runs(weight: torch.Tensor, shard_ids: list, weight_types: list):
         yield _shard_weight(weight, start, offsets[ids[-1]][1], size), types[0]
 
 
+def _q8_1_type(n: int, k: int, weight_types: list[int], weight_rows: list[int], packed: bool = False):
+    """The type the shared q8_1 of an [n, k] x is quantized for: the first run whose op reads
+    q8_1 (reference linear.py:251-268), or None when no run's op does (or n == 0)."""
+    q8_1 = [t for t, rows in zip(weight_types, weight_rows)
+            if t in ops.LCPP_QUANT_TYPES and _lcpp_op(n, t, rows, k, packed) not in (None, *_OWN_QUANTIZE_OPS)]
+    return q8_1[0] if n and q8_1 else None
+
+
 def _quantize_x_q8_1(x: torch.Tensor, weight_types: list[int], weight_rows: list[int],
                      packed: bool = False) -> torch.Tensor:
     """x as q8_1 blocks, quantized once for every product on x whose op reads q8_1 (with the
     first such run's type); an unfilled buffer of the same size when none does."""
-    n, k = x.shape
-    q8_1 = [t for t, rows in zip(weight_types, weight_rows)
-            if t in ops.LCPP_QUANT_TYPES and _lcpp_op(n, t, rows, k, packed) not in (None, *_OWN_QUANTIZE_OPS)]
-    if n and q8_1:
-        return torch.ops._C_gguf.lcpp_quantize_q8_1(x, q8_1[0], False, False)
+    qt = _q8_1_type(x.shape[0], x.shape[1], weight_types, weight_rows, packed)
+    if qt is not None:
+        return torch.ops._C_gguf.lcpp_quantize_q8_1(x, qt, False, False)
     return _quantize_x_q8_1_fake(x, weight_types, weight_rows)
 
 
