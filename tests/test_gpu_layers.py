@@ -32,7 +32,8 @@ def x_bf16(n, k, seed):
 
 
 def build_layer(shards, k, shard_ids=None):
-    """A linear layer of the method, loaded shard by shard as vLLM's loader does: create_weights,
+    """A linear layer of the method, loaded shard by shard as vLLM's loader does: create_weights
+    under the target device (vLLM's loader builds the model inside `with torch.device(...)`),
     each shard's bytes and type through the parameters' weight loaders, then
     process_weights_after_loading. shards: [(raw uint8 [rows, row_bytes], ggml type)]."""
     from vllm_gguf_plugin.quantization.linear import GGUFLinearMethod
@@ -40,8 +41,9 @@ def build_layer(shards, k, shard_ids=None):
     layer = torch.nn.Module()
     method = GGUFLinearMethod()
     sizes = [r.shape[0] for r, _ in shards]
-    method.create_weights(layer, input_size_per_partition=k, output_partition_sizes=sizes, input_size=k,
-                          output_size=sum(sizes), params_dtype=torch.bfloat16)
+    with torch.device("cuda"):
+        method.create_weights(layer, input_size_per_partition=k, output_partition_sizes=sizes, input_size=k,
+                              output_size=sum(sizes), params_dtype=torch.bfloat16)
     if shard_ids is None:
         shard_ids = list(range(len(shards))) if len(shards) > 1 else [None]
     for sid, (raw, qt) in zip(shard_ids, shards):
