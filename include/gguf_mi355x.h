@@ -90,6 +90,22 @@ GGUF_API int gguf_mul_mat(int op, const gguf_view* W, const gguf_view* X, int64_
                  const gguf_view* x_q8, void* y, size_t y_bytes, void* workspace, size_t workspace_bytes,
                  void* stream);
 
+/* Bytes of the static per-GPU scratch that gguf_mul_mat_noalloc uses as its workspace. */
+#define GGUF_SCRATCH_BYTES ((size_t)8 << 20)
+GGUF_API size_t gguf_scratch_bytes(void);
+
+/* gguf_mul_mat without a workspace argument and without any allocation: no counterpart in the
+ * reference; for callers that cannot allocate (code under stream capture, tight serving loops,
+ * harnesses that forbid hipMalloc). The workspace is a statically sized device array of
+ * GGUF_SCRATCH_BYTES per GPU, located once per device on the first call there and held until the
+ * process ends. A product whose workspace (gguf_op_workspace_bytes) exceeds it is rejected with
+ * GGUF_EINVAL; that covers the decode and small-batch products (e.g. 64 activation rows at
+ * K = 17408) but not large prefills. Every call on a GPU shares that GPU's array: calls that
+ * overlap on one GPU (other streams, other threads) race, so the caller serialises them; the
+ * scratch needs no clearing (every byte a kernel reads is written first by the same call). */
+GGUF_API int gguf_mul_mat_noalloc(int op, const gguf_view* W, const gguf_view* X, int64_t type, int64_t row,
+                         const gguf_view* x_q8, void* y, size_t y_bytes, void* stream);
+
 /* replaces lcpp_mul_mat_vec_q (lcpp_shim.cu:911-913): 1..8 activation rows */
 GGUF_API int gguf_lcpp_mul_mat_vec_q(const gguf_view* W, const gguf_view* X, int64_t type, int64_t row,
                             const gguf_view* x_q8, void* y, size_t y_bytes, void* workspace,

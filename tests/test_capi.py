@@ -19,7 +19,7 @@ def _declared():
 
 def test_header_declares_the_op_surface():
     names = _declared()
-    assert len(names) == 17
+    assert len(names) == 19
     for op in _capi.OPS:
         assert "gguf_" + op in names
     assert "gguf_lcpp_quantize_q8_1" in names
@@ -78,3 +78,18 @@ def test_guard_call_does_not_need_a_gpu(lib):
     rc = lib.gguf_check_op(0, _capi.ref(_capi.view(W)), _capi.ref(_capi.view(X)), 21, 32, None)
     assert rc == _capi.GGUF_EINVAL
     assert _capi.error(lib).endswith("W and X must be CUDA tensors")
+
+
+def test_noalloc_entry_guards_without_a_gpu(lib):
+    """The no-allocation entry point states its scratch size and runs the same guards first: host
+    views are rejected before any device or scratch lookup."""
+    import torch
+
+    assert lib.gguf_scratch_bytes() == 8 << 20
+    W = torch.zeros(32, 2200, dtype=torch.uint8)
+    X = torch.zeros(2, 5120, dtype=torch.bfloat16)
+    Y = torch.empty(2, 32, dtype=torch.bfloat16)
+    rc = lib.gguf_mul_mat_noalloc(6, _capi.ref(_capi.view(W)), _capi.ref(_capi.view(X)), 21, 32, None,
+                                  Y.data_ptr(), Y.numel() * 2, None)
+    assert rc == _capi.GGUF_EINVAL
+    assert _capi.error(lib) == "lcpp_mul_mat_vec_iq3_mma_packed: W and X must be CUDA tensors"

@@ -11,6 +11,7 @@
 #include <climits>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "../../include/gguf_mi355x.h"
@@ -344,6 +345,61 @@ int gguf_mul_mat(int op, const gguf_view* W, const gguf_view* X, int64_t type, i
              : gguf::launch_gemv_raw((int)type, w, row_bytes, (int)row, (int)k, q8, (int)n, y, ydt, s);
   if (e != hipSuccess) return hip_fail(e, name, "gemv");
   return GGUF_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+// The no-allocation variant's workspace: one statically sized device array per GPU, held until
+// the process ends. Host code never uses the array's name as an address (on the host it is only
+// a stand-in for the symbol); each device's address comes from hipGetSymbolAddress with that
+// device current, once, and is kept here.
+constexpr size_t kScratchBytes = GGUF_SCRATCH_BYTES;
+__device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+void* g_scratch_ptr[kMaxDevices] = {};
+std::mutex g_scratch_mu;
+
+// The current device's scratch address (the caller has made X's device current).
+hipError_t scratch_address(int device, void** out) {
+  if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[device]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    g_scratch_ptr[device] = p;
+  }
+  *out = g_scratch_ptr[device];
+  return hipSuccess;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t gguf_scratch_bytes(void) { return kScratchBytes; }
+
+int gguf_mul_mat_noalloc(int op, const gguf_view* W, const gguf_view* X, int64_t type, int64_t row,
+                         const gguf_view* x_q8, void* y, size_t y_bytes, void* stream) {
+  g_err.clear();
+  const int64_t k = check_op(op, W, X, type, row, x_q8);
+  if (k < 0) return GGUF_EINVAL;
+  const char* name = op_name(op);
+  const int64_t n = X->size[0];
+  if (n == 0) return GGUF_OK;
+  const DeviceScope scope(X->device);
+  if (scope.err != hipSuccess) return hip_fail(scope.err, name, "device select");
+  const size_t need = gguf_op_workspace_bytes(op, type, row, k, n, x_q8 != nullptr);
+  if (need > kScratchBytes)
+    return fail("%s: needs a %zu-byte workspace, more than the %zu-byte static scratch of the no-allocation "
+                "entry point (use gguf_mul_mat with a workspace)", name, need, kScratchBytes);
+  void* ws = nullptr;
+  const hipError_t e = scratch_address(X->device, &ws);
+  if (e != hipSuccess) return hip_fail(e, name, "scratch address");
+  return gguf_mul_mat(op, W, X, type, row, x_q8, y, y_bytes, ws, kScratchBytes, stream);
 }
 
 #define GGUF_OP_Q8(fn, OP)                                                                                    \

@@ -37,7 +37,8 @@ EXPORTS = (
     "gguf_lcpp_mul_mat_vec_q", "gguf_lcpp_mul_mat_q", "gguf_lcpp_mul_mat_vec_iq3",
     "gguf_lcpp_mul_mat_vec_iq3_mma", "gguf_lcpp_mul_mat_vec_own", "gguf_lcpp_mul_mat_mma_k",
     "gguf_lcpp_mul_mat_vec_iq3_mma_packed", "gguf_lcpp_mul_mat_iq3_packed", "gguf_q8_1_bytes",
-    "gguf_lcpp_quantize_q8_1", "gguf_iq3_pack_scratch_bytes", "gguf_iq3_pack",
+    "gguf_lcpp_quantize_q8_1", "gguf_iq3_pack_scratch_bytes", "gguf_iq3_pack", "gguf_scratch_bytes",
+    "gguf_mul_mat_noalloc",
 )
 
 
@@ -79,6 +80,8 @@ def load():
     lib.gguf_iq3_pack_scratch_bytes.argtypes = [I64, I64]
     lib.gguf_iq3_pack_scratch_bytes.restype = SZ
     lib.gguf_iq3_pack.argtypes = [VP, I64, I64, I32, VP, SZ, VP]
+    lib.gguf_scratch_bytes.restype = SZ
+    lib.gguf_mul_mat_noalloc.argtypes = [I32, P, P, I64, I64, P, VP, SZ, VP]
     _lib = lib
     return lib
 
