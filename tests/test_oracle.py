@@ -23,7 +23,7 @@ import gguf_oracle as o
 
 FILES = sorted(glob.glob(os.path.join(GOLDEN, "dequant", "*.npz")))
 IDS = [os.path.basename(f)[:-4] for f in FILES]
-TYPES = [o.IQ3_S, o.Q4_K, o.IQ4_XS, o.Q6_K]
+TYPES = [o.IQ3_S, o.Q4_K, o.IQ4_XS, o.Q6_K, o.Q2_K, o.IQ2_XXS, o.IQ2_XS, o.IQ2_S, o.IQ3_XXS, o.IQ1_M]
 
 
 def _load(path):
@@ -35,7 +35,7 @@ def test_manifest_matches_files():
     m = json.load(open(os.path.join(GOLDEN, "dequant", "manifest.json")))
     assert {f["file"] for f in m["fixtures"]} == {os.path.basename(f) for f in FILES}
     assert set(m["types"]) == {o.TYPE_NAMES[t] for t in TYPES}
-    assert len(FILES) == 36
+    assert len(FILES) == 84  # 9 rows per type, 3 for IQ1_M
 
 
 @pytest.mark.parametrize("path", FILES, ids=IDS)
@@ -76,19 +76,29 @@ def _ref_tables():
     if not os.path.exists(exe):
         pytest.skip("oracle/_ref not built (needs the reference tree; `make -C oracle`)")
     out = subprocess.run([exe], capture_output=True, text=True, check=True).stdout.split("\n")
-    grid = [int(l.split()[2]) for l in out if l.startswith("iq3s_grid")]
-    kv = [int(l.split()[2]) for l in out if l.startswith("kvalues_iq4nl")]
+    tables = {}
+    for l in out:
+        p = l.split()
+        if len(p) == 3 and p[0] != "sizeof":
+            tables.setdefault(p[0], []).append(int(p[2]))
     sizes = [l for l in out if l.startswith("sizeof")][0].split()
-    return grid, kv, dict(zip(sizes[1::2], map(int, sizes[2::2])))
+    return tables, dict(zip(sizes[1::2], map(int, sizes[2::2])))
 
 
 def test_tables_equal_reference_header():
-    grid, kv, sizes = _ref_tables()
-    assert o.IQ3S_GRID_U32.astype(np.int64).tolist() == grid
+    tables, sizes = _ref_tables()
+    kv = tables["kvalues_iq4nl"]
+    assert o.IQ3S_GRID_U32.astype(np.int64).tolist() == tables["iq3s_grid"]
+    names = {o.IQ3_S: "block_iq3_s", o.Q4_K: "block_q4_K", o.Q6_K: "block_q6_K", o.IQ4_XS: "block_iq4_xs",
+             o.Q2_K: "block_q2_K", o.IQ2_XXS: "block_iq2_xxs", o.IQ2_XS: "block_iq2_xs", o.IQ2_S: "block_iq2_s",
+             o.IQ3_XXS: "block_iq3_xxs", o.IQ1_M: "block_iq1_m"}
+    assert sizes["block_q8_1"] == 36
+    assert {t: sizes[nm] for t, nm in names.items()} == o.BLOCK_BYTES
+    for name, grid in (("iq2xxs_grid", o.IQ2XXS_GRID), ("iq2xs_grid", o.IQ2XS_GRID), ("iq2s_grid", o.IQ2S_GRID),
+                       ("iq3xxs_grid", o.IQ3XXS_GRID), ("iq1s_grid", o.IQ1S_GRID)):
+        assert o.grid_words(grid).tolist() == tables[name], name
     assert o.KVALUES_IQ4NL.astype(int).tolist() == kv
-    assert sizes == {"block_iq3_s": 110, "block_q4_K": 144, "block_q6_K": 210,
-                     "block_iq4_xs": 136, "block_q8_1": 36}
-    assert o.BLOCK_BYTES == {o.IQ3_S: 110, o.Q4_K: 144, o.Q6_K: 210, o.IQ4_XS: 136}
+    assert o.KSIGNS_IQ2XS.astype(int).tolist() == tables["ksigns_iq2xs"]
 
 
 # ------------------------------------------------------------------------------------ q8_1
@@ -272,6 +282,42 @@ def test_q8_1_mmq_ds4_sum_pinned():
     assert (serial != want).any()
 
 
+
+def test_q8_1_mmq_d2s6_pinned():
+    """Q2_K's MMQ layout D2S6 (mmq.cuh:60-100, lcpp_shim.cu:298-355 with 64 values per scale and 16
+    per sum): one half d per 64 values (d_inv = 127 / amax over the 64, q = roundf(x * d_inv)),
+    half sums of the 16-value groups 0..5 of every 128 values, none for groups 6, 7. Integer inputs
+    pin the sums (exact in every order) and the per-64 scale (a per-32 scale gives other q); the
+    absorbing lanes of the DS4 test, placed in one 16-value group, pin the order ((s0 + s2) +
+    (s1 + s3)) of its four 4-value lanes."""
+    rng = np.random.default_rng(31)
+    x = rng.integers(-20, 21, size=(2, 512)).astype(np.float32)
+    x[1, 64:128] = 0                                   # an all-zero 64-value half
+    x[0, 0:32] *= 0.25                                 # a 32-value half with a smaller amax
+    q8 = o.quantize_q8_1_mmq(x, o.Q2_K)
+    q, d = o.dequant_q8_1_mmq(q8, 2, 512, o.Q2_K)
+    sums = o.mmq_d2s6_sums(q8, 2, 512).reshape(2, 4, 8)
+    g16 = x.reshape(2, 4, 8, 16).sum(-1)
+    np.testing.assert_array_equal(sums[..., :6], g16[..., :6])
+    assert np.isnan(sums[..., 6:]).all()
+    for r in range(2):
+        for h in range(8):
+            xb = x[r, 64 * h:64 * h + 64]
+            amax = np.float32(np.abs(xb).max())
+            if amax == 0:
+                assert (q[r, 64 * h:64 * h + 64] == 0).all() and d[r, 2 * h] == 0
+                continue
+            dinv = np.float32(127) / amax
+            np.testing.assert_array_equal(q[r, 64 * h:64 * h + 64], o._roundf((xb * dinv).astype(np.float32)))
+            assert d[r, 2 * h] == d[r, 2 * h + 1] == np.float32(np.float16(np.float32(1) / dinv))
+    assert (np.abs(q[0, 0:32]).max() < 127)            # scaled by the 64-value amax, not its own
+    # order: lanes 0 and 2 of group 0 reduce to +-2^26 and cancel, the others survive exactly
+    xa = rng.integers(-9, 10, size=(1, 128)).astype(np.float32)
+    xa[0, 0], xa[0, 1:4], xa[0, 8], xa[0, 9:12] = 2.0 ** 26, [1, 2, 3], -(2.0 ** 26), [-1, -1, -1]
+    s0 = o.mmq_d2s6_sums(o.quantize_q8_1_mmq(xa, o.Q2_K), 1, 128)[0, 0]
+    assert s0 == xa[0, 4:8].sum() + xa[0, 12:16].sum()
+    assert xa[0, :16].astype(np.float64).sum() - s0 == 3.0
+
 def _residual_heavy_x(n, k, seed):
     """Per 32-value slice one value of magnitude a and 31 of magnitude 0.49 * a / 127, all of one
     sign: every small value rounds to q = 0, so sum(x) exceeds d * sum(q) by about 15 d."""
@@ -341,6 +387,10 @@ def _brute_dots(raw, qt, q):
                         sc = blk[192 + i // 16]
                         sc = sc - 256 if sc > 127 else sc
                         acc += sc * ((lo | (hi << 4)) - 32) * qx
+                    else:
+                        wv, scale, mv = _brute_value(blk, qt, i)
+                        acc += scale * wv * qx
+                        acc_m += mv * qx
                 if qt == o.IQ3_S:
                     ls = (blk[106 + u // 2] >> (4 * (u % 2))) & 0xF
                     acc *= 1 + 2 * ls
@@ -361,6 +411,58 @@ def _brute_dots(raw, qt, q):
     return out
 
 
+def _u16(blk, o2):
+    return blk[o2] | (blk[o2 + 1] << 8)
+
+
+def _u32(blk, o4):
+    return _u16(blk, o4) | (_u16(blk, o4 + 2) << 16)
+
+
+def _brute_value(blk, qt, i):
+    """(integer value, integer sub-scale, min factor) of value i of a block of the newer formats,
+    from the bytes with plain integer arithmetic (ggml-common.h layouts, dequantize.cuh formulas);
+    the value is d * scale * w / den (den 8 for the IQ2 / IQ1 formats, 4 for IQ3_XXS), and Q2_K's
+    is d * scale * w - dmin * min."""
+    s32, g8, j = i // 32, (i % 32) // 8, i % 8
+    if qt == o.Q2_K:
+        n, r = i // 128, i % 128
+        q = (blk[16 + 32 * n + r % 32] >> (2 * (r // 32))) & 3
+        sc = blk[i // 16]
+        return q, sc & 0xF, sc >> 4
+    if qt in (o.IQ2_XXS, o.IQ3_XXS):
+        aux = _u32(blk, 2 + 8 * s32 + 4) if qt == o.IQ2_XXS else _u32(blk, 66 + 4 * s32)
+        sign_idx = (aux >> (7 * g8)) & 127
+        signs = sign_idx | ((bin(sign_idx).count("1") & 1) << 7)
+        if qt == o.IQ2_XXS:
+            mag = int(o.IQ2XXS_GRID[blk[2 + 8 * s32 + g8]][j])
+        else:
+            mag = int(o.IQ3XXS_GRID[blk[2 + 8 * s32 + 2 * g8 + j // 4]][j % 4])
+        return (-mag if signs >> j & 1 else mag), 2 * (aux >> 28) + 1, 0
+    if qt == o.IQ2_XS:
+        v = _u16(blk, 2 + 2 * (4 * s32 + g8))
+        signs = (v >> 9) | ((bin(v >> 9).count("1") & 1) << 7)
+        mag = int(o.IQ2XS_GRID[v & 511][j])
+        sc = (blk[66 + s32] >> (4 * (g8 // 2))) & 0xF
+        return (-mag if signs >> j & 1 else mag), 2 * sc + 1, 0
+    if qt == o.IQ2_S:
+        idx = blk[2 + 4 * s32 + g8] | (((blk[66 + s32] >> (2 * g8)) & 3) << 8)
+        signs = blk[34 + 4 * s32 + g8]
+        mag = int(o.IQ2S_GRID[idx][j])
+        sc = (blk[74 + s32] >> (4 * (g8 // 2))) & 0xF
+        return (-mag if signs >> j & 1 else mag), 2 * sc + 1, 0
+    if qt == o.IQ1_M:
+        grp = i // 8
+        nib = (blk[32 + grp // 2] >> (4 * (grp % 2))) & 0xF
+        idx = blk[grp] | ((nib & 7) << 8)
+        g = int(o.IQ1S_GRID[idx][j])
+        delta = -1 if nib & 8 else 1
+        sc16 = i // 16
+        sc = (_u16(blk, 48 + 2 * (sc16 // 4)) >> (3 * (sc16 % 4))) & 7
+        return 8 * g + delta, 2 * sc + 1, 0
+    raise ValueError(qt)
+
+
 @pytest.mark.parametrize("qt", TYPES, ids=lambda t: o.TYPE_NAMES[t])
 def test_slice_dots_brute_force(qt):
     rng = np.random.default_rng(5)
@@ -370,7 +472,7 @@ def test_slice_dots_brute_force(qt):
     brute = _brute_dots(raw, qt, q)
     for (xr, wr, s), (a, m) in brute.items():
         assert dots["dot"][xr, wr, s] == a
-        if qt == o.Q4_K:
+        if qt in (o.Q4_K, o.Q2_K):
             assert dots["m"][xr, wr, s] == m
 
 
@@ -385,8 +487,8 @@ def test_slice_dots_scale_identity_on_golden_rows(path):
     dots = o.slice_dots(raw.reshape(1, -1), qt, q)
     t = o.decode_int(raw, qt)
     dw = np.repeat(t["d"].astype(np.float64), 8)
-    y = (dots["dot"][:, 0, :] * dw[None] * d8).sum(-1)
-    if qt == o.Q4_K:
+    y = (dots["dot"][:, 0, :] * dw[None] * d8).sum(-1) / dots.get("den", 1)
+    if "m" in dots:
         y -= (dots["m"][:, 0, :] * np.repeat(t["dmin"].astype(np.float64), 8)[None] * d8).sum(-1)
     want = (q.astype(np.float64).reshape(2, -1, 32) * d8[..., None]).reshape(2, k) @ ref.astype(np.float64)
     np.testing.assert_allclose(y, want, rtol=1e-12, atol=1e-12 * np.abs(want).max())
