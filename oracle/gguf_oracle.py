@@ -678,6 +678,48 @@ def slice_dots(raw: np.ndarray, qt: int, q: np.ndarray) -> dict:
     raise ValueError(qt)
 
 
+def _cdiv(a: np.ndarray, b: int) -> np.ndarray:
+    """C integer division of int64 values by a positive int: the quotient truncated toward zero."""
+    return np.sign(a) * (np.abs(a) // b)
+
+
+# the types whose slice value is d * (integer) / den with a single block d
+UNIT_TYPES = (IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ1_M)
+
+
+def mmvq_slice_units(raw: np.ndarray, qt: int, q: np.ndarray) -> np.ndarray:
+    """Per (activation row, weight row, 32-value slice) the decode ops' slice value in units of
+    d_w * d8, float64, formed as the reference's vec_dot functions form it, truncating C
+    divisions included (s: the raw 4-bit scale, ls = 2s + 1):
+      IQ2_XXS        sumi * ls / 8                                    (vecdotq.cuh:1074-1077)
+      IQ2_XS, IQ2_S  (sumi_a * s_a + sumi_b * s_b + (sumi_a + sumi_b) / 2) / 4, halves a, b
+                                                                      (:1116-1118, :1163-1166)
+      IQ3_XXS        (s * sumi + sumi / 2) / 2                         (:1201-1204)
+      IQ1_M          ((sumi_a + delta_a sum q8_a) * ls_a + ...) with sumi over grid + 1 and delta
+                     = -1 +- 1/8 (:1286-1328): exactly slice_dots' dot / 8 (no division)
+    raw: [rows, row_bytes]; q: int8 [n, K]. Returns [n, rows, K/32]."""
+    rows = raw.shape[0]
+    t = decode_int(raw.reshape(-1), qt)
+    n, k = q.shape
+    ns = k // 32
+    w = t["w"].astype(np.int64).reshape(rows, ns, 2, 16)
+    qq = q.astype(np.int64).reshape(n, ns, 2, 16)
+    s16 = np.einsum("rsth,nsth->nrst", w, qq)                          # [n, rows, ns, 2]
+    s = s16.sum(-1)
+    if qt == IQ2_XXS:
+        return _cdiv(s * t["ls"].reshape(rows, ns)[None].astype(np.int64), 8).astype(np.float64)
+    if qt == IQ3_XXS:
+        s4 = ((t["ls"].reshape(rows, ns).astype(np.int64) - 1) // 2)[None]
+        return _cdiv(s4 * s + _cdiv(s, 2), 2).astype(np.float64)
+    if qt in (IQ2_XS, IQ2_S):
+        s4 = ((t["ls16"].reshape(rows, ns, 2).astype(np.int64) - 1) // 2)[None]
+        a, b = s16[..., 0], s16[..., 1]
+        return _cdiv(a * s4[..., 0] + b * s4[..., 1] + _cdiv(a + b, 2), 4).astype(np.float64)
+    if qt == IQ1_M:
+        return (s16 * t["ls16"].reshape(rows, ns, 2)[None].astype(np.int64)).sum(-1) / 8.0
+    raise ValueError(f"mmvq_slice_units: type {qt} has no single-scale slice value")
+
+
 # --------------------------------------------------------------------------- reference models
 def q81_model(raw: np.ndarray, qt: int, x, layout: str = "mmvq") -> np.ndarray:
     """float64 y[n, rows] = dequant(q8_1(x)) @ dequant(W).T (tests/gpu/_refs.py:40-54,83).
@@ -698,13 +740,16 @@ def q81_model(raw: np.ndarray, qt: int, x, layout: str = "mmvq") -> np.ndarray:
         q, d = dequant_q8_1_mmq(q8, n, k, qt)
     xq = (q.astype(np.float64).reshape(n, k // 32, 32) * d.astype(np.float64)[..., None]).reshape(n, k)
     if qt == Q2_K and layout == "mmq":
-        # vec_dot_q2_K_q8_1_impl_mmq (vecdotq.cuh:396-445): the min term per 16 values is
-        # dmin * m * half(sum x) where D2S6 stores the sum (groups 0..5 of every 128 values), and
-        # dmin * m * d8 * sum(q8) for groups 6, 7
+        # ggml_cuda_mmq_vec_dot_q2_K_q8_1_mma (mmq-vec-dot.cuh:688-745, the scalar form
+        # vecdotq.cuh:396-445): the tile loader stores d * sc and dmin * m as fp16
+        # (mmq-load-tiles.cuh:582-591); the min term per 16 values is dmin * m * half(sum x) where
+        # D2S6 stores the sum (groups 0..5 of every 128 values), dmin * m * d8 * sum(q8) for
+        # groups 6, 7
         t = decode_int(raw.reshape(-1), qt)
-        dd = (t["d"][:, None] * t["sc16"].astype(np.float32)).astype(np.float64)      # [nb, 16]
+        f16 = np.float16
+        dd = (t["d"][:, None] * t["sc16"].astype(np.float32)).astype(f16).astype(np.float64)    # [nb, 16]
         main = (np.repeat(dd, 16, axis=1) * t["w"].astype(np.float64)).reshape(rows, k)
-        mins = (t["dmin"][:, None] * t["m16"].astype(np.float32)).astype(np.float64).reshape(rows, k // 16)
+        mins = (t["dmin"][:, None] * t["m16"].astype(np.float32)).astype(f16).astype(np.float64).reshape(rows, k // 16)
         S = mmq_d2s6_sums(q8, n, k).astype(np.float64)
         qsum = (q.astype(np.float64).reshape(n, k // 16, 16).sum(-1) * np.repeat(d.astype(np.float64), 2, axis=1))
         S = np.where(np.isnan(S), qsum, S)

@@ -67,18 +67,18 @@ def dev(a):
 
 
 def exact_weights(qt, rows, k, seed):
-    """Random codes with every block scale 1.0 (Q6_K sub-scales kept within +-31)."""
+    """Random codes with every block scale (d, and dmin where the type has one) 1.0 (Q6_K
+    sub-scales kept within +-31)."""
     w = w_rand(qt, rows, k, seed)
     b = w.reshape(-1, o.BLOCK_BYTES[qt])
     one = np.array([0x00, 0x3C], dtype=np.uint8)  # fp16 1.0
     if qt == o.Q6_K:
-        b[:, 208:210] = one
         sc = np.random.default_rng(seed + 1).integers(-31, 32, size=(b.shape[0], 16)).astype(np.int8)
         b[:, 192:208] = sc.view(np.uint8)
-    else:
-        b[:, 0:2] = one
-        if qt == o.Q4_K:
-            b[:, 2:4] = one
+    for off in o.SCALE_OFFSETS[qt]:
+        b[:, off:off + 2] = one
+    if qt == o.IQ1_M:
+        o.set_iq1m_d(b, np.ones(b.shape[0], dtype=np.float16))
     return w
 
 
@@ -91,13 +91,23 @@ def exact_x(n, k, seed, dtype=torch.bfloat16):
     return torch.from_numpy(x).to(dtype)
 
 
-def exact_ref(raw, qt, x):
-    """The int64 sum of the oracle's slice dots (every scale 1): the exact output."""
+def exact_ref(raw, qt, x, form="mmvq"):
+    """The exact output with every scale 1: the int64 sum of the oracle's slice dots, or for the
+    single-scale IQ types the sum of their slice values (a multiple of 1/8): the decode ops'
+    truncating MMVQ values (form 'mmvq') or the product ops' dot / den (form 'mmq')."""
     q, d, _ = o.dequant_q8_1(o.quantize_q8_1(x), x.shape[0], x.shape[1])
     assert (d == 1).all()
+    if qt in o.UNIT_TYPES:
+        if form == "mmvq":
+            y = o.mmvq_slice_units(raw, qt, q).sum(-1)
+        else:
+            dots = o.slice_dots(raw, qt, q)
+            y = dots["dot"].sum(-1) / dots["den"]
+        assert np.abs(y).max() < 2 ** 20
+        return y
     dots = o.slice_dots(raw, qt, q)
     y = dots["dot"].sum(-1)
-    if qt == o.Q4_K:
+    if qt in (o.Q4_K, o.Q2_K):
         y = y - dots["m"].sum(-1)
     assert np.abs(y).max() < 2 ** 24
     return y

@@ -502,3 +502,51 @@ def test_q81_model_close_to_full_and_not_equal():
     yf = o.full_model(raw, o.IQ3_S, x)
     e = o.rel_l2(y81, yf)
     assert 1e-4 < e < 2e-2, e
+
+
+# ------------------------------------------------------------------------------------ MMVQ forms
+def _units_inputs(qt, seed):
+    rng = np.random.default_rng(seed)
+    raw = o.random_blocks(rng, qt, 16, 1024)
+    q = rng.integers(-127, 128, size=(3, 1024)).astype(np.int8)
+    return raw, q, o.slice_dots(raw, qt, q)
+
+
+@pytest.mark.parametrize("qt", o.UNIT_TYPES, ids=lambda t: o.TYPE_NAMES[t])
+def test_mmvq_slice_units_pinned(qt):
+    """The decode ops' truncated slice values against what fixes them without the C expression:
+      * within 1.125 of the exact dot / den (truncations lose less than 1 plus 1/8);
+      * IQ2_XXS: the truncation of dot / 8; IQ1_M: dot / 8 itself (no division);
+      * IQ3_XXS: the truncation of dot / 4, the identity the reference's owned kernel states for
+        the vendored (s * sumi + sumi / 2) / 2 (lcpp_owned_iq3_mma.cu:31);
+      * IQ2_XS, IQ2_S: the truncation of dot / 8 wherever sumi_a + sumi_b is even (the inner
+        halving is then exact), and a different value somewhere it is odd with a negative total
+        (the inner truncation then rounds toward zero from the other side)."""
+    raw, q, dots = _units_inputs(qt, 9)
+    units = o.mmvq_slice_units(raw, qt, q)
+    exact = dots["dot"] / dots["den"]
+    assert np.abs(units - exact).max() < 1.125
+    assert (units == np.round(units)).all() or qt == o.IQ1_M
+    trunc = np.trunc(exact)
+    if qt == o.IQ2_XXS:
+        np.testing.assert_array_equal(units, np.trunc(dots["dot"] / 8))
+    elif qt == o.IQ1_M:
+        np.testing.assert_array_equal(units, dots["dot"] / 8)
+    elif qt == o.IQ3_XXS:
+        np.testing.assert_array_equal(units, np.trunc(dots["dot"] / 4))
+    else:
+        t = o.decode_int(raw.reshape(-1), qt)
+        w = t["w"].astype(np.int64).reshape(16, 32, 2, 16)
+        qq = q.astype(np.int64).reshape(3, 32, 2, 16)
+        tot = np.einsum("rsth,nsth->nrs", w, qq)
+        even = tot % 2 == 0
+        np.testing.assert_array_equal(units[even], trunc[even])
+        assert (units[~even] != trunc[~even]).any()
+
+
+def test_mmvq_planted_floor_division_is_visible():
+    """Floor division in place of C's truncation changes the IQ3_XXS values on these inputs."""
+    raw, q, dots = _units_inputs(o.IQ3_XXS, 10)
+    units = o.mmvq_slice_units(raw, o.IQ3_XXS, q)
+    assert (units != np.floor(dots["dot"] / 4)).any()
+    assert (dots["dot"] < 0).any()

@@ -51,9 +51,7 @@ def test_shared_q8_1_type(case):
     from vllm_gguf_plugin import ops
 
     types = [int(WeightType[t]) for t in case["types"]]
-    unserved = [t for t in case["types"] if int(WeightType[t]) not in ops.LCPP_QUANT_TYPES]
-    if unserved:
-        pytest.skip(f"{unserved} not served by this build's kernels")
+    assert all(t in ops.LCPP_QUANT_TYPES for t in types)
     want = case["quantize_as"]
     got = linear._q8_1_type(case["n"], 512, types, case["rows"], case["packed"])
     assert got == (None if want is None else int(WeightType[want]))
@@ -78,8 +76,16 @@ def test_empty_product_launches_nothing():
         assert y.shape == (0, 17408) and y.dtype == torch.float16
 
 
+def test_served_types_are_the_route_l_set():
+    """Every Route L type of the reference (ops.py:96-110) is served."""
+    from vllm_gguf_plugin import ops
+
+    names = {"Q2_K", "Q4_K", "Q6_K", "IQ2_XXS", "IQ2_XS", "IQ2_S", "IQ3_XXS", "IQ3_S", "IQ4_XS", "IQ1_M"}
+    assert {WeightType(t).name for t in ops.LCPP_QUANT_TYPES} == names
+
+
 def test_unserved_type_is_refused():
-    """A quantized type this build has no kernel for raises NotImplementedError naming it."""
+    """A quantized type outside the Route L set raises NotImplementedError naming it."""
     x = torch.zeros(2, 512, dtype=torch.bfloat16)
     with pytest.raises(NotImplementedError, match="IQ1_S"):
         linear._fused_mul_mat_gguf(x, torch.zeros(64, 2 * 50, dtype=torch.uint8), int(WeightType.IQ1_S))

@@ -4,8 +4,8 @@
 //
 // The guards restate the reference's run() type checks (lcpp_shim.cu:767-791) and check_inputs
 // (lcpp_shim.cu:690-732) in the same order with the same message fragments, so callers (and the
-// CPU guard tests) see the same rejections. Types served by this build: Q4_K, Q6_K, IQ3_S,
-// IQ4_XS; the reference's other Route L types report "unsupported ggml type".
+// CPU guard tests) see the same rejections. Types served: the reference's Route L set (Q2_K,
+// Q4_K, Q6_K, IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ4_XS, IQ1_M; lcpp_shim.cu:676-684).
 #include <hip/hip_runtime.h>
 
 #include <climits>
@@ -86,12 +86,20 @@ const char* op_name(int op) {
   }
 }
 
+// lcpp_type_supported (lcpp_shim.cu:676-684)
 bool type_served(int64_t t) {
-  return t == gguf::kQ4_K || t == gguf::kQ6_K || t == gguf::kIQ3_S || t == gguf::kIQ4_XS;
+  return t == gguf::kQ4_K || t == gguf::kQ6_K || t == gguf::kIQ3_S || t == gguf::kIQ4_XS || t == gguf::kQ2_K ||
+         t == gguf::kIQ2_XXS || t == gguf::kIQ2_XS || t == gguf::kIQ2_S || t == gguf::kIQ3_XXS || t == gguf::kIQ1_M;
 }
 
-// the reference's Route L type ids that the IQ3 / own / mma_k checks name
-constexpr int64_t kIQ3_XXS = 18, kIQ2_S = 22, kIQ1_M = 29;
+using gguf::kIQ1_M;
+using gguf::kIQ2_S;
+using gguf::kIQ3_XXS;
+
+// Q2_K, the IQ2 types, IQ3_XXS and IQ1_M run on the generic kernels: the dot4 GEMV for the decode
+// ops, the per-slice MFMA GEMM for the product ops (IQ3_XXS keeps the GGUF layout in the packed
+// ops: its repack is the identity)
+bool generic(int64_t t) { return gguf::generic_type((int)t); }
 
 bool is_float(int32_t dt) { return dt == GGUF_DT_F32 || dt == GGUF_DT_F16 || dt == GGUF_DT_BF16; }
 
@@ -256,6 +264,7 @@ bool small_fp16(int op, int64_t type, int64_t k, int64_t n) {
 
 size_t gguf_op_workspace_bytes(int op, int64_t type, int64_t row, int64_t k, int64_t n, int has_x_q8) {
   if (n <= 0) return 0;
+  if (generic(type)) return op_gemm(op) ? align256(gguf_q8_1_bytes(n, k, 1)) : has_x_q8 ? 0 : align256(gguf_q8_1_bytes(n, k, 0));
   if (op_gemm(op)) {
     const bool mmq_layout = !op_packed(op) && type == gguf::kIQ3_S;
     if (!mmq_layout && ((n >= kPrefillFrom && gguf::prefill_uses_xh((int)type, op_packed(op))) ||
@@ -276,7 +285,6 @@ int gguf_mul_mat(int op, const gguf_view* W, const gguf_view* X, int64_t type, i
   const char* name = op_name(op);
   const int64_t n = X->size[0];
   if (n == 0) return GGUF_OK;
-  if (type == kIQ3_XXS) return fail("%s: unsupported ggml type %lld", name, (long long)type);
   if (y_bytes < (size_t)(n * row * elem_size(X->dtype))) return fail("%s: output buffer too small", name);
   const bool packed = op_packed(op);
   const bool gemm = op_gemm(op);
@@ -293,6 +301,29 @@ int gguf_mul_mat(int op, const gguf_view* W, const gguf_view* X, int64_t type, i
   const uint8_t* w = (const uint8_t*)W->data;
   const int64_t row_bytes = W->size[1];
   const int ydt = X->dtype;
+
+  if (generic(type)) {
+    if (gemm) {  // the product ops' MMQ arithmetic: block_q8_1_mmq and the per-slice MFMA GEMM
+      e = gguf::launch_quantize(X->data, X->dtype, n, k, s01, (int)type, true, workspace, s);
+      if (e != hipSuccess) return hip_fail(e, name, "quantize");
+      e = gguf::launch_gemm((int)type, w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace, (int)n, y, ydt, s);
+      if (e != hipSuccess) return hip_fail(e, name, "gemm");
+      return GGUF_OK;
+    }
+    const uint8_t* q8 = x_q8 ? (const uint8_t*)x_q8->data : (const uint8_t*)workspace;
+    if (!x_q8) {
+      e = gguf::launch_quantize(X->data, X->dtype, n, k, s01, (int)type, false, workspace, s);
+      if (e != hipSuccess) return hip_fail(e, name, "quantize");
+    }
+    // the GEMV takes up to 8 activation rows per launch (the packed decode op allows 32)
+    for (int64_t c = 0; c < n; c += 8) {
+      const int64_t nc = n - c < 8 ? n - c : 8;
+      e = gguf::launch_gemv_raw((int)type, w, row_bytes, (int)row, (int)k, q8 + c * (k / gguf::kQ81) * 36, (int)nc,
+                                (uint8_t*)y + c * row * elem_size(X->dtype), ydt, s);
+      if (e != hipSuccess) return hip_fail(e, name, "gemv");
+    }
+    return GGUF_OK;
+  }
 
   // int8-MFMA GEMMs on the xq layout: the product ops with the MMQ arithmetic, the decode ops
   // (from vec_mma_from rows on, see decode_mma) with the decode ops' q8_1 arithmetic or the
@@ -428,7 +459,7 @@ int gguf_lcpp_quantize_q8_1(const gguf_view* X, int64_t type, int mmq, int vendo
   g_err.clear();
   // lcpp_shim.cu:950-955: one combined guard
   if (!(X && type_served(type) && X->device >= 0 && X->ndim == 2 && X->stride[1] == 1 && X->size[1] % 512 == 0 &&
-        is_float(X->dtype)))
+        !(mmq && type == kIQ1_M) && is_float(X->dtype)))
     return fail("lcpp_quantize_q8_1: bad arguments");
   if (vendored) return fail("lcpp_quantize_q8_1: no vendored quantizer in this build (vendored must be false)");
   const int64_t n = X->size[0], k = X->size[1];

@@ -8,6 +8,14 @@
 //   IQ4_XS: value = d * ls * w           ls = 6-bit scale - 32     (vecdotq.cuh:1357-1380)
 //   Q4_K  : value = d * sc * w - dmin * m, w = 4-bit quant         (vecdotq.cuh:508-530)
 //   Q6_K  : value = d * sc_h * w, sc_h int8 per 16 values          (vecdotq.cuh:627-648)
+//   Q2_K  : value = d * sc_h * w - dmin * m_h, w = 2-bit quant, sc_h, m_h per 16 values
+//   IQ2_XXS, IQ3_XXS: value = d * ls * w / den, ls = 2 * nibble + 1 per 32 values, den = 8 (IQ2),
+//           4 (IQ3_XXS), w = signed grid byte
+//   IQ2_XS, IQ2_S, IQ1_M: value = d * ls_h * w / 8, ls_h = 2 * scale + 1 per 16 values;
+//           IQ1_M's w = 8 * grid +- 1 (grid in {-1, 0, 1}, the +-1/8 delta folded in)
+// The /den forms are the gguf-py dequant's d * (0.5 + s) * 0.25 (or * 0.5) and d * (2s + 1) *
+// (grid +- 0.125) with the fractions moved into one power-of-two factor, so every slice dot
+// stays an exact integer.
 // Byte offsets inside a block are the format's (ggml-common.h block structs, see gguf_common.h).
 #pragma once
 
@@ -16,10 +24,11 @@
 namespace gguf {
 
 struct SliceScale {
-  float d;     // block scale (IQ3_S / IQ4_XS / Q6_K: d; Q4_K: d)
-  float dmin;  // Q4_K only
-  int ls;      // IQ3_S / IQ4_XS sub-scale; Q4_K sc; Q6_K first 16-value scale
-  int ls2;     // Q4_K m; Q6_K second 16-value scale
+  float d;     // the block's fp16 d
+  float dmin;  // Q4_K, Q2_K
+  int ls;      // IQ sub-scale; Q4_K sc; Q6_K / Q2_K / per-16 IQ: first 16-value scale
+  int ls2;     // Q4_K m; Q6_K / Q2_K / per-16 IQ: second 16-value scale
+  int m, m2;   // Q2_K: the two 16-value mins
 };
 
 // Q6_K bytes are 6-bit unsigned codes; bytewise q - 32 without borrows between bytes.
@@ -165,6 +174,273 @@ __device__ __forceinline__ void decode_q6k_q(const uint8_t* b, int u, int q, int
   s.d = half_bits_to_float(ld16(b + 208));
   s.ls = (int)(int8_t)b[192 + 2 * u + (q >> 1)];  // values 8q..8q+7 lie in one 16-value half
   s.ls2 = 0;
+}
+
+// ---------------------------------------------------------------------------------- IQ2 / IQ3_XXS / IQ1_M
+// These decoders report the block's fp16 d in s.d; the value is d * ls * w / iq_den(type).
+__host__ __device__ constexpr int iq_den(int type) {
+  return type == kIQ3_XXS ? 4 : (type == kIQ2_XXS || type == kIQ2_XS || type == kIQ2_S || type == kIQ1_M) ? 8 : 1;
+}
+
+// ksigns_iq2xs: 7 sign bits and an eighth that makes the byte's parity even
+__device__ __forceinline__ uint32_t ksigns8(uint32_t s7) { return s7 | ((__builtin_popcount(s7) & 1u) << 7); }
+
+// the 8 bytes of a grid entry, the bytes flagged in signs (bit j: byte j) negated
+__device__ __forceinline__ void signed_grid8(uint64_t g, uint32_t signs, int& w0, int& w1) {
+  w0 = apply_signs((uint32_t)g, signs & 0xFu);
+  w1 = apply_signs((uint32_t)(g >> 32), (signs >> 4) & 0xFu);
+}
+
+// block_iq2_xxs: d[0:2], per slice u 8 bytes at 2 + 8u: four grid indices, then a dword of four
+// 7-bit sign indices (bits 7g) and the scale (bits 28..31)
+__device__ __forceinline__ void decode_iq2xxs(const uint8_t* b, int u, const uint64_t* grid, int (&w)[8],
+                                              SliceScale& s) {
+  const uint32_t idx = ld32(b + 2 + 8 * u), aux = ld32(b + 6 + 8 * u);
+#pragma unroll
+  for (int g = 0; g < 4; ++g)
+    signed_grid8(grid[(idx >> (8 * g)) & 0xFF], ksigns8((aux >> (7 * g)) & 127), w[2 * g], w[2 * g + 1]);
+  s.d = half_bits_to_float(ld16(b));
+  s.ls = 2 * (int)(aux >> 28) + 1;
+}
+
+__device__ __forceinline__ void decode_iq2xxs_q(const uint8_t* b, int u, int q, const uint64_t* grid, int (&w)[2],
+                                                SliceScale& s) {
+  const uint32_t aux = ld32(b + 6 + 8 * u);
+  signed_grid8(grid[b[2 + 8 * u + q]], ksigns8((aux >> (7 * q)) & 127), w[0], w[1]);
+  s.d = half_bits_to_float(ld16(b));
+  s.ls = 2 * (int)(aux >> 28) + 1;
+}
+
+// block_iq2_xs: d[0:2], qs[2:66] 32 uint16 (9-bit grid index | 7-bit sign index << 9),
+// scales[66:74] (slice u: low nibble values 0..15, high nibble 16..31)
+__device__ __forceinline__ void decode_iq2xs(const uint8_t* b, int u, const uint64_t* grid, int (&w)[8],
+                                             SliceScale& s) {
+  const uint64_t q = ld64(b + 2 + 8 * u);
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const uint32_t v = (uint32_t)(q >> (16 * g)) & 0xFFFF;
+    signed_grid8(grid[v & 511], ksigns8(v >> 9), w[2 * g], w[2 * g + 1]);
+  }
+  const uint32_t sc = b[66 + u];
+  s.d = half_bits_to_float(ld16(b));
+  s.ls = 2 * (int)(sc & 0xF) + 1;
+  s.ls2 = 2 * (int)(sc >> 4) + 1;
+}
+
+__device__ __forceinline__ void decode_iq2xs_q(const uint8_t* b, int u, int q, const uint64_t* grid, int (&w)[2],
+                                               SliceScale& s) {
+  const uint32_t v = ld16(b + 2 + 8 * u + 2 * q);
+  signed_grid8(grid[v & 511], ksigns8(v >> 9), w[0], w[1]);
+  s.d = half_bits_to_float(ld16(b));
+  s.ls = 2 * (int)((b[66 + u] >> (4 * (q >> 1))) & 0xF) + 1;  // the 16-value half of values 8q..8q+7
+}
+
+// block_iq2_s: d[0:2], qs[2:34] grid index low bytes, signs[34:66] (one byte per 8 values),
+// qh[66:74] (index bits 8, 9 of group g at bits 2g), scales[74:82]
+__device__ __forceinline__ void decode_iq2s(const uint8_t* b, int u, const uint64_t* grid, int (&w)[8], SliceScale& s) {
+  const uint32_t lo = ld32(b + 2 + 4 * u), sg = ld32(b + 34 + 4 * u), qh = b[66 + u];
+#pragma unroll
+  for (int g = 0; g < 4; ++g)
+    signed_grid8(grid[((lo >> (8 * g)) & 0xFF) | (((qh >> (2 * g)) & 3u) << 8)], (sg >> (8 * g)) & 0xFF, w[2 * g],
+                 w[2 * g + 1]);
+  const uint32_t sc = b[74 + u];
+  s.d = half_bits_to_float(ld16(b));
+  s.ls = 2 * (int)(sc & 0xF) + 1;
+  s.ls2 = 2 * (int)(sc >> 4) + 1;
+}
+
+__device__ __forceinline__ void decode_iq2s_q(const uint8_t* b, int u, int q, const uint64_t* grid, int (&w)[2],
+                                              SliceScale& s) {
+  const uint32_t idx = b[2 + 4 * u + q] | (((uint32_t)(b[66 + u] >> (2 * q)) & 3u) << 8);
+  signed_grid8(grid[idx], b[34 + 4 * u + q], w[0], w[1]);
+  s.d = half_bits_to_float(ld16(b));
+  s.ls = 2 * (int)((b[74 + u] >> (4 * (q >> 1))) & 0xF) + 1;
+}
+
+// block_iq3_xxs: d[0:2], qs[2:66] grid indices (one per 4 values), then per slice u a dword at
+// 66 + 4u: four 7-bit sign indices (one per 8 values) and the scale (bits 28..31)
+__device__ __forceinline__ void decode_iq3xxs(const uint8_t* b, int u, const uint32_t* grid, int (&w)[8],
+                                              SliceScale& s) {
+  const uint64_t qi = ld64(b + 2 + 8 * u);
+  const uint32_t aux = ld32(b + 66 + 4 * u);
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const uint32_t sg = ksigns8((aux >> (7 * g)) & 127);
+    w[2 * g] = apply_signs(grid[(qi >> (16 * g)) & 0xFF], sg & 0xF);
+    w[2 * g + 1] = apply_signs(grid[(qi >> (16 * g + 8)) & 0xFF], sg >> 4);
+  }
+  s.d = half_bits_to_float(ld16(b));
+  s.ls = 2 * (int)(aux >> 28) + 1;
+}
+
+__device__ __forceinline__ void decode_iq3xxs_q(const uint8_t* b, int u, int q, const uint32_t* grid, int (&w)[2],
+                                                SliceScale& s) {
+  const uint32_t i2 = ld16(b + 2 + 8 * u + 2 * q);
+  const uint32_t aux = ld32(b + 66 + 4 * u);
+  const uint32_t sg = ksigns8((aux >> (7 * q)) & 127);
+  w[0] = apply_signs(grid[i2 & 0xFF], sg & 0xF);
+  w[1] = apply_signs(grid[i2 >> 8], sg >> 4);
+  s.d = half_bits_to_float(ld16(b));
+  s.ls = 2 * (int)(aux >> 28) + 1;
+}
+
+// block_iq1_m: qs[0:32] grid index low bytes (one per 8 values), qh[32:48] (a nibble per group:
+// index bits 8..10 and, in bit 3, the delta's sign), scales[48:56] as 4 uint16 holding the
+// 3-bit scale of every 16 values in bits 0..11 and the fp16 d in the four top nibbles. The grid
+// digits (value + 1, kIq1sNib) go through a byte permute to 8 * value + 1 (delta +) or
+// 8 * value - 1 (delta -).
+__device__ __forceinline__ float iq1m_d(const uint8_t* b) {
+  const uint64_t sc = ld64(b + 48);
+  const uint32_t s0 = (uint32_t)sc & 0xFFFF, s1 = (uint32_t)(sc >> 16) & 0xFFFF, s2 = (uint32_t)(sc >> 32) & 0xFFFF,
+                 s3 = (uint32_t)(sc >> 48);
+  return half_bits_to_float((s0 >> 12) | ((s1 >> 8) & 0xF0) | ((s2 >> 4) & 0xF00) | (s3 & 0xF000));
+}
+
+__device__ __forceinline__ int iq1m_scale(const uint8_t* b, int h) {  // h: 16-value group 0..15
+  return (int)((ld16(b + 48 + 2 * (h >> 2)) >> (3 * (h & 3))) & 7);
+}
+
+__device__ __forceinline__ void iq1m_group(const uint8_t* b, int grp, const uint32_t* grid, int& w0, int& w1) {
+  const uint32_t nib = (b[32 + (grp >> 1)] >> (4 * (grp & 1))) & 0xF;
+  const uint32_t g = grid[b[grp] | ((nib & 7) << 8)];
+  const uint32_t t = (nib & 8) ? 0x0007FFF7u : 0x000901F9u;  // bytes 0, 1, 2: digit 0 (-1), 1 (0), 2 (+1)
+  w0 = (int)__builtin_amdgcn_perm(t, t, g & 0x0F0F0F0Fu);
+  w1 = (int)__builtin_amdgcn_perm(t, t, (g >> 4) & 0x0F0F0F0Fu);
+}
+
+__device__ __forceinline__ void decode_iq1m(const uint8_t* b, int u, const uint32_t* grid, int (&w)[8],
+                                            SliceScale& s) {
+#pragma unroll
+  for (int g = 0; g < 4; ++g) iq1m_group(b, 4 * u + g, grid, w[2 * g], w[2 * g + 1]);
+  s.d = iq1m_d(b);
+  s.ls = 2 * iq1m_scale(b, 2 * u) + 1;
+  s.ls2 = 2 * iq1m_scale(b, 2 * u + 1) + 1;
+}
+
+__device__ __forceinline__ void decode_iq1m_q(const uint8_t* b, int u, int q, const uint32_t* grid, int (&w)[2],
+                                              SliceScale& s) {
+  iq1m_group(b, 4 * u + q, grid, w[0], w[1]);
+  s.d = iq1m_d(b);
+  s.ls = 2 * iq1m_scale(b, 2 * u + (q >> 1)) + 1;
+}
+
+// ---------------------------------------------------------------------------------- Q2_K
+// block_q2_K: scales[0:16] (low nibble scale, high nibble min, per 16 values), qs[16:80],
+// d[80:82], dmin[82:84]; value 128n + 32j + l is bits 2j of qs[32n + l]
+__device__ __forceinline__ void decode_q2k(const uint8_t* b, int u, int (&w)[8], SliceScale& s) {
+  const uint8_t* qs = b + 16 + 32 * (u >> 2);
+  const int sh = 2 * (u & 3);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) w[e] = (int)((ld32(qs + 4 * e) >> sh) & 0x03030303u);
+  const uint32_t dm = ld32(b + 80), sc = ld16(b + 2 * u);
+  s.d = half_bits_to_float(dm & 0xFFFF);
+  s.dmin = half_bits_to_float(dm >> 16);
+  s.ls = (int)(sc & 0xF);
+  s.m = (int)((sc >> 4) & 0xF);
+  s.ls2 = (int)((sc >> 8) & 0xF);
+  s.m2 = (int)(sc >> 12);
+}
+
+__device__ __forceinline__ void decode_q2k_q(const uint8_t* b, int u, int q, int (&w)[2], SliceScale& s) {
+  const uint64_t v = ld64(b + 16 + 32 * (u >> 2) + 8 * q);
+  const int sh = 2 * (u & 3);
+  w[0] = (int)(((uint32_t)v >> sh) & 0x03030303u);
+  w[1] = (int)(((uint32_t)(v >> 32) >> sh) & 0x03030303u);
+  const uint32_t dm = ld32(b + 80), sc = b[2 * u + (q >> 1)];
+  s.d = half_bits_to_float(dm & 0xFFFF);
+  s.dmin = half_bits_to_float(dm >> 16);
+  s.ls = (int)(sc & 0xF);
+  s.m = (int)(sc >> 4);
+}
+
+// ---------------------------------------------------------------------------------- dispatch
+// The codebook a type's decoder reads, staged in LDS by the kernels: entries and entry word.
+template <int TYPE>
+struct Codebook {
+  static constexpr int n = 1;  // no codebook
+  using T = uint32_t;
+  static __device__ T at(int) { return 0; }
+};
+template <>
+struct Codebook<kIQ3_S> {
+  static constexpr int n = 512;
+  using T = uint32_t;
+  static __device__ T at(int i) { return kIq3sGrid.v[i]; }
+};
+template <>
+struct Codebook<kIQ3_XXS> {
+  static constexpr int n = 256;
+  using T = uint32_t;
+  static __device__ T at(int i) { return kIq3xxsGrid.v[i]; }
+};
+template <>
+struct Codebook<kIQ2_XXS> {
+  static constexpr int n = 256;
+  using T = uint64_t;
+  static __device__ T at(int i) { return kIq2xxsGrid.v[i]; }
+};
+template <>
+struct Codebook<kIQ2_XS> {
+  static constexpr int n = 512;
+  using T = uint64_t;
+  static __device__ T at(int i) { return kIq2xsGrid.v[i]; }
+};
+template <>
+struct Codebook<kIQ2_S> {
+  static constexpr int n = 1024;
+  using T = uint64_t;
+  static __device__ T at(int i) { return kIq2sGrid.v[i]; }
+};
+template <>
+struct Codebook<kIQ1_M> {
+  static constexpr int n = 2048;
+  using T = uint32_t;
+  static __device__ T at(int i) { return kIq1sNib.v[i]; }
+};
+
+// Copies TYPE's codebook into `lds` with the workgroup's threads (the caller synchronises).
+template <int TYPE>
+__device__ __forceinline__ void stage_codebook(typename Codebook<TYPE>::T* lds) {
+  if constexpr (Codebook<TYPE>::n > 1)
+    for (int i = threadIdx.x; i < Codebook<TYPE>::n; i += blockDim.x) lds[i] = Codebook<TYPE>::at(i);
+}
+
+// the 32 values of slice u of block b
+template <int TYPE>
+__device__ __forceinline__ void decode_slice(const uint8_t* b, int u, const typename Codebook<TYPE>::T* grid,
+                                             int (&w)[8], SliceScale& s) {
+  if constexpr (TYPE == kIQ3_S) decode_iq3s(b, u, grid, w, s);
+  if constexpr (TYPE == kQ4_K) decode_q4k(b, u, w, s);
+  if constexpr (TYPE == kIQ4_XS) decode_iq4xs(b, u, w, s);
+  if constexpr (TYPE == kQ6_K) decode_q6k(b, u, w, s);
+  if constexpr (TYPE == kQ2_K) decode_q2k(b, u, w, s);
+  if constexpr (TYPE == kIQ2_XXS) decode_iq2xxs(b, u, grid, w, s);
+  if constexpr (TYPE == kIQ2_XS) decode_iq2xs(b, u, grid, w, s);
+  if constexpr (TYPE == kIQ2_S) decode_iq2s(b, u, grid, w, s);
+  if constexpr (TYPE == kIQ3_XXS) decode_iq3xxs(b, u, grid, w, s);
+  if constexpr (TYPE == kIQ1_M) decode_iq1m(b, u, grid, w, s);
+}
+
+// values 8q..8q+7 of slice u of block b; s.ls is the sub-scale of their 16-value half where the
+// type has one per 16 values
+template <int TYPE>
+__device__ __forceinline__ void decode_quarter(const uint8_t* b, int u, int q, const typename Codebook<TYPE>::T* grid,
+                                               int (&w)[2], SliceScale& s) {
+  if constexpr (TYPE == kIQ3_S) decode_iq3s_q(b, u, q, grid, w, s);
+  if constexpr (TYPE == kQ4_K) decode_q4k_q(b, u, q, w, s);
+  if constexpr (TYPE == kIQ4_XS) decode_iq4xs_q(b, u, q, w, s);
+  if constexpr (TYPE == kQ6_K) decode_q6k_q(b, u, q, w, s);
+  if constexpr (TYPE == kQ2_K) decode_q2k_q(b, u, q, w, s);
+  if constexpr (TYPE == kIQ2_XXS) decode_iq2xxs_q(b, u, q, grid, w, s);
+  if constexpr (TYPE == kIQ2_XS) decode_iq2xs_q(b, u, q, grid, w, s);
+  if constexpr (TYPE == kIQ2_S) decode_iq2s_q(b, u, q, grid, w, s);
+  if constexpr (TYPE == kIQ3_XXS) decode_iq3xxs_q(b, u, q, grid, w, s);
+  if constexpr (TYPE == kIQ1_M) decode_iq1m_q(b, u, q, grid, w, s);
+}
+
+// types with a sub-scale per 16 values (two integer dots per slice)
+__host__ __device__ constexpr bool per16_type(int type) {
+  return type == kQ6_K || type == kQ2_K || type == kIQ2_XS || type == kIQ2_S || type == kIQ1_M;
 }
 
 }  // namespace gguf

@@ -1,17 +1,19 @@
 // int8-MFMA GEMM for 9+ activation rows on GGUF bytes: Y[c, r] = sum_k X[c, k] * W[r, k].
 //
 // Replaces the reference's MMQ-class products on plain GGUF rows (vendored mul_mat_q via
-// lcpp_shim.cu:626-671 and the owned mma_k kernel lcpp_owned_mma_k.cu:354-540) with a gfx950
-// design on v_mfma_i32_16x16x32_i8 (IQ3_S in the tile layout has its own GEMM, gemm_tile.hip):
+// lcpp_shim.cu:626-671 and the owned mma_k kernel lcpp_owned_mma_k.cu:354-540) with gfx950
+// designs on v_mfma_i32_16x16x32_i8 (IQ3_S in the tile layout has its own GEMM, gemm_tile.hip).
+//
+// gemm_mfma_kernel (IQ3_S on plain rows; Q2_K, IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ1_M):
 //  * X is quantised to q8_1 in the MMQ block layout (quantize.hip); one 32-value slice is one
 //    MFMA K step, so every MFMA result is exactly the reference's per-slice int32 dot;
 //  * a workgroup owns 16 weight rows and 16*NT columns of X; its 4 waves split the K slices;
 //    lane l decodes values 8q..8q+7 (q = l/16) of the slice of weight row l%16 straight into
 //    the MFMA A operand, and reads the same 8 K positions of X column l%16 as the B operand;
 //  * per slice, each int32 result is scaled in fp32 by (weight scale x activation scale) and
-//    added to the accumulator; Q6_K takes two MFMAs per slice, one per 16-value sub-scale,
-//    combined in int32 as the reference does; Q4_K's min term uses the integer q8 sum;
+//    added to the accumulator; types with a sub-scale per 16 values take two MFMAs per slice;
 //  * the 4 waves' partial sums are added in wave order through LDS (deterministic).
+// gemm_raw_kernel (Q4_K, IQ4_XS, Q6_K) reads X in the xq layout; see its own description below.
 #include "decode.h"
 #include "xq.h"
 
@@ -24,16 +26,32 @@ __device__ __forceinline__ v4i mfma16x16x32(long a, long b) {
   return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, z, 0, 0, 0);
 }
 
+__device__ __forceinline__ float round_half(float v) { return __half2float(__float2half_rn(v)); }
+
+// The per-slice MFMA GEMM on plain GGUF rows for IQ3_S and the types served only by the generic
+// kernels, X in block_q8_1_mmq (D4; Q2_K D2S6). The slice terms are the reference's product-op
+// (MMQ) arithmetic:
+//   IQ3_S, IQ2_XXS, IQ3_XXS  C * (d * ls / den) * d4: the x_df of the MMQ tile loaders
+//       (mmq-load-tiles.cuh:1150-1152, :1348-1352; den 8 for IQ2, 4 for IQ3_XXS), exact in fp32
+//   IQ2_XS, IQ2_S, IQ1_M     per 16 values, ls_h = 2 * scale + 1: (C_a * ls_a + C_b * ls_b) *
+//       (d / 8) * d4, the same products as x_df = ((scale * d + d / 2) / 4) (:1207-1208, :1284-1285)
+//       combined in int32
+//   Q2_K  per 16 values h with dm_h = (half(d * sc_h), half(dmin * m_h)) (:582-591) and D2S6 d4:
+//       (C_h * dm_h.x) * d4 - dm_h.y * S_h, S_h the stored fp16 sum of x, for the groups 0..5 of
+//       each 128 values, and (C_h * dm_h.x - sum_h(q8) * dm_h.y) * d4 for groups 6, 7
+//       (ggml_cuda_mmq_vec_dot_q2_K_q8_1_mma, mmq-vec-dot.cuh:688-745)
 template <int TYPE, int NT>
 __global__ void __launch_bounds__(256) gemm_mfma_kernel(const uint8_t* __restrict__ W, int64_t row_bytes, int nrows,
                                                         int k, const uint8_t* __restrict__ q8, int n,
                                                         void* __restrict__ y, int y_dtype) {
-  __shared__ uint32_t grid[TYPE == kIQ3_S ? 512 : 1];
+  using G = typename Codebook<TYPE>::T;
+  __shared__ G grid[Codebook<TYPE>::n];
   __shared__ float part[3][NT][4][64];
-  if constexpr (TYPE == kIQ3_S) {
-    for (int i = threadIdx.x; i < 512; i += blockDim.x) grid[i] = kIq3sGrid.v[i];
+  if constexpr (Codebook<TYPE>::n > 1) {
+    stage_codebook<TYPE>(grid);
     __syncthreads();
   }
+  constexpr bool P16 = per16_type(TYPE);
   constexpr int BS = block_bytes(TYPE);
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -55,39 +73,34 @@ __global__ void __launch_bounds__(256) gemm_mfma_kernel(const uint8_t* __restric
 
   for (int s = s_begin; s < s_end; ++s) {
     const uint8_t* b = wrow + (int64_t)(s >> 3) * BS;
-    const int u = s & 7;
+    const int u = s & 7, s4 = s & 3;
     int wa[2];
     SliceScale sc;
-    if constexpr (TYPE == kIQ3_S) {
-      decode_iq3s_q(b, u, q, grid, wa, sc);
-    }
-    if constexpr (TYPE == kQ4_K) decode_q4k_q(b, u, q, wa, sc);
-    if constexpr (TYPE == kIQ4_XS) decode_iq4xs_q(b, u, q, wa, sc);
-    if constexpr (TYPE == kQ6_K) decode_q6k_q(b, u, q, wa, sc);
+    decode_quarter<TYPE>(b, u, q, grid, wa, sc);
     if (!row_ok) wa[0] = wa[1] = 0;
     const long a = (long)(((uint64_t)(uint32_t)wa[1] << 32) | (uint32_t)wa[0]);
 
-    // scales of the 4 output rows 4*q + v this lane accumulates (held by lanes 4q+v)
-    float rs[4], rm[4], rs2[4];
-    float my_s, my_m = 0.0f, my_s2 = 0.0f;
-    if constexpr (TYPE == kQ4_K) {
-      my_s = sc.d * (float)sc.ls;
-      my_m = sc.dmin * (float)sc.ls2;
-    } else if constexpr (TYPE == kQ6_K) {
-      my_s = sc.d;
-      // sub-scales of both halves: quarters 0,1 hold the first, 2,3 the second
-      my_s2 = (float)sc.ls;
+    // A-side scales of the 4 C rows 4q + v: lane 4q + v decoded that row's first 16 values
+    // (q = 0), lane 4q + v + 32 its second 16 (q = 2)
+    float my_s, my_m = 0.0f;
+    if constexpr (TYPE == kQ2_K) {
+      my_s = round_half(sc.d * (float)sc.ls);
+      my_m = round_half(sc.dmin * (float)sc.m);
+    } else if constexpr (P16) {
+      my_s = (float)sc.ls;
+      my_m = sc.d * 0.125f;
     } else {
-      my_s = sc.d * (float)sc.ls;
+      my_s = (sc.d * (float)sc.ls) * (1.0f / (float)iq_den(TYPE));
     }
+    float rs[4], rs2[4], rm[4], rm2[4];
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int src = 4 * q + v;
       rs[v] = __shfl(my_s, src, 64);
-      if constexpr (TYPE == kQ4_K) rm[v] = __shfl(my_m, src, 64);
-      if constexpr (TYPE == kQ6_K) {
-        rm[v] = __shfl(my_s2, src, 64);        // first-half scale (lane src has q = 0)
-        rs2[v] = __shfl(my_s2, src + 32, 64);  // second-half scale (lane src + 32 has q = 2)
+      if constexpr (P16) {
+        rs2[v] = __shfl(my_s, src + 32, 64);
+        rm[v] = __shfl(my_m, src, 64);
+        rm2[v] = __shfl(my_m, src + 32, 64);
       }
     }
 
@@ -95,40 +108,57 @@ __global__ void __launch_bounds__(256) gemm_mfma_kernel(const uint8_t* __restric
     for (int t = 0; t < NT; ++t) {
       const int col = col0 + 16 * t + li;
       long bq = 0;
-      float cd = 0.0f;
+      float cd = 0.0f, sx0 = 0.0f, sx1 = 0.0f;
       if (col < n) {
         const uint8_t* xb = q8 + ((int64_t)(s >> 2) * n + col) * 144;
-        bq = *(const long*)(xb + 16 + 32 * (s & 3) + 8 * q);
-        if constexpr (TYPE == kQ4_K) {
-          cd = half_bits_to_float(*(const uint16_t*)(xb + 4 * (s & 3)));
+        bq = *(const long*)(xb + 16 + 32 * s4 + 8 * q);
+        if constexpr (TYPE == kQ2_K) {
+          cd = half_bits_to_float(ld16(xb + 2 * (s4 >> 1)));
+          if (s4 < 3) {
+            sx0 = half_bits_to_float(ld16(xb + 4 + 4 * s4));
+            sx1 = half_bits_to_float(ld16(xb + 6 + 4 * s4));
+          }
         } else {
-          cd = *(const float*)(xb + 4 * (s & 3));
+          cd = *(const float*)(xb + 4 * s4);
         }
       }
-      if constexpr (TYPE == kQ6_K) {
+      if constexpr (P16) {
         // two MFMAs: K positions of the first 16 values (quarters 0,1), then the second 16
         const long a0 = q < 2 ? a : 0;
         const long a1 = q < 2 ? 0 : a;
         const v4i c0 = mfma16x16x32(a0, bq);
         const v4i c1 = mfma16x16x32(a1, bq);
+        if constexpr (TYPE == kQ2_K) {
+          int m0 = 0, m1 = 0;  // groups 6, 7: integer sums of the column's q8 over each half
+          if (s4 == 3) {
+            const int sq = dot4(0x01010101, (int)(uint32_t)bq, dot4(0x01010101, (int)(uint32_t)((uint64_t)bq >> 32), 0));
+            m0 = __shfl(sq, li, 64) + __shfl(sq, li + 16, 64);
+            m1 = __shfl(sq, li + 32, 64) + __shfl(sq, li + 48, 64);
+          }
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int isum = c0[v] * (int)rm[v] + c1[v] * (int)rs2[v];
-          acc[t][v] += (float)isum * (rs[v] * cd);
+          for (int v = 0; v < 4; ++v) {
+            float t0 = (float)c0[v] * rs[v];
+            float t1 = (float)c1[v] * rs2[v];
+            if (s4 == 3) {
+              t0 -= (float)m0 * rm[v];
+              t1 -= (float)m1 * rm2[v];
+            }
+            acc[t][v] += t0 * cd;
+            acc[t][v] -= rm[v] * sx0;
+            acc[t][v] += t1 * cd;
+            acc[t][v] -= rm2[v] * sx1;
+          }
+        } else {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int isum = c0[v] * (int)rs[v] + c1[v] * (int)rs2[v];
+            acc[t][v] += (float)isum * (rm[v] * cd);
+          }
         }
       } else {
         const v4i c = mfma16x16x32(a, bq);
-        if constexpr (TYPE == kQ4_K) {
-          // integer sum of the slice's q8 values of this column: 8 per quarter lane
-          int sq = dot4(0x01010101, (int)(uint32_t)bq, dot4(0x01010101, (int)(uint32_t)((uint64_t)bq >> 32), 0));
-          sq += __shfl_xor(sq, 16, 64);
-          sq += __shfl_xor(sq, 32, 64);
 #pragma unroll
-          for (int v = 0; v < 4; ++v) acc[t][v] += ((float)c[v] * rs[v] - (float)sq * rm[v]) * cd;
-        } else {
-#pragma unroll
-          for (int v = 0; v < 4; ++v) acc[t][v] += (float)c[v] * (rs[v] * cd);
-        }
+        for (int v = 0; v < 4; ++v) acc[t][v] += (float)c[v] * (rs[v] * cd);
       }
     }
   }
@@ -175,14 +205,18 @@ static void launch_gemm_t(const uint8_t* W, int64_t row_bytes, int nrows, int k,
   }
 }
 
-// q8: block_q8_1_mmq of X (n columns); y: [n, nrows] in y_dtype.
+// q8: block_q8_1_mmq of X (n columns; D4, Q2_K D2S6); y: [n, nrows] in y_dtype. IQ3_S on plain
+// rows and the generic types.
 hipError_t launch_gemm(int type, const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n,
                        void* y, int y_dtype, hipStream_t stream) {
   switch (type) {
     case kIQ3_S: launch_gemm_t<kIQ3_S>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream); break;
-    case kQ4_K: launch_gemm_t<kQ4_K>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream); break;
-    case kIQ4_XS: launch_gemm_t<kIQ4_XS>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream); break;
-    case kQ6_K: launch_gemm_t<kQ6_K>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream); break;
+    case kQ2_K: launch_gemm_t<kQ2_K>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream); break;
+    case kIQ2_XXS: launch_gemm_t<kIQ2_XXS>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream); break;
+    case kIQ2_XS: launch_gemm_t<kIQ2_XS>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream); break;
+    case kIQ2_S: launch_gemm_t<kIQ2_S>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream); break;
+    case kIQ3_XXS: launch_gemm_t<kIQ3_XXS>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream); break;
+    case kIQ1_M: launch_gemm_t<kIQ1_M>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

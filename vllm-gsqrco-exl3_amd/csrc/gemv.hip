@@ -24,100 +24,139 @@ constexpr int kGemvWaves = 4;
 
 static int persist_grid();
 
+// The slice term of one (row, column) pair in the reference's decode-op (MMVQ) arithmetic, from
+// the slice's decoded words w, the column's q8 words x, d8 and (Q4_K, Q2_K) q8 sums:
+//   IQ3_S, IQ4_XS  (float)(sumi * ls) * (d * d8)                    vecdotq.cuh:1211-1248,1357-1380
+//   Q4_K           (d * sc * sumi - dmin * m * sum q8) * d8         vecdotq.cuh:508-530
+//   Q6_K           (float)(sc_a * sumi_a + sc_b * sumi_b) * (d * d8) vecdotq.cuh:627-648
+//   Q2_K           d8 * (d * sum sc_h sumi_h - dmin * sum m_h sum_h q8) (vecdotq.cuh:367-392)
+//   IQ2_XXS        (float)(sumi * ls / 8) * (d * d8), C division     vecdotq.cuh:1074-1077
+//   IQ2_XS, IQ2_S  (float)((sumi_a * s_a + sumi_b * s_b + (sumi_a + sumi_b) / 2) / 4) * (d * d8)
+//                  with the raw 4-bit scales s                       vecdotq.cuh:1116-1118,1163-1166
+//   IQ3_XXS        (float)((s * sumi + sumi / 2) / 2) * (d * d8)    vecdotq.cuh:1201-1204
+//   IQ1_M          (float)(ls_a * sumi_a + ls_b * sumi_b) * ((d * d8) / 8), w = 8 grid +- 1: the
+//                  reference's d * ((sumi + delta * sum q8) * ls ...) holds the same multiple
+//                  of 1/8 exactly                                    vecdotq.cuh:1286-1328
+// The truncating divisions make these the reference's slice values, not just equal in exact
+// arithmetic; the fp32 order in which slices are added differs.
+template <int TYPE>
+__device__ __forceinline__ float mmvq_term(const int (&w)[8], const int (&x)[8], const SliceScale& sc, float d8,
+                                           int sq, int sq2) {
+  if constexpr (per16_type(TYPE)) {
+    int sa = 0, sb = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sa = dot4(w[e], x[e], sa);
+#pragma unroll
+    for (int e = 4; e < 8; ++e) sb = dot4(w[e], x[e], sb);
+    if constexpr (TYPE == kQ6_K) return (float)(sa * sc.ls + sb * sc.ls2) * (sc.d * d8);
+    if constexpr (TYPE == kQ2_K)
+      return d8 * (sc.d * (float)(sa * sc.ls + sb * sc.ls2) - sc.dmin * (float)(sq * sc.m + sq2 * sc.m2));
+    if constexpr (TYPE == kIQ1_M) return (float)(sa * sc.ls + sb * sc.ls2) * ((sc.d * d8) * 0.125f);
+    const int s0 = (sc.ls - 1) >> 1, s1 = (sc.ls2 - 1) >> 1;  // IQ2_XS, IQ2_S
+    return (float)((sa * s0 + sb * s1 + (sa + sb) / 2) / 4) * (sc.d * d8);
+  } else {
+    int sumi = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sumi = dot4(w[e], x[e], sumi);
+    if constexpr (TYPE == kQ4_K)
+      return ((sc.d * (float)sc.ls) * (float)sumi - (sc.dmin * (float)sc.ls2) * (float)sq) * d8;
+    if constexpr (TYPE == kIQ2_XXS) return (float)(sumi * sc.ls / 8) * (sc.d * d8);
+    if constexpr (TYPE == kIQ3_XXS) {
+      const int s4 = (sc.ls - 1) >> 1;
+      return (float)((s4 * sumi + sumi / 2) / 2) * (sc.d * d8);
+    }
+    return (float)(sumi * sc.ls) * (sc.d * d8);  // IQ3_S, IQ4_XS
+  }
+}
+
+// Workgroups of the generic GEMV: one per group of 4*RW rows, at most kGemvRawGrid of them, each
+// looping over groups (the types with a codebook stage it in LDS once per workgroup).
+constexpr int kGemvRawGrid = 2048;
+
 template <int TYPE, int NC, int RW>
 __global__ void __launch_bounds__(256) gemv_raw_kernel(const uint8_t* __restrict__ W, int64_t row_bytes, int nrows,
                                                        int k, const uint8_t* __restrict__ q8, void* __restrict__ y,
                                                        int y_dtype) {
-  __shared__ uint32_t grid[TYPE == kIQ3_S ? 512 : 1];
-  if constexpr (TYPE == kIQ3_S) {
-    for (int i = threadIdx.x; i < 512; i += blockDim.x) grid[i] = kIq3sGrid.v[i];
+  using G = typename Codebook<TYPE>::T;
+  __shared__ G grid[Codebook<TYPE>::n];
+  if constexpr (Codebook<TYPE>::n > 1) {
+    stage_codebook<TYPE>(grid);
     __syncthreads();
   }
+  constexpr bool SUMS = TYPE == kQ4_K || TYPE == kQ2_K;  // the min term reads sums of q8
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int row0 = (blockIdx.x * kGemvWaves + wave) * RW;
-  if (row0 >= nrows) return;
+  const int ngroups = (nrows + kGemvWaves * RW - 1) / (kGemvWaves * RW);
   constexpr int BS = block_bytes(TYPE);
   const int nslices = k / kQ81;
 
-  float acc[RW][NC];
+  for (int grp = blockIdx.x; grp < ngroups; grp += gridDim.x) {
+    const int row0 = (grp * kGemvWaves + wave) * RW;
+    if (row0 >= nrows) continue;
+    float acc[RW][NC];
 #pragma unroll
-  for (int r = 0; r < RW; ++r)
+    for (int r = 0; r < RW; ++r)
 #pragma unroll
-    for (int c = 0; c < NC; ++c) acc[r][c] = 0.0f;
+      for (int c = 0; c < NC; ++c) acc[r][c] = 0.0f;
 
-  for (int s = lane; s < nslices; s += 64) {
-    int xq[NC][8];
-    float d8[NC];
-    int sq[NC];  // Q4_K: sum of the slice's q8 values (the min term's integer part)
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const uint8_t* xb = q8 + ((int64_t)c * nslices + s) * 36;
-      d8[c] = half_bits_to_float(*(const uint16_t*)xb);
-      const u32x4 a = ld128a4(xb + 4);
-      const u32x4 b = ld128a4(xb + 20);
-      xq[c][0] = (int)a.x; xq[c][1] = (int)a.y; xq[c][2] = (int)a.z; xq[c][3] = (int)a.w;
-      xq[c][4] = (int)b.x; xq[c][5] = (int)b.y; xq[c][6] = (int)b.z; xq[c][7] = (int)b.w;
-      if constexpr (TYPE == kQ4_K) {
-        int t = 0;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) t = dot4(0x01010101, xq[c][e], t);
-        sq[c] = t;
-      }
-    }
-    const int blk = s >> 3, u = s & 7;
-#pragma unroll
-    for (int r = 0; r < RW; ++r) {
-      const int row = row0 + r;
-      if (row >= nrows) break;
-      const uint8_t* b = W + (int64_t)row * row_bytes + (int64_t)blk * BS;
-      int w[8];
-      SliceScale sc;
-      if constexpr (TYPE == kIQ3_S) decode_iq3s(b, u, grid, w, sc);
-      if constexpr (TYPE == kQ4_K) decode_q4k(b, u, w, sc);
-      if constexpr (TYPE == kIQ4_XS) decode_iq4xs(b, u, w, sc);
-      if constexpr (TYPE == kQ6_K) decode_q6k(b, u, w, sc);
+    for (int s = lane; s < nslices; s += 64) {
+      int xq[NC][8];
+      float d8[NC];
+      int sq[NC], sq2[NC];  // sums of the slice's q8 values: Q4_K all 32; Q2_K each 16-value half
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        if constexpr (TYPE == kQ6_K) {
-          int sa = 0, sb = 0;
+        const uint8_t* xb = q8 + ((int64_t)c * nslices + s) * 36;
+        d8[c] = half_bits_to_float(*(const uint16_t*)xb);
+        const u32x4 a = ld128a4(xb + 4);
+        const u32x4 b = ld128a4(xb + 20);
+        xq[c][0] = (int)a.x; xq[c][1] = (int)a.y; xq[c][2] = (int)a.z; xq[c][3] = (int)a.w;
+        xq[c][4] = (int)b.x; xq[c][5] = (int)b.y; xq[c][6] = (int)b.z; xq[c][7] = (int)b.w;
+        sq[c] = sq2[c] = 0;
+        if constexpr (SUMS) {
+          int t0 = 0, t1 = 0;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) sa = dot4(w[e], xq[c][e], sa);
+          for (int e = 0; e < 4; ++e) t0 = dot4(0x01010101, xq[c][e], t0);
 #pragma unroll
-          for (int e = 4; e < 8; ++e) sb = dot4(w[e], xq[c][e], sb);
-          const int sumi = sa * sc.ls + sb * sc.ls2;
-          acc[r][c] += (float)sumi * (sc.d * d8[c]);
-        } else {
-          int sumi = 0;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) sumi = dot4(w[e], xq[c][e], sumi);
+          for (int e = 4; e < 8; ++e) t1 = dot4(0x01010101, xq[c][e], t1);
           if constexpr (TYPE == kQ4_K) {
-            const float t = (sc.d * (float)sc.ls) * (float)sumi - (sc.dmin * (float)sc.ls2) * (float)sq[c];
-            acc[r][c] += t * d8[c];
+            sq[c] = t0 + t1;
           } else {
-            acc[r][c] += (float)(sumi * sc.ls) * (sc.d * d8[c]);
+            sq[c] = t0;
+            sq2[c] = t1;
           }
         }
       }
+      const int blk = s >> 3, u = s & 7;
+#pragma unroll
+      for (int r = 0; r < RW; ++r) {
+        const int row = row0 + r;
+        if (row >= nrows) break;
+        const uint8_t* b = W + (int64_t)row * row_bytes + (int64_t)blk * BS;
+        int w[8];
+        SliceScale sc;
+        decode_slice<TYPE>(b, u, grid, w, sc);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) acc[r][c] += mmvq_term<TYPE>(w, xq[c], sc, d8[c], sq[c], sq2[c]);
+      }
     }
-  }
 
 #pragma unroll
-  for (int r = 0; r < RW; ++r) {
+    for (int r = 0; r < RW; ++r) {
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      float v = acc[r][c];
+      for (int c = 0; c < NC; ++c) {
+        float v = acc[r][c];
 #pragma unroll
-      for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-      acc[r][c] = v;
+        for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+        acc[r][c] = v;
+      }
     }
+    // lane (r * NC + c) writes output (c, row0 + r)
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+        if (lane == r * NC + c && row0 + r < nrows) store_y(y, (int64_t)c * nrows + row0 + r, acc[r][c], y_dtype);
   }
-  // lane (r * NC + c) writes output (c, row0 + r)
-#pragma unroll
-  for (int r = 0; r < RW; ++r)
-#pragma unroll
-    for (int c = 0; c < NC; ++c)
-      if (lane == r * NC + c && row0 + r < nrows) store_y(y, (int64_t)c * nrows + row0 + r, acc[r][c], y_dtype);
 }
 
 // X of the row-chunk GEMV, staged in LDS: q8 values [NC][slice][8 dwords], then (d8, sum of q)
@@ -505,7 +544,7 @@ template <int TYPE, int NC>
 static void launch_nc(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, void* y, int y_dtype,
                       hipStream_t stream) {
   constexpr int RW = NC <= 4 ? 4 : 2;
-  const unsigned blocks = (unsigned)((nrows + kGemvWaves * RW - 1) / (kGemvWaves * RW));
+  const unsigned blocks = (unsigned)std::min((nrows + kGemvWaves * RW - 1) / (kGemvWaves * RW), kGemvRawGrid);
   gemv_raw_kernel<TYPE, NC, RW><<<blocks, 64 * kGemvWaves, 0, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype);
 }
 
@@ -542,6 +581,12 @@ hipError_t launch_gemv_raw(int type, const uint8_t* W, int64_t row_bytes, int nr
     case kQ4_K: launch_type<kQ4_K>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream); break;
     case kIQ4_XS: launch_type<kIQ4_XS>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream); break;
     case kQ6_K: launch_type<kQ6_K>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream); break;
+    case kQ2_K: launch_type<kQ2_K>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream); break;
+    case kIQ2_XXS: launch_type<kIQ2_XXS>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream); break;
+    case kIQ2_XS: launch_type<kIQ2_XS>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream); break;
+    case kIQ2_S: launch_type<kIQ2_S>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream); break;
+    case kIQ3_XXS: launch_type<kIQ3_XXS>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream); break;
+    case kIQ1_M: launch_type<kIQ1_M>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

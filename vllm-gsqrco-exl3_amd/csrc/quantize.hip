@@ -4,10 +4,11 @@
 //  * block_q8_1 (decode GEMV input), lcpp_shim.cu:274-294: per 32 values d = amax/127 (IEEE
 //    division), q = amax == 0 ? 0 : roundf(x/d), sum by a 32-lane xor butterfly with offsets
 //    16, 8, 4, 2, 1, stored as half2(d, sum) followed by 32 int8; block (row, k/32) row-major.
-//  * block_q8_1_mmq (GEMM input), lcpp_shim.cu:298-355: per 32 values d_inv = 127/amax,
-//    q = roundf(x*d_inv), d = 1/d_inv; 144-byte blocks of 128 values, block index
-//    (k/128)*n + row, 16 bytes of scales (4 x fp32 d, or 4 x half2(d, sum) for Q4_K) then 128
-//    int8. An all-zero 32-block stores q = 0, d = 0 (the reference's NaN -> 0 conversion).
+//  * block_q8_1_mmq (GEMM input), lcpp_shim.cu:298-355: per 32 values (64 for Q2_K) d_inv =
+//    127/amax, q = roundf(x*d_inv), d = 1/d_inv; 144-byte blocks of 128 values, block index
+//    (k/128)*n + row, 16 bytes of scales (4 x fp32 d; 4 x half2(d, sum) for Q4_K; for Q2_K
+//    half d of each 64 values and half sums of the first six 16-value groups) then 128 int8.
+//    An all-zero scale group stores q = 0, d = 0 (the reference's NaN -> 0 conversion).
 //  * the xq layout of the MFMA GEMMs (xq.h): either arithmetic above, values placed as MFMA B
 //    operands (and a converter from block_q8_1 bytes).
 //
@@ -56,9 +57,18 @@ __global__ void __launch_bounds__(256) quantize_q8_1_kernel(const void* __restri
   }
 }
 
-template <int DT, bool DS4>
+// block_q8_1_mmq scale layouts (mmq.cuh:60-100): D4 (IQ types, Q6_K), DS4 (Q4_K), D2S6 (Q2_K)
+constexpr int kD4 = 0, kDS4 = 1, kD2S6 = 2;
+
+__host__ __device__ constexpr int mmq_layout(int type) { return type == kQ4_K ? kDS4 : type == kQ2_K ? kD2S6 : kD4; }
+
+// One lane per 4 values. D4 / DS4: scale per 32 values (8 lanes); D2S6: d per 64 values (16
+// lanes) and the sums of 16 values (4 lanes) for the first 96 of each 128.
+template <int DT, int LAYOUT>
 __global__ void __launch_bounds__(128) quantize_q8_1_mmq_kernel(const void* __restrict__ x, uint8_t* __restrict__ y,
                                                                 int64_t k, int64_t s01, int n) {
+  constexpr int kScaleLanes = LAYOUT == kD2S6 ? 16 : 8;
+  constexpr int kSumLanes = LAYOUT == kD2S6 ? 4 : 8;
   const int64_t row = blockIdx.x;
   const int64_t i0 = ((int64_t)blockIdx.y * 128 + threadIdx.x) * 4;
   if (i0 >= k) return;  // k % 512 == 0: whole blocks exit together
@@ -68,9 +78,10 @@ __global__ void __launch_bounds__(128) quantize_q8_1_mmq_kernel(const void* __re
   float amax = fmaxf(fmaxf(fmaxf(fabsf(x0), fabsf(x1)), fabsf(x2)), fabsf(x3));
   float sum = ((x0 + x1) + x2) + x3;
 #pragma unroll
-  for (int off = 4; off > 0; off >>= 1) {
-    amax = fmaxf(amax, __shfl_xor(amax, off, 8));
-    if constexpr (DS4) sum += __shfl_xor(sum, off, 8);
+  for (int off = kScaleLanes / 2; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, kScaleLanes));
+  if constexpr (LAYOUT != kD4) {
+#pragma unroll
+    for (int off = kSumLanes / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off, kSumLanes);
   }
   int q0 = 0, q1 = 0, q2 = 0, q3 = 0;
   float d = 0.0f;
@@ -87,8 +98,14 @@ __global__ void __launch_bounds__(128) quantize_q8_1_mmq_kernel(const void* __re
   uint8_t* b = y + ib * 144;
   *(uint32_t*)(b + 16 + iqs) = (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) |
                                ((uint32_t)(q2 & 0xFF) << 16) | ((uint32_t)(q3 & 0xFF) << 24);
-  if (iqs % 32 == 0) {
-    if constexpr (DS4) {
+  if constexpr (LAYOUT == kD2S6) {
+    // halves: [d of values 0..63, d of 64..127, sums of the 16-value groups 0..5]
+    if (iqs % 16 == 0 && iqs < 96) {
+      ((__half*)b)[2 + iqs / 16] = __float2half_rn(sum);
+      if (iqs % 64 == 0) ((__half*)b)[iqs / 64] = __float2half_rn(d);
+    }
+  } else if (iqs % 32 == 0) {
+    if constexpr (LAYOUT == kDS4) {
       const uint32_t dh = __half_as_ushort(__float2half_rn(d));
       const uint32_t sh = __half_as_ushort(__float2half_rn(sum));
       *(uint32_t*)(b + 4 * (iqs / 32)) = dh | (sh << 16);
@@ -306,10 +323,11 @@ hipError_t launch_quantize(const void* x, int dtype, int64_t n, int64_t k, int64
     return hipGetLastError();
   }
   const dim3 grid((unsigned)n, (unsigned)((k + 511) / 512));
-  const bool ds4 = type == kQ4_K;
-#define GGUF_QMMQ(DT)                                                                                     \
-  if (ds4) quantize_q8_1_mmq_kernel<DT, true><<<grid, 128, 0, stream>>>(x, (uint8_t*)y, k, s01, (int)n); \
-  else quantize_q8_1_mmq_kernel<DT, false><<<grid, 128, 0, stream>>>(x, (uint8_t*)y, k, s01, (int)n);
+  const int layout = mmq_layout(type);
+#define GGUF_QMMQ(DT)                                                                                           \
+  if (layout == kDS4) quantize_q8_1_mmq_kernel<DT, kDS4><<<grid, 128, 0, stream>>>(x, (uint8_t*)y, k, s01, (int)n);   \
+  else if (layout == kD2S6) quantize_q8_1_mmq_kernel<DT, kD2S6><<<grid, 128, 0, stream>>>(x, (uint8_t*)y, k, s01, (int)n); \
+  else quantize_q8_1_mmq_kernel<DT, kD4><<<grid, 128, 0, stream>>>(x, (uint8_t*)y, k, s01, (int)n);
   switch (dtype) {
     case kF32: GGUF_QMMQ(kF32) break;
     case kF16: GGUF_QMMQ(kF16) break;

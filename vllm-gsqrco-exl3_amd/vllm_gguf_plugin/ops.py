@@ -11,8 +11,9 @@ from . import _C_gguf
 from .quantization.utils import WeightType
 
 LCPP_ENABLED = os.environ.get("VLLM_GGUF_LCPP", "1") != "0"
-# the types this build's kernels serve (the reference's Route L set also names Q2_K, IQ2_*,
-# IQ3_XXS and IQ1_M, which route to no op here)
-LCPP_QUANT_TYPES = frozenset({WeightType.Q4_K, WeightType.Q6_K, WeightType.IQ3_S, WeightType.IQ4_XS})
+# the Route L types (reference ops.py:85-115), all served by this build's kernels
+LCPP_QUANT_TYPES = frozenset({
+    WeightType.Q2_K, WeightType.Q4_K, WeightType.Q6_K, WeightType.IQ2_XXS, WeightType.IQ2_XS, WeightType.IQ2_S,
+    WeightType.IQ3_XXS, WeightType.IQ3_S, WeightType.IQ4_XS, WeightType.IQ1_M})
 
 _C_gguf.register()

@@ -1,11 +1,13 @@
-"""Load-time repack of IQ3_S weight rows into this build's tile layout, in place.
+"""Load-time repack of IQ3 weight rows into this build's layout, in place.
 
 Replaces the reference's quantization/iq3_pack.py (ROWS 36, pack_ 121-131, pack 134-138,
-unpack 141-181) with the same interface over a layout of this build's own: 16-row tiles whose
-1760-byte tile-blocks are ordered for the gfx950 decode GEMV's coalesced 16-byte loads
-(csrc/iq3_tile.h documents the byte map). The permutation runs on the GPU (gguf_iq3_pack in
-libgguf_mi355x.so); it is a bijection (unpack(pack(w)) == w) that keeps every 16-row tile inside
-its own rows' bytes.
+unpack 141-181) with the same interface over layouts of this build's own:
+  * IQ3_S: 16-row tiles whose 1760-byte tile-blocks are ordered for the gfx950 decode GEMV's
+    coalesced 16-byte loads (csrc/iq3_tile.h documents the byte map). The permutation runs on the
+    GPU (gguf_iq3_pack in libgguf_mi355x.so); it is a bijection (unpack(pack(w)) == w) that keeps
+    every 16-row tile inside its own rows' bytes.
+  * IQ3_XXS: the GGUF block layout itself (the identity map): this build's packed ops read IQ3_XXS
+    rows as stored, with the generic kernels.
 """
 
 import torch
@@ -16,14 +18,20 @@ from .utils import WeightType
 ROWS = 16  # rows per tile
 
 
+_BLOCK_BYTES = {WeightType.IQ3_S: 110, WeightType.IQ3_XXS: 98}
+
+
 def _run(w: torch.Tensor, weight_type: int, unpack: bool) -> None:
-    assert WeightType(weight_type) == WeightType.IQ3_S, WeightType(weight_type)
+    weight_type = WeightType(weight_type)
+    assert weight_type in _BLOCK_BYTES, weight_type
     assert w.dim() == 2 and w.dtype == torch.uint8, (w.dim(), w.dtype)
     rows, rb = w.shape
-    assert rows % ROWS == 0 and rb % 110 == 0, w.shape
+    assert rows % ROWS == 0 and rb % _BLOCK_BYTES[weight_type] == 0, w.shape
     assert rows == 1 or w.stride(0) == rb, "rows must be contiguous"
     if not w.is_cuda:
         raise RuntimeError("iq3_pack: W must be a CUDA tensor (the repack runs on the GPU)")
+    if weight_type == WeightType.IQ3_XXS:
+        return
     lib = _capi.load()
     sb = lib.gguf_iq3_pack_scratch_bytes(rows, rb)
     scratch = torch.empty(sb, dtype=torch.uint8, device=w.device)
@@ -33,12 +41,12 @@ def _run(w: torch.Tensor, weight_type: int, unpack: bool) -> None:
 
 
 def pack_(w: torch.Tensor, weight_type: int) -> None:
-    """GGUF IQ3_S rows [rows, row_bytes] (rows % 16 == 0) -> the tile layout, in place."""
+    """GGUF IQ3 rows [rows, row_bytes] (rows % 16 == 0) -> this build's layout, in place."""
     _run(w, weight_type, unpack=False)
 
 
 def pack(w: torch.Tensor, weight_type: int) -> torch.Tensor:
-    """The tile layout of w, as a new tensor of the same shape."""
+    """This build's layout of w, as a new tensor of the same shape."""
     p = w.clone()
     pack_(p, weight_type)
     return p

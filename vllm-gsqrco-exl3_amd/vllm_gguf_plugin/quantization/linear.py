@@ -270,9 +270,10 @@ class GGUFLinearMethod(LinearMethodBase):
             self._pack_iq3(layer)
 
     def _pack_iq3(self, layer: torch.nn.Module) -> None:
-        """Store the layer's IQ3_S runs in the tile layout, in place, and set weight.iq3_packed.
-        All or nothing per layer: every IQ3 run must be IQ3_S with a multiple of 16 rows and
-        16-byte aligned bytes, on the GPU."""
+        """Store the layer's IQ3_S / IQ3_XXS runs in iq3_pack's layout, in place, and set
+        weight.iq3_packed (reference linear.py:437-457); apply() then routes them to the packed
+        ops. All or nothing per layer: every IQ3 run must have a multiple of 16 rows and 16-byte
+        aligned bytes, and be on the GPU (the repack runs there)."""
         weight = layer.weight
         if getattr(weight, "iq3_packed", False):
             return
@@ -283,8 +284,7 @@ class GGUFLinearMethod(LinearMethodBase):
         else:
             runs = [(weight.data, layer.weight_type.weight_type)]
         runs = [(w, t) for w, t in runs if t in _IQ3_TYPES]
-        if (not runs or any(t != WeightType.IQ3_S or w.shape[0] % iq3_pack.ROWS or w.data_ptr() % 16
-                            or not w.is_cuda for w, t in runs)):
+        if not runs or any(w.shape[0] % iq3_pack.ROWS or w.data_ptr() % 16 or not w.is_cuda for w, _ in runs):
             return
         for w, t in runs:
             iq3_pack.pack_(w, t)

@@ -42,8 +42,10 @@ except ImportError:
     # (values per block, bytes per block) of the types this build serves, and the float types
     GGML_QUANT_SIZES = {
         WeightType.F32: (1, 4), WeightType.F16: (1, 2), WeightType.BF16: (1, 2),
-        WeightType.Q4_K: (256, 144), WeightType.Q6_K: (256, 210),
-        WeightType.IQ3_S: (256, 110), WeightType.IQ4_XS: (256, 136),
+        WeightType.Q2_K: (256, 84), WeightType.Q4_K: (256, 144), WeightType.Q6_K: (256, 210),
+        WeightType.IQ2_XXS: (256, 66), WeightType.IQ2_XS: (256, 74), WeightType.IQ2_S: (256, 82),
+        WeightType.IQ3_XXS: (256, 98), WeightType.IQ3_S: (256, 110), WeightType.IQ4_XS: (256, 136),
+        WeightType.IQ1_M: (256, 56),
     }
 
 UNQUANTIZED_TYPES = {WeightType.F32, WeightType.F16, WeightType.BF16}
