@@ -20,8 +20,8 @@ M = 1, 4, 16, 32, 48 on 17408 x 5120, each through the routing table's op), and 
 (numpy dequantise + torch fp32 matmul) timed on the host cores on a bounded sample; and the other
 benchmark configs under "configs": the CPU-path Q4_K 4096x4096 case next to its GPU op, the MTP
 small GEMM (IQ3_S / IQ4_XS / Q6_K at M = 4..48 on the attention shapes), the prefill GEMM
-(M = 512..8192, with MFMA utilisation) and the 64-layer decoder sweep under one CUDA graph
-with a replay bit-exactness check.
+(M = 512..8192, with MFMA utilisation), the six types served by the generic kernels at the gate/up
+shape, and the 64-layer decoder sweep under one CUDA graph with a replay bit-exactness check.
 
 `traffic` (HBM bytes per launch of the dominant kernel) is read from the committed PMC summary
 profiles/gemv_iq3s_persist_17408x5120_m1.traffic.json when present (null otherwise). That summary
@@ -47,9 +47,14 @@ ROTATE_BYTES = 512 << 20       # ... and at least this many weight bytes: twice 
 COPY_BYTES = 256 << 20         # calibration copy: bytes read (and written) per launch
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_iq3s_persist_17408x5120_m1.traffic.json")
 IQ3_S, Q4_K, Q6_K, IQ4_XS = 21, 12, 14, 23
-TYPE_NAME = {IQ3_S: "IQ3_S", Q4_K: "Q4_K", Q6_K: "Q6_K", IQ4_XS: "IQ4_XS"}
-BLOCK = {IQ3_S: 110, Q4_K: 144, Q6_K: 210, IQ4_XS: 136}
-SCALE_OFFSETS = {IQ3_S: (0,), Q4_K: (0, 2), Q6_K: (208,), IQ4_XS: (0,)}
+Q2_K, IQ2_XXS, IQ2_XS, IQ3_XXS, IQ2_S, IQ1_M = 10, 16, 17, 18, 22, 29
+TYPE_NAME = {IQ3_S: "IQ3_S", Q4_K: "Q4_K", Q6_K: "Q6_K", IQ4_XS: "IQ4_XS", Q2_K: "Q2_K", IQ2_XXS: "IQ2_XXS",
+             IQ2_XS: "IQ2_XS", IQ3_XXS: "IQ3_XXS", IQ2_S: "IQ2_S", IQ1_M: "IQ1_M"}
+BLOCK = {IQ3_S: 110, Q4_K: 144, Q6_K: 210, IQ4_XS: 136, Q2_K: 84, IQ2_XXS: 66, IQ2_XS: 74, IQ3_XXS: 98,
+         IQ2_S: 82, IQ1_M: 56}
+SCALE_OFFSETS = {IQ3_S: (0,), Q4_K: (0, 2), Q6_K: (208,), IQ4_XS: (0,), Q2_K: (80, 82), IQ2_XXS: (0,),
+                 IQ2_XS: (0,), IQ3_XXS: (0,), IQ2_S: (0,), IQ1_M: ()}
+PACKED_TYPES = (IQ3_S, IQ3_XXS)  # the types the linear method's repack hook stores packed
 MFMA_I8_PEAK_TOPS = 5000.0     # MI355X dense int8 MFMA
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 
@@ -67,6 +72,11 @@ def make_weights(torch, qt, rows, k, seed):
     for off in SCALE_OFFSETS[qt]:
         s = (torch.randn(nb, device="cuda", generator=g) * 2e-3).abs().half()
         w[:, off:off + 2] = s.view(torch.uint8).view(nb, 2)
+    if qt == IQ1_M:  # fp16 d in the top nibbles of the four scale words (bytes 49, 51, 53, 55)
+        bits = (torch.randn(nb, device="cuda", generator=g) * 2e-3).abs().half().view(torch.int16).int() & 0xFFFF
+        for j in range(4):
+            hi = ((bits >> (4 * j)) & 0xF).to(torch.uint8) << 4
+            w[:, 49 + 2 * j] = (w[:, 49 + 2 * j] & 0x0F) | hi
     return w.view(rows, -1)
 
 
@@ -108,7 +118,7 @@ def op_points(torch, C, iq3_pack, linear, qt, rows, k, ms, ncopies=None, reps=5,
     if ncopies is None:
         ncopies = rotation_copies(rows * (k // 256) * BLOCK[qt])
     ws = [make_weights(torch, qt, rows, k, seed + i) for i in range(ncopies)]
-    packed = qt == IQ3_S
+    packed = qt in PACKED_TYPES
     if packed:
         ws = [iq3_pack.pack(w, qt) for w in ws]
     out = []
@@ -155,6 +165,17 @@ def config_prefill(torch, C, iq3_pack, linear):
                 p["frac_mfma_i8"] = round(p["int8_tops"] / MFMA_I8_PEAK_TOPS, 4)
                 p["frac_mfma_f16"] = round(p["int8_tops"] / MFMA_F16_PEAK_TFLOPS, 4)
             out += pts
+    return out
+
+
+def config_types(torch, C, iq3_pack, linear):
+    """The types served by the generic kernels (Q2_K, IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS packed as the
+    repack hook stores it, IQ1_M) at the gate/up shape 17408 x 5120, M = 1, 4 (decode ops) and 16, 48
+    (product ops; IQ1_M's 8-row MMVQ calls), each through the routing table's op."""
+    out = []
+    for qt in (Q2_K, IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ1_M):
+        out += op_points(torch, C, iq3_pack, linear, qt, 17408, 5120, (1, 4) if qt == IQ1_M else (1, 4, 16, 48),
+                         seed=4000)
     return out
 
 
@@ -321,7 +342,7 @@ def main():
     ap.add_argument("--no-points", action="store_true", help="skip the metric's other (type, M) points")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the other benchmark configs (CPU Q4_K, MTP small GEMM, prefill, 64-layer sweep)")
-    ap.add_argument("--section", choices=["mtp", "prefill", "layers"],
+    ap.add_argument("--section", choices=["mtp", "prefill", "layers", "types"],
                     help="run only this benchmark config and print its JSON (for rocprofv3 counter runs)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--kernel-only", action="store_true",
@@ -345,6 +366,7 @@ def main():
     if args.section:
         fn = {"mtp": lambda: config_mtp(torch, C, iq3_pack, linear),
               "prefill": lambda: config_prefill(torch, C, iq3_pack, linear),
+              "types": lambda: config_types(torch, C, iq3_pack, linear),
               "layers": lambda: {"layer_sweep_64": config_layers(torch, C, iq3_pack, linear, args.steps),
                                  "layer_sweep_64_runs": config_layers(torch, C, iq3_pack, linear, args.steps,
                                                                       merged=True)}}[args.section]
@@ -397,6 +419,7 @@ def main():
         configs = {"cpu_q4k_4096": config_cpu_q4k(torch, C),
                    "mtp_small_gemm": config_mtp(torch, C, iq3_pack, linear),
                    "prefill": config_prefill(torch, C, iq3_pack, linear),
+                   "generic_types": config_types(torch, C, iq3_pack, linear),
                    "layer_sweep_64": config_layers(torch, C, iq3_pack, linear, args.steps),
                    "layer_sweep_64_runs": config_layers(torch, C, iq3_pack, linear, args.steps, merged=True)}
 

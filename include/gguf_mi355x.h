@@ -11,6 +11,9 @@
  *    aligned, K = row_bytes / block_bytes * 256, K % 512 == 0.
  *  - X: fp32 / fp16 / bf16 [n, K], unit inner stride, row stride >= K.
  *  - Y: [n, row] contiguous in X's dtype (the reference's output dtype).
+ *  - type: a GGUF type id of the reference's Route L set (lcpp_shim.cu:676-684): Q2_K 10,
+ *    Q4_K 12, Q6_K 14, IQ2_XXS 16, IQ2_XS 17, IQ3_XXS 18, IQ3_S 21, IQ2_S 22, IQ4_XS 23,
+ *    IQ1_M 29 (no product op for IQ1_M); each op's own type checks are the reference's.
  *  - x_q8 (optional): X already quantised to block_q8_1 by gguf_lcpp_quantize_q8_1(mmq = 0),
  *    contiguous uint8 of >= n*K/32*36 bytes, 16-byte aligned, on X's device.
  *  - Every guard runs before any launch, in the reference's order, with its message; a view
