@@ -1,9 +1,13 @@
-"""Builds libgguf_mi355x.so (the C-ABI library of include/gguf_mi355x.h) for gfx950 with hipcc.
+"""Builds libgguf_mi355x.so (the C-ABI library of include/gguf_mi355x.h) for gfx950 with hipcc,
+and the torch op registration over it.
 
     python vllm-gsqrco-exl3_amd/build.py [--jobs N]
 
 Each csrc/*.hip is compiled to an object in _build/ (in parallel), then linked into
 vllm_gguf_plugin/libgguf_mi355x.so, in-tree, where vllm_gguf_plugin._capi loads it.
+csrc/torch_ops.cpp (host C++ against PyTorch-ROCm's headers) is compiled alongside into
+vllm_gguf_plugin/_C_gguf_ops.so, which links libgguf_mi355x.so next to it and registers
+torch.ops._C_gguf when vllm_gguf_plugin._C_gguf loads it.
 """
 
 import argparse
@@ -16,6 +20,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 OUT = os.path.join(HERE, "vllm_gguf_plugin", "libgguf_mi355x.so")
+OPS_OUT = os.path.join(HERE, "vllm_gguf_plugin", "_C_gguf_ops.so")
+CXX = os.environ.get("CXX", "g++")
 ARCH = os.environ.get("GGUF_OFFLOAD_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
@@ -43,11 +49,49 @@ def _compile(src):
     return obj, err
 
 
+def _torch_flags():
+    """Include / library directories and ABI flag of the installed PyTorch (ROCm build)."""
+    import torch
+
+    tdir = os.path.dirname(torch.__file__)
+    inc = [os.path.join(tdir, "include"), os.path.join(tdir, "include", "torch", "csrc", "api", "include"),
+           "/opt/rocm/include"]
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    return inc, os.path.join(tdir, "lib"), abi
+
+
+def _compile_ops():
+    """csrc/torch_ops.cpp -> _build/torch_ops.o (host C++ only)."""
+    inc, _, abi = _torch_flags()
+    obj = os.path.join(BUILD, "torch_ops.o")
+    cmd = [CXX, "-O2", "-std=c++17", "-fPIC", "-c", os.path.join(CSRC, "torch_ops.cpp"), "-o", obj,
+           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           "-Wall", "-Wno-unused-function", *[f"-I{d}" for d in inc]]
+    p = subprocess.run(cmd, capture_output=True, text=True)
+    if p.returncode != 0:
+        raise RuntimeError(f"{CXX} failed on torch_ops.cpp:\n{p.stderr}")
+    return obj, p.stderr
+
+
+def _link_ops(obj):
+    _, libdir, _ = _torch_flags()
+    tmp = OPS_OUT + ".tmp"
+    cmd = [CXX, "-shared", "-fPIC", "-o", tmp, obj, f"-L{os.path.dirname(OUT)}", "-lgguf_mi355x",
+           f"-L{libdir}", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip",
+           "-L/opt/rocm/lib", "-lamdhip64", "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{libdir}"]
+    p = subprocess.run(cmd, capture_output=True, text=True)
+    if p.returncode != 0:
+        raise RuntimeError(f"link of _C_gguf_ops.so failed:\n{p.stderr}")
+    os.replace(tmp, OPS_OUT)
+
+
 def build(jobs: int = 8, verbose: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
     srcs = sources()
-    with cf.ThreadPoolExecutor(max_workers=max(1, min(jobs, len(srcs)))) as ex:
+    with cf.ThreadPoolExecutor(max_workers=max(1, min(jobs, len(srcs) + 1))) as ex:
+        ops = ex.submit(_compile_ops)
         results = list(ex.map(_compile, srcs))
+        ops_obj, ops_err = ops.result()
     for _, err in results:
         if err.strip() and verbose:
             print(err, file=sys.stderr)
@@ -58,6 +102,9 @@ def build(jobs: int = 8, verbose: bool = False) -> str:
     if p.returncode != 0:
         raise RuntimeError(f"link failed:\n{p.stderr}")
     os.replace(tmp, OUT)
+    if ops_err.strip() and verbose:
+        print(ops_err, file=sys.stderr)
+    _link_ops(ops_obj)
     return OUT
 
 
