@@ -111,10 +111,20 @@ def time_graphs(torch, graphs, reps):
     return s.elapsed_time(e) / reps
 
 
-def op_points(torch, C, iq3_pack, linear, qt, rows, k, ms, ncopies=None, reps=5, seed=0):
-    """us/call of the routing table's op for a qt weight [rows, k] at each M in ms (bf16 X N(0,1)),
-    over ncopies weight copies (default: rotation_copies) captured in one graph per M. IQ3_S in the
-    packed tile layout."""
+def x_outliers(torch, m, k, seed):
+    """BASELINE configs[3]'s activations: bf16 N(0,1) with a seeded 1 % of the entries set to +-20
+    (the same recipe as the tests' x_bench), drawn on the device."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    x = torch.randn(m, k, device="cuda", generator=g)
+    mask = torch.rand(m, k, device="cuda", generator=g) < 0.01
+    x = torch.where(mask, 20.0 * torch.sign(torch.randn(m, k, device="cuda", generator=g)), x)
+    return x.to(torch.bfloat16)
+
+
+def op_points(torch, C, iq3_pack, linear, qt, rows, k, ms, ncopies=None, reps=5, seed=0, outliers=False):
+    """us/call of the routing table's op for a qt weight [rows, k] at each M in ms (bf16 X N(0,1),
+    with outliers: x_outliers), over ncopies weight copies (default: rotation_copies) captured in
+    one graph per M. IQ3_S in the packed tile layout (IQ3_XXS packed too: the identity)."""
     if ncopies is None:
         ncopies = rotation_copies(rows * (k // 256) * BLOCK[qt])
     ws = [make_weights(torch, qt, rows, k, seed + i) for i in range(ncopies)]
@@ -125,7 +135,7 @@ def op_points(torch, C, iq3_pack, linear, qt, rows, k, ms, ncopies=None, reps=5,
     for m in ms:
         op = linear._lcpp_op(m, qt, rows, k, packed)
         fn = getattr(C, op)
-        x = torch.randn(m, k, device="cuda", dtype=torch.bfloat16)
+        x = x_outliers(torch, m, k, seed + m) if outliers else torch.randn(m, k, device="cuda", dtype=torch.bfloat16)
         g = graph(torch, [lambda w=w, x=x, fn=fn: fn(w, x, qt, rows) for w in ws])
         us = time_graphs(torch, [g], reps) * 1e3 / len(ws)
         wb = ws[0].numel()
@@ -152,13 +162,13 @@ def config_mtp(torch, C, iq3_pack, linear):
 
 def config_prefill(torch, C, iq3_pack, linear):
     """benchmark configs[3]: prefill GEMM at M = 512, 2048, 8192 over K = 5120, N = 17408 and 5120,
-    IQ3_S (packed), Q4_K, Q6_K; int8 TOP/s against the dense int8 MFMA peak (X bf16 N(0,1) with 1%
-    outliers of magnitude 20 in the reference recipe; plain N(0,1) here, which times the same)."""
+    IQ3_S (packed), Q4_K, Q6_K; int8 TOP/s against the dense int8 MFMA peak; X bf16 N(0,1) with 1 %
+    outliers of magnitude 20 (the config's recipe)."""
     out = []
     for qt in (IQ3_S, Q4_K, Q6_K):
         for rows in (17408, 5120):
             pts = op_points(torch, C, iq3_pack, linear, qt, rows, 5120, (512, 2048, 8192), ncopies=2, reps=2,
-                            seed=3000)
+                            seed=3000, outliers=True)
             for p in pts:
                 # IQ3_S and Q4_K run on fp16 MFMAs (exact sub-scaled integer operands), Q6_K on int8
                 p["mfma"] = "f16" if qt in (IQ3_S, Q4_K) else "i8"
@@ -230,9 +240,55 @@ def config_layers(torch, C, iq3_pack, linear, steps, ms=(1, 4, 16, 32), nlayers=
     return out
 
 
+def _cpu_model():
+    """The host CPU's model name (lscpu's 'Model name', from /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _median_s(fn, runs=5):
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times)
+
+
+def _cpu_path_times(torch, o, raw, qt, rows, k, ms, threads):
+    """The CPU reference path on GGUF rows raw [rows, ...]: numpy dequantise (median of 5), then
+    per M and thread count the q8_1 round trip of X plus the torch fp32 matmul (median of 5).
+    Returns (dequant seconds, {(m, threads): matmul seconds})."""
+    import numpy as np
+
+    holder = {}
+    t_deq = _median_s(lambda: holder.__setitem__("W", o.dequantize(raw.reshape(-1), qt).reshape(rows, k)))
+    W = torch.from_numpy(holder["W"])
+    mm = {}
+    for m in ms:
+        x = np.random.default_rng(m).standard_normal((m, k)).astype(np.float32)
+
+        def run():
+            q, d, _ = o.dequant_q8_1(o.quantize_q8_1(x), m, k)
+            xq = torch.from_numpy((q.astype(np.float32).reshape(m, -1, 32) * d[..., None]).reshape(m, k))
+            (xq @ W.T).sum().item()
+
+        for th in threads:
+            torch.set_num_threads(th)
+            mm[(m, th)] = _median_s(run)
+    return t_deq, mm
+
+
 def config_cpu_q4k(torch, C):
     """benchmark configs[0]: Q4_K 4096x4096 at M = 1, fp32 X N(0,1): the GPU op next to the CPU
-    reference path (numpy dequantise + q8_1 round trip + torch fp32 matmul), seed 0."""
+    reference path (numpy dequantise + q8_1 round trip + torch fp32 matmul), seed 0; dequantise and
+    matmul each the median of 5, the matmul on all threads and on one."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
 
@@ -240,48 +296,65 @@ def config_cpu_q4k(torch, C):
 
     rows = k = 4096
     raw = o.random_blocks(np.random.default_rng(0), o.Q4_K, rows, k, scale_sigma=1e-3)
+    threads = torch.get_num_threads()
+    t_deq, mm = _cpu_path_times(torch, o, raw, o.Q4_K, rows, k, (1,), (threads, 1))
+    torch.set_num_threads(threads)
     x = np.random.default_rng(0).standard_normal((1, k)).astype(np.float32)
-    times = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        W = torch.from_numpy(o.dequantize(raw.reshape(-1), o.Q4_K).reshape(rows, k))
-        q, d, _ = o.dequant_q8_1(o.quantize_q8_1(x), 1, k)
-        xq = torch.from_numpy((q.astype(np.float32).reshape(1, -1, 32) * d[..., None]).reshape(1, k))
-        (xq @ W.T).sum().item()
-        times.append(time.perf_counter() - t0)
     wd = torch.from_numpy(raw).cuda()
     xd = torch.from_numpy(x).cuda()
     g = graph(torch, [lambda: C.lcpp_mul_mat_vec_own(wd, xd, Q4_K, rows)] * 8)
     us = time_graphs(torch, [g], 10) * 1e3 / 8
     return {"shape": "4096x4096", "m": 1, "op": "lcpp_mul_mat_vec_own", "gpu_us_per_call": round(us, 2),
-            "cpu_us_per_call": round(statistics.median(times) * 1e6, 1), "cpu_cores": os.cpu_count() or 1}
+            "cpu_us_per_call": round((t_deq + mm[(1, threads)]) * 1e6, 1),
+            "cpu_us_per_call_1_thread": round((t_deq + mm[(1, 1)]) * 1e6, 1),
+            "cpu_dequant_us": round(t_deq * 1e6, 1), "cpu_matmul_us": round(mm[(1, threads)] * 1e6, 1),
+            "cpu_matmul_us_1_thread": round(mm[(1, 1)] * 1e6, 1), "cpu_threads": threads,
+            "nproc": os.cpu_count() or 1, "cpu_model": _cpu_model()}
+
+
+CPU_SAMPLE_ROWS = 2048  # rows of each config-2 shape the CPU path dequantises and multiplies
 
 
 def cpu_baseline(torch):
     """The oracle's CPU path (numpy dequantise, q8_1 round trip of X, torch fp32 matmul) on the
-    host cores: IQ3_S 17408 x 5120 at M = 1 (config 2's gate shape); median of 3 runs."""
+    host cores, on the headline workload (configs[1]: IQ3_S at M = 1 and 4 on 17408 x 5120 and
+    5120 x 17408), bounded: CPU_SAMPLE_ROWS weight rows of each shape, each part the median of 5,
+    per-call times scaled to the full row count (both parts are linear in the rows). `value`: the
+    four calls' weight bytes over their summed CPU time on all threads (torch's thread count; the
+    dequantise is numpy, one thread); also on one thread, per case, and dequantise / matmul apart."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
 
     import gguf_oracle as o
 
-    threads = os.cpu_count() or 1
+    threads = torch.get_num_threads()
+    cases, tot_bytes, tot_s, tot_s1 = [], 0, 0.0, 0.0
+    for rows, k in ((17408, 5120), (5120, 17408)):
+        rs = min(rows, CPU_SAMPLE_ROWS)
+        raw = o.random_blocks(np.random.default_rng(rows), o.IQ3_S, rs, k)
+        t_deq, mm = _cpu_path_times(torch, o, raw, o.IQ3_S, rs, k, (1, 4), (threads, 1))
+        scale = rows / rs
+        wbytes = rows * (k // 256) * BLOCK[IQ3_S]
+        for m in (1, 4):
+            t_all = (t_deq + mm[(m, threads)]) * scale
+            t_one = (t_deq + mm[(m, 1)]) * scale
+            tot_bytes += wbytes
+            tot_s += t_all
+            tot_s1 += t_one
+            cases.append({"shape": f"{rows}x{k}", "m": m, "us_per_call": round(t_all * 1e6, 1),
+                          "us_per_call_1_thread": round(t_one * 1e6, 1),
+                          "dequant_us": round(t_deq * scale * 1e6, 1),
+                          "matmul_us": round(mm[(m, threads)] * scale * 1e6, 1),
+                          "matmul_us_1_thread": round(mm[(m, 1)] * scale * 1e6, 1),
+                          "gbps": round(wbytes / t_all / 1e9, 4)})
     torch.set_num_threads(threads)
-    rows, k = 17408, 5120
-    raw = o.random_blocks(np.random.default_rng(0), o.IQ3_S, rows, k)
-    x = np.random.default_rng(1).standard_normal((1, k)).astype(np.float32)
-    times = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        W = torch.from_numpy(o.dequantize(raw.reshape(-1), o.IQ3_S).reshape(rows, k))
-        q, d, _ = o.dequant_q8_1(o.quantize_q8_1(x), 1, k)
-        xq = torch.from_numpy((q.astype(np.float32).reshape(1, -1, 32) * d[..., None]).reshape(1, k))
-        (xq @ W.T).sum().item()
-        times.append(time.perf_counter() - t0)
-    t = statistics.median(times)
-    return {"value": round(raw.nbytes / t / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"IQ3_S 17408x5120 M=1 (config 2 gate), numpy dequant + q8_1 + torch fp32 matmul, "
-                      f"median of 3: {t * 1e6:.0f} us/call"}
+    return {"value": round(tot_bytes / tot_s / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+            "value_1_thread": round(tot_bytes / tot_s1 / 1e9, 4), "nproc": os.cpu_count() or 1,
+            "cpu_model": _cpu_model(),
+            "sample": f"IQ3_S configs[1] (17408x5120 and 5120x17408, M = 1 and 4): the first "
+                      f"{CPU_SAMPLE_ROWS} rows of each shape, numpy dequantise + q8_1 round trip + torch "
+                      f"fp32 matmul, each part the median of 5, scaled to the full rows",
+            "cases": cases}
 
 
 def load_traffic():
