@@ -98,12 +98,12 @@ def exact_ref(raw, qt, x, form="mmvq"):
     q, d, _ = o.dequant_q8_1(o.quantize_q8_1(x), x.shape[0], x.shape[1])
     assert (d == 1).all()
     if qt in o.UNIT_TYPES:
-        if form == "mmvq":
-            y = o.mmvq_slice_units(raw, qt, q).sum(-1)
-        else:
+        if form == "mmvq":  # integers, IQ1_M multiples of 1/8
+            y, den = o.mmvq_slice_units(raw, qt, q).sum(-1), 8 if qt == o.IQ1_M else 1
+        else:               # multiples of 1/den
             dots = o.slice_dots(raw, qt, q)
-            y = dots["dot"].sum(-1) / dots["den"]
-        assert np.abs(y).max() < 2 ** 20
+            y, den = dots["dot"].sum(-1) / dots["den"], dots["den"]
+        assert np.abs(y).max() * den < 2 ** 23  # every partial sum stays exact in fp32
         return y
     dots = o.slice_dots(raw, qt, q)
     y = dots["dot"].sum(-1)

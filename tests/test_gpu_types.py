@@ -112,13 +112,21 @@ def test_iq1m_has_no_mmq_quantiser():
 
 
 # ------------------------------------------------------------------------------------ exact mode
+# (weight rows, K): the one-lane-per-slice GEMV (K / 256 below 8 blocks, or X past the LDS
+# budget of the slices GEMV) and the slices GEMV with X in LDS (rows not a multiple of its 8-row
+# tile; K = 17408 at 1-2 rows)
+DECODE_SHAPES = [(80, 1024), (100, 2048), (96, 17408)]
+
+
 @pytest.mark.parametrize("case", DECODE_CASES, ids=_id)
 @pytest.mark.parametrize("n", [1, 2, 5, 8, 13, 32])
-def test_decode_exact(case, n):
+@pytest.mark.parametrize("rows,k", DECODE_SHAPES)
+def test_decode_exact(case, n, rows, k):
     qt, op = case
     if n > MAX_ROWS.get(op, 8):
         pytest.skip(f"{op} takes at most {MAX_ROWS.get(op, 8)} rows")
-    rows, k = 80, 1024
+    if op.endswith("_packed") and rows % 16:
+        rows = 96
     raw = exact_weights(qt, rows, k, seed=10 * n + qt)
     x = exact_x(n, k, seed=20 * n + qt, dtype=torch.float32)
     y = _call(op, _weights(raw, op, qt), x.cuda(), qt, rows).cpu().numpy()
@@ -304,3 +312,19 @@ def test_iq3xxs_packed_layer(n):
     assert torch.equal(y, ref)
     layout = "mmvq" if n <= 8 else "mmq"
     assert o.rel_l2(y[:, :512].float().cpu().numpy(), o.q81_model(q, o.IQ3_XXS, x.cpu(), layout)) <= TIGHT[torch.bfloat16]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16], ids=str)
+@pytest.mark.parametrize("qt", [o.Q2_K, o.IQ3_XXS, o.IQ1_M], ids=lambda t: TN[t])
+@pytest.mark.parametrize("n,k", [(1, 2048), (3, 5120), (8, 2048), (2, 17408)])
+def test_own_quantisation_equals_x_q8(qt, dtype, n, k):
+    """The decode op quantising X itself (no x_q8; X in any dtype, rows strided) gives the same
+    bytes as on X quantised by lcpp_quantize_q8_1 (itself bit-exact with the oracle)."""
+    rows = 64
+    raw = w_rand(qt, rows, k, seed=1100 + qt)
+    x = x_rand(n, k + 64, seed=1101 + n, dtype=dtype)[:, :k].cuda()  # row stride k + 64
+    q8 = C().lcpp_quantize_q8_1(x, qt, False, False)
+    a = C().lcpp_mul_mat_vec_q(dev(raw), x, qt, rows)
+    b = C().lcpp_mul_mat_vec_q(dev(raw), x, qt, rows, q8)
+    assert torch.equal(a, b)
+    assert o.rel_l2(a.float().cpu().numpy(), o.q81_model(raw, qt, x.cpu())) <= TIGHT[dtype] if dtype != torch.float32 else 1e-3

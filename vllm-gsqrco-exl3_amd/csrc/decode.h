@@ -258,28 +258,29 @@ __device__ __forceinline__ void decode_iq2s_q(const uint8_t* b, int u, int q, co
 }
 
 // block_iq3_xxs: d[0:2], qs[2:66] grid indices (one per 4 values), then per slice u a dword at
-// 66 + 4u: four 7-bit sign indices (one per 8 values) and the scale (bits 28..31)
+// 66 + 4u: four 7-bit sign indices (one per 8 values) and the scale (bits 28..31). grid: the
+// signed table (kIq3xxsSigned), indexed by grid index | sign nibble << 8.
+__device__ __forceinline__ void iq3xxs_words(uint32_t q2, uint32_t aux, int g, const uint32_t* grid, int& w0,
+                                             int& w1) {  // q2: the two grid indices of group g
+  const uint32_t sg = ksigns8((aux >> (7 * g)) & 127);
+  w0 = (int)grid[(q2 & 0xFF) | ((sg & 0xF) << 8)];
+  w1 = (int)grid[((q2 >> 8) & 0xFF) | ((sg >> 4) << 8)];
+}
+
 __device__ __forceinline__ void decode_iq3xxs(const uint8_t* b, int u, const uint32_t* grid, int (&w)[8],
                                               SliceScale& s) {
   const uint64_t qi = ld64(b + 2 + 8 * u);
   const uint32_t aux = ld32(b + 66 + 4 * u);
 #pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    const uint32_t sg = ksigns8((aux >> (7 * g)) & 127);
-    w[2 * g] = apply_signs(grid[(qi >> (16 * g)) & 0xFF], sg & 0xF);
-    w[2 * g + 1] = apply_signs(grid[(qi >> (16 * g + 8)) & 0xFF], sg >> 4);
-  }
+  for (int g = 0; g < 4; ++g) iq3xxs_words((uint32_t)(qi >> (16 * g)), aux, g, grid, w[2 * g], w[2 * g + 1]);
   s.d = half_bits_to_float(ld16(b));
   s.ls = 2 * (int)(aux >> 28) + 1;
 }
 
 __device__ __forceinline__ void decode_iq3xxs_q(const uint8_t* b, int u, int q, const uint32_t* grid, int (&w)[2],
                                                 SliceScale& s) {
-  const uint32_t i2 = ld16(b + 2 + 8 * u + 2 * q);
   const uint32_t aux = ld32(b + 66 + 4 * u);
-  const uint32_t sg = ksigns8((aux >> (7 * q)) & 127);
-  w[0] = apply_signs(grid[i2 & 0xFF], sg & 0xF);
-  w[1] = apply_signs(grid[i2 >> 8], sg >> 4);
+  iq3xxs_words(ld16(b + 2 + 8 * u + 2 * q), aux, q, grid, w[0], w[1]);
   s.d = half_bits_to_float(ld16(b));
   s.ls = 2 * (int)(aux >> 28) + 1;
 }
@@ -369,9 +370,9 @@ struct Codebook<kIQ3_S> {
 };
 template <>
 struct Codebook<kIQ3_XXS> {
-  static constexpr int n = 256;
+  static constexpr int n = 4096;  // the signed table
   using T = uint32_t;
-  static __device__ T at(int i) { return kIq3xxsGrid.v[i]; }
+  static __device__ T at(int i) { return kIq3xxsSigned.v[i]; }
 };
 template <>
 struct Codebook<kIQ2_XXS> {
@@ -441,6 +442,132 @@ __device__ __forceinline__ void decode_quarter(const uint8_t* b, int u, int q, c
 // types with a sub-scale per 16 values (two integer dots per slice)
 __host__ __device__ constexpr bool per16_type(int type) {
   return type == kQ6_K || type == kQ2_K || type == kIQ2_XS || type == kIQ2_S || type == kIQ1_M;
+}
+
+// ---------------------------------------------------------------------------------- raw slices
+// The bytes one lane needs to decode slice u of a block of the generic types, loaded by
+// raw_load and decoded by raw_decode into the same words and scales as decode_slice: a GEMV can
+// issue the next block's loads before it computes the current one.
+template <int TYPE>
+struct RawSlice;
+template <>
+struct RawSlice<kIQ2_XXS> {
+  uint32_t d, idx, aux;
+};
+template <>
+struct RawSlice<kIQ2_XS> {
+  uint32_t d, sc;
+  uint64_t q;
+};
+template <>
+struct RawSlice<kIQ2_S> {
+  uint32_t d, lo, sg, qh, sc;
+};
+template <>
+struct RawSlice<kIQ3_XXS> {
+  uint32_t d, aux;
+  uint64_t qi;
+};
+template <>
+struct RawSlice<kIQ1_M> {
+  uint32_t qs, qh;
+  uint64_t sc;
+};
+template <>
+struct RawSlice<kQ2_K> {
+  uint32_t q[8], sc, dm;
+};
+
+template <int TYPE>
+__device__ __forceinline__ void raw_load(const uint8_t* b, int u, RawSlice<TYPE>& r) {
+  if constexpr (TYPE == kIQ2_XXS) {
+    r.d = ld16(b);
+    r.idx = ld32(b + 2 + 8 * u);
+    r.aux = ld32(b + 6 + 8 * u);
+  } else if constexpr (TYPE == kIQ2_XS) {
+    r.d = ld16(b);
+    r.q = ld64(b + 2 + 8 * u);
+    r.sc = b[66 + u];
+  } else if constexpr (TYPE == kIQ2_S) {
+    r.d = ld16(b);
+    r.lo = ld32(b + 2 + 4 * u);
+    r.sg = ld32(b + 34 + 4 * u);
+    r.qh = b[66 + u];
+    r.sc = b[74 + u];
+  } else if constexpr (TYPE == kIQ3_XXS) {
+    r.d = ld16(b);
+    r.qi = ld64(b + 2 + 8 * u);
+    r.aux = ld32(b + 66 + 4 * u);
+  } else if constexpr (TYPE == kIQ1_M) {
+    r.qs = ld32(b + 4 * u);
+    r.qh = ld16(b + 32 + 2 * u);
+    r.sc = ld64(b + 48);
+  } else {
+    const uint8_t* qs = b + 16 + 32 * (u >> 2);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r.q[e] = ld32(qs + 4 * e);
+    r.sc = ld16(b + 2 * u);
+    r.dm = ld32(b + 80);
+  }
+}
+
+template <int TYPE>
+__device__ __forceinline__ void raw_decode(const RawSlice<TYPE>& r, int u, const typename Codebook<TYPE>::T* grid,
+                                           int (&w)[8], SliceScale& s) {
+  if constexpr (TYPE == kIQ2_XXS) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      signed_grid8(grid[(r.idx >> (8 * g)) & 0xFF], ksigns8((r.aux >> (7 * g)) & 127), w[2 * g], w[2 * g + 1]);
+    s.d = half_bits_to_float(r.d);
+    s.ls = 2 * (int)(r.aux >> 28) + 1;
+  } else if constexpr (TYPE == kIQ2_XS) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const uint32_t v = (uint32_t)(r.q >> (16 * g)) & 0xFFFF;
+      signed_grid8(grid[v & 511], ksigns8(v >> 9), w[2 * g], w[2 * g + 1]);
+    }
+    s.d = half_bits_to_float(r.d);
+    s.ls = 2 * (int)(r.sc & 0xF) + 1;
+    s.ls2 = 2 * (int)(r.sc >> 4) + 1;
+  } else if constexpr (TYPE == kIQ2_S) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      signed_grid8(grid[((r.lo >> (8 * g)) & 0xFF) | (((r.qh >> (2 * g)) & 3u) << 8)], (r.sg >> (8 * g)) & 0xFF,
+                   w[2 * g], w[2 * g + 1]);
+    s.d = half_bits_to_float(r.d);
+    s.ls = 2 * (int)(r.sc & 0xF) + 1;
+    s.ls2 = 2 * (int)(r.sc >> 4) + 1;
+  } else if constexpr (TYPE == kIQ3_XXS) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) iq3xxs_words((uint32_t)(r.qi >> (16 * g)), r.aux, g, grid, w[2 * g], w[2 * g + 1]);
+    s.d = half_bits_to_float(r.d);
+    s.ls = 2 * (int)(r.aux >> 28) + 1;
+  } else if constexpr (TYPE == kIQ1_M) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const uint32_t nib = (r.qh >> (4 * g)) & 0xF;
+      const uint32_t e = grid[((r.qs >> (8 * g)) & 0xFF) | ((nib & 7) << 8)];
+      const uint32_t t = (nib & 8) ? 0x0007FFF7u : 0x000901F9u;
+      w[2 * g] = (int)__builtin_amdgcn_perm(t, t, e & 0x0F0F0F0Fu);
+      w[2 * g + 1] = (int)__builtin_amdgcn_perm(t, t, (e >> 4) & 0x0F0F0F0Fu);
+    }
+    const uint32_t s0 = (uint32_t)r.sc & 0xFFFF, s1 = (uint32_t)(r.sc >> 16) & 0xFFFF,
+                   s2 = (uint32_t)(r.sc >> 32) & 0xFFFF, s3 = (uint32_t)(r.sc >> 48);
+    s.d = half_bits_to_float((s0 >> 12) | ((s1 >> 8) & 0xF0) | ((s2 >> 4) & 0xF00) | (s3 & 0xF000));
+    const uint32_t sw = (uint32_t)(r.sc >> (16 * (u >> 1)));  // scales of 16-value groups 2u, 2u + 1
+    s.ls = 2 * (int)((sw >> (6 * (u & 1))) & 7) + 1;
+    s.ls2 = 2 * (int)((sw >> (6 * (u & 1) + 3)) & 7) + 1;
+  } else {
+    const int sh = 2 * (u & 3);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) w[e] = (int)((r.q[e] >> sh) & 0x03030303u);
+    s.d = half_bits_to_float(r.dm & 0xFFFF);
+    s.dmin = half_bits_to_float(r.dm >> 16);
+    s.ls = (int)(r.sc & 0xF);
+    s.m = (int)((r.sc >> 4) & 0xF);
+    s.ls2 = (int)((r.sc >> 8) & 0xF);
+    s.m2 = (int)(r.sc >> 12);
+  }
 }
 
 }  // namespace gguf

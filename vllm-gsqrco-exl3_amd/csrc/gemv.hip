@@ -159,6 +159,143 @@ __global__ void __launch_bounds__(256) gemv_raw_kernel(const uint8_t* __restrict
   }
 }
 
+// The generic types' decode GEMV with X in LDS: a persistent workgroup of 8 waves loops over
+// 8-row tiles; the waves split each tile's K blocks; lane 8r + c decodes slice c of row r of each
+// block of its share (decode.h, the codebook in LDS), so a row's 8 lanes read the block's bytes
+// contiguously and each load instruction covers 8 rows. X's q8_1 (values, d8 and, for Q2_K, the
+// int16 sums of each 16-value half) is copied into LDS once per workgroup and read by every tile;
+// lanes of the same slice read the same LDS words (broadcast). The slice term is mmvq_term (the
+// decode ops' arithmetic); partial sums over a row's 8 lanes by xor shuffles, then over the waves
+// in wave order. X quantised inside the kernel (as the packed
+// IQ3_S GEMV does) was measured slower at every row count: 24.1 against 18.5 us for IQ3_XXS
+// 17408 x 5120 at one row, quantise launch included.
+constexpr int kSlicesWaves = 8;
+constexpr int kSlicesXBudget = 48 * 1024;  // LDS bytes for X (40 per slice and activation row)
+
+template <int TYPE, int NC, int RPL>
+__global__ void __launch_bounds__(64 * kSlicesWaves) gemv_slices_kernel(const uint8_t* __restrict__ W,
+                                                                        int64_t row_bytes, int nrows, int k,
+                                                                        const uint8_t* __restrict__ q8,
+                                                                        void* __restrict__ y, int y_dtype) {
+  constexpr int TR = 8 * RPL;  // rows per tile: lane 8r + c takes rows r, r + 8, ...
+  __shared__ typename Codebook<TYPE>::T grid[Codebook<TYPE>::n];
+  __shared__ float red[2][kSlicesWaves][NC][TR];
+  extern __shared__ uint4 xdyn[];
+  constexpr int BS = block_bytes(TYPE);
+  const int nslices = k / kQ81, nb = k / kQK;
+  uint32_t* xq = (uint32_t*)xdyn;                // [NC][nslices][8] q8 words
+  float* xd = (float*)(xq + NC * nslices * 8);   // [NC][nslices] d8
+  int* xs = (int*)(xd + NC * nslices);           // [NC][nslices] Q2_K: sums of the halves
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane >> 3, c = lane & 7;
+  const int ntiles = (nrows + TR - 1) / TR;
+  const int G = gridDim.x;
+  const int b0 = wave * nb / kSlicesWaves, per = (wave + 1) * nb / kSlicesWaves - b0;  // per >= 1
+  const int my_tiles = (int)blockIdx.x < ntiles ? (ntiles - 1 - (int)blockIdx.x) / G + 1 : 0;
+  const int items = my_tiles * per;  // (tile, block) pairs of this wave, tile-major
+  // item it -> the block bytes of row r + 8i of its tile (rows past the end re-read the last row;
+  // items past the end re-read the last item: the loads need no branch)
+  auto block_ptr = [&](int it, int i) {
+    it = min(it, items - 1);
+    const int tile = (int)blockIdx.x + (it / per) * G;
+    const int row = min(tile * TR + 8 * i + r, nrows - 1);
+    return W + (int64_t)row * row_bytes + (int64_t)(b0 + it % per) * BS;
+  };
+  auto load = [&](int it, RawSlice<TYPE> (&raw)[RPL]) {
+#pragma unroll
+    for (int i = 0; i < RPL; ++i) raw_load<TYPE>(block_ptr(it, i), c, raw[i]);
+  };
+  float acc[RPL][NC];
+#pragma unroll
+  for (int i = 0; i < RPL; ++i)
+#pragma unroll
+    for (int cc = 0; cc < NC; ++cc) acc[i][cc] = 0.0f;
+  int par = 0;
+  auto compute = [&](const RawSlice<TYPE> (&raw)[RPL], int it) {
+    int w[RPL][8];
+    SliceScale sc[RPL];
+#pragma unroll
+    for (int i = 0; i < RPL; ++i) raw_decode<TYPE>(raw[i], c, grid, w[i], sc[i]);
+    const int s = (b0 + it % per) * 8 + c;
+#pragma unroll
+    for (int cc = 0; cc < NC; ++cc) {
+      const int xi = cc * nslices + s;
+      const uint4 x0 = *(const uint4*)(xq + 8 * xi), x1 = *(const uint4*)(xq + 8 * xi + 4);
+      const int xv[8] = {(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+      int sq = 0, sq2 = 0;
+      if constexpr (TYPE == kQ2_K) {
+        const int h = xs[xi];
+        sq = (int)(int16_t)(h & 0xFFFF);
+        sq2 = h >> 16;
+      }
+      const float d8 = xd[xi];
+#pragma unroll
+      for (int i = 0; i < RPL; ++i) acc[i][cc] += mmvq_term<TYPE>(w[i], xv, sc[i], d8, sq, sq2);
+    }
+    if (it % per == per - 1) {  // the wave's last block of the tile: reduce and store
+      const int tile = (int)blockIdx.x + (it / per) * G;
+#pragma unroll
+      for (int i = 0; i < RPL; ++i)
+#pragma unroll
+        for (int cc = 0; cc < NC; ++cc) {
+          float v = acc[i][cc];
+          v += __shfl_xor(v, 1, 64);
+          v += __shfl_xor(v, 2, 64);
+          v += __shfl_xor(v, 4, 64);
+          if (c == 0) red[par][wave][cc][8 * i + r] = v;
+          acc[i][cc] = 0.0f;
+        }
+      __syncthreads();
+      if (wave == 0) {
+        for (int o = lane; o < TR * NC; o += 64) {
+          const int rr = o % TR, cc = o / TR;
+          float v = red[par][0][cc][rr];
+#pragma unroll
+          for (int ww = 1; ww < kSlicesWaves; ++ww) v += red[par][ww][cc][rr];
+          const int orow = tile * TR + rr;
+          if (orow < nrows) store_y(y, (int64_t)cc * nrows + orow, v, y_dtype);
+        }
+      }
+      par ^= 1;
+    }
+  };
+  // two blocks in flight: the next item's bytes load while the current one is computed; the
+  // first item's are requested before X is copied
+  RawSlice<TYPE> ra[RPL], rb[RPL];
+  if (items > 0) load(0, ra);
+  __builtin_amdgcn_sched_barrier(0);
+  stage_codebook<TYPE>(grid);
+  for (int i = threadIdx.x; i < NC * nslices; i += blockDim.x) {
+    const uint8_t* src = q8 + (int64_t)i * 36;
+    const u32x4 a = ld128a4(src + 4), b = ld128a4(src + 20);
+    *(uint4*)(xq + 8 * i) = make_uint4(a.x, a.y, a.z, a.w);
+    *(uint4*)(xq + 8 * i + 4) = make_uint4(b.x, b.y, b.z, b.w);
+    xd[i] = half_bits_to_float(*(const uint16_t*)src);
+  }
+  if constexpr (TYPE == kQ2_K) {
+    __syncthreads();
+    for (int i = threadIdx.x; i < NC * nslices; i += blockDim.x) {
+      const uint4 a = *(const uint4*)(xq + 8 * i), b = *(const uint4*)(xq + 8 * i + 4);
+      const int s0 = dot4(0x01010101, (int)a.w, dot4(0x01010101, (int)a.z, dot4(0x01010101, (int)a.y,
+                                                                                 dot4(0x01010101, (int)a.x, 0))));
+      const int s1 = dot4(0x01010101, (int)b.w, dot4(0x01010101, (int)b.z, dot4(0x01010101, (int)b.y,
+                                                                                 dot4(0x01010101, (int)b.x, 0))));
+      xs[i] = (s0 & 0xFFFF) | (s1 << 16);
+    }
+  }
+  __syncthreads();
+  for (int it = 0; it < items; it += 2) {
+    load(it + 1, rb);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(ra, it);
+    if (it + 1 >= items) break;
+    load(it + 2, ra);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(rb, it + 1);
+  }
+}
+
 // X of the row-chunk GEMV, staged in LDS: q8 values [NC][slice][8 dwords], then (d8, sum of q)
 // [NC][slice]. Group g = part g & 3 (8 q bytes) of slice row g >> 2 of the block_q8_1 array; the
 // four lanes of a slice are consecutive, so the slice's sum of q is a quad sum (DPP).
@@ -548,9 +685,44 @@ static void launch_nc(const uint8_t* W, int64_t row_bytes, int nrows, int k, con
   gemv_raw_kernel<TYPE, NC, RW><<<blocks, 64 * kGemvWaves, 0, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype);
 }
 
+// The generic types at up to 8 activation rows whose X fits the LDS budget, on weights of at
+// least 8 K blocks (one per wave).
+static bool slices_supported(int type, int64_t k, int64_t n) {
+  return generic_type(type) && n >= 1 && n <= 8 && k / kQK >= kSlicesWaves &&
+         n * (k / kQ81) * 40 <= kSlicesXBudget;
+}
+
+template <int TYPE>
+static void launch_slices(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n, void* y,
+                          int y_dtype, hipStream_t stream) {
+  constexpr int RPL = 2;  // 16-row tiles: two rows' blocks per lane in flight
+  const int tiles = (nrows + 8 * RPL - 1) / (8 * RPL);
+  const unsigned g = (unsigned)std::min(tiles, persist_grid());
+  const size_t lds = (size_t)n * (k / kQ81) * 40;
+#define GGUF_SLICES(NC) \
+  gemv_slices_kernel<TYPE, NC, RPL><<<g, 64 * kSlicesWaves, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype)
+  switch (n) {
+    case 1: GGUF_SLICES(1); break;
+    case 2: GGUF_SLICES(2); break;
+    case 3: GGUF_SLICES(3); break;
+    case 4: GGUF_SLICES(4); break;
+    case 5: GGUF_SLICES(5); break;
+    case 6: GGUF_SLICES(6); break;
+    case 7: GGUF_SLICES(7); break;
+    default: GGUF_SLICES(8); break;
+  }
+#undef GGUF_SLICES
+}
+
 template <int TYPE>
 static void launch_type(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n, void* y,
                         int y_dtype, hipStream_t stream) {
+  if constexpr (generic_type(TYPE)) {
+    if (slices_supported(TYPE, k, n)) {
+      launch_slices<TYPE>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);
+      return;
+    }
+  }
   switch (n) {
     case 1: launch_nc<TYPE, 1>(W, row_bytes, nrows, k, q8, y, y_dtype, stream); break;
     case 2: launch_nc<TYPE, 2>(W, row_bytes, nrows, k, q8, y, y_dtype, stream); break;

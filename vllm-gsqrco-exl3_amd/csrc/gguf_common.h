@@ -279,6 +279,24 @@ constexpr Lattice32<256> kIq3xxsGrid = make_iq3xxs_grid();
 static_assert(kIq2xxsGrid.v[0] == 0x0808080808080808ull && kIq2sGrid.v[1023] != 0, "iq2 grids");
 static_assert(kIq3xxsGrid.v[0] == 0x04040404u, "iq3xxs grid");
 
+// iq3xxs_grid with the signs applied: entry g | n << 8 is grid word g with the bytes flagged in
+// the 4-bit sign nibble n negated (16 KB), so one lookup yields four signed int8 weights
+constexpr Lattice32<4096> make_iq3xxs_signed() {
+  Lattice32<4096> t{};
+  for (int n = 0; n < 16; ++n)
+    for (int g = 0; g < 256; ++g) {
+      uint32_t e = 0;
+      for (int b = 0; b < 4; ++b) {
+        const uint32_t v = (kIq3xxsGrid.v[g] >> (8 * b)) & 0xFF;
+        e |= (((n >> b) & 1) ? ((0x100u - v) & 0xFF) : v) << (8 * b);
+      }
+      t.v[g | (n << 8)] = e;
+    }
+  return t;
+}
+constexpr Lattice32<4096> kIq3xxsSigned = make_iq3xxs_signed();
+static_assert(kIq3xxsSigned.v[0x100] == 0x040404fcu, "iq3xxs signed grid");
+
 // iq1s_grid (values -1, 0, 1; base-3 digit = value + 1) in nibble form: byte j of entry e holds
 // the digit of value j in its low nibble and that of value j + 4 in its high nibble, so one
 // 32-bit word carries the 8 values and a byte permute maps the digits to weights.
