@@ -155,6 +155,13 @@ GGUF_API size_t gguf_iq3_pack_scratch_bytes(int64_t rows, int64_t row_bytes);
 GGUF_API int gguf_iq3_pack(void* w, int64_t rows, int64_t row_bytes, int unpack, void* scratch, size_t scratch_bytes,
                   void* stream);
 
+/* Dense product of a small unquantized weight: Y[n, rows] = X @ W.T in X's dtype, W [rows, K] and
+ * X [n, K] of one float dtype (fp32 / fp16 / bf16), 1 <= n <= 8 (n == 0: nothing), K % 32 == 0,
+ * unit inner strides, data and row strides 16-byte aligned. Replaces the reference's batched-GEMV
+ * route for the GGUF file's F32/F16/BF16 tensors of at most 128 rows at up to 8 activation rows
+ * (plugin/vllm_gguf_plugin/quantization/linear.py:281-291); any row count is accepted. */
+GGUF_API int gguf_dense_mul_mat(const gguf_view* W, const gguf_view* X, void* y, size_t y_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -19,7 +19,7 @@ def _declared():
 
 def test_header_declares_the_op_surface():
     names = _declared()
-    assert len(names) == 19
+    assert len(names) == 20
     for op in _capi.OPS:
         assert "gguf_" + op in names
     assert "gguf_lcpp_quantize_q8_1" in names

@@ -49,6 +49,8 @@ hipError_t launch_gemm_prefill(int type, bool packed, const uint8_t* W, int64_t 
 hipError_t launch_iq3_pack(uint8_t* w, int64_t rows, int64_t row_bytes, bool unpack, uint8_t* scratch,
                            size_t scratch_bytes, hipStream_t stream);
 size_t iq3_pack_scratch_bytes(int64_t rows, int64_t row_bytes);
+hipError_t launch_dense(int dtype, const void* W, int64_t ws0, int rows, int k, const void* X, int64_t xs0, int n,
+                        void* y, hipStream_t stream);
 }  // namespace gguf
 
 namespace {
@@ -475,6 +477,35 @@ int gguf_lcpp_quantize_q8_1(const gguf_view* X, int64_t type, int mmq, int vendo
 }
 
 size_t gguf_iq3_pack_scratch_bytes(int64_t rows, int64_t row_bytes) { return gguf::iq3_pack_scratch_bytes(rows, row_bytes); }
+
+int gguf_dense_mul_mat(const gguf_view* W, const gguf_view* X, void* y, size_t y_bytes, void* stream) {
+  g_err.clear();
+  const char* name = "gguf_dense_mul_mat";
+  if (!W || !X) return fail("%s: W and X must be given", name);
+  if (W->ndim != 2 || X->ndim != 2) return fail("%s: W and X must be 2-D", name);
+  if (!is_float(W->dtype) || X->dtype != W->dtype) return fail("%s: W and X must share one float dtype", name);
+  const int64_t rows = W->size[0], k = W->size[1], n = X->size[0];
+  if (X->size[1] != k) return fail("%s: X has %lld columns, W has %lld", name, (long long)X->size[1], (long long)k);
+  if (!(k > 0 && k % 32 == 0 && k <= INT_MAX)) return fail("%s: K=%lld must be a positive multiple of 32", name, (long long)k);
+  if (!(rows >= 1 && rows <= INT_MAX)) return fail("%s: W must have rows", name);
+  if (n > 8) return fail("%s: at most 8 rows, got %lld", name, (long long)n);
+  const int64_t es = elem_size(X->dtype);
+  if (W->stride[1] != 1 || X->stride[1] != 1) return fail("%s: W and X inner stride must be 1", name);
+  if ((rows > 1 && (W->stride[0] < k || (W->stride[0] * es) % 16)) || (n > 1 && (X->stride[0] < k || (X->stride[0] * es) % 16)))
+    return fail("%s: row strides must be at least K and 16-byte multiples", name);
+  if (reinterpret_cast<uintptr_t>(W->data) % 16 || reinterpret_cast<uintptr_t>(X->data) % 16)
+    return fail("%s: W and X data must be 16-byte aligned", name);
+  if (W->device < 0 || X->device < 0) return fail("%s: W and X must be CUDA tensors", name);
+  if (W->device != X->device) return fail("%s: W and X must be on the same device", name);
+  if (n == 0) return GGUF_OK;
+  if (y_bytes < (size_t)(n * rows * es)) return fail("%s: output buffer too small", name);
+  const DeviceScope scope(X->device);
+  if (scope.err != hipSuccess) return hip_fail(scope.err, name, "device select");
+  const hipError_t e = gguf::launch_dense(X->dtype, W->data, rows > 1 ? W->stride[0] : k, (int)rows, (int)k, X->data,
+                                          n > 1 ? X->stride[0] : k, (int)n, y, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, name, "gemv");
+  return GGUF_OK;
+}
 
 int gguf_iq3_pack(void* w, int64_t rows, int64_t row_bytes, int unpack, void* scratch, size_t scratch_bytes,
                   void* stream) {

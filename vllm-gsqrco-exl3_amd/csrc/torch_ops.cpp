@@ -84,6 +84,17 @@ at::Tensor op_own(const at::Tensor& W, const at::Tensor& X, int64_t type, int64_
   return mul_mat(OP, W, X, type, row, std::nullopt);
 }
 
+// the small dense product (gguf_dense_mul_mat): Y[n, rows] = X @ W.T in X's dtype
+at::Tensor dense_mul_mat(const at::Tensor& W, const at::Tensor& X) {
+  const gguf_view wv = make_view(W), xv = make_view(X);
+  const int64_t n = X.dim() == 2 ? X.size(0) : 0, rows = W.dim() == 2 ? W.size(0) : 0;
+  at::Tensor y = at::empty({n, rows}, X.options());
+  const int rc = gguf_dense_mul_mat(&wv, &xv, y.numel() ? y.data_ptr() : nullptr,
+                                    (size_t)(y.numel() * y.element_size()), stream_of(X));
+  if (rc != GGUF_OK) raise_last();
+  return y;
+}
+
 at::Tensor quantize_q8_1(const at::Tensor& X, int64_t type, bool mmq, bool vendored) {
   const gguf_view xv = make_view(X);
   const int64_t nbytes = X.dim() == 2 ? (int64_t)gguf_q8_1_bytes(X.size(0), X.size(1), mmq) : 0;
@@ -106,6 +117,7 @@ TORCH_LIBRARY(_C_gguf, m) {
   m.def("lcpp_mul_mat_vec_iq3_mma_packed(Tensor W, Tensor X, int type, SymInt row, Tensor? x_q8=None) -> Tensor");
   m.def("lcpp_mul_mat_iq3_packed(Tensor W, Tensor X, int type, SymInt row) -> Tensor");
   m.def("lcpp_quantize_q8_1(Tensor X, int type, bool mmq, bool vendored) -> Tensor");
+  m.def("dense_mul_mat(Tensor W, Tensor X) -> Tensor");
 }
 
 #define GGUF_IMPLS(KEY)                                                                   \
@@ -119,6 +131,7 @@ TORCH_LIBRARY(_C_gguf, m) {
     m.impl("lcpp_mul_mat_vec_iq3_mma_packed", &op_q8<GGUF_OP_MUL_MAT_VEC_IQ3_MMA_PACKED>); \
     m.impl("lcpp_mul_mat_iq3_packed", &op_own<GGUF_OP_MUL_MAT_IQ3_PACKED>);               \
     m.impl("lcpp_quantize_q8_1", &quantize_q8_1);                                         \
+    m.impl("dense_mul_mat", &dense_mul_mat);                                              \
   }
 GGUF_IMPLS(CUDA)
 GGUF_IMPLS(CPU)

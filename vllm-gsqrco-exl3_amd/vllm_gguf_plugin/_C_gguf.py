@@ -14,6 +14,9 @@ torch.ops._C_gguf.<op> runs unchanged:
   lcpp_mul_mat_iq3_packed(Tensor W, Tensor X, int type, SymInt row) -> Tensor
   lcpp_quantize_q8_1(Tensor X, int type, bool mmq, bool vendored) -> Tensor
 
+and this build's own dense_mul_mat(Tensor W, Tensor X) -> Tensor, the small unquantized product of
+quantization/linear.py's _unquantized_gemm.
+
 The ops are defined and implemented in C++ (csrc/torch_ops.cpp, built into _C_gguf_ops.so next
 to the library): for CUDA (HIP tensors on ROCm) and, as in the reference (lcpp_shim.cu:997-1008),
 for CPU, where every guard runs in the library and the call then ends with "must be CUDA
@@ -47,6 +50,10 @@ def _fake_own(W, X, type, row):
     return X.new_empty(X.shape[0], row)
 
 
+def _dense_fake(W, X):
+    return X.new_empty(X.shape[0], W.shape[0])
+
+
 def _quantize_fake(X, type, mmq, vendored):
     n, k = X.shape
     return X.new_empty((n * k // 128 * 144) if mmq else (n * k // 32 * 36), dtype=torch.uint8)
@@ -71,4 +78,5 @@ def register() -> None:
     for name in _OWN_OPS:
         torch.library.register_fake(f"{NAMESPACE}::{name}", _fake_own)
     torch.library.register_fake(f"{NAMESPACE}::lcpp_quantize_q8_1", _quantize_fake)
+    torch.library.register_fake(f"{NAMESPACE}::dense_mul_mat", _dense_fake)
     _registered = True

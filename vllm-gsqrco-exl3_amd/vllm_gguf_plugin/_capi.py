@@ -38,7 +38,7 @@ EXPORTS = (
     "gguf_lcpp_mul_mat_vec_iq3_mma", "gguf_lcpp_mul_mat_vec_own", "gguf_lcpp_mul_mat_mma_k",
     "gguf_lcpp_mul_mat_vec_iq3_mma_packed", "gguf_lcpp_mul_mat_iq3_packed", "gguf_q8_1_bytes",
     "gguf_lcpp_quantize_q8_1", "gguf_iq3_pack_scratch_bytes", "gguf_iq3_pack", "gguf_scratch_bytes",
-    "gguf_mul_mat_noalloc",
+    "gguf_mul_mat_noalloc", "gguf_dense_mul_mat",
 )
 
 
@@ -82,6 +82,7 @@ def load():
     lib.gguf_iq3_pack.argtypes = [VP, I64, I64, I32, VP, SZ, VP]
     lib.gguf_scratch_bytes.restype = SZ
     lib.gguf_mul_mat_noalloc.argtypes = [I32, P, P, I64, I64, P, VP, SZ, VP]
+    lib.gguf_dense_mul_mat.argtypes = [P, P, VP, SZ, VP]
     _lib = lib
     return lib
 

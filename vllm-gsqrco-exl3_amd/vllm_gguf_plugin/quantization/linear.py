@@ -182,7 +182,30 @@ def _quantize_x_q8_1_fake(x: torch.Tensor, weight_types: list[int], weight_rows:
     return torch.empty(x.shape[0] * x.shape[1] // 32 * 36, dtype=torch.uint8, device=x.device)
 
 
+_DENSE_MAX_ROWS = 128  # the small-weight route's limits (reference linear.py:281-291)
+_DENSE_MAX_N = 8
+
+
+def _dense_ok(x: torch.Tensor, weight: torch.Tensor, bias) -> bool:
+    """The layouts torch.ops._C_gguf.dense_mul_mat takes: one float dtype, unit inner strides,
+    K % 32 == 0, data and row strides 16-byte aligned."""
+    if bias is not None or not x.is_cuda or x.dim() != 2 or weight.dim() != 2 or x.dtype != weight.dtype:
+        return False
+    if x.shape[0] > _DENSE_MAX_N or weight.shape[0] > _DENSE_MAX_ROWS or x.shape[1] % 32:
+        return False
+    es = x.element_size()
+    return (x.stride(1) == 1 and weight.stride(1) == 1 and x.data_ptr() % 16 == 0 and weight.data_ptr() % 16 == 0
+            and (x.shape[0] <= 1 or (x.stride(0) * es) % 16 == 0)
+            and (weight.shape[0] <= 1 or (weight.stride(0) * es) % 16 == 0))
+
+
 def _unquantized_gemm(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
+    """x @ weight.T (+ bias) for a GGUF F32/F16/BF16 tensor (reference linear.py:281-291). A weight
+    of at most 128 rows times up to 8 activation rows runs the library's small dense GEMV (the
+    reference batches a GEMV there: a library GEMM picks a few tiny workgroups for that shape);
+    everything else is torch's linear."""
+    if _dense_ok(x, weight, bias):
+        return torch.ops._C_gguf.dense_mul_mat(weight, x)
     return torch.nn.functional.linear(x, weight, bias)
 
 
