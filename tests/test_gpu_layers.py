@@ -208,3 +208,25 @@ def test_vocab_head_prompt_rows(head, n):
     check_oracle(y, [(raw, o.Q6_K, False)], x, nsample=32)
     chunk_out = step * rows * 2 if len(chunks) > 1 else 0
     assert extra <= n * rows * 2 + chunk_out + (64 << 20), extra
+
+
+def test_headcheck_log(tmp_path, monkeypatch):
+    """VLLM_GGUF_HEADCHECK (reference linear.py:67-70,143-163): a product on a > 50,000-row weight
+    at more than 8 activation rows appends one JSON record comparing the routed op with the decode
+    op in 8-row calls; smaller products and 8-row products write nothing."""
+    import json
+
+    from vllm_gguf_plugin.quantization import linear
+
+    log = tmp_path / "head.jsonl"
+    monkeypatch.setattr(linear, "_HEADCHECK", str(log))
+    k, rows = 512, 50048
+    w = dev(w_rand(o.Q4_K, rows, k, 12))
+    for n in (8, 24):
+        linear._fused_mul_mat_gguf(x_bf16(n, k, seed=70 + n).cuda(), w, o.Q4_K)
+    linear._fused_mul_mat_gguf(x_bf16(24, k, seed=71).cuda(), w[:1000], o.Q4_K)
+    recs = [json.loads(line) for line in log.read_text().splitlines()]
+    assert len(recs) == 1
+    r = recs[0]
+    assert (r["n"], r["rows"], r["route"]) == (24, rows, linear._lcpp_op(24, o.Q4_K, rows, k))
+    assert r["max_rel"] < 0.05 and not r["bad_rows"] and r["x_finite"] and r["y_finite"]
