@@ -103,6 +103,10 @@ using gguf::kIQ3_XXS;
 // ops: its repack is the identity)
 bool generic(int64_t t) { return gguf::generic_type((int)t); }
 
+// the generic types whose product ops run on the xq-layout GEMM (D4 scales); Q2_K's D2S6 layout
+// stays on the per-slice GEMM over block_q8_1_mmq
+bool generic_xq(int64_t t) { return generic(t) && t != gguf::kQ2_K && t != kIQ1_M; }
+
 bool is_float(int32_t dt) { return dt == GGUF_DT_F32 || dt == GGUF_DT_F16 || dt == GGUF_DT_BF16; }
 
 int64_t elem_size(int32_t dt) { return dt == GGUF_DT_F32 ? 4 : dt == GGUF_DT_U8 ? 1 : 2; }
@@ -266,7 +270,10 @@ bool small_fp16(int op, int64_t type, int64_t k, int64_t n) {
 
 size_t gguf_op_workspace_bytes(int op, int64_t type, int64_t row, int64_t k, int64_t n, int has_x_q8) {
   if (n <= 0) return 0;
-  if (generic(type)) return op_gemm(op) ? align256(gguf_q8_1_bytes(n, k, 1)) : has_x_q8 ? 0 : align256(gguf_q8_1_bytes(n, k, 0));
+  if (generic(type)) {
+    if (op_gemm(op)) return align256(generic_xq(type) ? gguf::xq_bytes(n, k) : gguf_q8_1_bytes(n, k, 1));
+    return has_x_q8 ? 0 : align256(gguf_q8_1_bytes(n, k, 0));
+  }
   if (op_gemm(op)) {
     const bool mmq_layout = !op_packed(op) && type == gguf::kIQ3_S;
     if (!mmq_layout && ((n >= kPrefillFrom && gguf::prefill_uses_xh((int)type, op_packed(op))) ||
@@ -305,7 +312,15 @@ int gguf_mul_mat(int op, const gguf_view* W, const gguf_view* X, int64_t type, i
   const int ydt = X->dtype;
 
   if (generic(type)) {
-    if (gemm) {  // the product ops' MMQ arithmetic: block_q8_1_mmq and the per-slice MFMA GEMM
+    if (gemm && generic_xq(type)) {  // the product ops' MMQ arithmetic in the xq layout
+      e = gguf::launch_quantize_xq(X->data, X->dtype, n, k, s01, (int)type, false, workspace, s);
+      if (e != hipSuccess) return hip_fail(e, name, "quantize");
+      e = gguf::launch_gemm_xq((int)type, w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace, (int)n, y, ydt,
+                               true, s);
+      if (e != hipSuccess) return hip_fail(e, name, "gemm");
+      return GGUF_OK;
+    }
+    if (gemm) {  // Q2_K: the product ops' MMQ arithmetic, block_q8_1_mmq and the per-slice MFMA GEMM
       e = gguf::launch_quantize(X->data, X->dtype, n, k, s01, (int)type, true, workspace, s);
       if (e != hipSuccess) return hip_fail(e, name, "quantize");
       e = gguf::launch_gemm((int)type, w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace, (int)n, y, ydt, s);

@@ -507,6 +507,198 @@ __global__ void __launch_bounds__(64 * KS) gemm_raw_kernel(const uint8_t* __rest
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// IQ2_XXS, IQ2_XS, IQ2_S and IQ3_XXS on GGUF rows, X in the xq layout (MMQ arithmetic, fp32 d per
+// slice). A workgroup owns one 16-row tile and NT column tiles; its KS waves split the K blocks.
+// Per K block a wave copies the tile's 16 block-rows into a wave-private LDS buffer (lane l: 32
+// bytes of row l / 4, two 16-byte loads, contiguous along each row; the next block's copy is in
+// flight while the current block is computed), then lane 16q + j decodes values 8q..8q+7 of every
+// slice of row j from LDS (decode.h, codebook in LDS) straight into the MFMA A operand. The copy
+// starts at the 4-byte aligned address at or below the block (rows are 4-byte multiples, blocks
+// 2), so no dword it reads straddles the end of the tile's bytes; the block lies at byte 0 or 2
+// of its staged row. The B
+// operands and scales come from the xq unit as in gemm_raw_kernel. The slice terms are the product
+// ops' MMQ forms: (C * ls) * d4 per slice (two MFMAs and C_a * ls_a + C_b * ls_b for the
+// 16-value sub-scales), summed over the block, then times d / den of the row.
+constexpr int kGenRowStride = 144;  // LDS bytes per staged block-row: 2 + 128 copied, 16-byte multiple
+
+template <int TYPE>
+__device__ __forceinline__ void gen_row_scales(const uint8_t* rowp, int u, int& la, int& lb) {
+  if constexpr (TYPE == kIQ2_XXS) {
+    la = lb = 2 * (int)(ld32(rowp + 6 + 8 * u) >> 28) + 1;
+  } else if constexpr (TYPE == kIQ3_XXS) {
+    la = lb = 2 * (int)(ld32(rowp + 66 + 4 * u) >> 28) + 1;
+  } else {
+    const uint32_t sc = rowp[(TYPE == kIQ2_XS ? 66 : 74) + u];
+    la = 2 * (int)(sc & 0xF) + 1;
+    lb = 2 * (int)(sc >> 4) + 1;
+  }
+}
+
+template <int TYPE, int NT, int KS>
+__global__ void __launch_bounds__(64 * KS) gemm_generic_kernel(const uint8_t* __restrict__ W, int64_t row_bytes,
+                                                               int nrows, int k, const uint8_t* __restrict__ xq,
+                                                               int nct, int n, void* __restrict__ y, int y_dtype) {
+  constexpr int BS = block_bytes(TYPE);
+  constexpr bool P16 = per16_type(TYPE);
+  __shared__ typename Codebook<TYPE>::T grid[Codebook<TYPE>::n];
+  __shared__ uint4 stage[KS][2][16 * kGenRowStride / 16];
+  __shared__ float red[KS > 1 ? KS - 1 : 1][NT][4][64];
+  stage_codebook<TYPE>(grid);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 15, q = lane >> 4;
+  const int row0 = blockIdx.x * kRawRows;
+  const int rows_here = nrows - row0 < kRawRows ? nrows - row0 : kRawRows;
+  const int ct0 = blockIdx.y * NT;
+  const int nb = k / kQK;
+  const int b_begin = wave * nb / KS, b_end = (wave + 1) * nb / KS;
+  // rows past nrows, and the copy's read past the tile's last block-row, lie past the
+  // descriptor's size and read zeros
+  const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(W + (int64_t)row0 * row_bytes, (uint32_t)(rows_here * row_bytes));
+  const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(xq, (uint32_t)xq_bytes((int64_t)nct * kXqCols, k));
+  const int sbase = (int)xq_scale_base(nct, nb);
+  const int copy_off = (lane >> 2) * (int)row_bytes + 32 * (lane & 3);  // lane's 32 bytes of its row
+  int units[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) units[t] = (ct0 + t < nct ? ct0 + t : nct - 1) * nb;
+  uint8_t* buf0 = (uint8_t*)stage[wave][0];
+  uint8_t* buf1 = (uint8_t*)stage[wave][1];
+
+  float acc[NT][4];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[t][v] = 0.0f;
+
+  auto load_rows = [&](int b, u32x4 (&r)[2]) {
+    const int bb = b < b_end ? b : b_end - 1;  // past the wave's range: re-read its last block
+    r[0] = __builtin_amdgcn_raw_buffer_load_b128(wrs, copy_off, (bb * BS) & ~3, 0);
+    r[1] = __builtin_amdgcn_raw_buffer_load_b128(wrs, copy_off + 16, (bb * BS) & ~3, 0);
+  };
+  // the block lands at byte 2 of its staged row whatever its alignment in W, so that its 4-byte
+  // fields (at 2 mod 4 in every format here) are aligned LDS words
+  auto store_rows = [&](uint8_t* buf, int b, const u32x4 (&r)[2]) {
+    const int bb = b < b_end ? b : b_end - 1;
+    uint4* d = (uint4*)(buf + 2 - ((bb * BS) & 3) + (lane >> 2) * kGenRowStride + 32 * (lane & 3));
+    d[0] = make_uint4(r[0][0], r[0][1], r[0][2], r[0][3]);
+    d[1] = make_uint4(r[1][0], r[1][1], r[1][2], r[1][3]);
+  };
+  auto compute = [&](const uint8_t* buf0_, int b, const XRawFrag<NT>& x) {
+    const uint8_t* buf = buf0_ + 2;  // the block's first byte in each staged row
+    float accb[NT][4];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) accb[t][v] = 0.0f;
+    const uint8_t* rowj = buf + j * kGenRowStride;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      int wa[2];
+      SliceScale sc;
+      decode_quarter<TYPE>(rowj, u, q, grid, wa, sc);
+      const long a = (long)(((uint64_t)(uint32_t)wa[1] << 32) | (uint32_t)wa[0]);
+      int la[4], lb[4];  // sub-scales of the C rows 4q + v
+#pragma unroll
+      for (int v = 0; v < 4; ++v) gen_row_scales<TYPE>(buf + (4 * q + v) * kGenRowStride, u, la[v], lb[v]);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const long bq = xq_b_operand(x.b[t][u >> 1], u & 1);
+        const float cd = __uint_as_float(x.d[t][u >> 2][u & 3]);
+        const v4i zero = {0, 0, 0, 0};
+        if constexpr (P16) {
+          const v4i c0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(q < 2 ? a : 0, bq, zero, 0, 0, 0);
+          const v4i c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(q < 2 ? 0 : a, bq, zero, 0, 0, 0);
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            accb[t][v] = fmaf((float)(__mul24(c0[v], la[v]) + __mul24(c1[v], lb[v])), cd, accb[t][v]);
+        } else {
+          const v4i c = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bq, zero, 0, 0, 0);
+#pragma unroll
+          for (int v = 0; v < 4; ++v) accb[t][v] = fmaf((float)__mul24(c[v], la[v]), cd, accb[t][v]);
+        }
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float dd = half_bits_to_float(ld16(buf + (4 * q + v) * kGenRowStride)) * (1.0f / (float)iq_den(TYPE));
+#pragma unroll
+      for (int t = 0; t < NT; ++t) acc[t][v] = fmaf(accb[t][v], dd, acc[t][v]);
+    }
+  };
+
+  const int nblk = b_end - b_begin;
+  u32x4 ra[2], rb[2];
+  XRawFrag<NT> xa, xb;
+  if (nblk > 0) {
+    load_rows(b_begin, ra);
+    load_xraw<NT>(xrs, units, b_begin, sbase, lane, j, xa);
+  }
+  __syncthreads();  // the codebook
+  if (nblk > 0) {
+    store_rows(buf0, b_begin, ra);
+    load_rows(b_begin + 1, rb);
+  }
+  // block b is in buf[(b - b_begin) & 1] with its X in xa / xb; the next block's rows are in
+  // flight in rb / ra; a wave's LDS accesses complete in issue order, so each buffer's reads
+  // come before it is rewritten
+  int b = b_begin;
+  for (int it = 0; it < nblk / 2; ++it, b += 2) {
+    load_xraw<NT>(xrs, units, b + 1 < b_end ? b + 1 : b_end - 1, sbase, lane, j, xb);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(buf0, b, xa);
+    store_rows(buf1, b + 1, rb);
+    load_rows(b + 2, ra);
+    load_xraw<NT>(xrs, units, b + 2 < b_end ? b + 2 : b_end - 1, sbase, lane, j, xa);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(buf1, b + 1, xb);
+    store_rows(buf0, b + 2, ra);
+    load_rows(b + 3, rb);
+  }
+  if (nblk & 1) compute(buf0, b, xa);
+
+  if constexpr (KS > 1) {
+    if (wave > 0) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) red[wave - 1][t][v][lane] = acc[t][v];
+    }
+    __syncthreads();
+  }
+  if (wave == 0) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int col = (ct0 + t) * kXqCols + j;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        float sum = acc[t][v];
+        for (int w2 = 1; w2 < KS; ++w2) sum += red[w2 - 1][t][v][lane];
+        const int row = 4 * q + v;
+        if (col < n && row < rows_here) store_y(y, (int64_t)col * nrows + row0 + row, sum, y_dtype);
+      }
+    }
+  }
+}
+
+template <int TYPE, int NT>
+void launch_generic_t(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n, void* y,
+                      int y_dtype, hipStream_t stream) {
+  const int nct = (int)xq_col_tiles(n);
+  const dim3 grid((unsigned)((nrows + kRawRows - 1) / kRawRows), (unsigned)((nct + NT - 1) / NT));
+  gemm_generic_kernel<TYPE, NT, 4><<<grid, 256, 0, stream>>>(W, row_bytes, nrows, k, xq, nct, n, y, y_dtype);
+}
+
+template <int TYPE>
+void launch_generic_type(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n, void* y,
+                         int y_dtype, hipStream_t stream) {
+  const int nct = (int)xq_col_tiles(n);
+  if (nct == 1) launch_generic_t<TYPE, 1>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
+  else if (nct == 2) launch_generic_t<TYPE, 2>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
+  else if (nct == 3) launch_generic_t<TYPE, 3>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
+  else launch_generic_t<TYPE, 4>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
+}
+
 template <int TYPE, int NT, int KS, bool SX>
 void launch_raw_t(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n, void* y,
                   int y_dtype, hipStream_t stream) {
@@ -538,6 +730,10 @@ hipError_t launch_gemm_xq(int type, const uint8_t* W, int64_t row_bytes, int nro
       break;
     case kIQ4_XS: launch_raw_type<kIQ4_XS>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream); break;
     case kQ6_K: launch_raw_type<kQ6_K>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream); break;
+    case kIQ2_XXS: launch_generic_type<kIQ2_XXS>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream); break;
+    case kIQ2_XS: launch_generic_type<kIQ2_XS>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream); break;
+    case kIQ2_S: launch_generic_type<kIQ2_S>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream); break;
+    case kIQ3_XXS: launch_generic_type<kIQ3_XXS>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
