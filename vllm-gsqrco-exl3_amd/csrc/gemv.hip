@@ -775,6 +775,7 @@ hipError_t launch_gemv_raw(int type, const uint8_t* W, int64_t row_bytes, int nr
 // are added over the 8 slice lanes (xor butterfly), then over the waves in wave order.
 
 __device__ const Iq3sSignedTable kIq3sSignedDev = make_iq3s_signed_table();
+__device__ const Iq3sGrid kIq3sGridDev = kIq3sGrid;
 
 struct TileFrag {
   uint4 qs;
@@ -1157,16 +1158,23 @@ __device__ __forceinline__ void xgroup_store(const XGroup<XDT>& r, int g, bool l
 }
 
 // Persistent variant for weights with more tiles than the grid (two workgroups per CU): workgroup
-// g loops over tiles g, g + G, ...; the 32 KB table is copied once per workgroup. Each wave keeps
-// two tile-blocks of its stream in flight while it computes a third, and its prefetch runs on from
-// its last block of one tile to its first block of the next. The per-wave K ranges, partial sums
-// and reduction order are those of gemv_iq3s_tile_kernel, so the results are bit-identical. Every
-// wave needs at least one K block (k / 256 >= WPT).
+// g loops over tiles g, g + G, ...; the signed-grid table is built in LDS from the 2 KB grid once
+// per workgroup. Each wave keeps two tile-blocks of its stream in flight while it computes a third,
+// and its prefetch runs on from its last block of one tile to its first block of the next. The
+// per-wave K ranges, partial sums and reduction order are those of gemv_iq3s_tile_kernel, so the
+// results are bit-identical. Every wave needs at least one K block (k / 256 >= WPT).
 // X is staged in LDS first (dynamic LDS: NC * k / 32 * 36 bytes). XDT < 0: X given as block_q8_1,
 // copied. XDT >= 0: X itself (dtype XDT, row stride s01), quantised with the q8_1 quantiser's
-// arithmetic (bit-identical bytes), so the separate quantise launch goes. The first weight
-// blocks and the table copy are issued before the staging's arithmetic, which hides it.
-template <int NC, int WPT, int XDT>
+// arithmetic (bit-identical bytes), so the separate quantise launch goes.
+// XPL > 0: each wave stages only the X its own K range reads (activation rows c, slices [8 b_begin,
+// 8 b_end): NC * 32 * nblk groups of 8 values), at most XPL groups per lane, all loaded before the
+// first weight block. XPL == 0: the workgroup stages all of X together, two groups per thread
+// before the weights and the rest after them. A wave's loads complete in issue order, so a load
+// issued after the weights waits for them: measured at 5120 x 17408, M = 1, 16.3 us with the
+// workgroup staging against 12.7 us with the per-wave one (17408 x 5120: 11.8 against 11.5).
+// The grid word, X and the first weight blocks are loaded in that order; the table and X are
+// written to LDS while the weights are in flight.
+template <int NC, int WPT, int XDT, int XPL>
 __global__ void __launch_bounds__(64 * WPT) gemv_iq3s_persist_kernel(const uint8_t* __restrict__ W, int64_t row_bytes,
                                                                      int nrows, int k, const void* __restrict__ xsrc,
                                                                      int64_t s01, void* __restrict__ y, int y_dtype) {
@@ -1201,22 +1209,33 @@ __global__ void __launch_bounds__(64 * WPT) gemv_iq3s_persist_kernel(const uint8
       tt += G;
     }
   };
-  // the table, X's first two groups per thread and the first two weight blocks are loaded in that
-  // order; the table and X are written to LDS while the weights are in flight
+  static_assert(NT >= 512, "the table build takes 512 threads");
   const int ngroups = NC * nslices * 4;
-  const int ga = threadIdx.x, gb = threadIdx.x + NT;
-  // the table through VGPRs (16 B x 2048 / NT per thread): plain loads only, so the compiler's
-  // count of outstanding loads stays in order (an LDS DMA among them makes it wait for all)
-  constexpr int TPT = 2048 / NT;
-  static_assert(2048 % NT == 0, "table copy assumes NT divides 2048");
-  const __amdgpu_buffer_rsrc_t trs = buffer_rsrc(&kIq3sSignedDev, 2048 * 16);
-  u32x4 tv[TPT];
+  // X groups of this thread: XPL > 0, the wave's own (index li = lane + 64 j of the wave's
+  // NC * 32 * nblk, activation-row major); XPL == 0, groups threadIdx.x and threadIdx.x + NT
+  constexpr int XN = XPL > 0 ? XPL : 2;
+  int xg[XN];
+  bool xlive[XN];
+  const int wcnt = NC * 32 * nblk;
 #pragma unroll
-  for (int j = 0; j < TPT; ++j) tv[j] = __builtin_amdgcn_raw_buffer_load_b128(trs, 16 * threadIdx.x, 16 * j * NT, 0);
+  for (int j = 0; j < XN; ++j) {
+    if constexpr (XPL > 0) {
+      const int li0 = lane + 64 * j;
+      xlive[j] = li0 < wcnt;
+      const int li = xlive[j] ? li0 : wcnt - 1;
+      const int c = li / (32 * nblk), rem = li - c * 32 * nblk;
+      xg[j] = (c * nslices + 8 * b_begin + (rem >> 2)) * 4 + (rem & 3);
+    } else {
+      const int g = threadIdx.x + j * NT;
+      xlive[j] = g < ngroups;
+      xg[j] = xlive[j] ? g : ngroups - 1;
+    }
+  }
+  const uint32_t gword = __builtin_amdgcn_raw_buffer_load_b32(buffer_rsrc(&kIq3sGridDev, 2048), 4 * (threadIdx.x & 511), 0, 0);
   __builtin_amdgcn_sched_barrier(0);
-  XGroup<XDT> xa, xb;
-  xgroup_load<NC, XDT>(xsrc, xrs, s01, nslices, ga < ngroups ? ga : ngroups - 1, xa);
-  xgroup_load<NC, XDT>(xsrc, xrs, s01, nslices, gb < ngroups ? gb : ngroups - 1, xb);
+  XGroup<XDT> xa[XN];
+#pragma unroll
+  for (int j = 0; j < XN; ++j) xgroup_load<NC, XDT>(xsrc, xrs, s01, nslices, xg[j], xa[j]);
   __builtin_amdgcn_sched_barrier(0);
   TileFrag f0, f1, f2;
   int lt = blockIdx.x, lb = b_begin;  // next item to load
@@ -1225,14 +1244,15 @@ __global__ void __launch_bounds__(64 * WPT) gemv_iq3s_persist_kernel(const uint8
   load_tile_frag(tile_rs(lt), lb * kTileBlockBytes, off, f1);
   next(lt, lb);
   __builtin_amdgcn_sched_barrier(0);
+  if (threadIdx.x < 512) iq3_table_from_grid(table, gword, threadIdx.x);
 #pragma unroll
-  for (int j = 0; j < TPT; ++j) table[threadIdx.x + j * NT] = make_uint4(tv[j][0], tv[j][1], tv[j][2], tv[j][3]);
-  xgroup_store<XDT>(xa, ga, ga < ngroups, xq, xd, &sink);
-  xgroup_store<XDT>(xb, gb, gb < ngroups, xq, xd, &sink);
-  for (int g = threadIdx.x + 2 * NT; g < ngroups; g += NT) {  // K beyond 2 groups per thread
-    XGroup<XDT> xc;
-    xgroup_load<NC, XDT>(xsrc, xrs, s01, nslices, g, xc);
-    xgroup_store<XDT>(xc, g, true, xq, xd, &sink);
+  for (int j = 0; j < XN; ++j) xgroup_store<XDT>(xa[j], xg[j], xlive[j], xq, xd, &sink);
+  if constexpr (XPL == 0) {
+    for (int g = threadIdx.x + 2 * NT; g < ngroups; g += NT) {  // K beyond 2 groups per thread
+      XGroup<XDT> xc;
+      xgroup_load<NC, XDT>(xsrc, xrs, s01, nslices, g, xc);
+      xgroup_store<XDT>(xc, g, true, xq, xd, &sink);
+    }
   }
   __syncthreads();
   float acc[2][NC];
@@ -1332,17 +1352,37 @@ static void launch_gemv_packed_w(const uint8_t* W, int64_t row_bytes, int nrows,
 // One tile per workgroup. Eight waves split K for one or two columns (measured best at
 // 17408 x 5120: 12.3 us at M=1); from three columns on, the register file allows four.
 // The persistent kernel: g workgroups (two per CU, at most one per tile), n <= 4 rows (raw X:
-// n <= 2).
+// n <= 2). X groups per lane of the per-wave staging: NC * 32 * ceil(nb / 8) / 64 rounded up, up to
+// six; beyond that the workgroup staging.
+template <int NC, int XDT>
+static void launch_persist_nc(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x, int64_t s01,
+                              void* y, int y_dtype, unsigned g, size_t lds, hipStream_t stream) {
+  const int nblk_max = (k / kQK + 7) / 8;
+  const int xpl = (NC * 32 * nblk_max + 63) / 64;
+#define GGUF_PERSIST(XPL) \
+  gemv_iq3s_persist_kernel<NC, 8, XDT, XPL><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, x, s01, y, y_dtype)
+  switch (xpl) {
+    case 1: GGUF_PERSIST(1); break;
+    case 2: GGUF_PERSIST(2); break;
+    case 3: GGUF_PERSIST(3); break;
+    case 4: GGUF_PERSIST(4); break;
+    case 5: GGUF_PERSIST(5); break;
+    case 6: GGUF_PERSIST(6); break;
+    default: GGUF_PERSIST(0); break;
+  }
+#undef GGUF_PERSIST
+}
+
 template <int XDT>
 static void launch_gemv_persist(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x, int64_t s01, int n,
                                 void* y, int y_dtype, hipStream_t stream) {
   const unsigned g = (unsigned)std::min(nrows / kTileRows, persist_grid());
   const size_t lds = (size_t)n * (k / kQ81) * 36;  // X staged in LDS
-  if (n == 1) gemv_iq3s_persist_kernel<1, 8, XDT><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, x, s01, y, y_dtype);
-  else if (n == 2) gemv_iq3s_persist_kernel<2, 8, XDT><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, x, s01, y, y_dtype);
+  if (n == 1) launch_persist_nc<1, XDT>(W, row_bytes, nrows, k, x, s01, y, y_dtype, g, lds, stream);
+  else if (n == 2) launch_persist_nc<2, XDT>(W, row_bytes, nrows, k, x, s01, y, y_dtype, g, lds, stream);
   else if constexpr (XDT < 0) {  // three or four rows: q8_1 input only
-    if (n == 3) gemv_iq3s_persist_kernel<3, 8, XDT><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, x, s01, y, y_dtype);
-    else gemv_iq3s_persist_kernel<4, 8, XDT><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, x, s01, y, y_dtype);
+    if (n == 3) launch_persist_nc<3, XDT>(W, row_bytes, nrows, k, x, s01, y, y_dtype, g, lds, stream);
+    else launch_persist_nc<4, XDT>(W, row_bytes, nrows, k, x, s01, y, y_dtype, g, lds, stream);
   }
 }
 

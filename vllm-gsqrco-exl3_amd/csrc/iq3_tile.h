@@ -139,6 +139,33 @@ __device__ __forceinline__ void tile_lookup2(const uint8_t* tbl, uint32_t P, int
   w1 = *(const int*)(tbl + (P >> 14));  // bits 14, 15 of P are zero (ex has 5 bits)
 }
 
+// The signed-grid table built in LDS from the 512-word grid (2 KB read instead of 32 KB): thread
+// i < 512 holds grid word i (`gword`) and writes the 16 entries (i & 255) | (sign nibble | (i >> 8)
+// << 4) << 8. Every grid byte is odd (1..15), so the bytewise negation 256 - b of all four bytes is
+// the one subtraction 0x01010100 - g (each byte borrows from the next exactly once); the entry
+// takes the negated bytes where the sign nibble has a bit.
+constexpr bool iq3_grid_negation_is_bytewise() {
+  for (int i = 0; i < 512; ++i) {
+    const uint32_t g = kIq3sGrid.v[i], n = 0x01010100u - g;
+    for (int b = 0; b < 4; ++b)
+      if (((n >> (8 * b)) & 0xFF) != ((256u - ((g >> (8 * b)) & 0xFF)) & 0xFF)) return false;
+  }
+  return true;
+}
+static_assert(iq3_grid_negation_is_bytewise(), "0x01010100 - g negates every byte of every grid word");
+
+__device__ __forceinline__ void iq3_table_from_grid(uint4* table, uint32_t gword, int i) {
+  const uint32_t neg = 0x01010100u - gword;
+  uint32_t* t32 = (uint32_t*)table;
+  const uint32_t base = (uint32_t)(i & 255) | ((uint32_t)(i >> 8) << 12);
+#pragma unroll
+  for (int sg = 0; sg < 16; ++sg) {
+    const uint32_t m = ((sg & 1) ? 0xFFu : 0u) | ((sg & 2) ? 0xFF00u : 0u) | ((sg & 4) ? 0xFF0000u : 0u) |
+                       ((sg & 8) ? 0xFF000000u : 0u);
+    t32[base | ((uint32_t)sg << 8)] = (neg & m) | (gword & ~m);
+  }
+}
+
 // The 32 KB signed-grid table, global -> LDS without VGPRs: 32 wave-wide 1 KB DMA loads
 // (global_load_lds_dwordx4) shared out over the workgroup's NW waves (wave < NW). The caller waits
 // (vmcnt) and synchronises the workgroup before reading the table. When NW divides 32 every wave
