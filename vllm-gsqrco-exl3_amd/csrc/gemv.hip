@@ -1389,13 +1389,14 @@ static void launch_gemv_persist(const uint8_t* W, int64_t row_bytes, int nrows, 
 template <int XDT>
 static void launch_gemv_packed_dt(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x, int64_t s01,
                                   int n, void* y, int y_dtype, hipStream_t stream) {
-  if constexpr (XDT < 0) {  // q8 input: the persistent kernel when the tiles outnumber its grid
-    // (measured at 17408 x 5120: 1-2 rows level with or faster than one tile per workgroup, 3-4
-    // rows 15.3 / 17.1 us against 17.1 / 19.4; on weights with fewer tiles than the grid the
-    // one-tile kernel is faster at every row count)
-    // and at two rows on large weights (5120 x 17408: 15.2 us against 16.9)
+  if constexpr (XDT < 0) {  // q8 input: the persistent kernel from one tile per CU on, 1-4 rows
+    // (quantise + GEMV per op, graph-timed, against quantise + the one-tile kernel with 8 / 4
+    // waves: 17408 x 5120 M = 1-4 13.7 / 15.1 / 17.3 / 19.3 us against 15.1 / 17.2 / 19.9 / 22.3;
+    // 5120 x 17408 M = 1-2 15.9 / 17.9 against 16.2 / 20.0; 6144 x 5120 M = 1-4 8.9 / 9.5 / 10.9 /
+    // 11.9 against 9.0 / 10.3 / 11.3 / 12.4; 5120 x 6144 M = 2-4 10.0 / 11.4 / 12.4 against
+    // 10.6 / 12.2 / 13.8; with 64 tiles (1024 x 5120) the one-tile kernel stays faster at 3-4 rows)
     const bool fits = k / kQK >= 8 && n * (k / kQ81) * 36 <= 48 * 1024;
-    if (fits && ((nrows / kTileRows > persist_grid() && n <= 4) || (n == 2 && (int64_t)nrows * k >= ((int64_t)64 << 20)))) {
+    if (fits && n <= 4 && 2 * (nrows / kTileRows) >= persist_grid()) {
       launch_gemv_persist<XDT>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream);
       return;
     }
