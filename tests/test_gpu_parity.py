@@ -572,6 +572,46 @@ def test_fused_quantisation_ties(n, dtype, rows):
     assert torch.equal(a.view(bits), b.view(bits))
 
 
+ROWS_TYPES = [o.Q4_K, o.IQ4_XS, o.Q6_K]
+OP_ID = {"lcpp_mul_mat_vec_q": 0, "lcpp_mul_mat_vec_own": 4}
+
+
+@pytest.mark.parametrize("qt", ROWS_TYPES, ids=lambda t: TN[t])
+@pytest.mark.parametrize("n", [1, 2])
+@pytest.mark.parametrize("rows,k", [(16 * 700 + 5, 2048), (1000, 5120), (333, 6144)])
+def test_rows_fused_quantisation(lib, qt, n, rows, k):
+    """Without x_q8, a Q4_K / IQ4_XS / Q6_K decode op at one or two rows and K <= 8192 quantises X
+    inside the row-chunk GEMV, each wave its own part of X. It must give the bits of the q8_1
+    quantiser followed by the GEMV (partial last tile at 333 rows, three groups per lane at two rows
+    of K = 6144). The zero workspace shows that the fused path is the one taken."""
+    op = VEC_OP[qt]
+    assert lib.gguf_op_workspace_bytes(OP_ID[op], qt, rows, k, n, 0) == 0
+    w = _dev(_w(qt, rows, k, seed=210 + n))
+    x = _x(n, k, seed=211 + n, dtype=torch.bfloat16).cuda()
+    x[:, 96:128] = 0  # an all-zero slice (d = 0, q = 0)
+    q8 = C().lcpp_quantize_q8_1(x, qt, False, False)
+    a = getattr(C(), op)(w, x, qt, rows)
+    b = getattr(C(), op)(w, x, qt, rows, q8)
+    assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("qt", ROWS_TYPES, ids=lambda t: TN[t])
+@pytest.mark.parametrize("n", [1, 2])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16], ids=str)
+def test_rows_fused_quantisation_ties(qt, n, dtype):
+    """The row-chunk GEMV's in-kernel quantisation on values on and next to ties, infinities, NaN
+    and tiny scales: outputs equal to those of the q8_1 quantiser + GEMV bit for bit (NaN
+    included); Q4_K and Q6_K also take the sums of q from the quantised bytes."""
+    rows, k = 1000, 4096
+    w = _dev(_w(qt, rows, k, seed=220 + n))
+    x = torch.stack([_tie_slices(k, dtype, seed=221 + c) for c in range(n)]).cuda()
+    q8 = C().lcpp_quantize_q8_1(x, qt, False, False)
+    a = getattr(C(), VEC_OP[qt])(w, x, qt, rows)
+    b = getattr(C(), VEC_OP[qt])(w, x, qt, rows, q8)
+    bits = torch.int32 if dtype == torch.float32 else torch.int16
+    assert torch.equal(a.view(bits), b.view(bits))
+
+
 @pytest.mark.parametrize("op,qt,n,packed", [
     ("lcpp_mul_mat_vec_iq3_mma_packed", o.IQ3_S, 4, True),
     ("lcpp_mul_mat_iq3_packed", o.IQ3_S, 32, True),

@@ -36,6 +36,9 @@ hipError_t launch_gemv_packed_x(const uint8_t* W, int64_t row_bytes, int nrows, 
                                 int64_t s01, int n, void* y, int y_dtype, hipStream_t stream);
 bool gemv_rows_supported(int type, int64_t nrows, int64_t row_bytes, int64_t k, int64_t n);
 bool gemv_packed_x_supported(int64_t nrows, int64_t k, int64_t n);
+hipError_t launch_gemv_rows_x(int type, const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x,
+                              int x_dtype, int64_t s01, int n, void* y, int y_dtype, hipStream_t stream);
+bool gemv_rows_x_supported(int type, int64_t nrows, int64_t row_bytes, int64_t k, int64_t n);
 hipError_t launch_gemm_packed_xq(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n,
                                  void* y, int y_dtype, hipStream_t stream);
 hipError_t launch_quantize_xh(const void* x, int dtype, int64_t n, int64_t k, int64_t s01, int type, void* y,
@@ -237,6 +240,10 @@ bool packed_fused(int op, int64_t row, int64_t k, int64_t n, bool has_x_q8) {
   return op_packed(op) && !has_x_q8 && gguf::gemv_packed_x_supported(row, k, n);
 }
 
+// A Q4_K / IQ4_XS / Q6_K decode op on the row-chunk GEMV with no x_q8 from the caller quantises X
+// inside the GEMV at one or two rows where each wave's part of X is small (K <= 8192).
+bool rows_fused(int op, int64_t type, int64_t row, int64_t k, int64_t n, bool has_x_q8);
+
 // Product ops go to the 128 x 128-tile prefill GEMM from this many activation rows on (the small
 // GEMMs' one-column-tile-group plans re-decode the weights once per 16..64 activation rows).
 constexpr int64_t kPrefillFrom = 256;
@@ -254,6 +261,12 @@ bool decode_mma(int op, int64_t type, int64_t row, int64_t k, int64_t n) {
   if (n < vec_mma_from(op, type)) return false;
   const int64_t bb = type == gguf::kQ4_K ? 144 : type == gguf::kQ6_K ? 210 : type == gguf::kIQ4_XS ? 136 : 0;
   return !(op_packed(op) == false && bb > 0 && gguf::gemv_rows_supported((int)type, row, k / 256 * bb, k, n));
+}
+
+bool rows_fused(int op, int64_t type, int64_t row, int64_t k, int64_t n, bool has_x_q8) {
+  if (op_gemm(op) || op_packed(op) || has_x_q8 || decode_mma(op, type, row, k, n)) return false;
+  const int64_t bb = type == gguf::kQ4_K ? 144 : type == gguf::kQ6_K ? 210 : type == gguf::kIQ4_XS ? 136 : 0;
+  return bb > 0 && gguf::gemv_rows_x_supported((int)type, row, k / 256 * bb, k, n);
 }
 
 // The MFMA products of 64 to 255 activation rows with K <= 8192 run the fp16 small GEMM (X in the
@@ -282,7 +295,7 @@ size_t gguf_op_workspace_bytes(int op, int64_t type, int64_t row, int64_t k, int
     return align256(mmq_layout ? gguf_q8_1_bytes(n, k, 1) : gguf::xq_bytes(n, k));
   }
   if (decode_mma(op, type, row, k, n)) return align256(gguf::xq_bytes(n, k));  // x_q8 is converted into it
-  if (packed_fused(op, row, k, n, has_x_q8 != 0)) return 0;
+  if (packed_fused(op, row, k, n, has_x_q8 != 0) || rows_fused(op, type, row, k, n, has_x_q8 != 0)) return 0;
   return has_x_q8 ? 0 : align256(gguf_q8_1_bytes(n, k, 0));
 }
 
@@ -379,6 +392,11 @@ int gguf_mul_mat(int op, const gguf_view* W, const gguf_view* X, int64_t type, i
   }
   if (packed_fused(op, row, k, n, x_q8 != nullptr)) {  // quantisation inside the GEMV
     e = gguf::launch_gemv_packed_x(w, row_bytes, (int)row, (int)k, X->data, X->dtype, s01, (int)n, y, ydt, s);
+    if (e != hipSuccess) return hip_fail(e, name, "gemv");
+    return GGUF_OK;
+  }
+  if (rows_fused(op, type, row, k, n, x_q8 != nullptr)) {  // quantisation inside the row-chunk GEMV
+    e = gguf::launch_gemv_rows_x((int)type, w, row_bytes, (int)row, (int)k, X->data, X->dtype, s01, (int)n, y, ydt, s);
     if (e != hipSuccess) return hip_fail(e, name, "gemv");
     return GGUF_OK;
   }

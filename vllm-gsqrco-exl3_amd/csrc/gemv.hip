@@ -310,6 +310,103 @@ __device__ __forceinline__ void xgroup_q8_load(__amdgpu_buffer_rsrc_t xrs, int g
   r.q1 = __builtin_amdgcn_raw_buffer_load_b32(xrs, o + 8 + 8 * part, 0, 0);
 }
 
+// q8_1 bytes of N (4 or 8) values of one slice, given the slice's amax and d = amax / 127: q =
+// roundf(v / d) (q = 0 when amax == 0), bit for bit as the q8_1 quantiser computes them. The
+// quotient comes from the product v * rcp(d): for |v| <= amax it lies within 2^-15 of v / d (rcp
+// within 1 ulp), and the fp32 rounding of v / d moves that by less than 2^-16, so when the product
+// lies more than 2^-12 from every half-integer, roundf(v / d) is the integer nearest to it. Adding
+// 1.5 * 2^23 rounds to that integer and leaves it in the low mantissa bits. The largest distance
+// is taken over the bit patterns of |a - n|, where a NaN (a NaN or infinite value) ranks above
+// every number. A lane with a value near a tie, a non-finite product or a tiny amax (rcp of a
+// subnormal d) takes the IEEE division. out[j] holds the bytes of values 4j..4j+3.
+template <int N>
+__device__ __forceinline__ void quantize_q81(const float (&v)[N], float amax, float d, uint32_t (&out)[N / 4]) {
+  constexpr float kMagic = 12582912.0f;
+  const float r = __builtin_amdgcn_rcpf(d);
+  uint32_t m[N], dev = 0;
+#pragma unroll
+  for (int e = 0; e < N; ++e) {
+    const float a = v[e] * r;
+    const float t = a + kMagic;
+    m[e] = __float_as_uint(t);
+    dev = max(dev, __float_as_uint(a - (t - kMagic)) & 0x7FFFFFFFu);
+  }
+#pragma unroll
+  for (int j = 0; j < N / 4; ++j)
+    out[j] = __builtin_amdgcn_perm(__builtin_amdgcn_perm(m[4 * j + 3], m[4 * j + 2], 0x0c0c0400u),
+                                   __builtin_amdgcn_perm(m[4 * j + 1], m[4 * j], 0x0c0c0400u), 0x05040100u);
+  if (!(amax >= 0x1p-100f) || dev > __float_as_uint(0.5f - 0x1p-12f)) {
+#pragma unroll
+    for (int j = 0; j < N / 4; ++j) out[j] = 0;
+    if (amax != 0.0f) {
+#pragma unroll
+      for (int e = 0; e < N; ++e) out[e >> 2] |= ((uint32_t)(int)roundf(v[e] / d) & 0xFFu) << (8 * (e & 3));
+    }
+  }
+}
+
+template <int XDT>
+struct XGroup {
+  uint32_t v[XDT == kF32 ? 8 : (XDT < 0 ? 3 : 4)];
+};
+
+template <int NC, int XDT>
+__device__ __forceinline__ void xgroup_load(const void* x, __amdgpu_buffer_rsrc_t xrs, int64_t s01, int nslices, int g,
+                                            XGroup<XDT>& r) {
+  const int sr = g >> 2, part = g & 3;
+  if constexpr (XDT < 0) {  // block_q8_1: d (fp16) and s, then 32 q bytes
+    const int o = sr * 36;
+    r.v[0] = __builtin_amdgcn_raw_buffer_load_b32(xrs, o, 0, 0);
+    r.v[1] = __builtin_amdgcn_raw_buffer_load_b32(xrs, o + 4 + 8 * part, 0, 0);
+    r.v[2] = __builtin_amdgcn_raw_buffer_load_b32(xrs, o + 8 + 8 * part, 0, 0);
+  } else {
+    int c = 0, sl = sr;
+#pragma unroll
+    for (int i = 1; i < NC; ++i)
+      if (sl >= nslices) sl -= nslices, ++c;
+    const int64_t e0 = c * s01 + (int64_t)sl * kQ81 + 8 * part;
+    if constexpr (XDT == kF32) {
+      const uint4 a = *(const uint4*)((const float*)x + e0), b = *(const uint4*)((const float*)x + e0 + 4);
+      r.v[0] = a.x; r.v[1] = a.y; r.v[2] = a.z; r.v[3] = a.w;
+      r.v[4] = b.x; r.v[5] = b.y; r.v[6] = b.z; r.v[7] = b.w;
+    } else {
+      const uint4 a = *(const uint4*)((const uint16_t*)x + e0);
+      r.v[0] = a.x; r.v[1] = a.y; r.v[2] = a.z; r.v[3] = a.w;
+    }
+  }
+}
+
+// max over the four lanes of a quad, exchanged by DPP quad permutes (xor 1, then xor 2)
+__device__ __forceinline__ float quad_fmax(float v) {
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false)));
+  return v;
+}
+
+// q8_1 bytes (lo: values 0..3, hi: 4..7) and fp16 d of the group of 8 raw values in r: the four
+// lanes of the slice exchange their amax (the quantiser's arithmetic, bit-identical bytes)
+template <int XDT>
+__device__ __forceinline__ void xgroup_quantize(const XGroup<XDT>& r, uint32_t& lo, uint32_t& hi, uint32_t& dbits) {
+  float v[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    if constexpr (XDT == kF32) v[e] = __uint_as_float(r.v[e]);
+    else {
+      const uint32_t h = (r.v[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+      v[e] = XDT == kF16 ? half_bits_to_float(h) : __uint_as_float(h << 16);
+    }
+  }
+  float amax = fmaxf(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))),
+                     fmaxf(fmaxf(fabsf(v[4]), fabsf(v[5])), fmaxf(fabsf(v[6]), fabsf(v[7]))));
+  amax = quad_fmax(amax);
+  const float d = amax / 127.0f;
+  uint32_t qw[2];
+  quantize_q81<8>(v, amax, d, qw);
+  lo = qw[0];
+  hi = qw[1];
+  dbits = __half_as_ushort(__float2half_rn(d));
+}
+
 // SUMS: what the second word of a slice's (d8, .) pair holds. kSumSlice: the slice's sum of q (as
 // float; Q4_K's min term). kSumHalves: the sums of q over values 0..15 and 16..31 as two int16 in
 // the word's bits (Q6_K folds its -32 offset into them). A group past the end (live false) is
@@ -373,10 +470,16 @@ struct RowsFrag<kQ6_K> {
 // (between two barriers) when its waves reach it. Every wave has at least one block in every
 // phase. Without PH (one phase) the staging branch is compiled out: inside the K loop, a branch
 // with loads makes the compiler wait for every load in flight at its join.
-template <int TYPE, int NC, int WPT, bool PH, int RPL>
+// XDT < 0: X given as block_q8_1 (xsrc). XDT >= 0 (one phase only): X itself (dtype XDT, row
+// stride s01), quantised in the kernel with the q8_1 quantiser's arithmetic (bit-identical
+// bytes, sums of q formed as from the q8_1 bytes): each wave stages the X its own K range reads,
+// at most XPL groups of 8 values per lane, loaded before its first weight block.
+template <int TYPE, int NC, int WPT, bool PH, int RPL, int XDT = -1, int XPL = 0>
 __global__ void __launch_bounds__(64 * WPT) gemv_rows_kernel(const uint8_t* __restrict__ W, int64_t row_bytes,
-                                                             int nrows, int k, const uint8_t* __restrict__ q8,
-                                                             void* __restrict__ y, int y_dtype, int kp_arg) {
+                                                             int nrows, int k, const void* __restrict__ xsrc,
+                                                             int64_t s01, void* __restrict__ y, int y_dtype, int kp_arg) {
+  static_assert(XDT < 0 || (!PH && XPL > 0), "raw X: one phase, per-wave staging");
+  const uint8_t* q8 = (const uint8_t*)xsrc;
   const int kp = PH ? kp_arg : 1;
   constexpr int TR = 8 * RPL;  // rows per tile: lane 8r + c takes rows r (and 8 + r)
   constexpr int BS = block_bytes(TYPE);
@@ -396,7 +499,7 @@ __global__ void __launch_bounds__(64 * WPT) gemv_rows_kernel(const uint8_t* __re
   float2* xs = (float2*)(xq + NC * nsl * 8);
   const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(W, (uint32_t)((int64_t)nrows * row_bytes));
   const __amdgpu_buffer_rsrc_t nrs = buffer_rsrc(W, 0);
-  const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(q8, (uint32_t)(NC * nslices * 36));
+  const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(q8, XDT < 0 ? (uint32_t)(NC * nslices * 36) : 0u);
   auto load = [&](int t, int b, RowsFrag<TYPE>& f) {
     const __amdgpu_buffer_rsrc_t rs = t < ntiles ? wrs : nrs;
     const int t0 = (t < ntiles ? t : 0) * TR;
@@ -461,15 +564,34 @@ __global__ void __launch_bounds__(64 * WPT) gemv_rows_kernel(const uint8_t* __re
       xgroup_q8_store<SUMS>(xc, gL, true, xq, xs, &sink);
     }
   };
-  // phase 0: X's first two groups per thread, then the first two weight blocks, then X to LDS
+  // phase 0: X's first two groups per thread (raw X: the wave's own groups), then the first two
+  // weight blocks, then X to LDS
   const int ng0 = groups(0);
   const int ga = threadIdx.x, gb = threadIdx.x + NT;
   int gga, gLa, ggb, gLb;
   gmap(0, ga < ng0 ? ga : ng0 - 1, gga, gLa);
   gmap(0, gb < ng0 ? gb : ng0 - 1, ggb, gLb);
   XGroupQ8 xa, xb;
-  xgroup_q8_load(xrs, gga, xa);
-  xgroup_q8_load(xrs, ggb, xb);
+  constexpr int XN = XDT >= 0 ? XPL : 1;
+  XGroup<XDT> xr[XN];
+  int xgl[XN];
+  bool xlive[XN];
+  if constexpr (XDT >= 0) {  // activation rows cc, slices [8 wb(0), 8 we(0)): NC * 32 * nblk groups
+    const int nblk = we(0) - wb(0), wcnt = NC * 32 * nblk;
+#pragma unroll
+    for (int j = 0; j < XN; ++j) {
+      const int li0 = lane + 64 * j;
+      xlive[j] = li0 < wcnt;
+      const int li = xlive[j] ? li0 : wcnt - 1;
+      const int cc = li / (32 * nblk), rem = li - cc * 32 * nblk;
+      const int sg = 32 * wb(0) + rem;  // group within the activation row
+      xgl[j] = cc * nsl * 4 + sg;
+      xgroup_load<NC, XDT>(xsrc, xrs, s01, nslices, cc * nslices * 4 + sg, xr[j]);
+    }
+  } else {
+    xgroup_q8_load(xrs, gga, xa);
+    xgroup_q8_load(xrs, ggb, xb);
+  }
   __builtin_amdgcn_sched_barrier(0);
   RowsFrag<TYPE> f0, f1, f2;
   int lt = blockIdx.x, lp = 0, lb = wb(0);  // next item to load
@@ -478,14 +600,23 @@ __global__ void __launch_bounds__(64 * WPT) gemv_rows_kernel(const uint8_t* __re
   load(lt, lb, f1);
   next(lt, lp, lb);
   __builtin_amdgcn_sched_barrier(0);
-  xgroup_q8_store<SUMS>(xa, gLa, ga < ng0, xq, xs, &sink);
-  xgroup_q8_store<SUMS>(xb, gLb, gb < ng0, xq, xs, &sink);
-  for (int gl = threadIdx.x + 2 * NT; gl < ng0; gl += NT) {  // phase 0 beyond 2 groups per thread
-    int gg, gL;
-    gmap(0, gl, gg, gL);
-    XGroupQ8 xc;
-    xgroup_q8_load(xrs, gg, xc);
-    xgroup_q8_store<SUMS>(xc, gL, true, xq, xs, &sink);
+  if constexpr (XDT >= 0) {
+#pragma unroll
+    for (int j = 0; j < XN; ++j) {
+      XGroupQ8 xc;
+      xgroup_quantize<XDT>(xr[j], xc.q0, xc.q1, xc.d);
+      xgroup_q8_store<SUMS>(xc, xgl[j], xlive[j], xq, xs, &sink);
+    }
+  } else {
+    xgroup_q8_store<SUMS>(xa, gLa, ga < ng0, xq, xs, &sink);
+    xgroup_q8_store<SUMS>(xb, gLb, gb < ng0, xq, xs, &sink);
+    for (int gl = threadIdx.x + 2 * NT; gl < ng0; gl += NT) {  // phase 0 beyond 2 groups per thread
+      int gg, gL;
+      gmap(0, gl, gg, gL);
+      XGroupQ8 xc;
+      xgroup_q8_load(xrs, gg, xc);
+      xgroup_q8_store<SUMS>(xc, gL, true, xq, xs, &sink);
+    }
   }
   __syncthreads();
   float acc[2][NC];
@@ -652,9 +783,9 @@ static void launch_rows_rpl(const uint8_t* W, int64_t row_bytes, int nrows, int 
   const int tiles = (nrows + 8 * RPL - 1) / (8 * RPL);
   const unsigned g = (unsigned)std::min(tiles, persist_grid());
   const size_t lds = (size_t)n * ((k / kQK + kp - 1) / kp) * 8 * 40;
-#define GGUF_ROWS(NC)                                                                                            \
-  (kp > 1 ? gemv_rows_kernel<TYPE, NC, 8, true, RPL><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype, kp) \
-          : gemv_rows_kernel<TYPE, NC, 8, false, RPL><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, y, y_dtype, 1))
+#define GGUF_ROWS(NC)                                                                                                   \
+  (kp > 1 ? gemv_rows_kernel<TYPE, NC, 8, true, RPL><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, 0, y, y_dtype, kp) \
+          : gemv_rows_kernel<TYPE, NC, 8, false, RPL><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, q8, 0, y, y_dtype, 1))
   switch (n) {
     case 1: GGUF_ROWS(1); break;
     case 2: GGUF_ROWS(2); break;
@@ -675,6 +806,38 @@ static bool launch_rows(const uint8_t* W, int64_t row_bytes, int nrows, int k, c
   if (rows_phases(k, n) == 1 || TYPE == kQ6_K) launch_rows_rpl<TYPE, 1>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);
   else launch_rows_rpl<TYPE, 2>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);
   return true;
+}
+
+// X quantised inside the row-chunk kernel: one or two activation rows, one K phase, and each
+// wave's own part of X within two (one row) or three (two rows) groups of 8 values per lane
+// (K <= 8192 with eight waves). Larger K keeps quantise + GEMV: the per-lane quantisation then
+// costs as much as the launch it saves (measured on the packed IQ3_S GEMV at K = 17408).
+static int rows_x_groups(int64_t k, int64_t n) { return (int)((n * 32 * ((k / kQK + 7) / 8) + 63) / 64); }
+
+bool gemv_rows_x_supported(int type, int64_t nrows, int64_t row_bytes, int64_t k, int64_t n) {
+  return n >= 1 && n <= 2 && gemv_rows_supported(type, nrows, row_bytes, k, n) && rows_phases(k, n) == 1 &&
+         rows_x_groups(k, n) <= (n == 1 ? 2 : 3);
+}
+
+template <int TYPE, int XDT>
+static void launch_rows_x_dt(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x, int64_t s01, int n,
+                             void* y, int y_dtype, hipStream_t stream) {
+  const unsigned g = (unsigned)std::min((nrows + 7) / 8, persist_grid());
+  const size_t lds = (size_t)n * (k / kQK) * 8 * 40;
+  if (n == 1)
+    gemv_rows_kernel<TYPE, 1, 8, false, 1, XDT, 2><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, x, s01, y, y_dtype, 1);
+  else
+    gemv_rows_kernel<TYPE, 2, 8, false, 1, XDT, 3><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, x, s01, y, y_dtype, 1);
+}
+
+template <int TYPE>
+static void launch_rows_x_type(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x, int x_dtype,
+                               int64_t s01, int n, void* y, int y_dtype, hipStream_t stream) {
+  switch (x_dtype) {
+    case kF32: launch_rows_x_dt<TYPE, kF32>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream); break;
+    case kF16: launch_rows_x_dt<TYPE, kF16>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream); break;
+    default: launch_rows_x_dt<TYPE, kBF16>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream); break;
+  }
 }
 
 template <int TYPE, int NC>
@@ -733,6 +896,19 @@ static void launch_type(const uint8_t* W, int64_t row_bytes, int nrows, int k, c
     case 7: launch_nc<TYPE, 7>(W, row_bytes, nrows, k, q8, y, y_dtype, stream); break;
     default: launch_nc<TYPE, 8>(W, row_bytes, nrows, k, q8, y, y_dtype, stream); break;
   }
+}
+
+// Q4_K / IQ4_XS / Q6_K decode with X (dtype x_dtype, row stride s01) quantised in the GEMV, on
+// the shapes gemv_rows_x_supported admits; bit-identical to the q8_1 quantiser + launch_gemv_raw.
+hipError_t launch_gemv_rows_x(int type, const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x,
+                              int x_dtype, int64_t s01, int n, void* y, int y_dtype, hipStream_t stream) {
+  if (!gemv_rows_x_supported(type, nrows, row_bytes, k, n)) return hipErrorInvalidValue;
+  switch (type) {
+    case kQ4_K: launch_rows_x_type<kQ4_K>(W, row_bytes, nrows, k, x, x_dtype, s01, n, y, y_dtype, stream); break;
+    case kIQ4_XS: launch_rows_x_type<kIQ4_XS>(W, row_bytes, nrows, k, x, x_dtype, s01, n, y, y_dtype, stream); break;
+    default: launch_rows_x_type<kQ6_K>(W, row_bytes, nrows, k, x, x_dtype, s01, n, y, y_dtype, stream); break;
+  }
+  return hipGetLastError();
 }
 
 // n in 1..8 activation rows; q8: block_q8_1 of X; y: [n, nrows] in y_dtype.
@@ -859,41 +1035,6 @@ __device__ __forceinline__ float xraw_value(const uint32_t* v, int i) {
   const uint32_t h = (v[i >> 1] >> (16 * (i & 1))) & 0xFFFF;
   if constexpr (XDT == kF16) return half_bits_to_float(h);
   return __uint_as_float(h << 16);
-}
-
-// q8_1 bytes of N (4 or 8) values of one slice, given the slice's amax and d = amax / 127: q =
-// roundf(v / d) (q = 0 when amax == 0), bit for bit as the q8_1 quantiser computes them. The
-// quotient comes from the product v * rcp(d): for |v| <= amax it lies within 2^-15 of v / d (rcp
-// within 1 ulp), and the fp32 rounding of v / d moves that by less than 2^-16, so when the product
-// lies more than 2^-12 from every half-integer, roundf(v / d) is the integer nearest to it. Adding
-// 1.5 * 2^23 rounds to that integer and leaves it in the low mantissa bits. The largest distance
-// is taken over the bit patterns of |a - n|, where a NaN (a NaN or infinite value) ranks above
-// every number. A lane with a value near a tie, a non-finite product or a tiny amax (rcp of a
-// subnormal d) takes the IEEE division. out[j] holds the bytes of values 4j..4j+3.
-template <int N>
-__device__ __forceinline__ void quantize_q81(const float (&v)[N], float amax, float d, uint32_t (&out)[N / 4]) {
-  constexpr float kMagic = 12582912.0f;
-  const float r = __builtin_amdgcn_rcpf(d);
-  uint32_t m[N], dev = 0;
-#pragma unroll
-  for (int e = 0; e < N; ++e) {
-    const float a = v[e] * r;
-    const float t = a + kMagic;
-    m[e] = __float_as_uint(t);
-    dev = max(dev, __float_as_uint(a - (t - kMagic)) & 0x7FFFFFFFu);
-  }
-#pragma unroll
-  for (int j = 0; j < N / 4; ++j)
-    out[j] = __builtin_amdgcn_perm(__builtin_amdgcn_perm(m[4 * j + 3], m[4 * j + 2], 0x0c0c0400u),
-                                   __builtin_amdgcn_perm(m[4 * j + 1], m[4 * j], 0x0c0c0400u), 0x05040100u);
-  if (!(amax >= 0x1p-100f) || dev > __float_as_uint(0.5f - 0x1p-12f)) {
-#pragma unroll
-    for (int j = 0; j < N / 4; ++j) out[j] = 0;
-    if (amax != 0.0f) {
-#pragma unroll
-      for (int e = 0; e < N; ++e) out[e >> 2] |= ((uint32_t)(int)roundf(v[e] / d) & 0xFFu) << (8 * (e & 3));
-    }
-  }
 }
 
 // ex: the wave's 64-dword exchange area; the lane holds values 4p..4p+3 of slice s (the slice's
@@ -1083,44 +1224,6 @@ __global__ void __launch_bounds__(64 * TPW * WPT) gemv_iq3s_tile_kernel(const ui
 // X of the persistent GEMV, staged in LDS: q8 values [NC][slice][8 dwords], then each slice's fp16 d
 // [NC][slice] (one dword, low half). Work unit: group g = 8 values, part g & 3 of slice row
 // g >> 2 (= c * nslices + slice of activation row c). The four lanes of a slice are consecutive.
-template <int XDT>
-struct XGroup {
-  uint32_t v[XDT == kF32 ? 8 : (XDT < 0 ? 3 : 4)];
-};
-
-template <int NC, int XDT>
-__device__ __forceinline__ void xgroup_load(const void* x, __amdgpu_buffer_rsrc_t xrs, int64_t s01, int nslices, int g,
-                                            XGroup<XDT>& r) {
-  const int sr = g >> 2, part = g & 3;
-  if constexpr (XDT < 0) {  // block_q8_1: d (fp16) and s, then 32 q bytes
-    const int o = sr * 36;
-    r.v[0] = __builtin_amdgcn_raw_buffer_load_b32(xrs, o, 0, 0);
-    r.v[1] = __builtin_amdgcn_raw_buffer_load_b32(xrs, o + 4 + 8 * part, 0, 0);
-    r.v[2] = __builtin_amdgcn_raw_buffer_load_b32(xrs, o + 8 + 8 * part, 0, 0);
-  } else {
-    int c = 0, sl = sr;
-#pragma unroll
-    for (int i = 1; i < NC; ++i)
-      if (sl >= nslices) sl -= nslices, ++c;
-    const int64_t e0 = c * s01 + (int64_t)sl * kQ81 + 8 * part;
-    if constexpr (XDT == kF32) {
-      const uint4 a = *(const uint4*)((const float*)x + e0), b = *(const uint4*)((const float*)x + e0 + 4);
-      r.v[0] = a.x; r.v[1] = a.y; r.v[2] = a.z; r.v[3] = a.w;
-      r.v[4] = b.x; r.v[5] = b.y; r.v[6] = b.z; r.v[7] = b.w;
-    } else {
-      const uint4 a = *(const uint4*)((const uint16_t*)x + e0);
-      r.v[0] = a.x; r.v[1] = a.y; r.v[2] = a.z; r.v[3] = a.w;
-    }
-  }
-}
-
-// max over the four lanes of a quad, exchanged by DPP quad permutes (xor 1, then xor 2)
-__device__ __forceinline__ float quad_fmax(float v) {
-  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false)));
-  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false)));
-  return v;
-}
-
 // group g of X into the LDS staging area (every lane of a slice takes part in the amax exchange);
 // a group past the end (live false) is written to `sink`: a load whose only use is a conditional
 // store is moved under the condition by the compiler and then waited for (vmcnt(0)) at the join
@@ -1134,24 +1237,7 @@ __device__ __forceinline__ void xgroup_store(const XGroup<XDT>& r, int g, bool l
     hi = r.v[2];
     dbits = r.v[0] & 0xFFFFu;
   } else {
-    float v[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      if constexpr (XDT == kF32) v[e] = __uint_as_float(r.v[e]);
-      else {
-        const uint32_t h = (r.v[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
-        v[e] = XDT == kF16 ? half_bits_to_float(h) : __uint_as_float(h << 16);
-      }
-    }
-    float amax = fmaxf(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))),
-                       fmaxf(fmaxf(fabsf(v[4]), fabsf(v[5])), fmaxf(fabsf(v[6]), fabsf(v[7]))));
-    amax = quad_fmax(amax);
-    const float d = amax / 127.0f;
-    uint32_t qw[2];
-    quantize_q81<8>(v, amax, d, qw);
-    lo = qw[0];
-    hi = qw[1];
-    dbits = __half_as_ushort(__float2half_rn(d));
+    xgroup_quantize<XDT>(r, lo, hi, dbits);
   }
   *(live ? (uint2*)(xq + sr * 8 + 2 * part) : (uint2*)sink) = make_uint2(lo, hi);
   *(live && part == 0 ? xd + sr : (uint32_t*)sink) = dbits;
