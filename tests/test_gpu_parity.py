@@ -497,13 +497,15 @@ def test_rows_gemv_k_phases(qt, n, k):
     (16 * 700, 2048, 1, torch.bfloat16), (16 * 700, 2048, 1, torch.float16), (16 * 700, 2048, 1, torch.float32),
     (16 * 700, 2048, 2, torch.bfloat16), (16 * 700, 2048, 2, torch.float32),
     (17408, 5120, 1, torch.bfloat16), (17408, 5120, 2, torch.bfloat16),
-    (6144, 5120, 1, torch.bfloat16), (6144, 5120, 1, torch.float16), (6144, 5120, 1, torch.float32)])
+    (8192, 5120, 1, torch.bfloat16), (6144, 5120, 1, torch.bfloat16),
+    (5120, 6144, 1, torch.bfloat16), (5120, 6144, 1, torch.float16), (5120, 6144, 1, torch.float32)])
 def test_fused_quantisation_large_weights(lib, rows, k, n, dtype):
-    """Without x_q8, the packed decode op quantises X itself: all of X into LDS first on weights
-    with more 16-row tiles than the persistent grid (11200 and 17408 rows, one or two activation
-    rows), block by block at one row on weights of up to 32M values (6144 x 5120). It must give
-    the bits of the q8_1 quantiser followed by the GEMV. That these shapes take the fused path
-    is asserted from the op's workspace size (none: no q8_1 copy of X)."""
+    """Without x_q8, the packed decode op quantises X itself. The persistent kernel quantises all
+    of X into LDS first: one row from 3/4 of its grid's tiles on (6144, 8192 rows), two rows with
+    more tiles than its grid (11200 and 17408 rows). The one-tile kernel quantises block by block
+    at one row on weights of up to 32M values with fewer tiles (5120 x 6144). It must give the bits
+    of the q8_1 quantiser followed by the GEMV. That these shapes take the fused path is asserted
+    from the op's workspace size (none: no q8_1 copy of X)."""
     from vllm_gguf_plugin.quantization import iq3_pack
 
     assert lib.gguf_op_workspace_bytes(6, o.IQ3_S, rows, k, n, 0) == 0  # the fused GEMV

@@ -1499,21 +1499,27 @@ hipError_t launch_gemv_packed(const uint8_t* W, int64_t row_bytes, int nrows, in
 }
 
 // nrows % 16 == 0; X [n, k] of dtype x_dtype, quantised in the kernel (bit-identical to the q8_1
-// quantiser followed by the GEMV). n == 1 on weights of up to 32M values: the one-tile kernel,
-// which quantises each block as it goes (measured faster than the two launches for the attention
-// shapes). Otherwise n <= 2 with k / 256 >= 8, X's q8_1 fitting in 48 KB of LDS and more tiles
-// than the persistent grid: the persistent kernel, which quantises all of X into LDS first
-// (17408 x 5120 M = 1: 12.8 us per op against 13.8; with one tile per workgroup, as at
-// 5120 x 17408, the per-workgroup quantisation costs more than the launch it saves).
+// quantiser followed by the GEMV). The persistent kernel, which quantises all of X into LDS first,
+// needs k / 256 >= 8 and X's q8_1 within 48 KB of LDS; it takes one row from 3/4 of its grid's
+// tiles on (graph-timed per op: 6144 x 5120 7.7 us against 8.0 for the one-tile kernel; 8192 x
+// 5120 8.1 against 9.1 for quantise + the persistent GEMV) and two rows on weights with more
+// tiles than its grid (at two rows quantise + GEMV is faster below that: 6144 x 5120 9.5 against
+// 9.8 us). Otherwise one row on weights of up to 32M values: the one-tile kernel, which quantises
+// each block as it goes (measured faster than the two launches for the attention shapes).
+static bool packed_x_persist(int64_t nrows, int64_t k, int64_t n) {
+  const bool fits = k / kQK >= 8 && n * (k / kQ81) * 36 <= 48 * 1024;
+  const int64_t tiles = nrows / kTileRows;
+  return fits && ((n == 1 && 4 * tiles >= 3 * persist_grid()) || (n == 2 && tiles > persist_grid()));
+}
+
 bool gemv_packed_x_supported(int64_t nrows, int64_t k, int64_t n) {
-  if (n == 1 && nrows * k <= ((int64_t)32 << 20)) return true;
-  return n >= 1 && n <= 2 && k / kQK >= 8 && n * (k / kQ81) * 36 <= 48 * 1024 && nrows / kTileRows > persist_grid();
+  return packed_x_persist(nrows, k, n) || (n == 1 && nrows * k <= ((int64_t)32 << 20));
 }
 
 hipError_t launch_gemv_packed_x(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x, int x_dtype,
                                 int64_t s01, int n, void* y, int y_dtype, hipStream_t stream) {
   if (!gemv_packed_x_supported(nrows, k, n)) return hipErrorInvalidValue;
-  const bool small = n == 1 && (int64_t)nrows * k <= ((int64_t)32 << 20);
+  const bool small = !packed_x_persist(nrows, k, n);
   switch (x_dtype) {
     case kF32:
       if (small) launch_gemv_packed_dt<kF32>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream);
