@@ -344,6 +344,29 @@ def test_prefill_vs_q81(qt, n):
     assert o.rel_l2(y, ref) <= 1e-3, o.rel_l2(y, ref)
 
 
+def test_prefill_q6k_largest_subscales():
+    """Q6_K on the fp16 prefill GEMM folds each 16-value sub-scale into the decoded operand;
+    (q - 32) * sc is exact in fp16 up to 2048 and rounds beyond. Every sub-scale at +-127 (each
+    product of magnitude 2048..4064 then rounds): the output still meets the fp32 bar of the
+    float64 model, and an exact-integer run with sub-scales in [-64, 64] (odd products up to
+    2047 in magnitude, all exact) matches the integer sum."""
+    rows, k, n = 144, 1024, 300
+    raw = _w(o.Q6_K, rows, k, seed=611)
+    b = raw.reshape(-1, o.BLOCK_BYTES[o.Q6_K])
+    sign = np.random.default_rng(612).choice([-1, 1], size=(b.shape[0], 16))
+    b[:, 192:208] = (127 * sign).astype(np.int8).view(np.uint8)
+    x = _x(n, k, seed=613)
+    y = C().lcpp_mul_mat_q(_dev(raw), x.cuda(), o.Q6_K, rows).cpu().numpy()
+    ref = o.q81_model(raw, o.Q6_K, x, layout="mmq")
+    assert o.rel_l2(y, ref) <= 1e-3, o.rel_l2(y, ref)
+    raw = _exact_weights(o.Q6_K, rows, k, seed=614)
+    b = raw.reshape(-1, o.BLOCK_BYTES[o.Q6_K])
+    b[:, 192:208] = np.random.default_rng(615).integers(-64, 65, size=(b.shape[0], 16)).astype(np.int8).view(np.uint8)
+    x = _exact_x(n, k, seed=616, dtype=torch.float32)
+    y = C().lcpp_mul_mat_q(_dev(raw), x.cuda(), o.Q6_K, rows).cpu().numpy()
+    np.testing.assert_array_equal(y.astype(np.int64), _exact_ref(raw, o.Q6_K, x))
+
+
 @pytest.mark.parametrize("n", PREFILL_N)
 @pytest.mark.parametrize("k", [512, 5120])
 def test_prefill_packed_vs_q81(n, k):

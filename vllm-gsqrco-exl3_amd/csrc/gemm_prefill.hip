@@ -306,7 +306,10 @@ __global__ void __launch_bounds__(256, 2) gemm_prefill_kernel(const uint8_t* __r
 // or 945 (Q4_K), exact in fp16, and so are the activation's q8 values (the xh layout). One
 // v_mfma_f32_16x16x32_f16 with a zero accumulator then returns sub-scale x integer slice dot
 // exactly (every partial sum is an integer below 2^24), already in fp32, and the per-slice
-// epilogue is one FMA by the activation scale. The row's block scale d is not applied per
+// epilogue is one FMA by the activation scale. Q6_K: the 16-value sub-scale goes into the decoded
+// operand, (q - 32) * sc, so a 32-value slice with two sub-scales is one MFMA as well (the int8
+// GEMM needs one per sub-scale); that product is exact up to 2048 in magnitude and rounds to
+// fp16 beyond (xh_decode.h). The row's block scale d is not applied per
 // slice: each row's accumulator is held in units of the d of the block being summed (e, the last
 // nonzero d; a block with d = 0 decodes to zeros), and is multiplied by e_prev / e_cur when a new
 // block starts and by the last e at the end. The Q4_K min term, sum over slices of
@@ -326,12 +329,13 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW) gemm_prefill_h_kernel(const u
                                                                          const uint8_t* __restrict__ xh, int nct,
                                                                          int n, void* __restrict__ y, int y_dtype) {
   constexpr bool IQ3 = TYPE == kIQ3_S;
+  constexpr bool MIN = TYPE == kQ4_K;  // the min term
   constexpr int TPW = 8 / NW;  // row tiles a wave decodes per step
-  using Raw = typename std::conditional<IQ3, RawIq3, RawQ4k>::type;
+  using Raw = typename std::conditional<IQ3, RawIq3, typename std::conditional<MIN, RawQ4k, RawQ6k>::type>::type;
   __shared__ __attribute__((aligned(16))) uint8_t A[2 * kHA];
   __shared__ __attribute__((aligned(16))) float RT[128];
   __shared__ __attribute__((aligned(16))) float EF[128];
-  __shared__ __attribute__((aligned(16))) float AM[IQ3 ? 4 : 2 * 512];
+  __shared__ __attribute__((aligned(16))) float AM[MIN ? 2 * 512 : 4];
   __shared__ __attribute__((aligned(16))) uint32_t GH[IQ3 ? 1024 : 4];
   __shared__ __attribute__((aligned(16))) uint2 SM[16];
   const int lane = threadIdx.x & 63;
@@ -368,7 +372,7 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW) gemm_prefill_h_kernel(const u
       dxn[c][1] = v[1];
       dxn[c][2] = v[2];
       dxn[c][3] = v[3];
-      if constexpr (!IQ3) sqn[c] = *(const float*)(xs[c] + (int64_t)b * kXhScaleUnit + 512 + 16 * h + 4 * q);
+      if constexpr (MIN) sqn[c] = *(const float*)(xs[c] + (int64_t)b * kXhScaleUnit + 512 + 16 * h + 4 * q);
     }
   };
   auto take_scales = [&]() {
@@ -396,7 +400,7 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW) gemm_prefill_h_kernel(const u
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
       if constexpr (IQ3) load_step(raw[i], wp[i] + (int64_t)b * kTileBlockBytes, h, j, q);
-      else load_step(raw[i], wp[i] + (int64_t)b * block_bytes(kQ4_K), h, q);
+      else load_step(raw[i], wp[i] + (int64_t)b * block_bytes(TYPE), h, q);
     }
   };
   auto decode = [&](int h) {
@@ -405,7 +409,8 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW) gemm_prefill_h_kernel(const u
     for (int i = 0; i < TPW; ++i) {
       const int t = wave * TPW + i;
       if constexpr (IQ3) decode_step(raw[i], h, GH, SM, Ab, RT, EF, e[i], t, j, q);
-      else decode_step(raw[i], h, AM + h * 512, Ab, RT, EF, e[i], t, j, q);
+      else if constexpr (MIN) decode_step(raw[i], h, AM + h * 512, Ab, RT, EF, e[i], t, j, q);
+      else decode_step(raw[i], h, Ab, RT, EF, e[i], t, j, q);
     }
   };
 
@@ -457,7 +462,7 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW) gemm_prefill_h_kernel(const u
       acc[7][0][v] = fmaf(p0[v], dx[0][3], acc[7][0][v]);
       acc[7][1][v] = fmaf(p1[v], dx[1][3], acc[7][1][v]);
     }
-    if constexpr (!IQ3) {  // the min term of the half block
+    if constexpr (MIN) {  // the min term of the half block
 #pragma unroll
       for (int r = 0; r < 8; ++r) {
         const float am = AM[h * 512 + (r * 4 + q) * 16 + j];
@@ -547,7 +552,7 @@ void launch_prefill_t(const uint8_t* W, int64_t row_bytes, int nrows, int k, con
 }  // namespace
 
 // Whether the prefill GEMM of this type takes X in the xh layout (else xq).
-bool prefill_uses_xh(int type, bool packed) { return packed || type == kQ4_K; }
+bool prefill_uses_xh(int type, bool packed) { return packed || type == kQ4_K || type == kQ6_K; }
 
 // Large-M products; xq: X in the xq layout, or the xh layout where prefill_uses_xh. packed: IQ3_S
 // in the tile layout (nrows % 16 == 0).
@@ -559,7 +564,7 @@ hipError_t launch_gemm_prefill(int type, bool packed, const uint8_t* W, int64_t 
     switch (type) {
       case kQ4_K: launch_prefill_h<kQ4_K>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream); break;
       case kIQ4_XS: launch_prefill_t<kIQ4_XS, false>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream); break;
-      case kQ6_K: launch_prefill_t<kQ6_K, false>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream); break;
+      case kQ6_K: launch_prefill_h<kQ6_K>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream); break;
       default: return hipErrorInvalidValue;
     }
   }

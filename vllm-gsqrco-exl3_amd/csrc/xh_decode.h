@@ -1,7 +1,8 @@
 // fp16 decode of weight blocks for the fp16-operand MFMA GEMMs (the prefill GEMM's fp16 variant
-// and the small GEMM): IQ3_S in the tile layout (iq3_tile.h) and Q4_K rows, decoded to fp16
-// values with the slice sub-scale applied (exact integers: at most 465 for IQ3_S, 945 for Q4_K),
-// in the A-operand order of v_mfma_f32_16x16x32_f16.
+// and the small GEMM): IQ3_S in the tile layout (iq3_tile.h), Q4_K and Q6_K rows, decoded to fp16
+// values with the slice (Q6_K: 16-value) sub-scale applied (exact integers: at most 465 for
+// IQ3_S, 945 for Q4_K; Q6_K's up to 4064 round above 2048), in the A-operand order of
+// v_mfma_f32_16x16x32_f16.
 //
 // A decoding lane (row j = lane & 15, part q = lane >> 4) handles one row of a 16-row tile for
 // half a K block (4 slices): IQ3_S slice 4h + q of row j; Q4_K quarter q (8 values) of each of
@@ -159,6 +160,51 @@ __device__ __forceinline__ void decode_step(const RawQ4k& w, int h, float* AM, u
     const uint32_t w3 = h2_bits(__builtin_elementwise_fma(bits_h2(__builtin_amdgcn_perm(0x64646464u, x1, 0x04030402u)), mul, off));
     *(uint4*)(A + h_off(t, u, j, q)) = make_uint4(w0, w1, w2, w3);
     AM[(t * 4 + u) * 16 + j] = mf * (float)m;  // the 4 lanes of row j store the same value
+  }
+}
+
+// Q6_K lane (row j, part q) of the row's block for half block h (values 128h .. 128h + 127, slices
+// 4h + sub): ql bytes [64h + 8q, + 8) (low nibbles: sub 0, high: sub 2) and [64h + 32 + 8q, + 8)
+// (sub 1, 3), qh bytes [32h + 8q, + 8) (bit pair 2 sub), the half's 8 scales, d
+// (dequantize_row_q6_K, ggml-quants.c). Blocks are 210 bytes: 2-byte aligned loads.
+struct RawQ6k {
+  uint64_t la, lb, qh, sc;
+  uint32_t d;
+};
+
+__device__ __forceinline__ void load_step(RawQ6k& w, const uint8_t* blk, int h, int q) {
+  w.la = ld64(blk + 64 * h + 8 * q);
+  w.lb = ld64(blk + 64 * h + 32 + 8 * q);
+  w.qh = ld64(blk + 128 + 32 * h + 8 * q);
+  w.sc = ld64(blk + 192 + 8 * h);
+  w.d = ld16(blk + 208);
+}
+
+// Q6_K: fp16 (1024 + q) by a byte permute, q - 32 by one packed subtract (exact), then times the
+// 16-value sub-scale by one packed multiply. The product (q - 32) * sc is exact in fp16 up to 2048
+// in magnitude; beyond (sub-scales above 64) an odd product rounds to an even neighbour, 2^-12
+// relative at most. The lane's 8 values of slice 4h + sub share sub-scale 2 sub + (q >> 1).
+__device__ __forceinline__ void decode_step(const RawQ6k& w, int h, uint8_t* A, float* RT, float* EF, float& e,
+                                            int t, int j, int q) {
+  const float d = half_bits_to_float(w.d);
+  if (h == 0) next_scale(d, e, RT, EF, t * 16 + j);
+  else e = d != 0.0f ? d : e;
+  const bool nz = d != 0.0f;
+  const h2 bias = {(_Float16)-1056.0f, (_Float16)-1056.0f};
+#pragma unroll
+  for (int sub = 0; sub < 4; ++sub) {
+    const uint64_t l = (sub & 1) ? w.lb : w.la;
+    const int lsh = 4 * (sub >> 1), hsh = 2 * sub;
+    const uint32_t x0 = (((uint32_t)l >> lsh) & 0x0F0F0F0Fu) | ((((uint32_t)w.qh >> hsh) & 0x03030303u) << 4);
+    const uint32_t x1 = (((uint32_t)(l >> 32) >> lsh) & 0x0F0F0F0Fu) | ((((uint32_t)(w.qh >> 32) >> hsh) & 0x03030303u) << 4);
+    const int scv = (int)(int8_t)((w.sc >> (8 * (2 * sub + (q >> 1)))) & 0xFF);
+    const _Float16 scf = nz ? (_Float16)(float)scv : (_Float16)0.0f;
+    const h2 mul = {scf, scf};
+    const uint32_t w0 = h2_bits((bits_h2(__builtin_amdgcn_perm(0x64646464u, x0, 0x04010400u)) + bias) * mul);
+    const uint32_t w1 = h2_bits((bits_h2(__builtin_amdgcn_perm(0x64646464u, x0, 0x04030402u)) + bias) * mul);
+    const uint32_t w2 = h2_bits((bits_h2(__builtin_amdgcn_perm(0x64646464u, x1, 0x04010400u)) + bias) * mul);
+    const uint32_t w3 = h2_bits((bits_h2(__builtin_amdgcn_perm(0x64646464u, x1, 0x04030402u)) + bias) * mul);
+    *(uint4*)(A + h_off(t, sub, j, q)) = make_uint4(w0, w1, w2, w3);
   }
 }
 
