@@ -1,83 +1,104 @@
-"""numpy statement of this build's IQ3_S tile layout (csrc/iq3_tile.h), for checking the GPU
-repack. The layout is the build's own (not a reference format). Rows are grouped in tiles of 16;
-each 256-value block of a tile is one 1760-byte tile-block. Lane L = 8p + s owns rows 2p, 2p+1
-(r = 0, 1) of slice s; for group e (0..7) of row r,
+"""numpy statement of this build's IQ3_S unit layout (csrc/iq3_tile.h), for checking the GPU
+repack. The layout is the build's own (not a reference format). Rows are grouped in units of 4;
+the K blocks of a unit are taken four at a time, blocks 4kb..4kb+3 forming the 1760-byte
+unit-block kb at byte 1760 kb of the unit (a last unit-block of r = nb % 4 blocks takes 440 r
+bytes, its fields scaled by r/4). Lane L = 8p + s, p = 2 bi + rp, owns rows 2rp, 2rp+1 (r = 0, 1)
+of the unit in slice s of block 4kb + bi; for group e (0..7) of row r,
   ex(r, e) = sign nibble e of the slice's sign bytes | (bit e of qh[s]) << 4.
-  [   0, 1024) QS 16 B at 16L: qs[8s:8s+8] of row 2p, then of row 2p+1
-  [1024, 1536) E8  8 B at 8L : byte 4r+j = ex(r, j) | (ex(r, 4+j) & 7) << 5
-  [1536, 1664) L2  2 B at 2L : bits 8r+2j.. = ex(r, 4+j) >> 3
-  [1664, 1728) SC  2 B at 2(4p+j): scales[j] of row 2p, then of row 2p+1
-  [1728, 1760) D   4 B at 4p : d of row 2p, then of row 2p+1
+  [    0, 256 r) QS 16 B at 16L: qs[8s:8s+8] of row 2rp, then of row 2rp+1
+  [256 r, 384 r) E8  8 B at 8L : byte 4r+j = ex(r, j) | (ex(r, 4+j) & 7) << 5
+  [384 r, 416 r) L2  2 B at 2L : bits 8r+2j.. = ex(r, 4+j) >> 3
+  [416 r, 432 r) SC  2 B at 2(4p+j): scales[j] of row 2rp, then of row 2rp+1
+  [432 r, 440 r) D   4 B at 4p : d of row 2rp, then of row 2rp+1
 """
 
 import numpy as np
 
-QS, E8, L2, SC, D = 0, 1024, 1536, 1664, 1728
+QS, E8, L2, SC, D = 0, 256, 384, 416, 432   # field bases per block of the unit-block (times r)
 
 
-def _tileblocks(w):
-    rows, rb = w.shape
-    nb = rb // 110
-    return w.reshape(rows // 16, 16, nb, 110), nb
+def unit_blocks(nb):
+    """(kb, r, byte offset in the unit) of each unit-block of a unit of nb blocks."""
+    out, off = [], 0
+    for kb in range((nb + 3) // 4):
+        r = min(4, nb - 4 * kb)
+        out.append((kb, r, off))
+        off += 440 * r
+    return out
+
+
+def _lane_ex(blk, s):
+    """ex(r, e) of slice s for a [..., 110] array of GGUF blocks (uint32)."""
+    sg = blk[..., 74 + 4 * s] | blk[..., 75 + 4 * s] << 8 | blk[..., 76 + 4 * s] << 16 | blk[..., 77 + 4 * s] << 24
+    qh = blk[..., 66 + s]
+    return [((sg >> (4 * e)) & 0xF) | (((qh >> e) & 1) << 4) for e in range(8)]
 
 
 def pack(w: np.ndarray) -> np.ndarray:
-    """[rows, row_bytes] GGUF IQ3_S rows (rows % 16 == 0) -> the tile layout."""
+    """[rows, row_bytes] GGUF IQ3_S rows (rows % 4 == 0) -> the unit layout."""
     rows, rb = w.shape
-    t, nb = _tileblocks(w.astype(np.uint32))
-    nt = rows // 16
-    out = np.zeros((nt, nb, 1760), dtype=np.uint8)
-    for L in range(64):
-        p, s = L // 8, L % 8
-        l2 = np.zeros((nt, nb), dtype=np.uint32)
-        for r in range(2):
-            blk = t[:, 2 * p + r]                                   # [nt, nb, 110]
-            out[:, :, QS + 16 * L + 8 * r:QS + 16 * L + 8 * r + 8] = blk[..., 2 + 8 * s:10 + 8 * s]
-            sg = (blk[..., 74 + 4 * s] | blk[..., 75 + 4 * s] << 8 | blk[..., 76 + 4 * s] << 16
-                  | blk[..., 77 + 4 * s] << 24)
-            qh = blk[..., 66 + s]
-            ex = [((sg >> (4 * e)) & 0xF) | (((qh >> e) & 1) << 4) for e in range(8)]
-            for j in range(4):
-                out[:, :, E8 + 8 * L + 4 * r + j] = ex[j] | ((ex[4 + j] & 7) << 5)
-                l2 |= (ex[4 + j] >> 3) << (8 * r + 2 * j)
-        out[:, :, L2 + 2 * L] = l2 & 0xFF
-        out[:, :, L2 + 2 * L + 1] = l2 >> 8
-    for p in range(8):
-        for j in range(4):
-            for r in range(2):
-                out[:, :, SC + 2 * (4 * p + j) + r] = t[:, 2 * p + r, :, 106 + j]
-        for r in range(2):
-            out[:, :, D + 4 * p + 2 * r:D + 4 * p + 2 * r + 2] = t[:, 2 * p + r, :, 0:2]
-    return out.reshape(rows, rb)
+    nb = rb // 110
+    nu = rows // 4
+    g = w.astype(np.uint32).reshape(nu, 4, nb, 110)
+    out = np.zeros((nu, 4 * rb), dtype=np.uint8)
+    for kb, r, base in unit_blocks(nb):
+        for L in range(16 * r):
+            bi, rp, s = L // 16, (L // 8) % 2, L % 8
+            b = 4 * kb + bi
+            l2 = np.zeros(nu, dtype=np.uint32)
+            for rr in range(2):
+                blk = g[:, 2 * rp + rr, b]                          # [nu, 110]
+                o = base + QS * r + 16 * L + 8 * rr
+                out[:, o:o + 8] = blk[:, 2 + 8 * s:10 + 8 * s]
+                ex = _lane_ex(blk, s)
+                for j in range(4):
+                    out[:, base + E8 * r + 8 * L + 4 * rr + j] = ex[j] | ((ex[4 + j] & 7) << 5)
+                    l2 |= (ex[4 + j] >> 3) << (8 * rr + 2 * j)
+            out[:, base + L2 * r + 2 * L] = l2 & 0xFF
+            out[:, base + L2 * r + 2 * L + 1] = l2 >> 8
+        for p in range(2 * r):
+            bi, rp = p // 2, p % 2
+            b = 4 * kb + bi
+            for rr in range(2):
+                for j in range(4):
+                    out[:, base + SC * r + 2 * (4 * p + j) + rr] = g[:, 2 * rp + rr, b, 106 + j]
+                o = base + D * r + 4 * p + 2 * rr
+                out[:, o:o + 2] = g[:, 2 * rp + rr, b, 0:2]
+    return out.reshape(rows, rb)  # a unit's bytes occupy its 4 rows in order
 
 
 def unpack(pk: np.ndarray) -> np.ndarray:
     rows, rb = pk.shape
     nb = rb // 110
-    nt = rows // 16
-    tb = pk.reshape(nt, nb, 1760).astype(np.uint32)
-    out = np.zeros((nt, 16, nb, 110), dtype=np.uint32)
-    for L in range(64):
-        p, s = L // 8, L % 8
-        l2 = tb[..., L2 + 2 * L] | tb[..., L2 + 2 * L + 1] << 8
-        for r in range(2):
-            row = out[:, 2 * p + r]
-            row[..., 2 + 8 * s:10 + 8 * s] = tb[..., QS + 16 * L + 8 * r:QS + 16 * L + 8 * r + 8]
-            sg = np.zeros((nt, nb), dtype=np.uint32)
-            qh = np.zeros((nt, nb), dtype=np.uint32)
-            for e in range(8):
-                j = e % 4
-                byte = tb[..., E8 + 8 * L + 4 * r + j]
-                ex = (byte & 0x1F) if e < 4 else ((byte >> 5) | (((l2 >> (8 * r + 2 * j)) & 3) << 3))
-                sg |= (ex & 0xF) << (4 * e)
-                qh |= ((ex >> 4) & 1) << e
-            for i in range(4):
-                row[..., 74 + 4 * s + i] = (sg >> (8 * i)) & 0xFF
-            row[..., 66 + s] = qh
-    for p in range(8):
-        for j in range(4):
-            for r in range(2):
-                out[:, 2 * p + r, :, 106 + j] = tb[..., SC + 2 * (4 * p + j) + r]
-        for r in range(2):
-            out[:, 2 * p + r, :, 0:2] = tb[..., D + 4 * p + 2 * r:D + 4 * p + 2 * r + 2]
+    nu = rows // 4
+    t = pk.reshape(nu, 4 * rb).astype(np.uint32)
+    out = np.zeros((nu, 4, nb, 110), dtype=np.uint32)
+    for kb, r, base in unit_blocks(nb):
+        for L in range(16 * r):
+            bi, rp, s = L // 16, (L // 8) % 2, L % 8
+            b = 4 * kb + bi
+            l2 = t[:, base + L2 * r + 2 * L] | t[:, base + L2 * r + 2 * L + 1] << 8
+            for rr in range(2):
+                row = out[:, 2 * rp + rr, b]
+                o = base + QS * r + 16 * L + 8 * rr
+                row[:, 2 + 8 * s:10 + 8 * s] = t[:, o:o + 8]
+                sg = np.zeros(nu, dtype=np.uint32)
+                qh = np.zeros(nu, dtype=np.uint32)
+                for e in range(8):
+                    j = e % 4
+                    byte = t[:, base + E8 * r + 8 * L + 4 * rr + j]
+                    ex = (byte & 0x1F) if e < 4 else ((byte >> 5) | (((l2 >> (8 * rr + 2 * j)) & 3) << 3))
+                    sg |= (ex & 0xF) << (4 * e)
+                    qh |= ((ex >> 4) & 1) << e
+                for i in range(4):
+                    row[:, 74 + 4 * s + i] = (sg >> (8 * i)) & 0xFF
+                row[:, 66 + s] = qh
+        for p in range(2 * r):
+            bi, rp = p // 2, p % 2
+            b = 4 * kb + bi
+            for rr in range(2):
+                for j in range(4):
+                    out[:, 2 * rp + rr, b, 106 + j] = t[:, base + SC * r + 2 * (4 * p + j) + rr]
+                o = base + D * r + 4 * p + 2 * rr
+                out[:, 2 * rp + rr, b, 0:2] = t[:, o:o + 2]
     return out.astype(np.uint8).reshape(rows, rb)

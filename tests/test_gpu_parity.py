@@ -521,14 +521,14 @@ def test_rows_gemv_k_phases(qt, n, k):
     (16 * 700, 2048, 2, torch.bfloat16), (16 * 700, 2048, 2, torch.float32),
     (17408, 5120, 1, torch.bfloat16), (17408, 5120, 2, torch.bfloat16),
     (8192, 5120, 1, torch.bfloat16), (6144, 5120, 1, torch.bfloat16),
-    (5120, 6144, 1, torch.bfloat16), (5120, 6144, 1, torch.float16), (5120, 6144, 1, torch.float32)])
+    (5120, 6144, 1, torch.bfloat16), (5120, 6144, 1, torch.float16), (5120, 6144, 1, torch.float32),
+    (512, 6144, 1, torch.bfloat16), (512, 6144, 1, torch.float32)])
 def test_fused_quantisation_large_weights(lib, rows, k, n, dtype):
-    """Without x_q8, the packed decode op quantises X itself. The persistent kernel quantises all
-    of X into LDS first: one row from 3/4 of its grid's tiles on (6144, 8192 rows), two rows with
-    more tiles than its grid (11200 and 17408 rows). The one-tile kernel quantises block by block
-    at one row on weights of up to 32M values with fewer tiles (5120 x 6144). It must give the bits
-    of the q8_1 quantiser followed by the GEMV. That these shapes take the fused path is asserted
-    from the op's workspace size (none: no q8_1 copy of X)."""
+    """Without x_q8, the packed decode op quantises X itself. The stream kernel (weights of at least
+    one 4-row unit per CU, K <= 8192) quantises all of X into LDS first, at one or two rows; the
+    one-tile kernel quantises block by block at one row on smaller weights (512 rows). It must give
+    the bits of the q8_1 quantiser followed by the GEMV. That these shapes take the fused path is
+    asserted from the op's workspace size (none: no q8_1 copy of X)."""
     from vllm_gguf_plugin.quantization import iq3_pack
 
     assert lib.gguf_op_workspace_bytes(6, o.IQ3_S, rows, k, n, 0) == 0  # the fused GEMV
@@ -578,16 +578,16 @@ def _tie_slices(k, dtype, seed):
 
 @pytest.mark.parametrize("n,dtype,rows", [(1, torch.bfloat16, 16 * 700), (1, torch.float16, 16 * 700),
                                           (1, torch.float32, 16 * 700), (2, torch.bfloat16, 16 * 700),
-                                          (2, torch.float32, 16 * 700), (1, torch.bfloat16, 1024),
-                                          (1, torch.float16, 1024), (1, torch.float32, 1024)])
+                                          (2, torch.float32, 16 * 700), (1, torch.bfloat16, 512),
+                                          (1, torch.float16, 512), (1, torch.float32, 512)])
 def test_fused_quantisation_ties(n, dtype, rows):
-    """The packed GEMV's in-kernel quantisation (all of X into LDS on the persistent kernel, 11200
-    rows; block by block on the one-tile kernel, 1024 rows) rounds x / d from a reciprocal product
+    """The packed GEMV's in-kernel quantisation (all of X into LDS on the stream kernel, 11200 rows;
+    block by block on the one-tile kernel, 512 rows) rounds x / d from a reciprocal product
     and takes the IEEE division for values near a tie, non-finite values and tiny scales: its
     bytes, and so the outputs, must equal those of the q8_1 quantiser bit for bit (NaN included)."""
     from vllm_gguf_plugin.quantization import iq3_pack
 
-    k = 4096  # 11200 x 4096: more tiles than the persistent grid, above the one-tile path's size
+    k = 4096  # 11200 x 4096: more than one unit per CU (stream kernel); 512 rows: the one-tile kernel
     w = iq3_pack.pack(_dev(_w(o.IQ3_S, rows, k, seed=190 + n)), o.IQ3_S)
     x = torch.stack([_tie_slices(k, dtype, seed=191 + c) for c in range(n)]).cuda()
     q8 = C().lcpp_quantize_q8_1(x, o.IQ3_S, False, False)
@@ -595,6 +595,34 @@ def test_fused_quantisation_ties(n, dtype, rows):
     b = C().lcpp_mul_mat_vec_iq3_mma_packed(w, x, o.IQ3_S, rows, q8)
     bits = torch.int32 if dtype == torch.float32 else torch.int16
     assert torch.equal(a.view(bits), b.view(bits))
+
+
+@pytest.mark.parametrize("n", [1, 2, 3, 4])
+@pytest.mark.parametrize("rows,k", [(16 * 70, 5632), (16 * 70, 5120), (4096, 1536)])
+def test_stream_gemv_units(n, rows, k):
+    """The stream GEMV over 4-row units: 1120 rows give 280 units over the CUs, so workgroups own 1
+    or 2 units and waves' runs start and end inside units; K = 5632 (22 blocks) ends every unit in
+    a 2-block unit-block, whose other lanes must add nothing; 4096 x 1536 has 6 blocks per row.
+    With x_q8 (q8_1 input, 1-4 rows) and without (X quantised in the kernel, 1-2 rows): within 1e-3
+    of the q81 model, the two bit-identical, and graph replays bit-identical."""
+    from vllm_gguf_plugin.quantization import iq3_pack
+
+    raw = _w(o.IQ3_S, rows, k, seed=230 + n)
+    w = iq3_pack.pack(_dev(raw), o.IQ3_S)
+    x = _x(n, k, seed=231 + n, dtype=torch.bfloat16).cuda()
+    q8 = C().lcpp_quantize_q8_1(x, o.IQ3_S, False, False)
+    b = C().lcpp_mul_mat_vec_iq3_mma_packed(w, x, o.IQ3_S, rows, q8)
+    ref = o.q81_model(raw, o.IQ3_S, x.cpu())
+    assert o.rel_l2(b.float().cpu().numpy(), ref) <= TIGHT[torch.bfloat16]
+    a = C().lcpp_mul_mat_vec_iq3_mma_packed(w, x, o.IQ3_S, rows)
+    assert torch.equal(a, b)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = C().lcpp_mul_mat_vec_iq3_mma_packed(w, x, o.IQ3_S, rows, q8)
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, b)
 
 
 ROWS_TYPES = [o.Q4_K, o.IQ4_XS, o.Q6_K]

@@ -56,12 +56,14 @@ __device__ __forceinline__ uint32_t grid_signed(const uint32_t* grid, uint32_t q
   return (uint32_t)apply_signs(grid[qs | ((ex >> 4) << 8)], ex & 0xF);
 }
 
-__device__ __forceinline__ void stage_iq3_tile(const uint8_t* tb, const uint32_t* grid, uint8_t* A, uint8_t* S,
-                                               float* D, int t, int lane) {
+__device__ __forceinline__ void stage_iq3_tile(const uint8_t* tile, int64_t row_bytes, int nb, int b,
+                                               const uint32_t* grid, uint8_t* A, uint8_t* S, float* D, int t, int lane) {
   const int p = lane >> 3, s = lane & 7;
-  const u32x4 qs = *(const u32x4*)(tb + kTqs + 16 * lane);
-  const uint2 e8 = *(const uint2*)(tb + kTe8 + 8 * lane);
-  const uint32_t l2 = *(const uint16_t*)(tb + kTl2 + 2 * lane);
+  const Iq3Fields f = iq3_block_fields(nb, b), l = iq3_lane_fields(p & 1, s);
+  const uint8_t* u = tile + (int64_t)(p >> 1) * kUnitRows * row_bytes;  // rows 2p, 2p+1: unit p >> 1
+  const u32x4 qs = *(const u32x4*)(u + f.qs + l.qs);
+  const uint2 e8 = *(const uint2*)(u + f.e8 + l.e8);
+  const uint32_t l2 = *(const uint16_t*)(u + f.l2 + l.l2);
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
     uint32_t lo, hi;
@@ -76,10 +78,10 @@ __device__ __forceinline__ void stage_iq3_tile(const uint8_t* tb, const uint32_t
     const int j = 2 * p + r;
 #pragma unroll
     for (int q = 0; q < 4; ++q) *(uint2*)(A + a_off(t, s, j, q)) = make_uint2(w[2 * q], w[2 * q + 1]);
-    // sub-scale ls = 1 + 2 * nibble of (row j, slice s); SC byte 2 (4p + s/2) + r, nibble s & 1
-    const uint32_t scb = tb[kTsc + 2 * (4 * p + (s >> 1)) + r];
+    // sub-scale ls = 1 + 2 * nibble of (row j, slice s); SC byte 2 (s/2) + r of the row pair, nibble s & 1
+    const uint32_t scb = u[f.sc + l.sc + 2 * (s >> 1) + r];
     S[(t * 8 + s) * 32 + j] = (uint8_t)(1 + 2 * ((scb >> (4 * (s & 1))) & 0xF));
-    if (s == 0) D[(t * 16 + j) * 2] = half_bits_to_float(*(const uint16_t*)(tb + kTd + 4 * p + 2 * r));
+    if (s == 0) D[(t * 16 + j) * 2] = half_bits_to_float(*(const uint16_t*)(u + f.d + l.d + 2 * r));
   }
 }
 
@@ -210,7 +212,7 @@ __global__ void __launch_bounds__(256, 2) gemm_prefill_kernel(const uint8_t* __r
       const int t = wave * 2 + i;
       const int gt = tile0 + t < ntiles ? tile0 + t : ntiles - 1;
       if constexpr (TILE) {
-        stage_iq3_tile(W + (int64_t)gt * kTileRows * row_bytes + (int64_t)b * kTileBlockBytes, grid, A, S, D, t, lane);
+        stage_iq3_tile(W + (int64_t)gt * kTileRows * row_bytes, row_bytes, nb, b, grid, A, S, D, t, lane);
       } else {
         const int row = gt * 16 + j;
         const bool valid = row < nrows;
@@ -399,7 +401,7 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW) gemm_prefill_h_kernel(const u
   auto load_w = [&](int b, int h) {
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
-      if constexpr (IQ3) load_step(raw[i], wp[i] + (int64_t)b * kTileBlockBytes, h, j, q);
+      if constexpr (IQ3) load_step(raw[i], wp[i], row_bytes, nb, b, h, j, q);
       else load_step(raw[i], wp[i] + (int64_t)b * block_bytes(TYPE), h, q);
     }
   };

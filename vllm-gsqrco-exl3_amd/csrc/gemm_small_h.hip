@@ -125,7 +125,7 @@ __global__ void __launch_bounds__(64 * (2 * RT + NM), 4) gemm_small_h_kernel(con
     // the raw bytes of a block: two named sets, each refilled right after its decode and used
     // two steps later
     auto load_w = [&](int b, Raw& raw) {
-      if constexpr (IQ3) load_step(raw, wp + (int64_t)b * kTileBlockBytes, dh, j, q);
+      if constexpr (IQ3) load_step(raw, wp, row_bytes, nb, b, dh, j, q);
       else load_step(raw, wp + (int64_t)b * block_bytes(kQ4_K), dh, q);
     };
     auto decode = [&](int par, const Raw& raw) {

@@ -1,12 +1,12 @@
-// int8-MFMA GEMM for IQ3_S in the tile layout (iq3_tile.h) on activations in the xq layout (xq.h):
+// int8-MFMA GEMM for IQ3_S in the unit layout (iq3_tile.h) on activations in the xq layout (xq.h):
 // Y[c, r] = sum_k X[c, k] * W[r, k] for 9+ activation rows.
 //
 // Replaces the reference's tiled IQ3 products on packed weights (lcpp_owned_iq3_mma.cu:769-1020,
 // lcpp_mul_mat_iq3_packed / lcpp_mul_mat_vec_iq3_mma_packed above 8 rows) with a gfx950 design:
 //  * a workgroup owns RW 16-row tiles and NT column tiles of 16 activation rows; its KS waves
 //    split the K blocks;
-//  * per K block a wave loads each tile-block with the decode GEMV's contiguous loads (lane
-//    L = 8p + s: slice s of rows 2p, 2p+1), turns every 4-value group into one read of the 32 KB
+//  * per K block a wave loads each tile's block with the decode GEMV's loads (lane L = 8p + s:
+//    slice s of rows 2p, 2p+1, i.e. of row pair p & 1 of unit p >> 1), turns every 4-value group into one read of the 32 KB
 //    signed-grid table in LDS, and writes the int8 values to a per-wave LDS buffer from which
 //    lane 16q + j reads the MFMA A operand (values 8q..8q+7 of slice u of tile row j);
 //  * the B operands of the block come from the xq unit with four 16-byte loads per lane and
@@ -41,14 +41,29 @@ struct MmaFrag {
   uint32_t d01, d23;  // fp16 d of rows 4q .. 4q+3
 };
 
-__device__ __forceinline__ void load_mma_frag(__amdgpu_buffer_rsrc_t rs, int boff, int lane, int q, MmaFrag& f) {
-  f.qs = __builtin_amdgcn_raw_buffer_load_b128(rs, 16 * lane, boff, 0);
-  const auto e = __builtin_amdgcn_raw_buffer_load_b64(rs, kTe8 + 8 * lane, boff, 0);
+// a lane's byte offsets in one K block: decode view (rows 2p, 2p+1 of the tile: unit p >> 1, row
+// pair p & 1; slice s), MFMA view (the scale and d bytes of rows 4q..4q+3: unit q)
+struct MmaOffs {
+  uint32_t qs, e8, l2, sc, d;
+};
+
+__device__ __forceinline__ MmaOffs mma_offsets(int p, int s, int q, int64_t row_bytes) {
+  const uint32_t u = (uint32_t)((p >> 1) * kUnitRows * row_bytes), uq = (uint32_t)(q * kUnitRows * row_bytes);
+  const Iq3Fields l = iq3_lane_fields(p & 1, s);
+  return {u + l.qs, u + l.e8, u + l.l2, uq, uq};
+}
+
+// K block b of the tile at byte toff of rs (scalar field bases) at the lane's offsets
+__device__ __forceinline__ void load_mma_frag(__amdgpu_buffer_rsrc_t rs, uint32_t toff, int nb, int b, const MmaOffs& o,
+                                              MmaFrag& f) {
+  const Iq3Fields bf = iq3_block_fields(nb, b);
+  f.qs = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)o.qs, (int)(toff + bf.qs), 0);
+  const auto e = __builtin_amdgcn_raw_buffer_load_b64(rs, (int)o.e8, (int)(toff + bf.e8), 0);
   f.e8x = e[0];
   f.e8y = e[1];
-  f.l2 = __builtin_amdgcn_raw_buffer_load_b16(rs, kTl2 + 2 * lane, boff, 0);
-  f.sc = __builtin_amdgcn_raw_buffer_load_b128(rs, kTsc + 16 * q, boff, 0);
-  const auto d = __builtin_amdgcn_raw_buffer_load_b64(rs, kTd + 8 * q, boff, 0);
+  f.l2 = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)o.l2, (int)(toff + bf.l2), 0);
+  f.sc = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)o.sc, (int)(toff + bf.sc), 0);
+  const auto d = __builtin_amdgcn_raw_buffer_load_b64(rs, (int)o.d, (int)(toff + bf.d), 0);
   f.d01 = d[0];
   f.d23 = d[1];
 }
@@ -182,6 +197,7 @@ __global__ void __launch_bounds__(64 * KS) gemm_iq3s_tile_kernel(const uint8_t* 
   const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(xq, (uint32_t)xq_bytes((int64_t)nct * kXqCols, k));
   const uint8_t* tbl = (const uint8_t*)table;
   uint8_t* tr = (uint8_t*)trbuf[wave];
+  const MmaOffs mo = mma_offsets(p, s, q, row_bytes);
 
   float acc[RW][NT][4];
 #pragma unroll
@@ -197,9 +213,9 @@ __global__ void __launch_bounds__(64 * KS) gemm_iq3s_tile_kernel(const uint8_t* 
   int units[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) units[t] = (ct0 + t < nct ? ct0 + t : nct - 1) * nb;
-  int toff[RW];
+  uint32_t toff[RW];
 #pragma unroll
-  for (int r = 0; r < RW; ++r) toff[r] = (int)((r < tiles_here ? r : tiles_here - 1) * tile_bytes);
+  for (int r = 0; r < RW; ++r) toff[r] = (uint32_t)((r < tiles_here ? r : tiles_here - 1) * tile_bytes);
   // Two blocks per iteration (an odd last block after the loop); every load feeds a use that is
   // not behind a branch of its own (the compiler sinks a load whose only use is conditional to
   // that use, which would serialise the prefetch). The prefetch past the wave's last block reads
@@ -209,7 +225,7 @@ __global__ void __launch_bounds__(64 * KS) gemm_iq3s_tile_kernel(const uint8_t* 
   if (b_begin < b_end) {
     load_xq_frag<NT>(xrs, units, b_begin, sbase, lane, j, xa);
 #pragma unroll
-    for (int r = 0; r < RW; ++r) load_mma_frag(wrs, toff[r] + b_begin * kTileBlockBytes, lane, q, fa[r]);
+    for (int r = 0; r < RW; ++r) load_mma_frag(wrs, toff[r], nb, b_begin, mo, fa[r]);
   }
   iq3_table_to_lds<KS>(table, &kIq3sSignedMma, wave, lane);
   __builtin_amdgcn_s_waitcnt(0);
@@ -221,13 +237,13 @@ __global__ void __launch_bounds__(64 * KS) gemm_iq3s_tile_kernel(const uint8_t* 
     const __amdgpu_buffer_rsrc_t rs2 = b + 2 < b_end ? wrs : nrs;
     load_xq_frag<NT>(xrs, units, b + 1, sbase, lane, j, xb);
 #pragma unroll
-    for (int r = 0; r < RW; ++r) load_mma_frag(wrs, toff[r] + (b + 1) * kTileBlockBytes, lane, q, fb[r]);
+    for (int r = 0; r < RW; ++r) load_mma_frag(wrs, toff[r], nb, b + 1, mo, fb[r]);
     __builtin_amdgcn_sched_barrier(0);  // the scheduler hoists the next block's decode (and its
                                         // wait) above these loads otherwise
     mma_block<NT, RW>(tbl, tr, fa, xa, p, s, q, j, acc);
     load_xq_frag<NT>(xrs, units, b2, sbase, lane, j, xa);
 #pragma unroll
-    for (int r = 0; r < RW; ++r) load_mma_frag(rs2, toff[r] + (b + 2) * kTileBlockBytes, lane, q, fa[r]);
+    for (int r = 0; r < RW; ++r) load_mma_frag(rs2, toff[r], nb, b + 2, mo, fa[r]);
     __builtin_amdgcn_sched_barrier(0);
     mma_block<NT, RW>(tbl, tr, fb, xb, p, s, q, j, acc);
   }
@@ -273,7 +289,7 @@ void launch_tile_gemm(const uint8_t* W, int64_t row_bytes, int nrows, int k, con
 
 }  // namespace
 
-// IQ3_S in the tile layout; nrows % 16 == 0; xq: X in the xq layout (launch_quantize_xq).
+// IQ3_S in the unit layout; nrows % 16 == 0; xq: X in the xq layout (launch_quantize_xq).
 // Launch shapes measured at 17408 x 5120, 5120 x 17408 and 5120 x 5120: four waves per tile,
 // eight for one column tile on matrices of fewer than 512 tiles (more waves per tile to fill
 // the GPU); above 64 activation rows the y grid walks groups of four column tiles.

@@ -16,13 +16,12 @@
 #include <algorithm>
 
 #include "decode.h"
-#include "iq3_tile.h"
+#include "gemv_x.h"
 
 namespace gguf {
 
 constexpr int kGemvWaves = 4;
 
-static int persist_grid();
 
 // The slice term of one (row, column) pair in the reference's decode-op (MMVQ) arithmetic, from
 // the slice's decoded words w, the column's q8 words x, d8 and (Q4_K, Q2_K) q8 sums:
@@ -310,102 +309,6 @@ __device__ __forceinline__ void xgroup_q8_load(__amdgpu_buffer_rsrc_t xrs, int g
   r.q1 = __builtin_amdgcn_raw_buffer_load_b32(xrs, o + 8 + 8 * part, 0, 0);
 }
 
-// q8_1 bytes of N (4 or 8) values of one slice, given the slice's amax and d = amax / 127: q =
-// roundf(v / d) (q = 0 when amax == 0), bit for bit as the q8_1 quantiser computes them. The
-// quotient comes from the product v * rcp(d): for |v| <= amax it lies within 2^-15 of v / d (rcp
-// within 1 ulp), and the fp32 rounding of v / d moves that by less than 2^-16, so when the product
-// lies more than 2^-12 from every half-integer, roundf(v / d) is the integer nearest to it. Adding
-// 1.5 * 2^23 rounds to that integer and leaves it in the low mantissa bits. The largest distance
-// is taken over the bit patterns of |a - n|, where a NaN (a NaN or infinite value) ranks above
-// every number. A lane with a value near a tie, a non-finite product or a tiny amax (rcp of a
-// subnormal d) takes the IEEE division. out[j] holds the bytes of values 4j..4j+3.
-template <int N>
-__device__ __forceinline__ void quantize_q81(const float (&v)[N], float amax, float d, uint32_t (&out)[N / 4]) {
-  constexpr float kMagic = 12582912.0f;
-  const float r = __builtin_amdgcn_rcpf(d);
-  uint32_t m[N], dev = 0;
-#pragma unroll
-  for (int e = 0; e < N; ++e) {
-    const float a = v[e] * r;
-    const float t = a + kMagic;
-    m[e] = __float_as_uint(t);
-    dev = max(dev, __float_as_uint(a - (t - kMagic)) & 0x7FFFFFFFu);
-  }
-#pragma unroll
-  for (int j = 0; j < N / 4; ++j)
-    out[j] = __builtin_amdgcn_perm(__builtin_amdgcn_perm(m[4 * j + 3], m[4 * j + 2], 0x0c0c0400u),
-                                   __builtin_amdgcn_perm(m[4 * j + 1], m[4 * j], 0x0c0c0400u), 0x05040100u);
-  if (!(amax >= 0x1p-100f) || dev > __float_as_uint(0.5f - 0x1p-12f)) {
-#pragma unroll
-    for (int j = 0; j < N / 4; ++j) out[j] = 0;
-    if (amax != 0.0f) {
-#pragma unroll
-      for (int e = 0; e < N; ++e) out[e >> 2] |= ((uint32_t)(int)roundf(v[e] / d) & 0xFFu) << (8 * (e & 3));
-    }
-  }
-}
-
-template <int XDT>
-struct XGroup {
-  uint32_t v[XDT == kF32 ? 8 : (XDT < 0 ? 3 : 4)];
-};
-
-template <int NC, int XDT>
-__device__ __forceinline__ void xgroup_load(const void* x, __amdgpu_buffer_rsrc_t xrs, int64_t s01, int nslices, int g,
-                                            XGroup<XDT>& r) {
-  const int sr = g >> 2, part = g & 3;
-  if constexpr (XDT < 0) {  // block_q8_1: d (fp16) and s, then 32 q bytes
-    const int o = sr * 36;
-    r.v[0] = __builtin_amdgcn_raw_buffer_load_b32(xrs, o, 0, 0);
-    r.v[1] = __builtin_amdgcn_raw_buffer_load_b32(xrs, o + 4 + 8 * part, 0, 0);
-    r.v[2] = __builtin_amdgcn_raw_buffer_load_b32(xrs, o + 8 + 8 * part, 0, 0);
-  } else {
-    int c = 0, sl = sr;
-#pragma unroll
-    for (int i = 1; i < NC; ++i)
-      if (sl >= nslices) sl -= nslices, ++c;
-    const int64_t e0 = c * s01 + (int64_t)sl * kQ81 + 8 * part;
-    if constexpr (XDT == kF32) {
-      const uint4 a = *(const uint4*)((const float*)x + e0), b = *(const uint4*)((const float*)x + e0 + 4);
-      r.v[0] = a.x; r.v[1] = a.y; r.v[2] = a.z; r.v[3] = a.w;
-      r.v[4] = b.x; r.v[5] = b.y; r.v[6] = b.z; r.v[7] = b.w;
-    } else {
-      const uint4 a = *(const uint4*)((const uint16_t*)x + e0);
-      r.v[0] = a.x; r.v[1] = a.y; r.v[2] = a.z; r.v[3] = a.w;
-    }
-  }
-}
-
-// max over the four lanes of a quad, exchanged by DPP quad permutes (xor 1, then xor 2)
-__device__ __forceinline__ float quad_fmax(float v) {
-  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false)));
-  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false)));
-  return v;
-}
-
-// q8_1 bytes (lo: values 0..3, hi: 4..7) and fp16 d of the group of 8 raw values in r: the four
-// lanes of the slice exchange their amax (the quantiser's arithmetic, bit-identical bytes)
-template <int XDT>
-__device__ __forceinline__ void xgroup_quantize(const XGroup<XDT>& r, uint32_t& lo, uint32_t& hi, uint32_t& dbits) {
-  float v[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    if constexpr (XDT == kF32) v[e] = __uint_as_float(r.v[e]);
-    else {
-      const uint32_t h = (r.v[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
-      v[e] = XDT == kF16 ? half_bits_to_float(h) : __uint_as_float(h << 16);
-    }
-  }
-  float amax = fmaxf(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))),
-                     fmaxf(fmaxf(fabsf(v[4]), fabsf(v[5])), fmaxf(fabsf(v[6]), fabsf(v[7]))));
-  amax = quad_fmax(amax);
-  const float d = amax / 127.0f;
-  uint32_t qw[2];
-  quantize_q81<8>(v, amax, d, qw);
-  lo = qw[0];
-  hi = qw[1];
-  dbits = __half_as_ushort(__float2half_rn(d));
-}
 
 // SUMS: what the second word of a slice's (d8, .) pair holds. kSumSlice: the slice's sum of q (as
 // float; Q4_K's min term). kSumHalves: the sums of q over values 0..15 and 16..31 as two int16 in
@@ -940,601 +843,5 @@ hipError_t launch_gemv_raw(int type, const uint8_t* W, int64_t row_bytes, int nr
   return hipGetLastError();
 }
 
-
-// ---------------------------------------------------------------------------------------------
-// IQ3_S in the tile layout (iq3_tile.h). A workgroup owns one 16-row tile; its WPT waves split the
-// K blocks. Lane L = 8p + s decodes slice s of rows 2p, 2p+1 of each block it visits from one
-// 16-byte, one 8-byte and three small loads (contiguous across the wave), turning each 4-value
-// group into an index of the 32 KB signed-grid table in LDS with a byte permute: one LDS read per
-// group yields four signed int8 values. The next block's weight and q8_1 loads are issued before
-// the current block is computed. The q8_1 block of X for the slice serves both rows. Partial sums
-// are added over the 8 slice lanes (xor butterfly), then over the waves in wave order.
-
-__device__ const Iq3sSignedTable kIq3sSignedDev = make_iq3s_signed_table();
-__device__ const Iq3sGrid kIq3sGridDev = kIq3sGrid;
-
-struct TileFrag {
-  uint4 qs;
-  uint2 e8;
-  uint16_t l2, sc;  // 16-bit loads kept 16-bit: widening them is left to their uses
-  uint32_t dd;
-};
-
-// per-lane byte offsets of a lane's data inside a tile-block (constant over the K loop)
-struct TileOffs {
-  uint32_t qs, e8, l2, sc, dd;
-};
-
-__device__ __forceinline__ TileOffs tile_offsets(int lane, int p, int s) {
-  return {(uint32_t)(16 * lane), (uint32_t)(8 * lane), (uint32_t)(2 * lane), (uint32_t)(2 * (4 * p + (s >> 1))),
-          (uint32_t)(4 * p)};
-}
-
-// tile-block at byte `boff` of the tile described by `rs`
-__device__ __forceinline__ void load_tile_frag(__amdgpu_buffer_rsrc_t rs, uint32_t boff, const TileOffs& o,
-                                               TileFrag& f) {
-  const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)o.qs, (int)boff, 0);
-  f.qs = make_uint4(q.x, q.y, q.z, q.w);
-  const auto e = __builtin_amdgcn_raw_buffer_load_b64(rs, (int)(o.e8 + kTe8), (int)boff, 0);
-  f.e8 = make_uint2(e[0], e[1]);
-  f.l2 = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)(o.l2 + kTl2), (int)boff, 0);
-  f.sc = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)(o.sc + kTsc), (int)boff, 0);
-  f.dd = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(o.dd + kTd), (int)boff, 0);
-}
-
-template <int NC>
-struct XFrag {
-  int q[NC][8];
-  uint32_t d[NC];  // fp16 bits (converted where used, so a prefetch does not wait for its load)
-};
-
-// q8_1 blocks of X at slice `slice0 + s` for every activation row c (row c starts nslices
-// blocks after row c-1): rs describes the whole q8_1 buffer, lane_off = 36 * s
-template <int NC>
-__device__ __forceinline__ void load_x_frag(__amdgpu_buffer_rsrc_t rs, uint32_t lane_off, int nslices, int slice0,
-                                            XFrag<NC>& x) {
-#pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    const int so = (c * nslices + slice0) * 36;
-    x.d[c] = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)lane_off, so, 0);
-    const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)lane_off, so + 4, 0);
-    const u32x4 e = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)lane_off, so + 20, 0);
-    x.q[c][0] = (int)a.x; x.q[c][1] = (int)a.y; x.q[c][2] = (int)a.z; x.q[c][3] = (int)a.w;
-    x.q[c][4] = (int)e.x; x.q[c][5] = (int)e.y; x.q[c][6] = (int)e.z; x.q[c][7] = (int)e.w;
-  }
-}
-
-// Fused quantisation of X (the decode ops' block_q8_1 arithmetic, done inside the GEMV): lane
-// L = 8p + s loads values 4p..4p+3 of slice s of a block of every activation row; the 8 lanes of a
-// slice exchange their partial amax and then their 4 q bytes through a 64-dword LDS area of the
-// wave, so each lane ends up with the slice's 32 q values as the q8_1 path would load them.
-template <int NC, int XDT>
-struct XRawFrag {
-  uint32_t v[NC][XDT == kF32 ? 4 : 2];
-};
-
-template <int NC, int XDT>
-__device__ __forceinline__ void load_xraw_frag(const void* x, int64_t s01, int block, int p, int s,
-                                               XRawFrag<NC, XDT>& r) {
-  const int64_t e0 = (int64_t)block * kQK + 32 * s + 4 * p;  // values 4p..4p+3 of slice s
-#pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    if constexpr (XDT == kF32) {
-      const uint4 v = *(const uint4*)((const float*)x + c * s01 + e0);
-      r.v[c][0] = v.x; r.v[c][1] = v.y; r.v[c][2] = v.z; r.v[c][3] = v.w;
-    } else {
-      const uint2 v = *(const uint2*)((const uint16_t*)x + c * s01 + e0);
-      r.v[c][0] = v.x; r.v[c][1] = v.y;
-    }
-  }
-}
-
-template <int XDT>
-__device__ __forceinline__ float xraw_value(const uint32_t* v, int i) {
-  if constexpr (XDT == kF32) return __uint_as_float(v[i]);
-  const uint32_t h = (v[i >> 1] >> (16 * (i & 1))) & 0xFFFF;
-  if constexpr (XDT == kF16) return half_bits_to_float(h);
-  return __uint_as_float(h << 16);
-}
-
-// ex: the wave's 64-dword exchange area; the lane holds values 4p..4p+3 of slice s (the slice's
-// 8 lanes are s, s+8, ..., s+56)
-template <int NC, int XDT>
-__device__ __forceinline__ void quantize_xraw(const XRawFrag<NC, XDT>& r, uint32_t* ex, int p, int s,
-                                              XFrag<NC>& x) {
-#pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    float v[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = xraw_value<XDT>(r.v[c], i);
-    ex[8 * s + p] = __float_as_uint(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
-    const uint4 a0 = *(const uint4*)(ex + 8 * s), a1 = *(const uint4*)(ex + 8 * s + 4);
-    const float amax = fmaxf(fmaxf(fmaxf(__uint_as_float(a0.x), __uint_as_float(a0.y)),
-                                   fmaxf(__uint_as_float(a0.z), __uint_as_float(a0.w))),
-                             fmaxf(fmaxf(__uint_as_float(a1.x), __uint_as_float(a1.y)),
-                                   fmaxf(__uint_as_float(a1.z), __uint_as_float(a1.w))));
-    const float d = amax / 127.0f;
-    uint32_t qw[1];
-    quantize_q81<4>(v, amax, d, qw);
-    ex[8 * s + p] = qw[0];  // after this wave's reads above: a wave's LDS operations complete in order
-    const uint4 q0 = *(const uint4*)(ex + 8 * s), q1 = *(const uint4*)(ex + 8 * s + 4);
-    x.q[c][0] = (int)q0.x; x.q[c][1] = (int)q0.y; x.q[c][2] = (int)q0.z; x.q[c][3] = (int)q0.w;
-    x.q[c][4] = (int)q1.x; x.q[c][5] = (int)q1.y; x.q[c][6] = (int)q1.z; x.q[c][7] = (int)q1.w;
-    x.d[c] = __half_as_ushort(__float2half_rn(d));
-  }
-}
-
-template <int NC>
-__device__ __forceinline__ void tile_compute(const uint8_t* tbl, const TileFrag& f, const XFrag<NC>& x, int s,
-                                             float (&acc)[2][NC]) {
-#pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    const uint32_t q0 = r == 0 ? f.qs.x : f.qs.z;
-    const uint32_t q1 = r == 0 ? f.qs.y : f.qs.w;
-    uint32_t lo, hi;
-    iq3_tile_ex(r == 0 ? f.e8.x : f.e8.y, f.l2, r, lo, hi);
-    int w[8];
-    tile_lookup2(tbl, __builtin_amdgcn_perm(lo, q0, 0x05010400u), w[0], w[1]);
-    tile_lookup2(tbl, __builtin_amdgcn_perm(lo, q0, 0x07030602u), w[2], w[3]);
-    tile_lookup2(tbl, __builtin_amdgcn_perm(hi, q1, 0x05010400u), w[4], w[5]);
-    tile_lookup2(tbl, __builtin_amdgcn_perm(hi, q1, 0x07030602u), w[6], w[7]);
-    const int ls = 1 + 2 * (((f.sc >> (8 * r)) >> (4 * (s & 1))) & 0xF);
-    const float dl = half_bits_to_float((f.dd >> (16 * r)) & 0xFFFF) * (float)ls;
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      int sumi = 0;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) sumi = dot4(w[e], x.q[c][e], sumi);
-      acc[r][c] = fmaf((float)sumi, dl * half_bits_to_float(x.d[c]), acc[r][c]);
-    }
-  }
-}
-
-// XDT < 0: X given as block_q8_1 (q8); else X itself (dtype XDT, row stride s01), quantised in the
-// kernel with the same arithmetic.
-template <int NC, int TPW, int WPT, int XDT>
-__global__ void __launch_bounds__(64 * TPW * WPT) gemv_iq3s_tile_kernel(const uint8_t* __restrict__ W,
-                                                                        int64_t row_bytes, int nrows, int k,
-                                                                        const void* __restrict__ xsrc,
-                                                                        int64_t s01, void* __restrict__ y,
-                                                                        int y_dtype) {
-  constexpr bool FUSED = XDT >= 0;
-  __shared__ uint4 table[2048];  // the 8192-entry signed-grid table
-  __shared__ float red[TPW][WPT][NC][kTileRows];
-  __shared__ uint32_t xex[FUSED ? TPW * WPT : 1][64];  // per-wave exchange of the fused quantisation
-  const uint8_t* q8 = (const uint8_t*)xsrc;
-  const int lane = threadIdx.x & 63;
-  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave index, scalar
-  const int wave = wv % WPT;   // K part of the tile
-  const int tw = wv / WPT;     // tile of the workgroup
-  const int tile = blockIdx.x * TPW + tw;
-  const int ntiles = nrows / kTileRows;
-  const int p = lane >> 3, s = lane & 7;
-  const int nb = k / kQK;
-  const int nslices = k / kQ81;
-  const bool active = tile < ntiles;
-  const int b_begin = active ? wave * nb / WPT : 0, b_end = active ? (wave + 1) * nb / WPT : 0;
-  const uint8_t* tb = W + (int64_t)(active ? tile : 0) * kTileRows * row_bytes;  // scalar
-  const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(tb, (uint32_t)(kTileRows * row_bytes));
-  const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(q8, FUSED ? 0u : (uint32_t)(NC * nslices * 36));
-  const uint8_t* tbl = (const uint8_t*)table;
-  const TileOffs off = tile_offsets(lane, p, s);
-  const uint32_t xoff = 36u * (uint32_t)s;
-
-  float acc[2][NC];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int c = 0; c < NC; ++c) acc[i][c] = 0.0f;
-
-  // Two named register sets (A, B) for the weight tile-block and the q8_1 blocks of X; the next
-  // block's loads are issued before the current block is computed. Two blocks per iteration and
-  // an odd last block after the loop, so that no load is behind a branch: a load under a branch
-  // makes the compiler wait for it before the next compute (vmcnt(0) on the joined paths), and
-  // one whose only use is conditional is sunk to that use. The weight prefetch past the wave's
-  // last block reads zeros through an empty descriptor and is never used; the X prefetch is
-  // clamped to the last block. The scheduling barriers keep the next block's decode below the
-  // loads just issued.
-  const __amdgpu_buffer_rsrc_t nrs = buffer_rsrc(W, 0);
-  const int b_last = b_end - 1;
-  const int nblk = b_end - b_begin;
-  TileFrag fa, fb;
-  if constexpr (!FUSED) {
-    XFrag<NC> xa, xb;
-    if (nblk > 0) {
-      load_x_frag<NC>(xrs, xoff, nslices, b_begin * 8, xa);
-      load_tile_frag(wrs, b_begin * kTileBlockBytes, off, fa);
-    }
-    iq3_table_to_lds<TPW * WPT>(table, &kIq3sSignedDev, wv, lane);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    int b = b_begin;
-    for (int it = 0; it < nblk / 2; ++it, b += 2) {
-      const int b2 = b + 2 < b_last ? b + 2 : b_last;
-      const __amdgpu_buffer_rsrc_t rs2 = b + 2 < b_end ? wrs : nrs;
-      load_x_frag<NC>(xrs, xoff, nslices, (b + 1) * 8, xb);
-      load_tile_frag(wrs, (b + 1) * kTileBlockBytes, off, fb);
-      __builtin_amdgcn_sched_barrier(0);
-      tile_compute<NC>(tbl, fa, xa, s, acc);
-      load_x_frag<NC>(xrs, xoff, nslices, b2 * 8, xa);
-      load_tile_frag(rs2, (b + 2) * kTileBlockBytes, off, fa);
-      __builtin_amdgcn_sched_barrier(0);
-      tile_compute<NC>(tbl, fb, xb, s, acc);
-    }
-    if (nblk & 1) tile_compute<NC>(tbl, fa, xa, s, acc);
-  } else {
-    // Raw X runs two blocks ahead and is quantised one block ahead, so the slice exchange of
-    // the next block overlaps the current block's decode.
-    constexpr int XD = FUSED ? XDT : kBF16;
-    uint32_t* ex = xex[wv];
-    XRawFrag<NC, XD> ra, rb;
-    XFrag<NC> qa, qb;
-    auto clampb = [&](int bb) { return bb < b_last ? bb : b_last; };
-    if (nblk > 0) {
-      load_xraw_frag<NC, XD>(xsrc, s01, b_begin, p, s, ra);
-      load_xraw_frag<NC, XD>(xsrc, s01, clampb(b_begin + 1), p, s, rb);
-      load_tile_frag(wrs, b_begin * kTileBlockBytes, off, fa);
-    }
-    iq3_table_to_lds<TPW * WPT>(table, &kIq3sSignedDev, wv, lane);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    quantize_xraw<NC, XD>(ra, ex, p, s, qa);
-    int b = b_begin;
-    for (int it = 0; it < nblk / 2; ++it, b += 2) {
-      const __amdgpu_buffer_rsrc_t rs2 = b + 2 < b_end ? wrs : nrs;
-      load_xraw_frag<NC, XD>(xsrc, s01, clampb(b + 2), p, s, ra);
-      load_tile_frag(wrs, (b + 1) * kTileBlockBytes, off, fb);
-      __builtin_amdgcn_sched_barrier(0);
-      quantize_xraw<NC, XD>(rb, ex, p, s, qb);
-      tile_compute<NC>(tbl, fa, qa, s, acc);
-      load_xraw_frag<NC, XD>(xsrc, s01, clampb(b + 3), p, s, rb);
-      load_tile_frag(rs2, (b + 2) * kTileBlockBytes, off, fa);
-      __builtin_amdgcn_sched_barrier(0);
-      quantize_xraw<NC, XD>(ra, ex, p, s, qa);
-      tile_compute<NC>(tbl, fb, qb, s, acc);
-    }
-    if (nblk & 1) tile_compute<NC>(tbl, fa, qa, s, acc);
-  }
-
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      float v = acc[i][c];
-      v += __shfl_xor(v, 1, 64);
-      v += __shfl_xor(v, 2, 64);
-      v += __shfl_xor(v, 4, 64);
-      if (s == 0) red[tw][wave][c][2 * p + i] = v;
-    }
-  }
-  __syncthreads();
-  if (threadIdx.x < TPW * NC * kTileRows) {
-    const int t = threadIdx.x / (NC * kTileRows);
-    const int c = (threadIdx.x / kTileRows) % NC, r = threadIdx.x % kTileRows;
-    const int otile = blockIdx.x * TPW + t;
-    if (otile < ntiles) {
-      float v = red[t][0][c][r];
-#pragma unroll
-      for (int w2 = 1; w2 < WPT; ++w2) v += red[t][w2][c][r];
-      store_y(y, (int64_t)c * nrows + (int64_t)otile * kTileRows + r, v, y_dtype);
-    }
-  }
-}
-
-// X of the persistent GEMV, staged in LDS: q8 values [NC][slice][8 dwords], then each slice's fp16 d
-// [NC][slice] (one dword, low half). Work unit: group g = 8 values, part g & 3 of slice row
-// g >> 2 (= c * nslices + slice of activation row c). The four lanes of a slice are consecutive.
-// group g of X into the LDS staging area (every lane of a slice takes part in the amax exchange);
-// a group past the end (live false) is written to `sink`: a load whose only use is a conditional
-// store is moved under the condition by the compiler and then waited for (vmcnt(0)) at the join
-template <int XDT>
-__device__ __forceinline__ void xgroup_store(const XGroup<XDT>& r, int g, bool live, uint32_t* xq, uint32_t* xd,
-                                             uint4* sink) {
-  const int sr = g >> 2, part = g & 3;
-  uint32_t lo, hi, dbits;
-  if constexpr (XDT < 0) {
-    lo = r.v[1];
-    hi = r.v[2];
-    dbits = r.v[0] & 0xFFFFu;
-  } else {
-    xgroup_quantize<XDT>(r, lo, hi, dbits);
-  }
-  *(live ? (uint2*)(xq + sr * 8 + 2 * part) : (uint2*)sink) = make_uint2(lo, hi);
-  *(live && part == 0 ? xd + sr : (uint32_t*)sink) = dbits;
-}
-
-// Persistent variant for weights with more tiles than the grid (two workgroups per CU): workgroup
-// g loops over tiles g, g + G, ...; the signed-grid table is built in LDS from the 2 KB grid once
-// per workgroup. Each wave keeps two tile-blocks of its stream in flight while it computes a third,
-// and its prefetch runs on from its last block of one tile to its first block of the next. The
-// per-wave K ranges, partial sums and reduction order are those of gemv_iq3s_tile_kernel, so the
-// results are bit-identical. Every wave needs at least one K block (k / 256 >= WPT).
-// X is staged in LDS first (dynamic LDS: NC * k / 32 * 36 bytes). XDT < 0: X given as block_q8_1,
-// copied. XDT >= 0: X itself (dtype XDT, row stride s01), quantised with the q8_1 quantiser's
-// arithmetic (bit-identical bytes), so the separate quantise launch goes.
-// XPL > 0: each wave stages only the X its own K range reads (activation rows c, slices [8 b_begin,
-// 8 b_end): NC * 32 * nblk groups of 8 values), at most XPL groups per lane, all loaded before the
-// first weight block. XPL == 0: the workgroup stages all of X together, two groups per thread
-// before the weights and the rest after them. A wave's loads complete in issue order, so a load
-// issued after the weights waits for them: measured at 5120 x 17408, M = 1, 16.3 us with the
-// workgroup staging against 12.7 us with the per-wave one (17408 x 5120: 11.8 against 11.5).
-// The grid word, X and the first weight blocks are loaded in that order; the table and X are
-// written to LDS while the weights are in flight.
-template <int NC, int WPT, int XDT, int XPL>
-__global__ void __launch_bounds__(64 * WPT) gemv_iq3s_persist_kernel(const uint8_t* __restrict__ W, int64_t row_bytes,
-                                                                     int nrows, int k, const void* __restrict__ xsrc,
-                                                                     int64_t s01, void* __restrict__ y, int y_dtype) {
-  constexpr int NT = 64 * WPT;
-  __shared__ uint4 table[2048];
-  __shared__ float red[2][WPT][NC][kTileRows];  // by tile parity: one barrier per tile
-  __shared__ uint4 sink;                        // staging writes of groups past the end of X
-  extern __shared__ uint4 xdyn[];               // X: q values [NC][slice][8 dwords], then d [NC][slice]
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int ntiles = nrows / kTileRows;
-  const int p = lane >> 3, s = lane & 7;
-  const int nb = k / kQK, nslices = k / kQ81;
-  const int b_begin = wave * nb / WPT, b_end = (wave + 1) * nb / WPT;
-  const int nblk = b_end - b_begin;
-  const int G = gridDim.x;
-  const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(xsrc, XDT < 0 ? (uint32_t)(NC * nslices * 36) : 0u);
-  const __amdgpu_buffer_rsrc_t nrs = buffer_rsrc(W, 0);
-  const uint8_t* tbl = (const uint8_t*)table;
-  const TileOffs off = tile_offsets(lane, p, s);
-  uint32_t* xq = (uint32_t*)xdyn;
-  uint32_t* xd = xq + NC * nslices * 8;
-  // tile t's rows, or an empty descriptor past the last tile (prefetch beyond the stream)
-  auto tile_rs = [&](int t) {
-    return t < ntiles ? buffer_rsrc(W + (int64_t)t * kTileRows * row_bytes, (uint32_t)(kTileRows * row_bytes)) : nrs;
-  };
-  // the wave's stream: (tile t, block b) for t = blockIdx.x, blockIdx.x + G, ..., b in [b_begin, b_end)
-  const int items = ((int)blockIdx.x < ntiles ? (ntiles - 1 - (int)blockIdx.x) / G + 1 : 0) * nblk;
-  auto next = [&](int& tt, int& bb) {
-    if (++bb == b_end) {
-      bb = b_begin;
-      tt += G;
-    }
-  };
-  static_assert(NT >= 512, "the table build takes 512 threads");
-  const int ngroups = NC * nslices * 4;
-  // X groups of this thread: XPL > 0, the wave's own (index li = lane + 64 j of the wave's
-  // NC * 32 * nblk, activation-row major); XPL == 0, groups threadIdx.x and threadIdx.x + NT
-  constexpr int XN = XPL > 0 ? XPL : 2;
-  int xg[XN];
-  bool xlive[XN];
-  const int wcnt = NC * 32 * nblk;
-#pragma unroll
-  for (int j = 0; j < XN; ++j) {
-    if constexpr (XPL > 0) {
-      const int li0 = lane + 64 * j;
-      xlive[j] = li0 < wcnt;
-      const int li = xlive[j] ? li0 : wcnt - 1;
-      const int c = li / (32 * nblk), rem = li - c * 32 * nblk;
-      xg[j] = (c * nslices + 8 * b_begin + (rem >> 2)) * 4 + (rem & 3);
-    } else {
-      const int g = threadIdx.x + j * NT;
-      xlive[j] = g < ngroups;
-      xg[j] = xlive[j] ? g : ngroups - 1;
-    }
-  }
-  const uint32_t gword = __builtin_amdgcn_raw_buffer_load_b32(buffer_rsrc(&kIq3sGridDev, 2048), 4 * (threadIdx.x & 511), 0, 0);
-  __builtin_amdgcn_sched_barrier(0);
-  XGroup<XDT> xa[XN];
-#pragma unroll
-  for (int j = 0; j < XN; ++j) xgroup_load<NC, XDT>(xsrc, xrs, s01, nslices, xg[j], xa[j]);
-  __builtin_amdgcn_sched_barrier(0);
-  TileFrag f0, f1, f2;
-  int lt = blockIdx.x, lb = b_begin;  // next item to load
-  load_tile_frag(tile_rs(lt), lb * kTileBlockBytes, off, f0);
-  next(lt, lb);
-  load_tile_frag(tile_rs(lt), lb * kTileBlockBytes, off, f1);
-  next(lt, lb);
-  __builtin_amdgcn_sched_barrier(0);
-  if (threadIdx.x < 512) iq3_table_from_grid(table, gword, threadIdx.x);
-#pragma unroll
-  for (int j = 0; j < XN; ++j) xgroup_store<XDT>(xa[j], xg[j], xlive[j], xq, xd, &sink);
-  if constexpr (XPL == 0) {
-    for (int g = threadIdx.x + 2 * NT; g < ngroups; g += NT) {  // K beyond 2 groups per thread
-      XGroup<XDT> xc;
-      xgroup_load<NC, XDT>(xsrc, xrs, s01, nslices, g, xc);
-      xgroup_store<XDT>(xc, g, true, xq, xd, &sink);
-    }
-  }
-  __syncthreads();
-  float acc[2][NC];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int c = 0; c < NC; ++c) acc[i][c] = 0.0f;
-  int t = blockIdx.x, b = b_begin, it = 0;  // item being computed
-  // compute fc (item i) while item i + 2 loads into fl
-  auto step = [&](const TileFrag& fc, TileFrag& fl) {
-    load_tile_frag(tile_rs(lt), lb * kTileBlockBytes, off, fl);
-    next(lt, lb);
-    __builtin_amdgcn_sched_barrier(0);
-    XFrag<NC> x;
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const int sl = c * nslices + b * 8 + s;
-      const uint4 a0 = *(const uint4*)(xq + sl * 8), a1 = *(const uint4*)(xq + sl * 8 + 4);
-      x.q[c][0] = (int)a0.x; x.q[c][1] = (int)a0.y; x.q[c][2] = (int)a0.z; x.q[c][3] = (int)a0.w;
-      x.q[c][4] = (int)a1.x; x.q[c][5] = (int)a1.y; x.q[c][6] = (int)a1.z; x.q[c][7] = (int)a1.w;
-      x.d[c] = xd[sl];
-    }
-    tile_compute<NC>(tbl, fc, x, s, acc);
-    if (b == b_end - 1) {  // the wave's last block of tile t: reduce and store the tile
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          float v = acc[i][c];
-          v += __shfl_xor(v, 1, 64);
-          v += __shfl_xor(v, 2, 64);
-          v += __shfl_xor(v, 4, 64);
-          if (s == 0) red[it & 1][wave][c][2 * p + i] = v;
-          acc[i][c] = 0.0f;
-        }
-      }
-      __syncthreads();
-      if (threadIdx.x < NC * kTileRows) {
-        const int c = threadIdx.x / kTileRows, r = threadIdx.x % kTileRows;
-        float v = red[it & 1][0][c][r];
-#pragma unroll
-        for (int w2 = 1; w2 < WPT; ++w2) v += red[it & 1][w2][c][r];
-        store_y(y, (int64_t)c * nrows + (int64_t)t * kTileRows + r, v, y_dtype);
-      }
-      ++it;
-    }
-    next(t, b);
-  };
-  int i = 0;
-  for (; i + 3 <= items; i += 3) {
-    step(f0, f2);
-    step(f1, f0);
-    step(f2, f1);
-  }
-  if (i < items) step(f0, f2);
-  if (i + 1 < items) step(f1, f0);
-}
-
-// workgroups of the persistent GEMV: two per CU of the current device
-static int persist_grid() {
-  static int cus[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 512;
-  if (cus[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cus[dev] = n;
-  }
-  return 2 * cus[dev];
-}
-
-template <int TPW, int WPT, int XDT>
-static void launch_gemv_packed_w(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x, int64_t s01,
-                                 int n, void* y, int y_dtype, hipStream_t stream) {
-  const int tiles = nrows / kTileRows;
-  const unsigned blocks = (unsigned)((tiles + TPW - 1) / TPW);
-#define GGUF_GT(NC)                                                                                             \
-  gemv_iq3s_tile_kernel<NC, TPW, WPT, XDT><<<blocks, 64 * TPW * WPT, 0, stream>>>(W, row_bytes, nrows, k, x, s01, y, \
-                                                                                  y_dtype)
-  if constexpr (XDT >= 0) {  // the fused path serves one row
-    GGUF_GT(1);
-  } else {
-    switch (n) {
-      case 1: GGUF_GT(1); break;
-      case 2: GGUF_GT(2); break;
-      case 3: GGUF_GT(3); break;
-      case 4: GGUF_GT(4); break;
-      case 5: GGUF_GT(5); break;
-      case 6: GGUF_GT(6); break;
-      case 7: GGUF_GT(7); break;
-      default: GGUF_GT(8); break;
-    }
-  }
-#undef GGUF_GT
-}
-
-// One tile per workgroup. Eight waves split K for one or two columns (measured best at
-// 17408 x 5120: 12.3 us at M=1); from three columns on, the register file allows four.
-// The persistent kernel: g workgroups (two per CU, at most one per tile), n <= 4 rows (raw X:
-// n <= 2). X groups per lane of the per-wave staging: NC * 32 * ceil(nb / 8) / 64 rounded up, up to
-// six; beyond that the workgroup staging.
-template <int NC, int XDT>
-static void launch_persist_nc(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x, int64_t s01,
-                              void* y, int y_dtype, unsigned g, size_t lds, hipStream_t stream) {
-  const int nblk_max = (k / kQK + 7) / 8;
-  const int xpl = (NC * 32 * nblk_max + 63) / 64;
-#define GGUF_PERSIST(XPL) \
-  gemv_iq3s_persist_kernel<NC, 8, XDT, XPL><<<g, 512, lds, stream>>>(W, row_bytes, nrows, k, x, s01, y, y_dtype)
-  switch (xpl) {
-    case 1: GGUF_PERSIST(1); break;
-    case 2: GGUF_PERSIST(2); break;
-    case 3: GGUF_PERSIST(3); break;
-    case 4: GGUF_PERSIST(4); break;
-    case 5: GGUF_PERSIST(5); break;
-    case 6: GGUF_PERSIST(6); break;
-    default: GGUF_PERSIST(0); break;
-  }
-#undef GGUF_PERSIST
-}
-
-template <int XDT>
-static void launch_gemv_persist(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x, int64_t s01, int n,
-                                void* y, int y_dtype, hipStream_t stream) {
-  const unsigned g = (unsigned)std::min(nrows / kTileRows, persist_grid());
-  const size_t lds = (size_t)n * (k / kQ81) * 36;  // X staged in LDS
-  if (n == 1) launch_persist_nc<1, XDT>(W, row_bytes, nrows, k, x, s01, y, y_dtype, g, lds, stream);
-  else if (n == 2) launch_persist_nc<2, XDT>(W, row_bytes, nrows, k, x, s01, y, y_dtype, g, lds, stream);
-  else if constexpr (XDT < 0) {  // three or four rows: q8_1 input only
-    if (n == 3) launch_persist_nc<3, XDT>(W, row_bytes, nrows, k, x, s01, y, y_dtype, g, lds, stream);
-    else launch_persist_nc<4, XDT>(W, row_bytes, nrows, k, x, s01, y, y_dtype, g, lds, stream);
-  }
-}
-
-template <int XDT>
-static void launch_gemv_packed_dt(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x, int64_t s01,
-                                  int n, void* y, int y_dtype, hipStream_t stream) {
-  if constexpr (XDT < 0) {  // q8 input: the persistent kernel from one tile per CU on, 1-4 rows
-    // (quantise + GEMV per op, graph-timed, against quantise + the one-tile kernel with 8 / 4
-    // waves: 17408 x 5120 M = 1-4 13.7 / 15.1 / 17.3 / 19.3 us against 15.1 / 17.2 / 19.9 / 22.3;
-    // 5120 x 17408 M = 1-2 15.9 / 17.9 against 16.2 / 20.0; 6144 x 5120 M = 1-4 8.9 / 9.5 / 10.9 /
-    // 11.9 against 9.0 / 10.3 / 11.3 / 12.4; 5120 x 6144 M = 2-4 10.0 / 11.4 / 12.4 against
-    // 10.6 / 12.2 / 13.8; with 64 tiles (1024 x 5120) the one-tile kernel stays faster at 3-4 rows)
-    const bool fits = k / kQK >= 8 && n * (k / kQ81) * 36 <= 48 * 1024;
-    if (fits && n <= 4 && 2 * (nrows / kTileRows) >= persist_grid()) {
-      launch_gemv_persist<XDT>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream);
-      return;
-    }
-  }
-  if (n <= 2) launch_gemv_packed_w<1, 8, XDT>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream);
-  else launch_gemv_packed_w<1, 4, XDT>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream);
-}
-
-// nrows % 16 == 0, n in 1..8; q8: block_q8_1 of X.
-hipError_t launch_gemv_packed(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n,
-                              void* y, int y_dtype, hipStream_t stream) {
-  launch_gemv_packed_dt<-1>(W, row_bytes, nrows, k, q8, 0, n, y, y_dtype, stream);
-  return hipGetLastError();
-}
-
-// nrows % 16 == 0; X [n, k] of dtype x_dtype, quantised in the kernel (bit-identical to the q8_1
-// quantiser followed by the GEMV). The persistent kernel, which quantises all of X into LDS first,
-// needs k / 256 >= 8 and X's q8_1 within 48 KB of LDS; it takes one row from 3/4 of its grid's
-// tiles on (graph-timed per op: 6144 x 5120 7.7 us against 8.0 for the one-tile kernel; 8192 x
-// 5120 8.1 against 9.1 for quantise + the persistent GEMV) and two rows on weights with more
-// tiles than its grid (at two rows quantise + GEMV is faster below that: 6144 x 5120 9.5 against
-// 9.8 us). Otherwise one row on weights of up to 32M values: the one-tile kernel, which quantises
-// each block as it goes (measured faster than the two launches for the attention shapes).
-static bool packed_x_persist(int64_t nrows, int64_t k, int64_t n) {
-  const bool fits = k / kQK >= 8 && n * (k / kQ81) * 36 <= 48 * 1024;
-  const int64_t tiles = nrows / kTileRows;
-  return fits && ((n == 1 && 4 * tiles >= 3 * persist_grid()) || (n == 2 && tiles > persist_grid()));
-}
-
-bool gemv_packed_x_supported(int64_t nrows, int64_t k, int64_t n) {
-  return packed_x_persist(nrows, k, n) || (n == 1 && nrows * k <= ((int64_t)32 << 20));
-}
-
-hipError_t launch_gemv_packed_x(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x, int x_dtype,
-                                int64_t s01, int n, void* y, int y_dtype, hipStream_t stream) {
-  if (!gemv_packed_x_supported(nrows, k, n)) return hipErrorInvalidValue;
-  const bool small = !packed_x_persist(nrows, k, n);
-  switch (x_dtype) {
-    case kF32:
-      if (small) launch_gemv_packed_dt<kF32>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream);
-      else launch_gemv_persist<kF32>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream);
-      break;
-    case kF16:
-      if (small) launch_gemv_packed_dt<kF16>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream);
-      else launch_gemv_persist<kF16>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream);
-      break;
-    default:
-      if (small) launch_gemv_packed_dt<kBF16>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream);
-      else launch_gemv_persist<kBF16>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream);
-      break;
-  }
-  return hipGetLastError();
-}
 
 }  // namespace gguf

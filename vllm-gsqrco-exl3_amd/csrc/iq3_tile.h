@@ -1,29 +1,74 @@
-// The build's IQ3_S tile layout (its own; the reference's iq3_pack.py layout serves its CUDA mma
+// The build's IQ3_S unit layout (its own; the reference's iq3_pack.py layout serves its CUDA mma
 // fragments and is not reproduced), and the signed-grid table the decode kernels read.
 //
-// Rows are grouped in tiles of 16. Tile t's bytes stay where rows 16t..16t+15 were; block b of
-// the tile becomes one 1760-byte "tile-block" at byte 1760*b of the tile. Lane L = 8p + s of a
-// decode wave (p = row pair 0..7, s = 32-value slice 0..7) owns rows 2p, 2p+1 (r = 0, 1) of
-// slice s. For group e (values 4e..4e+3 of the slice, e = 0..7) of row r define the 5-bit
+// Rows are grouped in units of 4. Unit u's bytes stay where rows 4u..4u+3 were; its K blocks are
+// taken four at a time: blocks 4kb..4kb+3 of the unit become one 1760-byte unit-block at byte
+// 1760*kb of the unit (when nb % 4 = r != 0 the last unit-block holds the r remaining blocks in
+// 440*r bytes, with every field below scaled by r/4). A decode lane L = 8p + s (p = 2*bi + rp,
+// s = 32-value slice 0..7) owns rows 2rp, 2rp+1 (r = 0, 1) of the unit in slice s of block
+// 4kb + bi. For group e (values 4e..4e+3 of the slice, e = 0..7) of row r define the 5-bit
 //   ex(r, e) = sign nibble e of the slice's 4 sign bytes | (bit e of qh[s]) << 4
-// so that (qs byte | ex << 8) is a 13-bit index into the signed-grid table (below). The
-// tile-block holds, for every lane L:
-//   [   0, 1024)  QS  16 B at 16L : qs[8s..8s+8) of row 2p, then of row 2p+1
+// so that (qs byte | ex << 8) is a 13-bit index into the signed-grid table (below). A full
+// unit-block holds, for every lane L:
+//   [   0, 1024)  QS  16 B at 16L : qs[8s..8s+8) of row 2rp, then of row 2rp+1
 //   [1024, 1536)  E8   8 B at 8L  : byte 4r+j (j = 0..3) = ex(r, j) | (ex(r, 4+j) & 7) << 5
 //   [1536, 1664)  L2   2 B at 2L  : bits 8r+2j, 8r+2j+1 = ex(r, 4+j) >> 3
-//   [1664, 1728)  SC   2 B at 2(4p + j) : scales[j] of row 2p, then of row 2p+1 (j = 0..3)
-//   [1728, 1760)  D    4 B at 4p  : d of row 2p, then of row 2p+1
-// (block_iq3_s byte offsets: d 0, qs 2, qh 66, signs 74, scales 106.) Same size, bijective, and
-// every load of the decode GEMV is contiguous across the wave (16 / 8 / 2 B per lane).
+//   [1664, 1728)  SC   2 B at 2(4p + j) : scales[j] of row 2rp, then of row 2rp+1 (j = 0..3)
+//   [1728, 1760)  D    4 B at 4p  : d of row 2rp, then of row 2rp+1
+// (block_iq3_s byte offsets: d 0, qs 2, qh 66, signs 74, scales 106.) Same size, bijective,
+// local to each unit, and every load of a decode wave is contiguous across the wave (16 / 8 / 2 B
+// per lane). Fields are ordered by bi, so the data of one K block b = 4kb + bi is, inside its
+// unit-block, QS at 256 bi, E8 at 1024 + 128 bi, L2 at 1536 + 32 bi, SC at 1664 + 16 bi and D at
+// 1728 + 8 bi. The MFMA kernels work on 16-row tiles = 4 consecutive units and read one K block
+// of each unit per step; the decode GEMV reads whole unit-blocks. 4-row units split the
+// 27B-class shapes evenly over 256 CUs (17408 rows = 17 units per CU, 5120 rows = 5).
 #pragma once
 
 #include "gguf_common.h"
 
 namespace gguf {
 
-constexpr int kTileRows = 16;
-constexpr int kTileBlockBytes = kTileRows * 110;  // 1760
-constexpr int kTqs = 0, kTe8 = 1024, kTl2 = 1536, kTsc = 1664, kTd = 1728;
+constexpr int kTileRows = 16;            // row tile of the MFMA kernels: 4 units
+constexpr int kUnitRows = 4;
+constexpr int kUnitBlockBytes = 4 * 4 * 110;  // 1760
+constexpr int kTe8 = 1024, kTl2 = 1536, kTsc = 1664, kTd = 1728;  // field bases of a full unit-block
+
+// field bases inside a unit-block of r blocks (r = 4 except a ragged last one)
+__host__ __device__ constexpr uint32_t iq3_e8_base(int r) { return 256u * r; }
+__host__ __device__ constexpr uint32_t iq3_l2_base(int r) { return 384u * r; }
+__host__ __device__ constexpr uint32_t iq3_sc_base(int r) { return 416u * r; }
+__host__ __device__ constexpr uint32_t iq3_d_base(int r) { return 432u * r; }
+
+// blocks held by unit-block kb of a unit of nb blocks
+__host__ __device__ constexpr int iq3_unit_blocks(int nb, int kb) { return kb < (nb >> 2) ? 4 : (nb & 3); }
+
+// Byte offsets, from the unit's first byte, of the five fields of K block b (for every lane: add
+// the lane's part, iq3_lane_fields)
+struct Iq3Fields {
+  uint32_t qs, e8, l2, sc, d;
+};
+
+__host__ __device__ inline Iq3Fields iq3_block_fields(int nb, int b) {
+  const int kb = b >> 2, bi = b & 3, r = iq3_unit_blocks(nb, kb);
+  const uint32_t u = (uint32_t)kUnitBlockBytes * kb;
+  return {u + 256u * bi, u + iq3_e8_base(r) + 128u * bi, u + iq3_l2_base(r) + 32u * bi, u + iq3_sc_base(r) + 16u * bi,
+          u + iq3_d_base(r) + 8u * bi};
+}
+
+// The whole unit-block kb (the decode GEMV's work item): field bases, lanes add 16L / 8L / 2L /
+// 2(4p + j) / 4p
+__host__ __device__ inline Iq3Fields iq3_unitblock_fields(int nb, int kb) {
+  const int r = iq3_unit_blocks(nb, kb);
+  const uint32_t u = (uint32_t)kUnitBlockBytes * kb;
+  return {u, u + iq3_e8_base(r), u + iq3_l2_base(r), u + iq3_sc_base(r), u + iq3_d_base(r)};
+}
+
+// A lane's part of one K block's fields: rows 2rp, 2rp+1 of the unit, slice s (the SC byte of
+// scales[j] of row r at sc + 2j + r, the d of row r at d + 2r)
+__host__ __device__ inline Iq3Fields iq3_lane_fields(int rp, int s) {
+  return {(uint32_t)(128 * rp + 16 * s), (uint32_t)(64 * rp + 8 * s), (uint32_t)(16 * rp + 2 * s), (uint32_t)(8 * rp),
+          (uint32_t)(4 * rp)};
+}
 
 // Signed-grid table: entry (qs | ex << 8) = the grid word of index qs | (ex >> 4) << 8 with the
 // bytes whose bit is set in ex & 0xF negated; 8192 x int8x4 = 32 KB, staged in LDS by the
@@ -49,18 +94,16 @@ constexpr Iq3sSignedTable make_iq3s_signed_table() {
 }
 
 // ---------------------------------------------------------------------------------------------
-// Pack / unpack of one lane's share of a tile-block (host and device).
+// Pack / unpack of one lane's share of a K block (host and device).
 
 // ex of group e (0..7) of a slice, from its 4 sign bytes (as a dword) and its qh byte
 __host__ __device__ inline uint32_t iq3_ex(uint32_t signs, uint32_t qh, int e) {
   return ((signs >> (4 * e)) & 0xF) | (((qh >> e) & 1u) << 4);
 }
 
-// GGUF block pointers of rows 2p, 2p+1 -> lane L's QS / E8 / L2 bytes written at tb
-__host__ __device__ inline void iq3_tile_pack_lane(const uint8_t* const rowblk[2], int L, uint8_t* tb) {
-  const int s = L & 7;
-  uint8_t* qs = tb + kTqs + 16 * L;
-  uint8_t* e8 = tb + kTe8 + 8 * L;
+// GGUF block pointers of rows 2rp, 2rp+1 (slice s) -> the lane's QS / E8 / L2 bytes at qs / e8 / l2
+__host__ __device__ inline void iq3_tile_pack_lane(const uint8_t* const rowblk[2], int s, uint8_t* qs, uint8_t* e8,
+                                                   uint8_t* l2p) {
   uint32_t l2 = 0;
   for (int r = 0; r < 2; ++r) {
     const uint8_t* b = rowblk[r];
@@ -74,16 +117,14 @@ __host__ __device__ inline void iq3_tile_pack_lane(const uint8_t* const rowblk[2
       l2 |= (hi >> 3) << (8 * r + 2 * j);
     }
   }
-  tb[kTl2 + 2 * L] = (uint8_t)(l2 & 0xFF);
-  tb[kTl2 + 2 * L + 1] = (uint8_t)(l2 >> 8);
+  l2p[0] = (uint8_t)(l2 & 0xFF);
+  l2p[1] = (uint8_t)(l2 >> 8);
 }
 
-// lane L's QS / E8 / L2 bytes at tb -> qs, qh and sign bytes of rows 2p, 2p+1 (GGUF blocks)
-__host__ __device__ inline void iq3_tile_unpack_lane(const uint8_t* tb, int L, uint8_t* const rowblk[2]) {
-  const int s = L & 7;
-  const uint8_t* qs = tb + kTqs + 16 * L;
-  const uint8_t* e8 = tb + kTe8 + 8 * L;
-  const uint32_t l2 = (uint32_t)tb[kTl2 + 2 * L] | ((uint32_t)tb[kTl2 + 2 * L + 1] << 8);
+// the lane's QS / E8 / L2 bytes -> qs, qh and sign bytes of rows 2rp, 2rp+1 (GGUF blocks, slice s)
+__host__ __device__ inline void iq3_tile_unpack_lane(const uint8_t* qs, const uint8_t* e8, const uint8_t* l2p, int s,
+                                                     uint8_t* const rowblk[2]) {
+  const uint32_t l2 = (uint32_t)l2p[0] | ((uint32_t)l2p[1] << 8);
   for (int r = 0; r < 2; ++r) {
     uint8_t* b = rowblk[r];
     for (int i = 0; i < 8; ++i) b[2 + 8 * s + i] = qs[8 * r + i];
@@ -100,16 +141,19 @@ __host__ __device__ inline void iq3_tile_unpack_lane(const uint8_t* tb, int L, u
   }
 }
 
-// SC and D bytes: tile-block byte j in [kTsc, 1760) <-> (row in tile, byte in the row's block)
-__host__ __device__ inline void iq3_tile_scale_source(int j, int& r, int& o) {
-  if (j < kTd) {
-    const int jj = j - kTsc, m = jj >> 1;
-    r = 2 * (m >> 2) + (jj & 1);
-    o = 106 + (m & 3);
+// SC and D bytes of a unit-block of r blocks: byte j in [iq3_sc_base(r), 440 r) <-> (row in the
+// unit, block bi in the unit-block, byte in the row's block)
+__host__ __device__ inline void iq3_tile_scale_source(int j, int r, int& row, int& bi, int& o) {
+  if (j < (int)iq3_d_base(r)) {
+    const int jj = j - (int)iq3_sc_base(r), rem = jj & 15;  // 16 bi + 8 rp + 2 jsc + rr
+    bi = jj >> 4;
+    row = 2 * (rem >> 3) + (rem & 1);
+    o = 106 + ((rem >> 1) & 3);
   } else {
-    const int jj = j - kTd;
-    r = 2 * (jj >> 2) + ((jj >> 1) & 1);
-    o = jj & 1;
+    const int jj = j - (int)iq3_d_base(r), rem = jj & 7;    // 8 bi + 4 rp + 2 rr + byte
+    bi = jj >> 3;
+    row = 2 * (rem >> 2) + ((rem >> 1) & 1);
+    o = rem & 1;
   }
 }
 

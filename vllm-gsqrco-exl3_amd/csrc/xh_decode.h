@@ -74,14 +74,18 @@ struct RawQ4k {
   uint2 v0, v1; // quarter q of the two 32-byte quant groups of the half block
 };
 
-// IQ3_S lane (row j, slice 4h + sp) of a tile-block in the tile layout
-__device__ __forceinline__ void load_step(RawIq3& w, const uint8_t* tb, int h, int j, int sp) {
-  const int p = j >> 1, r = j & 1, s = 4 * h + sp, L = 8 * p + s;
-  w.qs = *(const uint2*)(tb + kTqs + 16 * L + 8 * r);
-  w.e8 = *(const uint32_t*)(tb + kTe8 + 8 * L + 4 * r);
-  w.l2 = *(const uint16_t*)(tb + kTl2 + 2 * L);
-  w.sc = tb[kTsc + 2 * (4 * p + (s >> 1)) + r];
-  w.d = *(const uint16_t*)(tb + kTd + 4 * p + 2 * r);
+// IQ3_S lane (row j, slice 4h + sp) of K block b of a 16-row tile in the unit layout (tile: the
+// tile's first byte; tile row j is in unit j >> 2, row pair (j >> 1) & 1)
+__device__ __forceinline__ void load_step(RawIq3& w, const uint8_t* tile, int64_t row_bytes, int nb, int b, int h,
+                                          int j, int sp) {
+  const int r = j & 1, s = 4 * h + sp;
+  const Iq3Fields f = iq3_block_fields(nb, b), l = iq3_lane_fields((j >> 1) & 1, s);
+  const uint8_t* u = tile + (int64_t)(j >> 2) * kUnitRows * row_bytes;
+  w.qs = *(const uint2*)(u + f.qs + l.qs + 8 * r);
+  w.e8 = *(const uint32_t*)(u + f.e8 + l.e8 + 4 * r);
+  w.l2 = *(const uint16_t*)(u + f.l2 + l.l2);
+  w.sc = u[f.sc + l.sc + 2 * (s >> 1) + r];
+  w.d = *(const uint16_t*)(u + f.d + l.d + 2 * r);
 }
 
 // Q4_K lane (row j, quarter q) of the row's block
