@@ -7,7 +7,7 @@
 Workload: IQ3_S decode GEMV at M = 1 and 4 on the two 27B-layer
 shapes, gate/up 17408 x 5120 and down 5120 x 17408, bf16 activations N(0,1) quantised to q8_1,
 weights in IQ3_S super-blocks with uniform random codes and d ~ |N(0, 2e-3)|, in the build's
-packed tile layout (the route the linear method takes for IQ3_S). A step is one op call
+packed unit layout (the route the linear method takes for IQ3_S). A step is one op call
 (quantise + GEMV, torch.ops._C_gguf.lcpp_mul_mat_vec_iq3_mma_packed) per (shape, M) on each of
 8 distinct weight copies per shape (>= 306 MB per shape, beyond the 256 MB Infinity Cache), all
 captured in CUDA graphs; K steps are timed with HIP events on torch's current stream between a
@@ -24,7 +24,7 @@ small GEMM (IQ3_S / IQ4_XS / Q6_K at M = 4..48 on the attention shapes), the pre
 shape, and the 64-layer decoder sweep under one CUDA graph with a replay bit-exactness check.
 
 `traffic` (HBM bytes per launch of the dominant kernel) is read from the committed PMC summary
-profiles/gemv_iq3s_persist_17408x5120_m1.traffic.json when present (null otherwise). That summary
+profiles/gemv_iq3s_stream_17408x5120_m1.traffic.json when present (null otherwise). That summary
 comes from `rocprofv3 --pmc FETCH_SIZE` and `--pmc WRITE_SIZE` runs of `bench.py --kernel-only`,
 which times only the dominant kernel and then runs a plain elementwise copy of 256 MiB (read
 256 MiB, write 256 MiB) whose counter readings calibrate the counters' byte scale.
@@ -45,7 +45,7 @@ NBUF = 8                       # the fewest distinct weight copies a timed graph
 ROTATE_BYTES = 512 << 20       # ... and at least this many weight bytes: twice the 256 MB MALL,
                                # so that no copy is still cached when its turn comes again
 COPY_BYTES = 256 << 20         # calibration copy: bytes read (and written) per launch
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_iq3s_persist_17408x5120_m1.traffic.json")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_iq3s_stream_17408x5120_m1.traffic.json")
 IQ3_S, Q4_K, Q6_K, IQ4_XS = 21, 12, 14, 23
 Q2_K, IQ2_XXS, IQ2_XS, IQ3_XXS, IQ2_S, IQ1_M = 10, 16, 17, 18, 22, 29
 TYPE_NAME = {IQ3_S: "IQ3_S", Q4_K: "Q4_K", Q6_K: "Q6_K", IQ4_XS: "IQ4_XS", Q2_K: "Q2_K", IQ2_XXS: "IQ2_XXS",
@@ -124,7 +124,7 @@ def x_outliers(torch, m, k, seed):
 def op_points(torch, C, iq3_pack, linear, qt, rows, k, ms, ncopies=None, reps=5, seed=0, outliers=False):
     """us/call of the routing table's op for a qt weight [rows, k] at each M in ms (bf16 X N(0,1),
     with outliers: x_outliers), over ncopies weight copies (default: rotation_copies) captured in
-    one graph per M. IQ3_S in the packed tile layout (IQ3_XXS packed too: the identity)."""
+    one graph per M. IQ3_S in the packed unit layout (IQ3_XXS packed too: the identity)."""
     if ncopies is None:
         ncopies = rotation_copies(rows * (k // 256) * BLOCK[qt])
     ws = [make_weights(torch, qt, rows, k, seed + i) for i in range(ncopies)]
@@ -368,8 +368,8 @@ def load_traffic():
 
 def dominant_kernel(torch, C, ws, steps):
     """The headline's dominant kernel alone: the packed decode op at 17408 x 5120, M = 1, bf16 X,
-    which is one launch of the persistent GEMV that quantises X itself
-    (gemv_iq3s_persist_kernel<1, 8, bf16>); one graph of one launch per weight copy, timed with
+    which is one launch of the stream GEMV that quantises X itself
+    (gemv_iq3s_stream_kernel<1, bf16, 2>); one graph of one launch per weight copy, timed with
     HIP events on the stream the op launches on."""
     rows, k, m = 17408, 5120, 1
     x = torch.randn(m, k, device="cuda", dtype=torch.bfloat16)
@@ -379,7 +379,7 @@ def dominant_kernel(torch, C, ws, steps):
     achieved = alg_bytes / (kernel_us * 1e-6) / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic(),
-            "kernel": "gemv_iq3s_persist_kernel<1,8,bf16> (17408x5120, M=1, X quantised in the kernel)",
+            "kernel": "gemv_iq3s_stream_kernel<1,bf16,2> (17408x5120, M=1, X quantised in the kernel)",
             "us_per_launch": round(kernel_us, 3), "alg_bytes_per_launch": alg_bytes}
 
 
@@ -511,7 +511,7 @@ def main():
         "vs_baseline": None,
         "dtype": "int8",
         "data": "synthetic (uniform random IQ3_S codes, d ~ |N(0,2e-3)|; X bf16 N(0,1))",
-        "config": {"workload": "IQ3_S decode GEMV (packed tile layout) at M=1,4 on 17408x5120 and 5120x17408, "
+        "config": {"workload": "IQ3_S decode GEMV (packed unit layout) at M=1,4 on 17408x5120 and 5120x17408, "
                                "benchmark configs[1]; per shape, weight copies of at least 512 MiB in all",
                    "calls_per_step": sum(n for *_, n, _ in per_case), "bytes_per_step": step_bytes},
         "detail": detail,

@@ -340,7 +340,8 @@ constexpr int kStreamWaves = 8;
 // mirror: the same sums, in the same order, as an xor-4 butterfly) and the lanes of slice 0 store
 // 16 partial row sums to LDS, slot (unit, wave). The output adds, per row, the slots of the waves
 // that touched the unit in wave order, the four bi partials in bi order within each. In a last
-// unit-block of r < 4 blocks the lanes of bi >= r add nothing (d and X's d taken as 0).
+// unit-block of r < 4 blocks the lanes of bi >= r add nothing (d and X's d taken as 0). The slots
+// start at zero, so every wave's slot of a unit is added (zeros where the wave did not touch it).
 // X: XDT < 0 the caller's block_q8_1 copied into LDS, XDT >= 0 X itself (row stride s01)
 // quantised into LDS with the q8_1 arithmetic. Each thread stages XPT groups of 8 values, their
 // loads issued first, then the grid word, then the wave's first two unit-blocks.
@@ -358,17 +359,11 @@ __global__ void __launch_bounds__(64 * kStreamWaves) gemv_iq3s_stream_kernel(con
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int p = lane >> 3, s = lane & 7, bi = p >> 1;
   const int nb = k / kQK, nkb = (nb + 3) >> 2, nslices = k / kQ81;
-  const int nunits = nrows / kUnitRows, G = gridDim.x;
-  const int u0 = (int)((int64_t)blockIdx.x * nunits / G), u1 = (int)((int64_t)(blockIdx.x + 1) * nunits / G);
-  const int nu = u1 - u0, items = nu * nkb;
-  const uint32_t ubytes = (uint32_t)(kUnitRows * row_bytes), rbytes = (uint32_t)nu * ubytes;
+  const int nslots_x = NC * nslices * 8;
   uint32_t* xq = (uint32_t*)xdyn;
-  uint32_t* xd = xq + NC * nslices * 8;
+  uint32_t* xd = xq + nslots_x;
   float* part = (float*)(xd + NC * nslices);  // [unit][wave][NC][16]
-  const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(W + (int64_t)u0 * ubytes, rbytes);
   const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(xsrc, XDT < 0 ? (uint32_t)(NC * nslices * 36) : 0u);
-  const TileOffs off = unit_lane_offsets(lane, p, s);
-  const uint8_t* tbl = (const uint8_t*)table;
   const int ngroups = NC * nslices * 4;
   int xg[XPT];
   bool xlive[XPT];
@@ -378,14 +373,25 @@ __global__ void __launch_bounds__(64 * kStreamWaves) gemv_iq3s_stream_kernel(con
     xlive[j] = g < ngroups;
     xg[j] = xlive[j] ? g : ngroups - 1;
   }
+  // X and the grid word first; every wave's staging loads are issued before any weight load
+  // (barrier below), since a CU's loads return in order
   XGroup<XDT> xa[XPT];
 #pragma unroll
   for (int j = 0; j < XPT; ++j) xgroup_load<NC, XDT>(xsrc, xrs, s01, nslices, xg[j], xa[j]);
   const uint32_t gword = __builtin_amdgcn_raw_buffer_load_b32(buffer_rsrc(&kIq3sGridDev, 2048), 4 * threadIdx.x, 0, 0);
   __builtin_amdgcn_sched_barrier(0);
-  // the wave's run of items [j0, j1), and the next item to load (lu, lkb)
+  // the workgroup's units [u0, u1) and the wave's run of items [j0, j1) (32-bit: units * grid
+  // < 2^31 for any weight of fewer than 2^23 rows)
+  const uint32_t nunits = (uint32_t)nrows / kUnitRows, G = gridDim.x;
+  const int u0 = (int)(blockIdx.x * nunits / G), u1 = (int)((blockIdx.x + 1) * nunits / G);
+  const int nu = u1 - u0, items = nu * nkb;
+  const uint32_t ubytes = (uint32_t)(kUnitRows * row_bytes), rbytes = (uint32_t)nu * ubytes;
+  const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(W + (int64_t)u0 * ubytes, rbytes);
+  const TileOffs off = unit_lane_offsets(lane, p, s);
+  const uint8_t* tbl = (const uint8_t*)table;
   const int j0 = wave * items / NW, j1 = (wave + 1) * items / NW;
-  int lj = j0, lu = j0 / nkb, lkb = j0 - lu * nkb;
+  const int cu0 = (int)((uint32_t)j0 / (uint32_t)nkb);
+  int lj = j0, lu = cu0, lkb = j0 - cu0 * nkb;  // the next item to load
   auto fields = [&](int u, int kb) {
     Iq3Fields f = iq3_unitblock_fields(nb, kb);
     const uint32_t ub = (uint32_t)u * ubytes;
@@ -402,15 +408,21 @@ __global__ void __launch_bounds__(64 * kStreamWaves) gemv_iq3s_stream_kernel(con
       ++lu;
     }
   };
+  __syncthreads();
   TileFrag f0, f1, f2;
   load_next(f0);
   load_next(f1);
   __builtin_amdgcn_sched_barrier(0);
   iq3_table_from_grid(table, gword, threadIdx.x);
 #pragma unroll
-  for (int j = 0; j < XPT; ++j) xgroup_store<XDT>(xa[j], xg[j], xlive[j], xq, xd, &sink);
+  for (int j = 0; j < XPT; ++j) {
+    if (wave * 64 + j * NT < ngroups)  // waves with no group left skip the (fused) quantisation
+      xgroup_store<XDT>(xa[j], xg[j], xlive[j], xq, xd, &sink);
+  }
+  // the partial-sum slots start at zero: the output adds every wave's slot of a unit
+  for (int t = threadIdx.x; t < nu * NW * NC * 4; t += NT) ((float4*)part)[t] = make_float4(0.f, 0.f, 0.f, 0.f);
   __syncthreads();
-  int cu = j0 / nkb, ckb = j0 - (j0 / nkb) * nkb, j = j0;  // the item being computed
+  int cu = cu0, ckb = j0 - cu0 * nkb, j = j0;  // the item being computed
   const int xl = 8 * bi + s;
   float acc[2][NC];
 #pragma unroll
@@ -467,19 +479,22 @@ __global__ void __launch_bounds__(64 * kStreamWaves) gemv_iq3s_stream_kernel(con
   if (i < nmine) step(f0, f2);
   if (i + 1 < nmine) step(f1, f0);
   __syncthreads();
-  for (int t = threadIdx.x; t < nu * kUnitRows * NC; t += NT) {
-    const int uu = t / (kUnitRows * NC), c = (t >> 2) % NC, row = t & 3;
-    const int q0 = uu * nkb, q1 = q0 + nkb;  // the unit's items
+  // output o = (unit, column, row) by the quad of lanes 4o + bi: each adds its bi partial of every
+  // wave's slot in wave order, then the quad adds the four (xor 1, then xor 2)
+  const int nout = nu * kUnitRows * NC;
+  for (int t0 = 0; t0 < 4 * nout; t0 += NT) {
+    const int t = t0 + (int)threadIdx.x, o = t >> 2, q = t & 3;
+    const int uu = o / (kUnitRows * NC), c = (o >> 2) % NC, row = o & 3;
     float v = 0.0f;
-    for (int w = 0; w < NW; ++w) {
-      const int a = w * items / NW, b = (w + 1) * items / NW;
-      if (a < q1 && b > q0 && a < b) {
-        const float* pp = part + ((uu * NW + w) * NC + c) * 16 + 2 * (row >> 1) + (row & 1);
+    if (o < nout) {
+      const float* pp = part + (uu * NW * NC + c) * 16 + 4 * q + 2 * (row >> 1) + (row & 1);
 #pragma unroll
-        for (int b2 = 0; b2 < 4; ++b2) v += pp[4 * b2];
-      }
+      for (int w = 0; w < NW; ++w) v += pp[w * NC * 16];
     }
-    store_y(y, (int64_t)c * nrows + (int64_t)(u0 + uu) * kUnitRows + row, v, y_dtype);
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    if (q == 0 && o < nout)
+      store_y(y, (int64_t)c * nrows + (int64_t)(u0 + uu) * kUnitRows + row, v, y_dtype);
   }
 }
 
