@@ -56,12 +56,20 @@ def test_host_helpers(lib):
 def test_workspace_follows_the_product_plan(lib):
     """Product ops size their workspace for the activation layout of the GEMM they run: the int8
     layout (4,608 B per 16 rows x 256 values) below 64 rows, the fp16 one (9,216 B) for packed
-    IQ3_S and Q4_K from 64 rows at K <= 8192 and for the prefill from 256 rows; IQ4_XS and
-    K = 17408 stay on the int8 layout below the prefill."""
+    IQ3_S and Q4_K from 64 rows at K <= 8192, below that where the fp16 GEMM's range plan takes
+    the weight (1..5 row tiles per CU, 256 CUs assumed without a GPU; IQ3_S from 33 rows, Q4_K
+    from 17), and for the prefill from 256 rows; IQ4_XS and K = 17408 stay on the int8 layout below the prefill."""
     xq = lambda n, k: -(-n // 16) * (k // 256) * 4608
     xh = lambda n, k: -(-n // 16) * (k // 256) * 9216
     packed, mmq = 7, 1
-    assert lib.gguf_op_workspace_bytes(packed, 21, 17408, 5120, 48, 0) == xq(48, 5120)
+    assert lib.gguf_op_workspace_bytes(packed, 21, 17408, 5120, 48, 0) == xh(48, 5120)
+    assert lib.gguf_op_workspace_bytes(packed, 21, 17408, 5120, 33, 0) == xh(33, 5120)
+    assert lib.gguf_op_workspace_bytes(packed, 21, 17408, 5120, 32, 0) == xq(32, 5120)
+    assert lib.gguf_op_workspace_bytes(packed, 21, 17408, 5120, 8, 0) == xq(8, 5120)
+    assert lib.gguf_op_workspace_bytes(packed, 21, 17408, 5120, 49, 0) == xq(49, 5120)
+    assert lib.gguf_op_workspace_bytes(packed, 21, 1024, 5120, 48, 0) == xq(48, 5120)
+    assert lib.gguf_op_workspace_bytes(mmq, 12, 17408, 5120, 32, 0) == xh(32, 5120)
+    assert lib.gguf_op_workspace_bytes(mmq, 12, 17408, 5120, 16, 0) == xq(16, 5120)
     assert lib.gguf_op_workspace_bytes(packed, 21, 17408, 5120, 64, 0) == xh(64, 5120)
     assert lib.gguf_op_workspace_bytes(packed, 21, 17408, 5120, 255, 0) == xh(255, 5120)
     assert lib.gguf_op_workspace_bytes(packed, 21, 17408, 5120, 256, 0) == xh(256, 5120)

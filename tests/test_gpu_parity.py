@@ -236,6 +236,61 @@ def test_small_fp16_vs_q81_with_zero_blocks(qt, tiles, n):
         assert (y[:, 3] == 0).all()
 
 
+# Product ops of up to 48 activation rows (IQ3_S from 33, Q4_K from 17) on weights of 1..5 row tiles
+# per CU run the fp16 small GEMM's range plan: one workgroup per CU over its run of row tiles (300
+# tiles: runs of 1 or 2; 1100: 4 or 5; 1280: 5), all column tiles in the workgroup.
+RANGE_ROWS = {o.IQ3_S: (16 * 300, 16 * 1100, 16 * 1280), o.Q4_K: (16 * 300 + 9, 16 * 1100, 16 * 1280)}
+RANGE_N = {o.IQ3_S: [33, 40, 48], o.Q4_K: [17, 32, 33, 48]}
+
+
+@pytest.mark.parametrize("qt,n", [(qt, n) for qt in (o.IQ3_S, o.Q4_K) for n in RANGE_N[qt]],
+                         ids=[f"{TN[qt]}-{n}" for qt in (o.IQ3_S, o.Q4_K) for n in RANGE_N[qt]])
+@pytest.mark.parametrize("ri", [0, 1, 2], ids=["runs1-2", "runs4-5", "runs5"])
+def test_small_fp16_range_exact_integer_dots(lib, qt, ri, n):
+    """Exact-integer mode through the range plan (asserted from the op's workspace: the fp16
+    activation layout): every output is the oracle's int64 sum of slice dots."""
+    rows, k = RANGE_ROWS[qt][ri], 512
+    op = 7 if qt == o.IQ3_S else 1
+    assert lib.gguf_op_workspace_bytes(op, qt, rows, k, n, 0) == -(-n // 16) * (k // 256) * 9216
+    raw = _exact_weights(qt, rows, k, seed=240 + n + ri)
+    x = _exact_x(n, k, seed=250 + n, dtype=torch.float32)
+    y = _small_h_op(qt, raw, rows)(x.cuda()).cpu().numpy()
+    np.testing.assert_array_equal(y.astype(np.int64), _exact_ref(raw, qt, x))
+
+
+@pytest.mark.parametrize("qt,n", [(o.IQ3_S, 33), (o.IQ3_S, 48), (o.Q4_K, 17), (o.Q4_K, 48)])
+def test_small_fp16_range_vs_q81_with_zero_blocks(qt, n):
+    """The range plan against the q81 model with zero-d blocks (running block scale), bf16 output,
+    and graph replays bit-identical."""
+    rows, k = RANGE_ROWS[qt][1], 2048
+    raw = _w(qt, rows, k, seed=260 + n)
+    b = raw.reshape(rows, k // 256, o.BLOCK_BYTES[qt])
+    rng = np.random.default_rng(270 + n)
+    zero = rng.random((rows, k // 256)) < 0.2
+    zero[:, 0] |= rng.random(rows) < 0.5
+    b[zero, 0:2] = 0
+    from vllm_gguf_plugin.quantization import iq3_pack
+
+    x = _x(n, k, seed=n + 280, dtype=torch.bfloat16)
+    if qt == o.IQ3_S:
+        w = iq3_pack.pack(_dev(raw), qt)
+        f = lambda xx: C().lcpp_mul_mat_iq3_packed(w, xx, qt, rows)
+    else:
+        w = _dev(raw)
+        f = lambda xx: C().lcpp_mul_mat_q(w, xx, qt, rows)
+    xc = x.cuda()
+    y = f(xc)
+    ref = o.q81_model(raw, qt, x, layout="mmq")
+    assert o.rel_l2(y.float().cpu().numpy(), ref) <= TIGHT[torch.bfloat16]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = f(xc)
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, y)
+
+
 @pytest.mark.parametrize("qt", [o.IQ3_S, o.Q4_K], ids=lambda t: TN[t])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
 def test_small_fp16_16bit_x(qt, dtype):

@@ -45,6 +45,7 @@ hipError_t launch_quantize_xh(const void* x, int dtype, int64_t n, int64_t k, in
                               hipStream_t stream);
 bool prefill_uses_xh(int type, bool packed);
 bool small_h_supported(int type, bool packed);
+bool small_h_range(int type, int64_t nrows, int64_t n);
 hipError_t launch_gemm_small_h(int type, bool packed, const uint8_t* W, int64_t row_bytes, int nrows, int k,
                                const uint8_t* xh, int n, void* y, int y_dtype, hipStream_t stream);
 hipError_t launch_gemm_prefill(int type, bool packed, const uint8_t* W, int64_t row_bytes, int nrows, int k,
@@ -269,14 +270,16 @@ bool rows_fused(int op, int64_t type, int64_t row, int64_t k, int64_t n, bool ha
   return bb > 0 && gguf::gemv_rows_x_supported((int)type, row, k / 256 * bb, k, n);
 }
 
-// The MFMA products of 64 to 255 activation rows with K <= 8192 run the fp16 small GEMM (X in the
-// xh layout) for packed IQ3_S and Q4_K; the rest below the prefill rows the int8 small GEMM (xq
-// layout). Measured at the 27B-layer shapes: from 64 rows the fp16 GEMM's shared decode beats
-// re-decoding the weights per group of 4 column tiles (17408 x 5120 IQ3_S, 128 rows: 84 against
-// 134 us); below 64 rows, and over K = 17408 (68 blocks in one workgroup's loop, 320
-// workgroups), the int8 GEMM's K split across waves is faster.
-bool small_fp16(int op, int64_t type, int64_t k, int64_t n) {
-  return op_gemm(op) && n >= 64 && n < kPrefillFrom && k <= 8192 && gguf::small_h_supported((int)type, op_packed(op));
+// The MFMA products with K <= 8192 run the fp16 small GEMM (X in the xh layout) for packed IQ3_S
+// and Q4_K from 64 to 255 activation rows, and below 64 rows where its one-workgroup-per-CU range
+// plan applies (1..5 row tiles per CU; 33..48 rows for IQ3_S, 17..48 for Q4_K); the rest below the
+// prefill rows the int8 small GEMM (xq layout). Measured at the 27B-layer shapes: from 64 rows the fp16 GEMM's
+// shared decode beats re-decoding the weights per group of 4 column tiles (17408 x 5120 IQ3_S,
+// 128 rows: 84 against 134 us); over K = 17408 (68 blocks in one workgroup's loop, 320
+// workgroups) the int8 GEMM's K split across waves is faster.
+bool small_fp16(int op, int64_t type, int64_t row, int64_t k, int64_t n) {
+  if (!op_gemm(op) || k > 8192 || !gguf::small_h_supported((int)type, op_packed(op))) return false;
+  return (n >= 64 && n < kPrefillFrom) || gguf::small_h_range((int)type, row, n);
 }
 
 }  // namespace
@@ -290,7 +293,7 @@ size_t gguf_op_workspace_bytes(int op, int64_t type, int64_t row, int64_t k, int
   if (op_gemm(op)) {
     const bool mmq_layout = !op_packed(op) && type == gguf::kIQ3_S;
     if (!mmq_layout && ((n >= kPrefillFrom && gguf::prefill_uses_xh((int)type, op_packed(op))) ||
-                        small_fp16(op, type, k, n)))
+                        small_fp16(op, type, row, k, n)))
       return align256(gguf::xh_bytes(n, k));
     return align256(mmq_layout ? gguf_q8_1_bytes(n, k, 1) : gguf::xq_bytes(n, k));
   }
@@ -360,7 +363,7 @@ int gguf_mul_mat(int op, const gguf_view* W, const gguf_view* X, int64_t type, i
   // caller's x_q8
   if ((gemm && (packed || type != gguf::kIQ3_S)) || (!gemm && decode_mma(op, type, row, k, n))) {
     const bool prefill = gemm && n >= kPrefillFrom;
-    const bool fp16 = small_fp16(op, type, k, n);
+    const bool fp16 = small_fp16(op, type, row, k, n);
     const bool xh = fp16 || (prefill && gguf::prefill_uses_xh((int)type, packed));
     if (!gemm && x_q8)
       e = gguf::launch_q8_1_to_xq(x_q8->data, n, k, (int)type, workspace, s);

@@ -81,14 +81,17 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-template <int TYPE, int RT, int NM>
-__global__ void __launch_bounds__(64 * (2 * RT + NM), 4) gemm_small_h_kernel(const uint8_t* __restrict__ W,
-                                                                             int64_t row_bytes, int nrows, int k,
-                                                                             const uint8_t* __restrict__ xh, int nct,
-                                                                             int n, void* __restrict__ y, int y_dtype) {
+// RANGE: workgroup g owns the row tiles [g T / G, (g + 1) T / G) of the T tiles (at most RT; one
+// workgroup per CU on the 27B-class weights, X read once per CU), else tiles [RT g, RT g + RT).
+// DPT decoder waves per row tile: 2 (each one half block per step) or 1 (both halves).
+template <int TYPE, int RT, int NM, int DPT, bool RANGE, int MW = 1>
+__global__ void __launch_bounds__(64 * (DPT * RT + NM * MW), RANGE ? 1 : 4) gemm_small_h_kernel(
+    const uint8_t* __restrict__ W, int64_t row_bytes, int nrows, int k, const uint8_t* __restrict__ xh, int nct, int n,
+    void* __restrict__ y, int y_dtype) {
   constexpr bool IQ3 = TYPE == kIQ3_S;
-  constexpr int ND = 2 * RT;       // decoding waves: tile w >> 1, half block w & 1
-  constexpr int NT = 64 * (ND + NM);
+  constexpr int ND = DPT * RT;     // decoding waves: tile w / DPT, half block w % DPT (DPT = 2) or both
+  constexpr int NT = 64 * (ND + NM * MW);
+  constexpr int TPM = (RT + MW - 1) / MW;  // row tiles per multiplier wave: MW waves share a column tile
   constexpr int kHalf = RT * 4 * kHRegion;  // A bytes of one half block of the RT tiles
   using Raw = typename std::conditional<IQ3, RawIq3, RawQ4k>::type;
   __shared__ __attribute__((aligned(16))) uint8_t A[2][2][kHalf];  // [block parity][half]
@@ -100,7 +103,14 @@ __global__ void __launch_bounds__(64 * (2 * RT + NM), 4) gemm_small_h_kernel(con
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 15, q = lane >> 4;
   const int ntiles = (nrows + 15) / 16;
-  const int tile0 = blockIdx.x * RT;
+  int tile0, tile1;  // the workgroup's row tiles
+  if constexpr (RANGE) {
+    tile0 = (int)(blockIdx.x * (uint32_t)ntiles / gridDim.x);
+    tile1 = (int)((blockIdx.x + 1) * (uint32_t)ntiles / gridDim.x);
+  } else {
+    tile0 = blockIdx.x * RT;
+    tile1 = min(tile0 + RT, ntiles);
+  }
   const int nb = k / kQK;
   if constexpr (IQ3) {
     // all loads first, then the stores (indices past the table repeat its last entry)
@@ -115,51 +125,99 @@ __global__ void __launch_bounds__(64 * (2 * RT + NM), 4) gemm_small_h_kernel(con
 
   if (wave < ND) {
     // ---- decoder: block b + 1 into the A area of its parity while the multipliers use block b.
-    // Rows past the weight re-read its last tile / row (decoded, never stored). Past the end,
-    // the loads re-read block nb - 1 and the decode repeats it, which leaves e and EF as they are.
-    const int dt = wave >> 1, dh = wave & 1;
+    // Tiles past the workgroup's last re-read it, rows past the weight its last row (decoded,
+    // never stored). Past the end, the loads re-read block nb - 1 and the decode repeats it, which
+    // leaves e and EF as they are.
+    const int dt = wave / DPT;
+    const int dtile = min(tile0 + dt, tile1 - 1);
     const uint8_t* wp;
-    if constexpr (IQ3) wp = W + (int64_t)min(tile0 + dt, ntiles - 1) * kTileRows * row_bytes;
-    else wp = W + (int64_t)min((tile0 + dt) * 16 + j, nrows - 1) * row_bytes;
+    if constexpr (IQ3) wp = W + (int64_t)dtile * kTileRows * row_bytes;
+    else wp = W + (int64_t)min(dtile * 16 + j, nrows - 1) * row_bytes;
     float e = 1.0f;
-    // the raw bytes of a block: two named sets, each refilled right after its decode and used
-    // two steps later
-    auto load_w = [&](int b, Raw& raw) {
-      if constexpr (IQ3) load_step(raw, wp, row_bytes, nb, b, dh, j, q);
-      else load_step(raw, wp + (int64_t)b * block_bytes(kQ4_K), dh, q);
+    // the raw bytes of a block (per half this wave decodes): two named sets, each refilled right
+    // after its decode and used two steps later
+    constexpr int NH = 2 / DPT;
+    const int h0 = DPT == 2 ? (wave & 1) : 0;
+    struct RawSet {
+      Raw r[NH];
     };
-    auto decode = [&](int par, const Raw& raw) {
-      uint8_t* Ab = A[par][dh];
-      if constexpr (IQ3) decode_step_tb(raw, dh, (const uint8_t*)TB, Ab, RTs[par], EFs[par], e, dt, j, q);
-      else decode_step(raw, dh, AM[par][dh], Ab, RTs[par], EFs[par], e, dt, j, q);
+    auto load_w = [&](int b, RawSet& raw) {
+#pragma unroll
+      for (int i = 0; i < NH; ++i) {
+        const int h = h0 + i;
+        if constexpr (IQ3) load_step(raw.r[i], wp, row_bytes, nb, b, h, j, q);
+        else load_step(raw.r[i], wp + (int64_t)b * block_bytes(kQ4_K), h, q);
+      }
     };
-    Raw r0, r1;
-    load_w(0, r0);
-    load_w(min(1, nb - 1), r1);
-    decode(0, r0);
-    __builtin_amdgcn_sched_barrier(0);
-    load_w(min(2, nb - 1), r0);
-    lds_barrier();
-    auto step = [&](int b, Raw& rdec) {
-      decode((b & 1) ^ 1, rdec);
+    auto decode = [&](int par, const RawSet& raw) {
+#pragma unroll
+      for (int i = 0; i < NH; ++i) {
+        const int h = h0 + i;
+        uint8_t* Ab = A[par][h];
+        if constexpr (IQ3) decode_step_tb(raw.r[i], h, (const uint8_t*)TB, Ab, RTs[par], EFs[par], e, dt, j, q);
+        else decode_step(raw.r[i], h, AM[par][h], Ab, RTs[par], EFs[par], e, dt, j, q);
+      }
+    };
+    if constexpr (DPT == 2) {
+      RawSet r0, r1;
+      load_w(0, r0);
+      load_w(min(1, nb - 1), r1);
+      decode(0, r0);
       __builtin_amdgcn_sched_barrier(0);
-      load_w(min(b + 3, nb - 1), rdec);
+      load_w(min(2, nb - 1), r0);
       lds_barrier();
-    };
-    int b = 0;
-    for (; b + 1 < nb; b += 2) {
-      step(b, r1);
-      step(b + 1, r0);
+      auto step = [&](int b, RawSet& rdec) {
+        decode((b & 1) ^ 1, rdec);
+        __builtin_amdgcn_sched_barrier(0);
+        load_w(min(b + 3, nb - 1), rdec);
+        lds_barrier();
+      };
+      int b = 0;
+      for (; b + 1 < nb; b += 2) {
+        step(b, r1);
+        step(b + 1, r0);
+      }
+      if (b < nb) step(b, r1);
+    } else {
+      // three named sets: block b + 1 decoded while blocks b + 2 and b + 3 load
+      RawSet r0, r1, r2;
+      load_w(0, r0);
+      load_w(min(1, nb - 1), r1);
+      load_w(min(2, nb - 1), r2);
+      __builtin_amdgcn_sched_barrier(0);
+      decode(0, r0);
+      __builtin_amdgcn_sched_barrier(0);
+      load_w(min(3, nb - 1), r0);
+      __builtin_amdgcn_sched_barrier(0);
+      lds_barrier();
+      auto step = [&](int b, RawSet& rdec) {
+        decode((b & 1) ^ 1, rdec);
+        __builtin_amdgcn_sched_barrier(0);
+        load_w(min(b + 4, nb - 1), rdec);
+        __builtin_amdgcn_sched_barrier(0);
+        lds_barrier();
+      };
+      int b = 0;
+      for (; b + 2 < nb; b += 3) {
+        step(b, r1);
+        step(b + 1, r2);
+        step(b + 2, r0);
+      }
+      if (b < nb) step(b, r1);
+      if (b + 1 < nb) step(b + 1, r2);
     }
-    if (b < nb) step(b, r1);
     return;
   }
 
-  // ---- multiplier: column tile ct against the RT decoded tiles (past nct: the last one again,
-  // never stored). The B operand and activation scale of each slice (and Q4_K's d x sum q per
+  // ---- multiplier: column tile ct against its row tiles tm + MW i of the RT decoded tiles (past
+  // nct: the last column tile again, past RT: tile RT - 1 again; never stored). The B operand and activation scale of each slice (and Q4_K's d x sum q per
   // half block) are refilled in place with the next block's once consumed: a copy of a value
   // still to be used would make the compiler wait for the refill.
-  const int ctw = (int)blockIdx.y * NM + (wave - ND);
+  const int mw = wave - ND, tm = mw % MW;
+  const int ctw = (int)blockIdx.y * NM + mw / MW;
+  int tix[TPM];  // the multiplier's row tiles in the decoded set
+#pragma unroll
+  for (int i = 0; i < TPM; ++i) tix[i] = min(tm + MW * i, RT - 1);
   const int ct = min(ctw, nct - 1);
   const uint8_t* xv = xh + (int64_t)ct * nb * kXhUnit + 16 * lane;
   const uint8_t* xs = xh + xh_scale_base(nct, nb) + (int64_t)ct * nb * kXhScaleUnit + 32 * j;
@@ -175,37 +233,37 @@ __global__ void __launch_bounds__(64 * (2 * RT + NM), 4) gemm_small_h_kernel(con
     if constexpr (!IQ3)
       if ((s & 3) == 0) o.sqv[s >> 2] = *(const float*)(xs + (int64_t)b * kXhScaleUnit + 512 + 4 * (s + q));
   };
-  f4 acc[RT];
+  f4 acc[TPM];
 #pragma unroll
-  for (int t = 0; t < RT; ++t) acc[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int t = 0; t < TPM; ++t) acc[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
   const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
   // block b from the A area of parity b & 1 with operand set o, refilled with block bn's
   auto compute = [&](int b, int bn, BSet& o) {
     const int par = b & 1;
 #pragma unroll
-    for (int t = 0; t < RT; ++t) acc[t] *= *(const f4*)(RTs[par] + t * 16 + 4 * q);
+    for (int t = 0; t < TPM; ++t) acc[t] *= *(const f4*)(RTs[par] + tix[t] * 16 + 4 * q);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
 #pragma unroll
       for (int qq = 0; qq < 2; ++qq) {
         // all A operands of a quarter block (2 slices), then its MFMAs back to back, then the
         // FMAs: a chain of LDS read, MFMA and FMA per slice would be paid 8 times per block
-        h8 a[2][RT];
+        h8 a[2][TPM];
 #pragma unroll
         for (int uu = 0; uu < 2; ++uu)
 #pragma unroll
-          for (int t = 0; t < RT; ++t) a[uu][t] = *(const h8*)(A[par][h] + h_off(t, 2 * qq + uu, j, q));
-        f4 p[2][RT];
+          for (int t = 0; t < TPM; ++t) a[uu][t] = *(const h8*)(A[par][h] + h_off(tix[t], 2 * qq + uu, j, q));
+        f4 p[2][TPM];
 #pragma unroll
         for (int uu = 0; uu < 2; ++uu)
 #pragma unroll
-          for (int t = 0; t < RT; ++t)
+          for (int t = 0; t < TPM; ++t)
             p[uu][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[uu][t], __builtin_bit_cast(h8, o.bq[4 * h + 2 * qq + uu]),
                                                               zero, 0, 0, 0);
 #pragma unroll
         for (int uu = 0; uu < 2; ++uu) {
 #pragma unroll
-          for (int t = 0; t < RT; ++t) {
+          for (int t = 0; t < TPM; ++t) {
 #pragma unroll
             for (int v = 0; v < 4; ++v) acc[t][v] = fmaf(p[uu][t][v], o.dq[4 * h + 2 * qq + uu], acc[t][v]);
             // keeps the FMAs here: the compiler otherwise sinks them to the next block's use of
@@ -216,8 +274,8 @@ __global__ void __launch_bounds__(64 * (2 * RT + NM), 4) gemm_small_h_kernel(con
       }
       if constexpr (!IQ3) {  // the min term of the half block
 #pragma unroll
-        for (int t = 0; t < RT; ++t) {
-          const float am = AM[par][h][(t * 4 + q) * 16 + j];
+        for (int t = 0; t < TPM; ++t) {
+          const float am = AM[par][h][(tix[t] * 4 + q) * 16 + j];
           acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(am, o.sqv[h], acc[t], 0, 0, 0);
           asm volatile("" : "+v"(acc[t]));
         }
@@ -249,46 +307,88 @@ __global__ void __launch_bounds__(64 * (2 * RT + NM), 4) gemm_small_h_kernel(con
   const float* EF = EFs[(nb - 1) & 1];
   const int col = ctw * kXqCols + j;
 #pragma unroll
-  for (int t = 0; t < RT; ++t) {
-    const int tile = tile0 + t;
-    const f4 ef = *(const f4*)(EF + t * 16 + 4 * q);
+  for (int t = 0; t < TPM; ++t) {
+    if (tm + MW * t >= RT) break;
+    const int tile = tile0 + tix[t];
+    const f4 ef = *(const f4*)(EF + tix[t] * 16 + 4 * q);
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int row = tile * 16 + 4 * q + v;
-      if (col < n && tile < ntiles && row < nrows) store_y(y, (int64_t)col * nrows + row, acc[t][v] * ef[v], y_dtype);
+      if (col < n && tile < tile1 && row < nrows) store_y(y, (int64_t)col * nrows + row, acc[t][v] * ef[v], y_dtype);
     }
   }
 }
 
-template <int TYPE, int RT, int NM>
+template <int TYPE, int RT, int NM, int DPT, bool RANGE, int MW = 1>
 void launch_small_h_t(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xh, int n, void* y,
-                      int y_dtype, hipStream_t stream) {
+                      int y_dtype, unsigned gx, hipStream_t stream) {
   const int nct = (int)xq_col_tiles(n);
-  const int ntiles = (nrows + 15) / 16;
-  const dim3 grid((unsigned)((ntiles + RT - 1) / RT), (unsigned)((nct + NM - 1) / NM));
-  gemm_small_h_kernel<TYPE, RT, NM><<<grid, 64 * (2 * RT + NM), 0, stream>>>(W, row_bytes, nrows, k, xh, nct, n, y,
-                                                                             y_dtype);
+  const dim3 grid(gx, (unsigned)((nct + NM - 1) / NM));
+  gemm_small_h_kernel<TYPE, RT, NM, DPT, RANGE, MW><<<grid, 64 * (DPT * RT + NM * MW), 0, stream>>>(
+      W, row_bytes, nrows, k, xh, nct, n, y, y_dtype);
 }
 
 template <int TYPE, int RT>
 void launch_small_h_rt(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xh, int n, void* y,
                        int y_dtype, hipStream_t stream) {
   const int nct = (int)xq_col_tiles(n);
-  if (nct <= 1) launch_small_h_t<TYPE, RT, 1>(W, row_bytes, nrows, k, xh, n, y, y_dtype, stream);
-  else if (nct <= 2) launch_small_h_t<TYPE, RT, 2>(W, row_bytes, nrows, k, xh, n, y, y_dtype, stream);
-  else launch_small_h_t<TYPE, RT, 4>(W, row_bytes, nrows, k, xh, n, y, y_dtype, stream);
+  const unsigned gx = (unsigned)(((nrows + 15) / 16 + RT - 1) / RT);
+  if (nct <= 1) launch_small_h_t<TYPE, RT, 1, 2, false>(W, row_bytes, nrows, k, xh, n, y, y_dtype, gx, stream);
+  else if (nct <= 2) launch_small_h_t<TYPE, RT, 2, 2, false>(W, row_bytes, nrows, k, xh, n, y, y_dtype, gx, stream);
+  else launch_small_h_t<TYPE, RT, 4, 2, false>(W, row_bytes, nrows, k, xh, n, y, y_dtype, gx, stream);
+}
+
+// one workgroup per CU over at most kRangeTiles row tiles each, 1..3 column tiles
+constexpr int kRangeTiles = 5;
+
+static int small_h_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int c = 0;
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+    cus[dev] = c;
+  }
+  return cus[dev];
 }
 
 }  // namespace
 
-// Types the fp16 small GEMM serves: IQ3_S in the tile layout (packed) and Q4_K rows.
+// Types the fp16 small GEMM serves: IQ3_S in the unit layout (packed) and Q4_K rows.
 bool small_h_supported(int type, bool packed) { return packed ? type == kIQ3_S : type == kQ4_K; }
 
-// xh: X in the xh layout (launch_quantize_xh / launch_q8_1_to_xh). Two row tiles per workgroup
-// from 1024 tiles on (X read once per tile pair), one below (more workgroups on smaller weights).
+// The range plan: 2..3 column tiles on weights of between one and kRangeTiles row tiles per CU:
+// every CU's workgroup decodes its 4-5 tiles once per block for all columns and reads X once.
+// Measured at 17408 x 5120 (op level, quantise included) against the int8 small GEMM: IQ3_S
+// packed 48 rows 42.9 against 50.1 us, 32 rows 40.2 against 39.3; Q4_K 48 rows 41.8 against 66.8,
+// 32 rows 39.6 against 51.4, 16 rows 36.8 against 28.7 (one column tile stays on the int8 GEMM).
+bool small_h_range(int type, int64_t nrows, int64_t n) {
+  const int64_t tiles = (nrows + 15) / 16, cus = small_h_cus();
+  const int64_t from = type == kIQ3_S ? 33 : 17;
+  return n >= from && n <= 3 * 16 && tiles >= cus && tiles <= kRangeTiles * cus;
+}
+
+// xh: X in the xh layout (launch_quantize_xh / launch_q8_1_to_xh). The range plan where it
+// applies; else two row tiles per workgroup from 1024 tiles on (X read once per tile pair), one
+// below (more workgroups on smaller weights).
 hipError_t launch_gemm_small_h(int type, bool packed, const uint8_t* W, int64_t row_bytes, int nrows, int k,
                                const uint8_t* xh, int n, void* y, int y_dtype, hipStream_t stream) {
   if (!small_h_supported(type, packed)) return hipErrorInvalidValue;
+  if (small_h_range(type, nrows, n)) {
+    const int nct = (int)xq_col_tiles(n);
+    const unsigned gx = (unsigned)small_h_cus();
+#define GGUF_RANGE(T)                                                                                                      \
+  if (nct <= 2) launch_small_h_t<T, kRangeTiles, 2, 1, true, 1>(W, row_bytes, nrows, k, xh, n, y, y_dtype, gx, stream); \
+  else launch_small_h_t<T, kRangeTiles, 3, 1, true, 1>(W, row_bytes, nrows, k, xh, n, y, y_dtype, gx, stream);
+    if (type == kIQ3_S) {
+      GGUF_RANGE(kIQ3_S)
+    } else {
+      GGUF_RANGE(kQ4_K)
+    }
+#undef GGUF_RANGE
+    return hipGetLastError();
+  }
   const bool two = (nrows + 15) / 16 >= 1024;
   if (type == kIQ3_S) {
     if (two) launch_small_h_rt<kIQ3_S, 2>(W, row_bytes, nrows, k, xh, n, y, y_dtype, stream);

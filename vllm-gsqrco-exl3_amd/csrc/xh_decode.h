@@ -62,12 +62,14 @@ __device__ __forceinline__ uint32_t h2_bits(h2 v) { return __builtin_bit_cast(ui
 __device__ __forceinline__ h2 bits_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
 
 // A decoding lane's raw weight bytes for one step, loaded two steps ahead.
+// (16- and 8-bit loads kept narrow: a 32-bit field is widened where the loop's register sets meet,
+// at its head, which waits for every load in flight, the prefetch of the next steps included)
 struct RawIq3 {
   uint2 qs;     // qs of the lane's row and slice
   uint32_t e8;  // E8 dword of the row
-  uint32_t l2;  // L2 halfword of the row pair
-  uint32_t sc;  // SC byte (two 4-bit sub-scales)
-  uint32_t d;   // fp16 d of the row
+  uint16_t l2;  // L2 halfword of the row pair
+  uint8_t sc;   // SC byte (two 4-bit sub-scales)
+  uint16_t d;   // fp16 d of the row
 };
 struct RawQ4k {
   u32x4 hdr;    // d, dmin, scales[12]
@@ -173,7 +175,7 @@ __device__ __forceinline__ void decode_step(const RawQ4k& w, int h, float* AM, u
 // (dequantize_row_q6_K, ggml-quants.c). Blocks are 210 bytes: 2-byte aligned loads.
 struct RawQ6k {
   uint64_t la, lb, qh, sc;
-  uint32_t d;
+  uint16_t d;  // kept 16-bit (see RawIq3)
 };
 
 __device__ __forceinline__ void load_step(RawQ6k& w, const uint8_t* blk, int h, int q) {
