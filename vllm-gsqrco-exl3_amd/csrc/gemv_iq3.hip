@@ -345,13 +345,14 @@ constexpr int kStreamWaves = 8;
 // X: XDT < 0 the caller's block_q8_1 copied into LDS, XDT >= 0 X itself (row stride s01)
 // quantised into LDS with the q8_1 arithmetic. Each thread stages XPT groups of 8 values, their
 // loads issued first, then the grid word, then the wave's first two unit-blocks.
-template <int NC, int XDT, int XPT>
-__global__ void __launch_bounds__(64 * kStreamWaves) gemv_iq3s_stream_kernel(const uint8_t* __restrict__ W,
+template <int NC, int XDT, int XPT, int NW = kStreamWaves>
+__global__ void __launch_bounds__(64 * NW) gemv_iq3s_stream_kernel(const uint8_t* __restrict__ W,
                                                                               int64_t row_bytes, int nrows, int k,
                                                                               const void* __restrict__ xsrc,
                                                                               int64_t s01, void* __restrict__ y,
                                                                               int y_dtype) {
-  constexpr int NW = kStreamWaves, NT = 64 * NW;
+  constexpr int NT = 64 * NW;
+  static_assert(NT >= 512, "the table build takes 512 threads");
   __shared__ uint4 table[2048];
   __shared__ uint4 sink;    // staging writes of groups past the end of X
   extern __shared__ uint4 xdyn[];  // X: q [NC][slice][8 dwords], d [NC][slice]; then the partial sums
@@ -378,7 +379,8 @@ __global__ void __launch_bounds__(64 * kStreamWaves) gemv_iq3s_stream_kernel(con
   XGroup<XDT> xa[XPT];
 #pragma unroll
   for (int j = 0; j < XPT; ++j) xgroup_load<NC, XDT>(xsrc, xrs, s01, nslices, xg[j], xa[j]);
-  const uint32_t gword = __builtin_amdgcn_raw_buffer_load_b32(buffer_rsrc(&kIq3sGridDev, 2048), 4 * threadIdx.x, 0, 0);
+  const uint32_t gword =
+      __builtin_amdgcn_raw_buffer_load_b32(buffer_rsrc(&kIq3sGridDev, 2048), 4 * (threadIdx.x & 511), 0, 0);
   __builtin_amdgcn_sched_barrier(0);
   // the workgroup's units [u0, u1) and the wave's run of items [j0, j1) (32-bit: units * grid
   // < 2^31 for any weight of fewer than 2^23 rows)
@@ -413,7 +415,7 @@ __global__ void __launch_bounds__(64 * kStreamWaves) gemv_iq3s_stream_kernel(con
   load_next(f0);
   load_next(f1);
   __builtin_amdgcn_sched_barrier(0);
-  iq3_table_from_grid(table, gword, threadIdx.x);
+  if (NT == 512 || threadIdx.x < 512) iq3_table_from_grid(table, gword, threadIdx.x);
 #pragma unroll
   for (int j = 0; j < XPT; ++j) {
     if (wave * 64 + j * NT < ngroups)  // waves with no group left skip the (fused) quantisation

@@ -14,10 +14,15 @@
 //
 // Wave64 mapping: the MMVQ kernel gives each 32-lane half-wave one block (one value per lane);
 // the MMQ kernel gives each lane 4 consecutive values, 8 lanes per 32-block.
+#include <algorithm>
+
 #include "gguf_common.h"
 #include "xq.h"
 
 namespace gguf {
+
+// activation rows per launch of the xq / xh quantisers (grid y)
+constexpr int kQuantRowsPerLaunch = 65520;
 
 template <int DT>
 __device__ __forceinline__ float ldx(const void* x, int64_t i) {
@@ -124,18 +129,15 @@ __global__ void __launch_bounds__(128) quantize_q8_1_mmq_kernel(const void* __re
 // form, vecdotq.cuh:525: d8 * sum(q8)), else the fp16 of the slice's sum of x, the half2 sum of
 // block_q8_1_mmq's DS4 layout (the product ops' MMQ form, vecdotq.cuh:549-552).
 template <bool VEC, bool DS4>
-__device__ __forceinline__ void xq_store(uint8_t* y, int64_t k, int64_t c, int64_t kk, int64_t total, uint32_t lo,
-                                         uint32_t hi, float d, int qsum, float xsum) {
-  const int64_t per_row = k / 8;
-  const int64_t nb = k / kQK;
-  const int64_t b = kk / kQK;
-  const int u = (int)((kk / kQ81) & 7), q = (int)((kk / 8) & 3);
-  const int64_t t = c / kXqCols;
-  const int j = (int)(c % kXqCols);
-  const int64_t unit = t * nb + b;
+__device__ __forceinline__ void xq_store(uint8_t* y, int k, int c, int kk, int nct, uint32_t lo, uint32_t hi, float d,
+                                         int qsum, float xsum) {
+  const int nb = k / kQK;
+  const int b = kk / kQK;
+  const int u = (kk / kQ81) & 7, q = (kk / 8) & 3;
+  const int t = c / kXqCols, j = c % kXqCols;
+  const int64_t unit = (int64_t)t * nb + b;
   *(uint2*)(y + unit * kXqUnit + (16 * q + j) * 64 + 8 * u) = make_uint2(lo, hi);
   if (q == 0) {
-    const int64_t nct = total / per_row / kXqCols;
     const uint32_t dh = __half_as_ushort(__float2half_rn(d));
     uint32_t word = VEC ? __float_as_uint(half_bits_to_float(dh)) : __float_as_uint(d);
     if constexpr (DS4)
@@ -147,15 +149,13 @@ __device__ __forceinline__ void xq_store(uint8_t* y, int64_t k, int64_t c, int64
 // The prefill GEMM's fp16 layout (xq.h, "xh"); same thread mapping and values as xq_store (MMQ
 // arithmetic: for DS4 the min term's activation side is the fp16 sum of x, widened to fp32).
 template <bool DS4>
-__device__ __forceinline__ void xh_store(uint8_t* y, int64_t k, int64_t c, int64_t kk, int64_t total, uint32_t lo,
-                                         uint32_t hi, float d, float xsum) {
-  const int64_t per_row = k / 8;
-  const int64_t nb = k / kQK;
-  const int64_t b = kk / kQK;
-  const int u = (int)((kk / kQ81) & 7), q = (int)((kk / 8) & 3);
-  const int64_t t = c / kXqCols;
-  const int j = (int)(c % kXqCols);
-  const int64_t unit = t * nb + b;
+__device__ __forceinline__ void xh_store(uint8_t* y, int k, int c, int kk, int nct, uint32_t lo, uint32_t hi, float d,
+                                         float xsum) {
+  const int nb = k / kQK;
+  const int b = kk / kQK;
+  const int u = (kk / kQ81) & 7, q = (kk / 8) & 3;
+  const int t = c / kXqCols, j = c % kXqCols;
+  const int64_t unit = (int64_t)t * nb + b;
   uint32_t h[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
@@ -166,7 +166,6 @@ __device__ __forceinline__ void xh_store(uint8_t* y, int64_t k, int64_t c, int64
   }
   *(uint4*)(y + unit * kXhUnit + 1024 * u + 16 * (16 * q + j)) = make_uint4(h[0], h[1], h[2], h[3]);
   if (q == 0) {
-    const int64_t nct = total / per_row / kXqCols;
     uint8_t* sc = y + xh_scale_base(nct, nb) + unit * kXhScaleUnit + 32 * j + 4 * u;
     const float dd = DS4 ? half_bits_to_float(__half_as_ushort(__float2half_rn(d))) : d;
     *(float*)sc = dd;
@@ -174,14 +173,14 @@ __device__ __forceinline__ void xh_store(uint8_t* y, int64_t k, int64_t c, int64
   }
 }
 
+// Thread (x, y) of the grid: values 8 x .. 8 x + 7 of activation row c0 + y (rows past n, the last
+// column tile's padding, quantise zeros). k % 32 == 0, so a slice's four threads exit together.
 template <int DT, bool VEC, bool DS4, bool XH = false>
-__global__ void __launch_bounds__(256) quantize_xq_kernel(const void* __restrict__ x, uint8_t* __restrict__ y,
-                                                          int64_t k, int64_t s01, int n, int64_t total) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= total) return;  // total % 4 == 0: whole slices exit together
-  const int64_t per_row = k / 8;
-  const int64_t c = i / per_row;
-  const int64_t kk = (i - c * per_row) * 8;
+__global__ void __launch_bounds__(256) quantize_xq_kernel(const void* __restrict__ x, uint8_t* __restrict__ y, int k,
+                                                          int64_t s01, int n, int nct, int c0) {
+  const int kk = ((int)blockIdx.x * 256 + (int)threadIdx.x) * 8;
+  if (kk >= k) return;
+  const int c = c0 + (int)blockIdx.y;
   float v[8];
   if (c < n) {
 #pragma unroll
@@ -225,23 +224,21 @@ __global__ void __launch_bounds__(256) quantize_xq_kernel(const void* __restrict
     b += __shfl_xor(b, 1, 64);
     xsum = a + b;
   }
-  if constexpr (XH) xh_store<DS4>(y, k, c, kk, total, lo, hi, d, xsum);
-  else xq_store<VEC, DS4>(y, k, c, kk, total, lo, hi, d, qsum, xsum);
+  if constexpr (XH) xh_store<DS4>(y, k, c, kk, nct, lo, hi, d, xsum);
+  else xq_store<VEC, DS4>(y, k, c, kk, nct, lo, hi, d, qsum, xsum);
 }
 
 // block_q8_1 bytes of X (a caller's x_q8) -> the xq layout with the same values and fp16 scales.
 template <bool DS4>
 __global__ void __launch_bounds__(256) q8_1_to_xq_kernel(const uint8_t* __restrict__ q8, uint8_t* __restrict__ y,
-                                                         int64_t k, int n, int64_t total) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= total) return;
-  const int64_t per_row = k / 8;
-  const int64_t c = i / per_row;
-  const int64_t kk = (i - c * per_row) * 8;
+                                                         int k, int n, int nct, int c0) {
+  const int kk = ((int)blockIdx.x * 256 + (int)threadIdx.x) * 8;
+  if (kk >= k) return;
+  const int c = c0 + (int)blockIdx.y;
   uint32_t lo = 0, hi = 0;
   float d = 0.0f;
   if (c < n) {
-    const uint8_t* blk = q8 + (c * (k / kQ81) + kk / kQ81) * 36;
+    const uint8_t* blk = q8 + ((int64_t)c * (k / kQ81) + kk / kQ81) * 36;
     const uint32_t* qv = (const uint32_t*)(blk + 4 + (kk % kQ81));
     lo = qv[0];
     hi = qv[1];
@@ -250,7 +247,7 @@ __global__ void __launch_bounds__(256) q8_1_to_xq_kernel(const uint8_t* __restri
   int qsum = dot4((int)lo, 0x01010101, dot4((int)hi, 0x01010101, 0));
   qsum += __shfl_xor(qsum, 1, 64);
   qsum += __shfl_xor(qsum, 2, 64);
-  xq_store<true, DS4>(y, k, c, kk, total, lo, hi, d, qsum, 0.0f);
+  xq_store<true, DS4>(y, k, c, kk, nct, lo, hi, d, qsum, 0.0f);
 }
 
 // X [n, k] -> the xq layout at y (xq_bytes(n, k) bytes) for weights of ggml type `type`; vec:
@@ -258,10 +255,13 @@ __global__ void __launch_bounds__(256) q8_1_to_xq_kernel(const uint8_t* __restri
 hipError_t launch_quantize_xq(const void* x, int dtype, int64_t n, int64_t k, int64_t s01, int type, bool vec,
                               void* y, hipStream_t stream) {
   if (n == 0) return hipSuccess;
-  const int64_t total = xq_col_tiles(n) * kXqCols * (k / 8);
-  const unsigned blocks = (unsigned)((total + 255) / 256);
+  const int nct = (int)xq_col_tiles(n), rows = nct * kXqCols;
+  const unsigned gx = (unsigned)((k / 8 + 255) / 256);
   const bool ds4 = type == kQ4_K;
-#define GGUF_QXQ(DT, V, D) quantize_xq_kernel<DT, V, D><<<blocks, 256, 0, stream>>>(x, (uint8_t*)y, k, s01, (int)n, total)
+  for (int c0 = 0; c0 < rows; c0 += kQuantRowsPerLaunch) {
+    const dim3 grid(gx, (unsigned)std::min(rows - c0, kQuantRowsPerLaunch));
+#define GGUF_QXQ(DT, V, D) \
+  quantize_xq_kernel<DT, V, D><<<grid, 256, 0, stream>>>(x, (uint8_t*)y, (int)k, s01, (int)n, nct, c0)
 #define GGUF_QXQ_DT(DT)                          \
   if (vec) {                                     \
     if (ds4) GGUF_QXQ(DT, true, true);           \
@@ -270,13 +270,14 @@ hipError_t launch_quantize_xq(const void* x, int dtype, int64_t n, int64_t k, in
     if (ds4) GGUF_QXQ(DT, false, true);          \
     else GGUF_QXQ(DT, false, false);             \
   }
-  switch (dtype) {
-    case kF32: GGUF_QXQ_DT(kF32) break;
-    case kF16: GGUF_QXQ_DT(kF16) break;
-    default: GGUF_QXQ_DT(kBF16) break;
-  }
+    switch (dtype) {
+      case kF32: GGUF_QXQ_DT(kF32) break;
+      case kF16: GGUF_QXQ_DT(kF16) break;
+      default: GGUF_QXQ_DT(kBF16) break;
+    }
 #undef GGUF_QXQ_DT
 #undef GGUF_QXQ
+  }
   return hipGetLastError();
 }
 
@@ -284,28 +285,38 @@ hipError_t launch_quantize_xq(const void* x, int dtype, int64_t n, int64_t k, in
 hipError_t launch_quantize_xh(const void* x, int dtype, int64_t n, int64_t k, int64_t s01, int type, void* y,
                               hipStream_t stream) {
   if (n == 0) return hipSuccess;
-  const int64_t total = xq_col_tiles(n) * kXqCols * (k / 8);
-  const unsigned blocks = (unsigned)((total + 255) / 256);
+  const int nct = (int)xq_col_tiles(n), rows = nct * kXqCols;
+  const unsigned gx = (unsigned)((k / 8 + 255) / 256);
   const bool ds4 = type == kQ4_K;
-#define GGUF_QXH(DT)                                                                                          \
-  if (ds4) quantize_xq_kernel<DT, false, true, true><<<blocks, 256, 0, stream>>>(x, (uint8_t*)y, k, s01, (int)n, total); \
-  else quantize_xq_kernel<DT, false, false, true><<<blocks, 256, 0, stream>>>(x, (uint8_t*)y, k, s01, (int)n, total);
-  switch (dtype) {
-    case kF32: GGUF_QXH(kF32) break;
-    case kF16: GGUF_QXH(kF16) break;
-    default: GGUF_QXH(kBF16) break;
-  }
+  for (int c0 = 0; c0 < rows; c0 += kQuantRowsPerLaunch) {
+    const dim3 grid(gx, (unsigned)std::min(rows - c0, kQuantRowsPerLaunch));
+#define GGUF_QXH(DT)                                                                                               \
+  if (ds4)                                                                                                         \
+    quantize_xq_kernel<DT, false, true, true><<<grid, 256, 0, stream>>>(x, (uint8_t*)y, (int)k, s01, (int)n, nct, c0); \
+  else                                                                                                             \
+    quantize_xq_kernel<DT, false, false, true><<<grid, 256, 0, stream>>>(x, (uint8_t*)y, (int)k, s01, (int)n, nct, c0);
+    switch (dtype) {
+      case kF32: GGUF_QXH(kF32) break;
+      case kF16: GGUF_QXH(kF16) break;
+      default: GGUF_QXH(kBF16) break;
+    }
 #undef GGUF_QXH
+  }
   return hipGetLastError();
 }
 
 // block_q8_1 of X [n, k] -> the xq layout at y.
 hipError_t launch_q8_1_to_xq(const void* q8, int64_t n, int64_t k, int type, void* y, hipStream_t stream) {
   if (n == 0) return hipSuccess;
-  const int64_t total = xq_col_tiles(n) * kXqCols * (k / 8);
-  const unsigned blocks = (unsigned)((total + 255) / 256);
-  if (type == kQ4_K) q8_1_to_xq_kernel<true><<<blocks, 256, 0, stream>>>((const uint8_t*)q8, (uint8_t*)y, k, (int)n, total);
-  else q8_1_to_xq_kernel<false><<<blocks, 256, 0, stream>>>((const uint8_t*)q8, (uint8_t*)y, k, (int)n, total);
+  const int nct = (int)xq_col_tiles(n), rows = nct * kXqCols;
+  const unsigned gx = (unsigned)((k / 8 + 255) / 256);
+  for (int c0 = 0; c0 < rows; c0 += kQuantRowsPerLaunch) {
+    const dim3 grid(gx, (unsigned)std::min(rows - c0, kQuantRowsPerLaunch));
+    if (type == kQ4_K)
+      q8_1_to_xq_kernel<true><<<grid, 256, 0, stream>>>((const uint8_t*)q8, (uint8_t*)y, (int)k, (int)n, nct, c0);
+    else
+      q8_1_to_xq_kernel<false><<<grid, 256, 0, stream>>>((const uint8_t*)q8, (uint8_t*)y, (int)k, (int)n, nct, c0);
+  }
   return hipGetLastError();
 }
 
