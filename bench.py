@@ -22,6 +22,8 @@ benchmark configs under "configs": the CPU-path Q4_K 4096x4096 case next to its 
 small GEMM (IQ3_S / IQ4_XS / Q6_K at M = 4..48 on the attention shapes), the prefill GEMM
 (M = 512..8192, with MFMA utilisation), the six types served by the generic kernels at the gate/up
 shape, and the 64-layer decoder sweep under one CUDA graph with a replay bit-exactness check.
+Under "eager": the headline op called eagerly (no graph) at M = 1 and a 512-row prefill chunk, with
+the host's time per call.
 
 `traffic` (HBM bytes per launch of the dominant kernel) is read from the committed PMC summary
 profiles/gemv_iq3s_stream_17408x5120_m1.traffic.json when present (null otherwise). That summary
@@ -383,6 +385,44 @@ def dominant_kernel(torch, C, ws, steps):
             "us_per_launch": round(kernel_us, 3), "alg_bytes_per_launch": alg_bytes}
 
 
+def eager_calls(torch, C, ws, rows, k, ms=(1, 512), calls=200, reps=5):
+    """The op called eagerly (no graph), as under enforce_eager or in prefill chunks, cycling through
+    the weight copies ws as the timed graphs do:
+    `us_per_call` is the time per call of a run of calls issued back to back (one synchronize at
+    the end), `host_issue_us` the host's time to issue one call of that run (torch dispatch, the
+    op's views and guards, the caching-allocator allocations, the launches), `call_sync_us` one call
+    followed by a synchronize. With host_issue_us below the graph-replayed kernel time, eager calls
+    keep the GPU busy."""
+    out = []
+    for m in ms:
+        op = C.lcpp_mul_mat_vec_iq3_mma_packed if m <= 32 else C.lcpp_mul_mat_iq3_packed
+        x = torch.randn(m, k, device="cuda", dtype=torch.bfloat16)
+        for i in range(20):
+            op(ws[i % len(ws)], x, IQ3_S, rows)
+        runs, issue, sync = [], [], []
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for i in range(calls):
+                op(ws[i % len(ws)], x, IQ3_S, rows)
+            t1 = time.perf_counter()
+            torch.cuda.synchronize()
+            t2 = time.perf_counter()
+            issue.append((t1 - t0) / calls)
+            runs.append((t2 - t0) / calls)
+        for i in range(10 * reps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            op(ws[i % len(ws)], x, IQ3_S, rows)
+            torch.cuda.synchronize()
+            sync.append(time.perf_counter() - t0)
+        out.append({"shape": f"{rows}x{k}", "m": m, "op": "lcpp_mul_mat_vec_iq3_mma_packed" if m <= 32
+                    else "lcpp_mul_mat_iq3_packed", "us_per_call": round(statistics.median(runs) * 1e6, 2),
+                    "host_issue_us": round(statistics.median(issue) * 1e6, 2),
+                    "call_sync_us": round(statistics.median(sync) * 1e6, 2)})
+    return out
+
+
 def copy_calibration(torch):
     """A plain elementwise map over COPY_BYTES (torch.neg, float32 in, float32 out: COPY_BYTES read,
     COPY_BYTES written), three launches, so that a PMC run can read what FETCH_SIZE / WRITE_SIZE
@@ -478,6 +518,7 @@ def main():
                        "gbps": round(cb / (us * 1e-6) / 1e9, 1), "frac_hbm": round(cb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 3)})
 
     roofline = dominant_kernel(torch, C, weights[(17408, 5120)], args.steps)
+    eager = eager_calls(torch, C, weights[(17408, 5120)], 17408, 5120)
     del weights
     torch.cuda.empty_cache()
 
@@ -516,6 +557,7 @@ def main():
                    "calls_per_step": sum(n for *_, n, _ in per_case), "bytes_per_step": step_bytes},
         "detail": detail,
         "roofline": roofline,
+        "eager": eager,
         "cpu_baseline": cpu,
         "points": points,
         "configs": configs,

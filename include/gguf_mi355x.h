@@ -93,6 +93,20 @@ GGUF_API int gguf_mul_mat(int op, const gguf_view* W, const gguf_view* X, int64_
                  const gguf_view* x_q8, void* y, size_t y_bytes, void* workspace, size_t workspace_bytes,
                  void* stream);
 
+/* The caller's allocator for gguf_mul_mat_alloc: device memory of `bytes` bytes on X's device,
+ * 16-byte aligned, for the output (what = GGUF_ALLOC_OUTPUT; bytes may be 0) or the workspace
+ * (GGUF_ALLOC_WORKSPACE), or NULL on failure. It must stay valid until the product's launches have
+ * run on `stream`. */
+enum { GGUF_ALLOC_OUTPUT = 0, GGUF_ALLOC_WORKSPACE = 1 };
+typedef void* (*gguf_alloc_fn)(void* ctx, int what, size_t bytes);
+
+/* gguf_mul_mat that takes its output and workspace from the caller's allocator once the guards
+ * have passed: the order of the reference's run() (lcpp_shim.cu:767-805: the guards, then the
+ * output from torch's allocator, then the launches), with one guard pass per call. The output is
+ * asked for first, also when X has no rows; the workspace only when the plan needs one. */
+GGUF_API int gguf_mul_mat_alloc(int op, const gguf_view* W, const gguf_view* X, int64_t type, int64_t row,
+                                const gguf_view* x_q8, gguf_alloc_fn alloc, void* alloc_ctx, void* stream);
+
 /* Bytes of the static per-GPU scratch that gguf_mul_mat_noalloc uses as its workspace. */
 #define GGUF_SCRATCH_BYTES ((size_t)8 << 20)
 GGUF_API size_t gguf_scratch_bytes(void);

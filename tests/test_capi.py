@@ -19,7 +19,7 @@ def _declared():
 
 def test_header_declares_the_op_surface():
     names = _declared()
-    assert len(names) == 20
+    assert len(names) == 21
     for op in _capi.OPS:
         assert "gguf_" + op in names
     assert "gguf_lcpp_quantize_q8_1" in names
@@ -101,3 +101,27 @@ def test_noalloc_entry_guards_without_a_gpu(lib):
                                   Y.data_ptr(), Y.numel() * 2, None)
     assert rc == _capi.GGUF_EINVAL
     assert _capi.error(lib) == "lcpp_mul_mat_vec_iq3_mma_packed: W and X must be CUDA tensors"
+
+
+def test_alloc_entry_guards_before_allocating(lib):
+    """gguf_mul_mat_alloc runs the guards once, before it asks the caller's allocator for anything:
+    a rejected call (bad row, then host views) never reaches the allocator."""
+    import torch
+
+    asked = []
+
+    @_capi.ALLOC_FN
+    def alloc(ctx, what, nbytes):
+        asked.append((what, nbytes))
+        return None
+
+    W = torch.zeros(32, 2200, dtype=torch.uint8)
+    X = torch.zeros(2, 5120, dtype=torch.bfloat16)
+    wv, xv = _capi.view(W), _capi.view(X)
+    rc = lib.gguf_mul_mat_alloc(6, _capi.ref(wv), _capi.ref(xv), 21, 24, None, alloc, None, None)
+    assert rc == _capi.GGUF_EINVAL
+    assert "must be a multiple of 16" in _capi.error(lib)
+    rc = lib.gguf_mul_mat_alloc(6, _capi.ref(wv), _capi.ref(xv), 21, 32, None, alloc, None, None)
+    assert rc == _capi.GGUF_EINVAL
+    assert _capi.error(lib) == "lcpp_mul_mat_vec_iq3_mma_packed: W and X must be CUDA tensors"
+    assert asked == []

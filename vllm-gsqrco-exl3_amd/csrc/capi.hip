@@ -302,11 +302,14 @@ size_t gguf_op_workspace_bytes(int op, int64_t type, int64_t row, int64_t k, int
   return has_x_q8 ? 0 : align256(gguf_q8_1_bytes(n, k, 0));
 }
 
-int gguf_mul_mat(int op, const gguf_view* W, const gguf_view* X, int64_t type, int64_t row, const gguf_view* x_q8,
-                 void* y, size_t y_bytes, void* workspace, size_t workspace_bytes, void* stream) {
-  g_err.clear();
-  const int64_t k = check_op(op, W, X, type, row, x_q8);
-  if (k < 0) return GGUF_EINVAL;
+}  // extern "C"
+
+namespace {
+
+// One product whose guards have passed (check_op returned k): the buffer checks, the plan and the
+// launches. Every entry point runs the guards once and then this.
+int run_checked(int op, const gguf_view* W, const gguf_view* X, int64_t type, int64_t row, const gguf_view* x_q8,
+                int64_t k, void* y, size_t y_bytes, void* workspace, size_t workspace_bytes, void* stream) {
   const char* name = op_name(op);
   const int64_t n = X->size[0];
   if (n == 0) return GGUF_OK;
@@ -416,6 +419,41 @@ int gguf_mul_mat(int op, const gguf_view* W, const gguf_view* X, int64_t type, i
   return GGUF_OK;
 }
 
+}  // namespace
+
+extern "C" {
+
+int gguf_mul_mat(int op, const gguf_view* W, const gguf_view* X, int64_t type, int64_t row, const gguf_view* x_q8,
+                 void* y, size_t y_bytes, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err.clear();
+  const int64_t k = check_op(op, W, X, type, row, x_q8);
+  if (k < 0) return GGUF_EINVAL;
+  return run_checked(op, W, X, type, row, x_q8, k, y, y_bytes, workspace, workspace_bytes, stream);
+}
+
+int gguf_mul_mat_alloc(int op, const gguf_view* W, const gguf_view* X, int64_t type, int64_t row,
+                       const gguf_view* x_q8, gguf_alloc_fn alloc, void* alloc_ctx, void* stream) {
+  g_err.clear();
+  const int64_t k = check_op(op, W, X, type, row, x_q8);
+  if (k < 0) return GGUF_EINVAL;
+  const char* name = op_name(op);
+  if (!alloc) return fail("%s: no allocator given", name);
+  const int64_t n = X->size[0];
+  const size_t y_bytes = (size_t)(n * row * elem_size(X->dtype));
+  void* y = alloc(alloc_ctx, GGUF_ALLOC_OUTPUT, y_bytes);
+  if (!y && y_bytes) return fail("%s: the allocator returned no output buffer", name);
+  if (n == 0) return GGUF_OK;
+  const DeviceScope scope(X->device);
+  if (scope.err != hipSuccess) return hip_fail(scope.err, name, "device select");
+  const size_t need = gguf_op_workspace_bytes(op, type, row, k, n, x_q8 != nullptr);
+  void* ws = nullptr;
+  if (need) {
+    ws = alloc(alloc_ctx, GGUF_ALLOC_WORKSPACE, need);
+    if (!ws) return fail("%s: the allocator returned no workspace", name);
+  }
+  return run_checked(op, W, X, type, row, x_q8, k, y, y_bytes, ws, need, stream);
+}
+
 }  // extern "C"
 
 namespace {
@@ -468,7 +506,7 @@ int gguf_mul_mat_noalloc(int op, const gguf_view* W, const gguf_view* X, int64_t
   void* ws = nullptr;
   const hipError_t e = scratch_address(X->device, &ws);
   if (e != hipSuccess) return hip_fail(e, name, "scratch address");
-  return gguf_mul_mat(op, W, X, type, row, x_q8, y, y_bytes, ws, kScratchBytes, stream);
+  return run_checked(op, W, X, type, row, x_q8, k, y, y_bytes, ws, kScratchBytes, stream);
 }
 
 #define GGUF_OP_Q8(fn, OP)                                                                                    \

@@ -14,6 +14,7 @@
 #include <c10/hip/HIPStream.h>
 #include <torch/library.h>
 
+#include <exception>
 #include <optional>
 
 #include "../../include/gguf_mi355x.h"
@@ -49,8 +50,32 @@ void* stream_of(const at::Tensor& t) {
   return t.is_cuda() ? (void*)c10::hip::getCurrentHIPStream(t.get_device()).stream() : nullptr;
 }
 
-// One product through gguf_mul_mat. The guards run first (host only), then the output and the
-// workspace are allocated, then the library launches on the current stream.
+// The output and workspace tensors of one product, made by the library's allocator callback once
+// its guards have passed. A failed allocation (torch raises) is kept and raised after the call.
+struct OpAlloc {
+  const at::Tensor& X;
+  int64_t row;
+  at::Tensor y, ws;
+  std::exception_ptr err;
+};
+
+void* op_alloc(void* ctx, int what, size_t bytes) {
+  OpAlloc& a = *static_cast<OpAlloc*>(ctx);
+  try {
+    if (what == GGUF_ALLOC_OUTPUT) {
+      a.y = at::empty({a.X.size(0), a.row}, a.X.options());
+      return a.y.numel() ? a.y.data_ptr() : nullptr;
+    }
+    a.ws = at::empty({(int64_t)bytes}, a.X.options().dtype(at::kByte));
+    return a.ws.data_ptr();
+  } catch (...) {
+    a.err = std::current_exception();
+    return nullptr;
+  }
+}
+
+// One product through gguf_mul_mat_alloc: the guards (host only, once), then the output and the
+// workspace from torch's caching allocator, then the launches on the current stream.
 at::Tensor mul_mat(int op, const at::Tensor& W, const at::Tensor& X, int64_t type, int64_t row,
                    const std::optional<at::Tensor>& x_q8) {
   const gguf_view wv = make_view(W), xv = make_view(X);
@@ -60,17 +85,11 @@ at::Tensor mul_mat(int op, const at::Tensor& W, const at::Tensor& X, int64_t typ
     qv = make_view(*x_q8);
     qp = &qv;
   }
-  if (gguf_check_op(op, &wv, &xv, type, row, qp) != GGUF_OK) raise_last();
-  const int64_t n = X.size(0), k = X.size(1);
-  at::Tensor y = at::empty({n, row}, X.options());
-  if (n == 0) return y;
-  const size_t wsb = gguf_op_workspace_bytes(op, type, row, k, n, qp != nullptr);
-  at::Tensor ws;
-  if (wsb) ws = at::empty({(int64_t)wsb}, X.options().dtype(at::kByte));
-  const int rc = gguf_mul_mat(op, &wv, &xv, type, row, qp, y.data_ptr(), (size_t)(y.numel() * y.element_size()),
-                              wsb ? ws.data_ptr() : nullptr, wsb, stream_of(X));
+  OpAlloc a{X, row, {}, {}, nullptr};
+  const int rc = gguf_mul_mat_alloc(op, &wv, &xv, type, row, qp, &op_alloc, &a, stream_of(X));
+  if (a.err) std::rethrow_exception(a.err);
   if (rc != GGUF_OK) raise_last();
-  return y;
+  return a.y;
 }
 
 template <int OP>

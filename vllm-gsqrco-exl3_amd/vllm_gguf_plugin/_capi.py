@@ -38,7 +38,7 @@ EXPORTS = (
     "gguf_lcpp_mul_mat_vec_iq3_mma", "gguf_lcpp_mul_mat_vec_own", "gguf_lcpp_mul_mat_mma_k",
     "gguf_lcpp_mul_mat_vec_iq3_mma_packed", "gguf_lcpp_mul_mat_iq3_packed", "gguf_q8_1_bytes",
     "gguf_lcpp_quantize_q8_1", "gguf_iq3_pack_scratch_bytes", "gguf_iq3_pack", "gguf_scratch_bytes",
-    "gguf_mul_mat_noalloc", "gguf_dense_mul_mat",
+    "gguf_mul_mat_noalloc", "gguf_dense_mul_mat", "gguf_mul_mat_alloc",
 )
 
 
@@ -54,6 +54,10 @@ class View(ctypes.Structure):
         ("device", ctypes.c_int32),
     ]
 
+
+# gguf_alloc_fn: void* (*)(void* ctx, int what, size_t bytes)
+ALLOC_FN = ctypes.CFUNCTYPE(ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t)
+ALLOC_OUTPUT, ALLOC_WORKSPACE = 0, 1
 
 _lib = None
 
@@ -83,6 +87,7 @@ def load():
     lib.gguf_scratch_bytes.restype = SZ
     lib.gguf_mul_mat_noalloc.argtypes = [I32, P, P, I64, I64, P, VP, SZ, VP]
     lib.gguf_dense_mul_mat.argtypes = [P, P, VP, SZ, VP]
+    lib.gguf_mul_mat_alloc.argtypes = [I32, P, P, I64, I64, P, ALLOC_FN, VP, VP]
     _lib = lib
     return lib
 
