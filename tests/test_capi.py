@@ -68,6 +68,7 @@ def test_workspace_follows_the_product_plan(lib):
     assert lib.gguf_op_workspace_bytes(packed, 21, 17408, 5120, 8, 0) == xq(8, 5120)
     assert lib.gguf_op_workspace_bytes(packed, 21, 17408, 5120, 49, 0) == xq(49, 5120)
     assert lib.gguf_op_workspace_bytes(packed, 21, 1024, 5120, 48, 0) == xq(48, 5120)
+    assert lib.gguf_op_workspace_bytes(packed, 21, 6144, 5120, 48, 0) == xq(48, 5120)  # 1.5 tiles per CU
     assert lib.gguf_op_workspace_bytes(mmq, 12, 17408, 5120, 32, 0) == xh(32, 5120)
     assert lib.gguf_op_workspace_bytes(mmq, 12, 17408, 5120, 16, 0) == xq(16, 5120)
     assert lib.gguf_op_workspace_bytes(packed, 21, 17408, 5120, 64, 0) == xh(64, 5120)

@@ -239,13 +239,13 @@ def test_small_fp16_vs_q81_with_zero_blocks(qt, tiles, n):
 # Product ops of up to 48 activation rows (IQ3_S from 33, Q4_K from 17) on weights of 1..5 row tiles
 # per CU run the fp16 small GEMM's range plan: one workgroup per CU over its run of row tiles (300
 # tiles: runs of 1 or 2; 1100: 4 or 5; 1280: 5), all column tiles in the workgroup.
-RANGE_ROWS = {o.IQ3_S: (16 * 300, 16 * 1100, 16 * 1280), o.Q4_K: (16 * 300 + 9, 16 * 1100, 16 * 1280)}
+RANGE_ROWS = {o.IQ3_S: (16 * 1030, 16 * 1100, 16 * 1280), o.Q4_K: (16 * 1030 + 9, 16 * 1100, 16 * 1280)}
 RANGE_N = {o.IQ3_S: [33, 40, 48], o.Q4_K: [17, 32, 33, 48]}
 
 
 @pytest.mark.parametrize("qt,n", [(qt, n) for qt in (o.IQ3_S, o.Q4_K) for n in RANGE_N[qt]],
                          ids=[f"{TN[qt]}-{n}" for qt in (o.IQ3_S, o.Q4_K) for n in RANGE_N[qt]])
-@pytest.mark.parametrize("ri", [0, 1, 2], ids=["runs1-2", "runs4-5", "runs5"])
+@pytest.mark.parametrize("ri", [0, 1, 2], ids=["runs4-5a", "runs4-5b", "runs5"])
 def test_small_fp16_range_exact_integer_dots(lib, qt, ri, n):
     """Exact-integer mode through the range plan (asserted from the op's workspace: the fp16
     activation layout): every output is the oracle's int64 sum of slice dots."""

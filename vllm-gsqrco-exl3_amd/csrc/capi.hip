@@ -272,7 +272,7 @@ bool rows_fused(int op, int64_t type, int64_t row, int64_t k, int64_t n, bool ha
 
 // The MFMA products with K <= 8192 run the fp16 small GEMM (X in the xh layout) for packed IQ3_S
 // and Q4_K from 64 to 255 activation rows, and below 64 rows where its one-workgroup-per-CU range
-// plan applies (1..5 row tiles per CU; 33..48 rows for IQ3_S, 17..48 for Q4_K); the rest below the
+// plan applies (4..5 row tiles per CU; 33..48 rows for IQ3_S, 17..48 for Q4_K); the rest below the
 // prefill rows the int8 small GEMM (xq layout). Measured at the 27B-layer shapes: from 64 rows the fp16 GEMM's
 // shared decode beats re-decoding the weights per group of 4 column tiles (17408 x 5120 IQ3_S,
 // 128 rows: 84 against 134 us); over K = 17408 (68 blocks in one workgroup's loop, 320

@@ -358,15 +358,17 @@ static int small_h_cus() {
 // Types the fp16 small GEMM serves: IQ3_S in the unit layout (packed) and Q4_K rows.
 bool small_h_supported(int type, bool packed) { return packed ? type == kIQ3_S : type == kQ4_K; }
 
-// The range plan: 2..3 column tiles on weights of between one and kRangeTiles row tiles per CU:
-// every CU's workgroup decodes its 4-5 tiles once per block for all columns and reads X once.
-// Measured at 17408 x 5120 (op level, quantise included) against the int8 small GEMM: IQ3_S
-// packed 48 rows 42.9 against 50.1 us, 32 rows 40.2 against 39.3; Q4_K 48 rows 41.8 against 66.8,
-// 32 rows 39.6 against 51.4, 16 rows 36.8 against 28.7 (one column tile stays on the int8 GEMM).
+// The range plan: 2..3 column tiles on weights of 4 to kRangeTiles row tiles per CU: every CU's
+// workgroup decodes its 4-5 tiles once per block for all columns and reads X once. Measured at
+// 17408 x 5120 (op level, quantise included) against the int8 small GEMM: IQ3_S packed 48 rows
+// 42.9 against 50.1 us, 32 rows 40.2 against 39.3; Q4_K 48 rows 41.8 against 66.8, 32 rows 39.6
+// against 51.4, 16 rows 36.8 against 28.7 (one column tile stays on the int8 GEMM). With fewer
+// tiles per CU the int8 GEMM's grid is the faster one: 6144 x 5120 (1.5 tiles per CU), IQ3_S 48
+// rows 39.8 us on the range plan against 19.0 us for 32 rows on the int8 GEMM.
 bool small_h_range(int type, int64_t nrows, int64_t n) {
   const int64_t tiles = (nrows + 15) / 16, cus = small_h_cus();
   const int64_t from = type == kIQ3_S ? 33 : 17;
-  return n >= from && n <= 3 * 16 && tiles >= cus && tiles <= kRangeTiles * cus;
+  return n >= from && n <= 3 * 16 && tiles >= 4 * cus && tiles <= kRangeTiles * cus;
 }
 
 // xh: X in the xh layout (launch_quantize_xh / launch_q8_1_to_xh). The range plan where it
