@@ -15,7 +15,8 @@ synchronize on each side. `value` is the whole-job algorithmic throughput (weigh
 per call) in GB/s.
 
 Also reported: the dominant kernel's roofline (the packed decode GEMV kernel at 17408 x 5120,
-M = 1, which quantises X itself, timed alone), the metric's other points (IQ3_S and Q4_K at
+M = 1, which quantises X itself, timed alone, with the per-launch floor of as many graph-replayed
+launches of a 512 KB fill beside it), the metric's other points (IQ3_S and Q4_K at
 M = 1, 4, 16, 32, 48 on 17408 x 5120, each through the routing table's op), and the CPU oracle
 (numpy dequantise + torch fp32 matmul) timed on the host cores on a bounded sample; and the other
 benchmark configs under "configs": the CPU-path Q4_K 4096x4096 case next to its GPU op, the MTP
@@ -379,10 +380,15 @@ def dominant_kernel(torch, C, ws, steps):
     kernel_us = time_graphs(torch, [kg], max(5, steps)) * 1e3 / len(ws)
     alg_bytes = ws[0].numel() + m * k * 2 + m * rows * 2
     achieved = alg_bytes / (kernel_us * 1e-6) / 1e9
+    # the per-launch floor of back-to-back graph launches: as many launches of a 512 KB fill
+    t = torch.empty(131072, device="cuda", dtype=torch.float32)
+    fg = graph(torch, [lambda: t.fill_(0.0) for _ in ws])
+    floor_us = time_graphs(torch, [fg], max(5, steps)) * 1e3 / len(ws)
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic(),
             "kernel": "gemv_iq3s_stream_kernel<1,bf16,2> (17408x5120, M=1, X quantised in the kernel)",
-            "us_per_launch": round(kernel_us, 3), "alg_bytes_per_launch": alg_bytes}
+            "us_per_launch": round(kernel_us, 3), "alg_bytes_per_launch": alg_bytes,
+            "launch_floor_us": round(floor_us, 3)}
 
 
 def eager_calls(torch, C, ws, rows, k, ms=(1, 512), calls=200, reps=5):
