@@ -325,8 +325,8 @@ __device__ __forceinline__ void xgroup_q8_store(const XGroupQ8& r, int g, bool l
   float sum = 0.0f;
   if constexpr (SUMS != kSumNone) {
     int t = dot4(0x01010101, (int)r.q1, dot4(0x01010101, (int)r.q0, 0));
-    t += __builtin_amdgcn_mov_dpp(t, 0xB1, 0xF, 0xF, false);  // quad xor 1: this half's sum
-    const int o = __builtin_amdgcn_mov_dpp(t, 0x4E, 0xF, 0xF, false);  // quad xor 2: the other half's
+    t += __builtin_amdgcn_update_dpp(0, t, 0xB1, 0xF, 0xF, true);  // quad xor 1: this half's sum
+    const int o = __builtin_amdgcn_update_dpp(0, t, 0x4E, 0xF, 0xF, true);  // quad xor 2: the other half's
     if constexpr (SUMS == kSumSlice) sum = (float)(t + o);
     else sum = __uint_as_float(((uint32_t)t & 0xFFFFu) | ((uint32_t)o << 16));
   }
@@ -631,9 +631,9 @@ __global__ void __launch_bounds__(64 * WPT) gemv_rows_kernel(const uint8_t* __re
 #pragma unroll
         for (int cc = 0; cc < NC; ++cc) {
           float v = acc[i][cc];
-          v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));   // xor 1
-          v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));   // xor 2
-          v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false));  // 7 - lane
+          v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, true));   // xor 1
+          v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, true));   // xor 2
+          v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, true));  // 7 - lane
           if (c == 0) red[it & 1][wave][cc][8 * i + r] = v;
           acc[i][cc] = 0.0f;
         }

@@ -327,7 +327,9 @@ __device__ __forceinline__ void xgroup_store(const XGroup<XDT>& r, int g, bool l
 
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+  // every control used here reads a valid lane; bound_ctrl with old = 0 lets hipcc fold the move
+  // into the add that consumes it (one v_add_f32 with a DPP source)
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
 }
 
 constexpr int kStreamWaves = 8;

@@ -87,8 +87,8 @@ __device__ __forceinline__ void xgroup_load(const void* x, __amdgpu_buffer_rsrc_
 
 // max over the four lanes of a quad, exchanged by DPP quad permutes (xor 1, then xor 2)
 __device__ __forceinline__ float quad_fmax(float v) {
-  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false)));
-  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, true)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, true)));
   return v;
 }
 
