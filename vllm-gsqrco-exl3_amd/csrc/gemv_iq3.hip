@@ -542,13 +542,13 @@ static void launch_stream_k(const uint8_t* W, int64_t row_bytes, int nrows, int 
 }
 
 template <int NC, int XDT>
-static void launch_stream_nc(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x, int64_t s01,
-                             void* y, int y_dtype, hipStream_t stream) {
+static hipError_t launch_stream_nc(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x,
+                                   int64_t s01, void* y, int y_dtype, hipStream_t stream) {
   const int need = (NC * (k / kQ81) * 4 + 64 * kStreamWaves - 1) / (64 * kStreamWaves);
 #define GGUF_XPT(X)                                                                     \
   if (need <= X) {                                                                      \
     launch_stream_k<NC, XDT, X>(W, row_bytes, nrows, k, x, s01, y, y_dtype, stream);    \
-    return;                                                                             \
+    return hipSuccess;                                                                  \
   }
   if constexpr (XDT >= 0) {  // fused: K <= 8192, at most 4 groups per thread
     GGUF_XPT(1) GGUF_XPT(2) GGUF_XPT(3) GGUF_XPT(4)
@@ -557,17 +557,19 @@ static void launch_stream_nc(const uint8_t* W, int64_t row_bytes, int nrows, int
     GGUF_XPT(24)
   }
 #undef GGUF_XPT
+  return hipErrorInvalidValue;  // no instantiation stages this much of X (stream_supported excludes it)
 }
 
 template <int XDT>
-static void launch_stream(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x, int64_t s01, int n,
-                          void* y, int y_dtype, hipStream_t stream) {
-  if (n == 1) launch_stream_nc<1, XDT>(W, row_bytes, nrows, k, x, s01, y, y_dtype, stream);
-  else if (n == 2) launch_stream_nc<2, XDT>(W, row_bytes, nrows, k, x, s01, y, y_dtype, stream);
-  else if constexpr (XDT < 0) {
-    if (n == 3) launch_stream_nc<3, XDT>(W, row_bytes, nrows, k, x, s01, y, y_dtype, stream);
-    else launch_stream_nc<4, XDT>(W, row_bytes, nrows, k, x, s01, y, y_dtype, stream);
+static hipError_t launch_stream(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x, int64_t s01,
+                                int n, void* y, int y_dtype, hipStream_t stream) {
+  if (n == 1) return launch_stream_nc<1, XDT>(W, row_bytes, nrows, k, x, s01, y, y_dtype, stream);
+  if (n == 2) return launch_stream_nc<2, XDT>(W, row_bytes, nrows, k, x, s01, y, y_dtype, stream);
+  if constexpr (XDT < 0) {
+    if (n == 3) return launch_stream_nc<3, XDT>(W, row_bytes, nrows, k, x, s01, y, y_dtype, stream);
+    if (n == 4) return launch_stream_nc<4, XDT>(W, row_bytes, nrows, k, x, s01, y, y_dtype, stream);
   }
+  return hipErrorInvalidValue;
 }
 
 // one 16-row tile per workgroup: 8 waves split K for one or two activation rows, 4 from three on
@@ -597,8 +599,10 @@ static void launch_tile(const uint8_t* W, int64_t row_bytes, int nrows, int k, c
 // nrows % 16 == 0, n in 1..8; q8: block_q8_1 of X.
 hipError_t launch_gemv_packed(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n,
                               void* y, int y_dtype, hipStream_t stream) {
-  if (stream_supported(nrows, k, n, false)) launch_stream<-1>(W, row_bytes, nrows, k, q8, 0, n, y, y_dtype, stream);
-  else if (n <= 2) launch_tile<8, -1>(W, row_bytes, nrows, k, q8, 0, n, y, y_dtype, stream);
+  if (stream_supported(nrows, k, n, false)) {
+    const hipError_t e = launch_stream<-1>(W, row_bytes, nrows, k, q8, 0, n, y, y_dtype, stream);
+    if (e != hipSuccess) return e;
+  } else if (n <= 2) launch_tile<8, -1>(W, row_bytes, nrows, k, q8, 0, n, y, y_dtype, stream);
   else launch_tile<4, -1>(W, row_bytes, nrows, k, q8, 0, n, y, y_dtype, stream);
   return hipGetLastError();
 }
@@ -618,16 +622,28 @@ hipError_t launch_gemv_packed_x(const uint8_t* W, int64_t row_bytes, int nrows, 
   const bool st = stream_supported(nrows, k, n, true);
   switch (x_dtype) {
     case kF32:
-      if (st) launch_stream<kF32>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream);
-      else launch_tile<8, kF32>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream);
+      if (st) {
+        const hipError_t e = launch_stream<kF32>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream);
+        if (e != hipSuccess) return e;
+      } else {
+        launch_tile<8, kF32>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream);
+      }
       break;
     case kF16:
-      if (st) launch_stream<kF16>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream);
-      else launch_tile<8, kF16>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream);
+      if (st) {
+        const hipError_t e = launch_stream<kF16>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream);
+        if (e != hipSuccess) return e;
+      } else {
+        launch_tile<8, kF16>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream);
+      }
       break;
     default:
-      if (st) launch_stream<kBF16>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream);
-      else launch_tile<8, kBF16>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream);
+      if (st) {
+        const hipError_t e = launch_stream<kBF16>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream);
+        if (e != hipSuccess) return e;
+      } else {
+        launch_tile<8, kBF16>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream);
+      }
       break;
   }
   return hipGetLastError();
