@@ -79,6 +79,30 @@ def test_workspace_follows_the_product_plan(lib):
     assert lib.gguf_op_workspace_bytes(mmq, 23, 17408, 5120, 64, 0) == xq(64, 5120)
 
 
+def test_workspace_of_the_split_raw_gemm(lib):
+    """Q4_K / IQ4_XS / Q6_K on the int8 GEMM with fewer than two (16-row tile, column group)
+    workgroups per CU split K over 2 or 4 workgroups where that cuts the rounds of workgroups per
+    CU: the workspace adds a 1 KiB slot per column tile, tile and split, then one counter per tile
+    and column group (256-B aligned). 256 CUs assumed without a GPU."""
+    xq = lambda n, k: -(-n // 16) * (k // 256) * 4608
+    a256 = lambda b: -(-b // 256) * 256
+    mmq, vec = 1, 0
+    # 320 tiles, one column tile, 68 blocks: 4 ways
+    assert lib.gguf_op_workspace_bytes(mmq, 23, 5120, 17408, 16, 0) == xq(16, 17408) + 320 * 4 * 1024 + a256(320 * 4)
+    # 320 tiles, 2 column tiles, 24 blocks: 2 ways
+    assert lib.gguf_op_workspace_bytes(mmq, 14, 5120, 6144, 32, 0) == xq(32, 6144) + 320 * 2 * 2048 + a256(320 * 4)
+    # 64 tiles (under half a workgroup per CU): 4 ways; a decode op at 8 rows likewise
+    assert lib.gguf_op_workspace_bytes(mmq, 14, 1024, 5120, 16, 0) == xq(16, 5120) + 64 * 4 * 1024 + a256(64 * 4)
+    assert lib.gguf_op_workspace_bytes(vec, 14, 1024, 5120, 8, 1) == xq(8, 5120) + 64 * 4 * 1024 + a256(64 * 4)
+    # unsplit: K = 512 (2 blocks); 512+ tiles; 256 workgroups (one round either way); 20 blocks
+    # at 320 or 384 tiles (under 3 blocks per wave for a 2-way split)
+    assert lib.gguf_op_workspace_bytes(mmq, 14, 1024, 512, 16, 0) == xq(16, 512)
+    assert lib.gguf_op_workspace_bytes(mmq, 23, 8192, 5120, 16, 0) == xq(16, 5120)
+    assert lib.gguf_op_workspace_bytes(vec, 23, 4096, 4096, 8, 0) == xq(8, 4096)
+    assert lib.gguf_op_workspace_bytes(mmq, 12, 5120, 5120, 48, 0) == xq(48, 5120)
+    assert lib.gguf_op_workspace_bytes(mmq, 23, 6144, 5120, 32, 0) == xq(32, 5120)
+
+
 def test_guard_call_does_not_need_a_gpu(lib):
     import torch
 

@@ -149,6 +149,84 @@ def test_gemm_vs_q81(qt, n):
     assert o.rel_l2(y, ref) <= 1e-3, o.rel_l2(y, ref)
 
 
+# the int8 raw GEMM with K split over workgroups (grids of fewer than two workgroups per CU):
+# (rows, k, n); 48 x 5120 splits 4 ways, 1000 x 2048 (ragged last tile, 3 column tiles) and
+# 5120 x 6144 2 ways, 64 x 17408 4 ways
+SPLIT_SHAPES = [(48, 5120, 16), (1000, 2048, 33), (5120, 6144, 9), (64, 17408, 48)]
+RAW_TYPES = [o.Q4_K, o.IQ4_XS, o.Q6_K]
+
+
+def _split_ws(lib, op, qt, rows, k, n, has_q8=0):
+    """Asserts that the op's plan splits K: its workspace holds more than the xq copy of X."""
+    xq = -(-n // 16) * (k // 256) * 4608
+    assert lib.gguf_op_workspace_bytes(op, qt, rows, k, n, has_q8) > xq
+
+
+@pytest.mark.parametrize("qt", RAW_TYPES, ids=lambda t: TN[t])
+@pytest.mark.parametrize("rows,k,n", SPLIT_SHAPES, ids=lambda v: str(v))
+def test_split_k_exact_integer_dots(lib, qt, rows, k, n):
+    """Exact-integer mode through the K-split raw GEMM: each split's partial sums and their
+    fixed-order total are integers, so the output equals the oracle's int64 sum exactly."""
+    op = GEMM_OP[qt]
+    _split_ws(lib, _capi_op(op), qt, rows, k, n)
+    raw = _exact_weights(qt, rows, k, seed=300 + rows + n)
+    x = _exact_x(n, k, seed=310 + n, dtype=torch.float32)
+    y = getattr(C(), op)(_dev(raw), x.cuda(), qt, rows).cpu().numpy()
+    np.testing.assert_array_equal(y.astype(np.int64), _exact_ref(raw, qt, x))
+
+
+@pytest.mark.parametrize("qt", RAW_TYPES, ids=lambda t: TN[t])
+@pytest.mark.parametrize("with_q8", [False, True], ids=["x", "x_q8"])
+def test_split_k_decode_op(lib, qt, with_q8):
+    """A decode op at 8 rows on the split GEMM, with X or the caller's q8_1 (converted by the
+    kernel that also clears the split counters): exact-integer output."""
+    rows, k, n = 48, 5120, 8
+    op = "lcpp_mul_mat_vec_q"
+    _split_ws(lib, 0, qt, rows, k, n, int(with_q8))
+    raw = _exact_weights(qt, rows, k, seed=320 + qt)
+    x = _exact_x(n, k, seed=330, dtype=torch.float32).cuda()
+    q8 = C().lcpp_quantize_q8_1(x, qt, False, False) if with_q8 else None
+    y = getattr(C(), op)(_dev(raw), x, qt, rows, q8).cpu().numpy()
+    np.testing.assert_array_equal(y.astype(np.int64), _exact_ref(raw, qt, x.cpu()))
+
+
+@pytest.mark.parametrize("qt", RAW_TYPES, ids=lambda t: TN[t])
+def test_split_k_vs_q81_deterministic_and_graph_replays(lib, qt):
+    """The split GEMM on random weights with zero-d blocks against the q81 model (bf16 bar);
+    repeated calls and graph replays are bit-identical: the counters are cleared on every call
+    and the partial sums are added in split order."""
+    rows, k, n = 1000, 2048, 40
+    op = GEMM_OP[qt]
+    _split_ws(lib, _capi_op(op), qt, rows, k, n)
+    raw = _w(qt, rows, k, seed=340 + qt)
+    b = raw.reshape(rows, k // 256, o.BLOCK_BYTES[qt])
+    zero = np.random.default_rng(341).random((rows, k // 256)) < 0.2
+    for off in o.SCALE_OFFSETS[qt]:
+        b[zero, off:off + 2] = 0
+    x = _x(n, k, seed=342, dtype=torch.bfloat16)
+    w, xc = _dev(raw), x.cuda()
+    f = lambda: getattr(C(), op)(w, xc, qt, rows)
+    y = f()
+    ref = o.q81_model(raw, qt, x, layout="mmq")
+    assert o.rel_l2(y.float().cpu().numpy(), ref) <= TIGHT[torch.bfloat16]
+    for _ in range(3):
+        assert torch.equal(f(), y)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = f()
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, y)
+        assert torch.equal(f(), y)  # eager work between the replays
+
+
+def _capi_op(name):
+    from vllm_gguf_plugin import _capi
+
+    return _capi.OPS[name]
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
 @pytest.mark.parametrize("qt", TYPES, ids=lambda t: TN[t])
 @pytest.mark.parametrize("n", [1, 4, 16])

@@ -28,10 +28,14 @@ hipError_t launch_gemm(int type, const uint8_t* W, int64_t row_bytes, int nrows,
 hipError_t launch_gemv_packed(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n,
                               void* y, int y_dtype, hipStream_t stream);
 hipError_t launch_quantize_xq(const void* x, int dtype, int64_t n, int64_t k, int64_t s01, int type, bool vec,
-                              void* y, hipStream_t stream);
-hipError_t launch_q8_1_to_xq(const void* q8, int64_t n, int64_t k, int type, void* y, hipStream_t stream);
+                              void* y, hipStream_t stream, uint32_t* zero = nullptr, int zero_words = 0);
+hipError_t launch_q8_1_to_xq(const void* q8, int64_t n, int64_t k, int type, void* y, hipStream_t stream,
+                             uint32_t* zero = nullptr, int zero_words = 0);
 hipError_t launch_gemm_xq(int type, const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n,
-                          void* y, int y_dtype, bool mmq, hipStream_t stream);
+                          void* y, int y_dtype, bool mmq, void* split_ws, hipStream_t stream);
+int raw_split(int type, int64_t nrows, int64_t k, int64_t n);
+size_t raw_split_part_bytes(int type, int64_t nrows, int64_t k, int64_t n);
+int raw_split_counters(int type, int64_t nrows, int64_t k, int64_t n);
 hipError_t launch_gemv_packed_x(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x, int x_dtype,
                                 int64_t s01, int n, void* y, int y_dtype, hipStream_t stream);
 bool gemv_rows_supported(int type, int64_t nrows, int64_t row_bytes, int64_t k, int64_t n);
@@ -282,6 +286,21 @@ bool small_fp16(int op, int64_t type, int64_t row, int64_t k, int64_t n) {
   return (n >= 64 && n < kPrefillFrom) || gguf::small_h_range((int)type, row, n);
 }
 
+// The int8 small GEMM on Q4_K / IQ4_XS / Q6_K rows (gemm_raw_kernel): product ops below the
+// prefill rows off the fp16 GEMM's plans, and decode ops from vec_mma_from rows on.
+bool raw_gemm(int op, int64_t type, int64_t row, int64_t k, int64_t n) {
+  if (op_packed(op) || !(type == gguf::kQ4_K || type == gguf::kIQ4_XS || type == gguf::kQ6_K)) return false;
+  if (op_gemm(op)) return n < kPrefillFrom && !small_fp16(op, type, row, k, n);
+  return decode_mma(op, type, row, k, n);
+}
+
+// Bytes after the xq copy of X that a K-split raw GEMM needs (partial sums, then its counters).
+size_t raw_split_ws(int op, int64_t type, int64_t row, int64_t k, int64_t n) {
+  if (!raw_gemm(op, type, row, k, n) || gguf::raw_split((int)type, row, k, n) == 1) return 0;
+  return gguf::raw_split_part_bytes((int)type, row, k, n) +
+         align256((size_t)gguf::raw_split_counters((int)type, row, k, n) * sizeof(uint32_t));
+}
+
 }  // namespace
 
 size_t gguf_op_workspace_bytes(int op, int64_t type, int64_t row, int64_t k, int64_t n, int has_x_q8) {
@@ -295,9 +314,10 @@ size_t gguf_op_workspace_bytes(int op, int64_t type, int64_t row, int64_t k, int
     if (!mmq_layout && ((n >= kPrefillFrom && gguf::prefill_uses_xh((int)type, op_packed(op))) ||
                         small_fp16(op, type, row, k, n)))
       return align256(gguf::xh_bytes(n, k));
-    return align256(mmq_layout ? gguf_q8_1_bytes(n, k, 1) : gguf::xq_bytes(n, k));
+    return align256(mmq_layout ? gguf_q8_1_bytes(n, k, 1) : gguf::xq_bytes(n, k)) + raw_split_ws(op, type, row, k, n);
   }
-  if (decode_mma(op, type, row, k, n)) return align256(gguf::xq_bytes(n, k));  // x_q8 is converted into it
+  if (decode_mma(op, type, row, k, n))  // x_q8 is converted into it
+    return align256(gguf::xq_bytes(n, k)) + raw_split_ws(op, type, row, k, n);
   if (packed_fused(op, row, k, n, has_x_q8 != 0) || rows_fused(op, type, row, k, n, has_x_q8 != 0)) return 0;
   return has_x_q8 ? 0 : align256(gguf_q8_1_bytes(n, k, 0));
 }
@@ -335,7 +355,7 @@ int run_checked(int op, const gguf_view* W, const gguf_view* X, int64_t type, in
       e = gguf::launch_quantize_xq(X->data, X->dtype, n, k, s01, (int)type, false, workspace, s);
       if (e != hipSuccess) return hip_fail(e, name, "quantize");
       e = gguf::launch_gemm_xq((int)type, w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace, (int)n, y, ydt,
-                               true, s);
+                               true, nullptr, s);
       if (e != hipSuccess) return hip_fail(e, name, "gemm");
       return GGUF_OK;
     }
@@ -368,12 +388,22 @@ int run_checked(int op, const gguf_view* W, const gguf_view* X, int64_t type, in
     const bool prefill = gemm && n >= kPrefillFrom;
     const bool fp16 = small_fp16(op, type, row, k, n);
     const bool xh = fp16 || (prefill && gguf::prefill_uses_xh((int)type, packed));
+    // a K-split raw GEMM's partial sums and counters follow the xq copy; the quantise launch
+    // clears the counters
+    uint8_t* split_ws = nullptr;
+    uint32_t* counters = nullptr;
+    int nctr = 0;
+    if (raw_split_ws(op, type, row, k, n) > 0) {
+      split_ws = (uint8_t*)workspace + align256(gguf::xq_bytes(n, k));
+      counters = (uint32_t*)(split_ws + gguf::raw_split_part_bytes((int)type, row, k, n));
+      nctr = gguf::raw_split_counters((int)type, row, k, n);
+    }
     if (!gemm && x_q8)
-      e = gguf::launch_q8_1_to_xq(x_q8->data, n, k, (int)type, workspace, s);
+      e = gguf::launch_q8_1_to_xq(x_q8->data, n, k, (int)type, workspace, s, counters, nctr);
     else if (xh)
       e = gguf::launch_quantize_xh(X->data, X->dtype, n, k, s01, (int)type, workspace, s);
     else
-      e = gguf::launch_quantize_xq(X->data, X->dtype, n, k, s01, (int)type, !gemm, workspace, s);
+      e = gguf::launch_quantize_xq(X->data, X->dtype, n, k, s01, (int)type, !gemm, workspace, s, counters, nctr);
     if (e != hipSuccess) return hip_fail(e, name, "quantize");
     if (prefill)
       e = gguf::launch_gemm_prefill((int)type, packed, w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace,
@@ -385,7 +415,7 @@ int run_checked(int op, const gguf_view* W, const gguf_view* X, int64_t type, in
       e = gguf::launch_gemm_packed_xq(w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace, (int)n, y, ydt, s);
     else
       e = gguf::launch_gemm_xq((int)type, w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace, (int)n, y, ydt,
-                               gemm, s);
+                               gemm, split_ws, s);
     if (e != hipSuccess) return hip_fail(e, name, "gemm");
     return GGUF_OK;
   }

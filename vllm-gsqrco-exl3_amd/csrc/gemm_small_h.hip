@@ -341,18 +341,6 @@ void launch_small_h_rt(const uint8_t* W, int64_t row_bytes, int nrows, int k, co
 // one workgroup per CU over at most kRangeTiles row tiles each, 1..3 column tiles
 constexpr int kRangeTiles = 5;
 
-static int small_h_cus() {
-  static int cus[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cus[dev] == 0) {
-    int c = 0;
-    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
-    cus[dev] = c;
-  }
-  return cus[dev];
-}
-
 }  // namespace
 
 // Types the fp16 small GEMM serves: IQ3_S in the unit layout (packed) and Q4_K rows.
@@ -366,7 +354,7 @@ bool small_h_supported(int type, bool packed) { return packed ? type == kIQ3_S :
 // tiles per CU the int8 GEMM's grid is the faster one: 6144 x 5120 (1.5 tiles per CU), IQ3_S 48
 // rows 39.8 us on the range plan against 19.0 us for 32 rows on the int8 GEMM.
 bool small_h_range(int type, int64_t nrows, int64_t n) {
-  const int64_t tiles = (nrows + 15) / 16, cus = small_h_cus();
+  const int64_t tiles = (nrows + 15) / 16, cus = device_cus();
   const int64_t from = type == kIQ3_S ? 33 : 17;
   return n >= from && n <= 3 * 16 && tiles >= 4 * cus && tiles <= kRangeTiles * cus;
 }
@@ -379,7 +367,7 @@ hipError_t launch_gemm_small_h(int type, bool packed, const uint8_t* W, int64_t 
   if (!small_h_supported(type, packed)) return hipErrorInvalidValue;
   if (small_h_range(type, nrows, n)) {
     const int nct = (int)xq_col_tiles(n);
-    const unsigned gx = (unsigned)small_h_cus();
+    const unsigned gx = (unsigned)device_cus();
 #define GGUF_RANGE(T)                                                                                                      \
   if (nct <= 2) launch_small_h_t<T, kRangeTiles, 2, 1, true, 1>(W, row_bytes, nrows, k, xh, n, y, y_dtype, gx, stream); \
   else launch_small_h_t<T, kRangeTiles, 3, 1, true, 1>(W, row_bytes, nrows, k, xh, n, y, y_dtype, gx, stream);

@@ -505,8 +505,6 @@ __global__ void __launch_bounds__(64 * NW) gemv_iq3s_stream_kernel(const uint8_t
 // ---------------------------------------------------------------------------------------------
 // Launch plans
 
-static int device_cus() { return persist_grid() / 2; }
-
 constexpr size_t kStreamXMax = 96 * 1024;        // X staged in the stream kernel's LDS
 constexpr size_t kStreamLdsMin = 82 * 1024;      // dynamic LDS floor: one workgroup per CU
 constexpr int kStreamXpt[] = {1, 2, 3, 4, 5, 6, 9, 13, 17, 24};

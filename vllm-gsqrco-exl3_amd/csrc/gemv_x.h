@@ -7,17 +7,7 @@
 namespace gguf {
 
 // workgroups of the persistent GEMVs: two per CU of the current device
-inline int persist_grid() {
-  static int cus[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 512;
-  if (cus[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cus[dev] = n;
-  }
-  return 2 * cus[dev];
-}
+inline int persist_grid() { return 2 * device_cus(); }
 
 // q8_1 bytes of N (4 or 8) values of one slice, given the slice's amax and d = amax / 127: q =
 // roundf(v / d) (q = 0 when amax == 0), bit for bit as the q8_1 quantiser computes them. The

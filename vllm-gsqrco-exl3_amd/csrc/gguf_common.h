@@ -399,4 +399,17 @@ __device__ __forceinline__ int iq4nl(uint32_t q, int sh) {
   return (int)((hi & sel) | (lo & ~sel));
 }
 
+// compute units of the current device (256 on MI355X; 256 when the query fails), cached per device
+inline int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
 }  // namespace gguf

@@ -173,11 +173,20 @@ __device__ __forceinline__ void xh_store(uint8_t* y, int k, int c, int kk, int n
   }
 }
 
+// Workgroup (0, 0) of a quantise launch clears `zero_words` dwords at `zero` (the split GEMM's
+// counters, which the GEMM that follows in stream order reads; null: none).
+__device__ __forceinline__ void clear_words(uint32_t* zero, int zero_words) {
+  if (zero != nullptr && blockIdx.x == 0 && blockIdx.y == 0)
+    for (int i = (int)threadIdx.x; i < zero_words; i += (int)blockDim.x) zero[i] = 0u;
+}
+
 // Thread (x, y) of the grid: values 8 x .. 8 x + 7 of activation row c0 + y (rows past n, the last
 // column tile's padding, quantise zeros). k % 32 == 0, so a slice's four threads exit together.
 template <int DT, bool VEC, bool DS4, bool XH = false>
 __global__ void __launch_bounds__(256) quantize_xq_kernel(const void* __restrict__ x, uint8_t* __restrict__ y, int k,
-                                                          int64_t s01, int n, int nct, int c0) {
+                                                          int64_t s01, int n, int nct, int c0, uint32_t* zero,
+                                                          int zero_words) {
+  clear_words(zero, zero_words);
   const int kk = ((int)blockIdx.x * 256 + (int)threadIdx.x) * 8;
   if (kk >= k) return;
   const int c = c0 + (int)blockIdx.y;
@@ -231,7 +240,8 @@ __global__ void __launch_bounds__(256) quantize_xq_kernel(const void* __restrict
 // block_q8_1 bytes of X (a caller's x_q8) -> the xq layout with the same values and fp16 scales.
 template <bool DS4>
 __global__ void __launch_bounds__(256) q8_1_to_xq_kernel(const uint8_t* __restrict__ q8, uint8_t* __restrict__ y,
-                                                         int k, int n, int nct, int c0) {
+                                                         int k, int n, int nct, int c0, uint32_t* zero, int zero_words) {
+  clear_words(zero, zero_words);
   const int kk = ((int)blockIdx.x * 256 + (int)threadIdx.x) * 8;
   if (kk >= k) return;
   const int c = c0 + (int)blockIdx.y;
@@ -251,9 +261,10 @@ __global__ void __launch_bounds__(256) q8_1_to_xq_kernel(const uint8_t* __restri
 }
 
 // X [n, k] -> the xq layout at y (xq_bytes(n, k) bytes) for weights of ggml type `type`; vec:
-// the decode ops' q8_1 arithmetic, else the MMQ arithmetic.
+// the decode ops' q8_1 arithmetic, else the MMQ arithmetic. The first launch also clears
+// zero_words dwords at zero (null: none).
 hipError_t launch_quantize_xq(const void* x, int dtype, int64_t n, int64_t k, int64_t s01, int type, bool vec,
-                              void* y, hipStream_t stream) {
+                              void* y, hipStream_t stream, uint32_t* zero, int zero_words) {
   if (n == 0) return hipSuccess;
   const int nct = (int)xq_col_tiles(n), rows = nct * kXqCols;
   const unsigned gx = (unsigned)((k / 8 + 255) / 256);
@@ -261,7 +272,8 @@ hipError_t launch_quantize_xq(const void* x, int dtype, int64_t n, int64_t k, in
   for (int c0 = 0; c0 < rows; c0 += kQuantRowsPerLaunch) {
     const dim3 grid(gx, (unsigned)std::min(rows - c0, kQuantRowsPerLaunch));
 #define GGUF_QXQ(DT, V, D) \
-  quantize_xq_kernel<DT, V, D><<<grid, 256, 0, stream>>>(x, (uint8_t*)y, (int)k, s01, (int)n, nct, c0)
+  quantize_xq_kernel<DT, V, D><<<grid, 256, 0, stream>>>(x, (uint8_t*)y, (int)k, s01, (int)n, nct, c0, \
+                                                         c0 == 0 ? zero : nullptr, zero_words)
 #define GGUF_QXQ_DT(DT)                          \
   if (vec) {                                     \
     if (ds4) GGUF_QXQ(DT, true, true);           \
@@ -292,9 +304,11 @@ hipError_t launch_quantize_xh(const void* x, int dtype, int64_t n, int64_t k, in
     const dim3 grid(gx, (unsigned)std::min(rows - c0, kQuantRowsPerLaunch));
 #define GGUF_QXH(DT)                                                                                               \
   if (ds4)                                                                                                         \
-    quantize_xq_kernel<DT, false, true, true><<<grid, 256, 0, stream>>>(x, (uint8_t*)y, (int)k, s01, (int)n, nct, c0); \
+    quantize_xq_kernel<DT, false, true, true><<<grid, 256, 0, stream>>>(x, (uint8_t*)y, (int)k, s01, (int)n, nct, c0, \
+                                                                        nullptr, 0);                              \
   else                                                                                                             \
-    quantize_xq_kernel<DT, false, false, true><<<grid, 256, 0, stream>>>(x, (uint8_t*)y, (int)k, s01, (int)n, nct, c0);
+    quantize_xq_kernel<DT, false, false, true><<<grid, 256, 0, stream>>>(x, (uint8_t*)y, (int)k, s01, (int)n, nct, c0, \
+                                                                         nullptr, 0);
     switch (dtype) {
       case kF32: GGUF_QXH(kF32) break;
       case kF16: GGUF_QXH(kF16) break;
@@ -305,17 +319,21 @@ hipError_t launch_quantize_xh(const void* x, int dtype, int64_t n, int64_t k, in
   return hipGetLastError();
 }
 
-// block_q8_1 of X [n, k] -> the xq layout at y.
-hipError_t launch_q8_1_to_xq(const void* q8, int64_t n, int64_t k, int type, void* y, hipStream_t stream) {
+// block_q8_1 of X [n, k] -> the xq layout at y; the first launch also clears zero_words dwords at
+// zero (null: none).
+hipError_t launch_q8_1_to_xq(const void* q8, int64_t n, int64_t k, int type, void* y, hipStream_t stream,
+                             uint32_t* zero, int zero_words) {
   if (n == 0) return hipSuccess;
   const int nct = (int)xq_col_tiles(n), rows = nct * kXqCols;
   const unsigned gx = (unsigned)((k / 8 + 255) / 256);
   for (int c0 = 0; c0 < rows; c0 += kQuantRowsPerLaunch) {
     const dim3 grid(gx, (unsigned)std::min(rows - c0, kQuantRowsPerLaunch));
     if (type == kQ4_K)
-      q8_1_to_xq_kernel<true><<<grid, 256, 0, stream>>>((const uint8_t*)q8, (uint8_t*)y, (int)k, (int)n, nct, c0);
+      q8_1_to_xq_kernel<true><<<grid, 256, 0, stream>>>((const uint8_t*)q8, (uint8_t*)y, (int)k, (int)n, nct, c0,
+                                                        c0 == 0 ? zero : nullptr, zero_words);
     else
-      q8_1_to_xq_kernel<false><<<grid, 256, 0, stream>>>((const uint8_t*)q8, (uint8_t*)y, (int)k, (int)n, nct, c0);
+      q8_1_to_xq_kernel<false><<<grid, 256, 0, stream>>>((const uint8_t*)q8, (uint8_t*)y, (int)k, (int)n, nct, c0,
+                                                         c0 == 0 ? zero : nullptr, zero_words);
   }
   return hipGetLastError();
 }
