@@ -58,7 +58,8 @@ def test_workspace_follows_the_product_plan(lib):
     layout (4,608 B per 16 rows x 256 values) below 64 rows, the fp16 one (9,216 B) for packed
     IQ3_S and Q4_K from 64 rows at K <= 8192, below that where the fp16 GEMM's range plan takes
     the weight (1..5 row tiles per CU, 256 CUs assumed without a GPU; IQ3_S from 33 rows, Q4_K
-    from 17), and for the prefill from 256 rows; IQ4_XS and K = 17408 stay on the int8 layout below the prefill."""
+    from 17), and for the prefill from 256 rows; IQ4_XS and K = 17408 stay on the int8 layout below the prefill
+    (plus a K split's slots and counters on grids of few tiles)."""
     xq = lambda n, k: -(-n // 16) * (k // 256) * 4608
     xh = lambda n, k: -(-n // 16) * (k // 256) * 9216
     packed, mmq = 7, 1
@@ -67,14 +68,15 @@ def test_workspace_follows_the_product_plan(lib):
     assert lib.gguf_op_workspace_bytes(packed, 21, 17408, 5120, 32, 0) == xq(32, 5120)
     assert lib.gguf_op_workspace_bytes(packed, 21, 17408, 5120, 8, 0) == xq(8, 5120)
     assert lib.gguf_op_workspace_bytes(packed, 21, 17408, 5120, 49, 0) == xq(49, 5120)
-    assert lib.gguf_op_workspace_bytes(packed, 21, 1024, 5120, 48, 0) == xq(48, 5120)
+    # 64 tiles: the tile GEMM splits K 2 ways (slots and counters after the xq copy)
+    assert lib.gguf_op_workspace_bytes(packed, 21, 1024, 5120, 48, 0) == xq(48, 5120) + 64 * 2 * 3072 + 256
     assert lib.gguf_op_workspace_bytes(packed, 21, 6144, 5120, 48, 0) == xq(48, 5120)  # 1.5 tiles per CU
     assert lib.gguf_op_workspace_bytes(mmq, 12, 17408, 5120, 32, 0) == xh(32, 5120)
     assert lib.gguf_op_workspace_bytes(mmq, 12, 17408, 5120, 16, 0) == xq(16, 5120)
     assert lib.gguf_op_workspace_bytes(packed, 21, 17408, 5120, 64, 0) == xh(64, 5120)
     assert lib.gguf_op_workspace_bytes(packed, 21, 17408, 5120, 255, 0) == xh(255, 5120)
     assert lib.gguf_op_workspace_bytes(packed, 21, 17408, 5120, 256, 0) == xh(256, 5120)
-    assert lib.gguf_op_workspace_bytes(packed, 21, 5120, 17408, 64, 0) == xq(64, 17408)
+    assert lib.gguf_op_workspace_bytes(packed, 21, 5120, 17408, 64, 0) == xq(64, 17408) + 320 * 4 * 4096 + 1280
     assert lib.gguf_op_workspace_bytes(mmq, 12, 17408, 5120, 64, 0) == xh(64, 5120)
     assert lib.gguf_op_workspace_bytes(mmq, 23, 17408, 5120, 64, 0) == xq(64, 5120)
 
@@ -101,6 +103,20 @@ def test_workspace_of_the_split_raw_gemm(lib):
     assert lib.gguf_op_workspace_bytes(vec, 23, 4096, 4096, 8, 0) == xq(8, 4096)
     assert lib.gguf_op_workspace_bytes(mmq, 12, 5120, 5120, 48, 0) == xq(48, 5120)
     assert lib.gguf_op_workspace_bytes(mmq, 23, 6144, 5120, 32, 0) == xq(32, 5120)
+
+
+def test_workspace_of_the_split_tile_gemm(lib):
+    """Packed IQ3_S on the int8 tile GEMM splits K on 48+ blocks (4 ways from 2 column tiles, 2 at
+    one) and 2 ways where the grid fills under half the CUs; same workspace layout as the raw GEMM."""
+    xq = lambda n, k: -(-n // 16) * (k // 256) * 4608
+    a256 = lambda b: -(-b // 256) * 256
+    packed_vec, packed = 6, 7
+    assert lib.gguf_op_workspace_bytes(packed, 21, 5120, 17408, 48, 0) == xq(48, 17408) + 320 * 4 * 3072 + a256(320 * 4)
+    assert lib.gguf_op_workspace_bytes(packed_vec, 21, 5120, 17408, 8, 0) == xq(8, 17408) + 320 * 2 * 1024 + a256(320 * 4)
+    assert lib.gguf_op_workspace_bytes(packed, 21, 1024, 5120, 16, 0) == xq(16, 5120) + 64 * 2 * 1024 + a256(64 * 4)
+    # unsplit: 20 blocks on 384 tiles; 1088 tiles
+    assert lib.gguf_op_workspace_bytes(packed, 21, 6144, 5120, 16, 0) == xq(16, 5120)
+    assert lib.gguf_op_workspace_bytes(packed, 21, 17408, 5120, 16, 0) == xq(16, 5120)
 
 
 def test_guard_call_does_not_need_a_gpu(lib):

@@ -221,6 +221,56 @@ def test_split_k_vs_q81_deterministic_and_graph_replays(lib, qt):
         assert torch.equal(f(), y)  # eager work between the replays
 
 
+# the packed IQ3_S tile GEMM with K split over workgroups: (rows, k, n, op); 64 x 17408 splits
+# 4 ways at 2+ column tiles, 256 x 12288 2 ways at one, 1024 x 5120 (64 tiles) 2 ways
+PACKED_SPLIT = [(64, 17408, 48, "lcpp_mul_mat_iq3_packed"), (1024, 5120, 16, "lcpp_mul_mat_iq3_packed"),
+                (256, 12288, 8, "lcpp_mul_mat_vec_iq3_mma_packed"), (64, 17408, 24, "lcpp_mul_mat_vec_iq3_mma_packed")]
+
+
+@pytest.mark.parametrize("rows,k,n,op", PACKED_SPLIT, ids=lambda v: str(v))
+@pytest.mark.parametrize("with_q8", [False, True], ids=["x", "x_q8"])
+def test_packed_split_k_exact_integer_dots(lib, rows, k, n, op, with_q8):
+    """Exact-integer mode through the K-split tile GEMM on the unit layout, from X or (decode op)
+    from the caller's q8_1: the output equals the oracle's int64 sum exactly."""
+    from vllm_gguf_plugin.quantization import iq3_pack
+
+    if with_q8 and op != "lcpp_mul_mat_vec_iq3_mma_packed":
+        pytest.skip("x_q8 is an argument of the decode ops only")
+    _split_ws(lib, _capi_op(op), o.IQ3_S, rows, k, n, int(with_q8))
+    raw = _exact_weights(o.IQ3_S, rows, k, seed=350 + rows + n)
+    w = iq3_pack.pack(_dev(raw), o.IQ3_S)
+    x = _exact_x(n, k, seed=360 + n, dtype=torch.float32).cuda()
+    args = (C().lcpp_quantize_q8_1(x, o.IQ3_S, False, False),) if with_q8 else ()
+    y = getattr(C(), op)(w, x, o.IQ3_S, rows, *args).cpu().numpy()
+    np.testing.assert_array_equal(y.astype(np.int64), _exact_ref(raw, o.IQ3_S, x.cpu()))
+
+
+def test_packed_split_k_vs_q81_deterministic_and_graph_replays(lib):
+    """The split tile GEMM (1024 rows: 64 tiles, 2 ways, 3 column tiles) on random weights against
+    the q81 model (bf16 bar); repeated calls and graph replays are bit-identical."""
+    from vllm_gguf_plugin.quantization import iq3_pack
+
+    rows, k, n = 1024, 5120, 40
+    _split_ws(lib, _capi_op("lcpp_mul_mat_iq3_packed"), o.IQ3_S, rows, k, n)
+    raw = _w(o.IQ3_S, rows, k, seed=370)
+    w = iq3_pack.pack(_dev(raw), o.IQ3_S)
+    xc = _x(n, k, seed=371, dtype=torch.bfloat16).cuda()
+    f = lambda: C().lcpp_mul_mat_iq3_packed(w, xc, o.IQ3_S, rows)
+    y = f()
+    ref = o.q81_model(raw, o.IQ3_S, xc.cpu(), layout="mmq")
+    assert o.rel_l2(y.float().cpu().numpy(), ref) <= TIGHT[torch.bfloat16]
+    for _ in range(3):
+        assert torch.equal(f(), y)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = f()
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, y)
+        assert torch.equal(f(), y)
+
+
 def _capi_op(name):
     from vllm_gguf_plugin import _capi
 

@@ -16,7 +16,7 @@
 
 #include "../../include/gguf_mi355x.h"
 #include "gguf_common.h"
-#include "xq.h"
+#include "split_k.h"
 
 namespace gguf {
 hipError_t launch_quantize(const void* x, int dtype, int64_t n, int64_t k, int64_t s01, int type, bool mmq, void* y,
@@ -34,8 +34,7 @@ hipError_t launch_q8_1_to_xq(const void* q8, int64_t n, int64_t k, int type, voi
 hipError_t launch_gemm_xq(int type, const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n,
                           void* y, int y_dtype, bool mmq, void* split_ws, hipStream_t stream);
 int raw_split(int type, int64_t nrows, int64_t k, int64_t n);
-size_t raw_split_part_bytes(int type, int64_t nrows, int64_t k, int64_t n);
-int raw_split_counters(int type, int64_t nrows, int64_t k, int64_t n);
+int tile_split(int64_t nrows, int64_t k, int64_t n);
 hipError_t launch_gemv_packed_x(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x, int x_dtype,
                                 int64_t s01, int n, void* y, int y_dtype, hipStream_t stream);
 bool gemv_rows_supported(int type, int64_t nrows, int64_t row_bytes, int64_t k, int64_t n);
@@ -44,7 +43,7 @@ hipError_t launch_gemv_rows_x(int type, const uint8_t* W, int64_t row_bytes, int
                               int x_dtype, int64_t s01, int n, void* y, int y_dtype, hipStream_t stream);
 bool gemv_rows_x_supported(int type, int64_t nrows, int64_t row_bytes, int64_t k, int64_t n);
 hipError_t launch_gemm_packed_xq(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n,
-                                 void* y, int y_dtype, hipStream_t stream);
+                                 void* y, int y_dtype, void* split_ws, hipStream_t stream);
 hipError_t launch_quantize_xh(const void* x, int dtype, int64_t n, int64_t k, int64_t s01, int type, void* y,
                               hipStream_t stream);
 bool prefill_uses_xh(int type, bool packed);
@@ -294,11 +293,30 @@ bool raw_gemm(int op, int64_t type, int64_t row, int64_t k, int64_t n) {
   return decode_mma(op, type, row, k, n);
 }
 
-// Bytes after the xq copy of X that a K-split raw GEMM needs (partial sums, then its counters).
-size_t raw_split_ws(int op, int64_t type, int64_t row, int64_t k, int64_t n) {
-  if (!raw_gemm(op, type, row, k, n) || gguf::raw_split((int)type, row, k, n) == 1) return 0;
-  return gguf::raw_split_part_bytes((int)type, row, k, n) +
-         align256((size_t)gguf::raw_split_counters((int)type, row, k, n) * sizeof(uint32_t));
+// The int8 tile GEMM on packed IQ3_S (gemm_iq3s_tile_kernel), on the same terms.
+bool tile_gemm(int op, int64_t type, int64_t row, int64_t k, int64_t n) {
+  if (!op_packed(op) || type != gguf::kIQ3_S) return false;
+  if (op_gemm(op)) return n < kPrefillFrom && !small_fp16(op, type, row, k, n);
+  return decode_mma(op, type, row, k, n);
+}
+
+// Either GEMM's K split over workgroups (split_k.h): the workgroups per tile and the row tiles.
+struct SplitPlan {
+  int split = 1;
+  int64_t tiles = 0;
+};
+
+SplitPlan split_plan(int op, int64_t type, int64_t row, int64_t k, int64_t n) {
+  SplitPlan p;
+  if (raw_gemm(op, type, row, k, n)) p = {gguf::raw_split((int)type, row, k, n), (row + 15) / 16};
+  else if (tile_gemm(op, type, row, k, n)) p = {gguf::tile_split(row, k, n), row / 16};
+  return p;
+}
+
+// Bytes after the xq copy of X that a split GEMM needs (slots, then its counters).
+size_t split_ws(int op, int64_t type, int64_t row, int64_t k, int64_t n) {
+  const SplitPlan p = split_plan(op, type, row, k, n);
+  return gguf::split_ws_bytes(p.split, p.tiles, n);
 }
 
 }  // namespace
@@ -314,10 +332,10 @@ size_t gguf_op_workspace_bytes(int op, int64_t type, int64_t row, int64_t k, int
     if (!mmq_layout && ((n >= kPrefillFrom && gguf::prefill_uses_xh((int)type, op_packed(op))) ||
                         small_fp16(op, type, row, k, n)))
       return align256(gguf::xh_bytes(n, k));
-    return align256(mmq_layout ? gguf_q8_1_bytes(n, k, 1) : gguf::xq_bytes(n, k)) + raw_split_ws(op, type, row, k, n);
+    return align256(mmq_layout ? gguf_q8_1_bytes(n, k, 1) : gguf::xq_bytes(n, k)) + split_ws(op, type, row, k, n);
   }
   if (decode_mma(op, type, row, k, n))  // x_q8 is converted into it
-    return align256(gguf::xq_bytes(n, k)) + raw_split_ws(op, type, row, k, n);
+    return align256(gguf::xq_bytes(n, k)) + split_ws(op, type, row, k, n);
   if (packed_fused(op, row, k, n, has_x_q8 != 0) || rows_fused(op, type, row, k, n, has_x_q8 != 0)) return 0;
   return has_x_q8 ? 0 : align256(gguf_q8_1_bytes(n, k, 0));
 }
@@ -388,15 +406,16 @@ int run_checked(int op, const gguf_view* W, const gguf_view* X, int64_t type, in
     const bool prefill = gemm && n >= kPrefillFrom;
     const bool fp16 = small_fp16(op, type, row, k, n);
     const bool xh = fp16 || (prefill && gguf::prefill_uses_xh((int)type, packed));
-    // a K-split raw GEMM's partial sums and counters follow the xq copy; the quantise launch
-    // clears the counters
-    uint8_t* split_ws = nullptr;
+    // a K-split GEMM's slots and counters follow the xq copy; the quantise launch clears the
+    // counters
+    uint8_t* sws = nullptr;
     uint32_t* counters = nullptr;
     int nctr = 0;
-    if (raw_split_ws(op, type, row, k, n) > 0) {
-      split_ws = (uint8_t*)workspace + align256(gguf::xq_bytes(n, k));
-      counters = (uint32_t*)(split_ws + gguf::raw_split_part_bytes((int)type, row, k, n));
-      nctr = gguf::raw_split_counters((int)type, row, k, n);
+    const SplitPlan sp = split_plan(op, type, row, k, n);
+    if (sp.split > 1) {
+      sws = (uint8_t*)workspace + align256(gguf::xq_bytes(n, k));
+      counters = (uint32_t*)(sws + gguf::split_part_bytes(sp.split, sp.tiles, n));
+      nctr = gguf::split_counters(sp.split, sp.tiles, n);
     }
     if (!gemm && x_q8)
       e = gguf::launch_q8_1_to_xq(x_q8->data, n, k, (int)type, workspace, s, counters, nctr);
@@ -412,10 +431,11 @@ int run_checked(int op, const gguf_view* W, const gguf_view* X, int64_t type, in
       e = gguf::launch_gemm_small_h((int)type, packed, w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace,
                                     (int)n, y, ydt, s);
     else if (packed)
-      e = gguf::launch_gemm_packed_xq(w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace, (int)n, y, ydt, s);
+      e = gguf::launch_gemm_packed_xq(w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace, (int)n, y, ydt, sws,
+                                      s);
     else
       e = gguf::launch_gemm_xq((int)type, w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace, (int)n, y, ydt,
-                               gemm, split_ws, s);
+                               gemm, sws, s);
     if (e != hipSuccess) return hip_fail(e, name, "gemm");
     return GGUF_OK;
   }

@@ -15,6 +15,7 @@
 //  * the 4 waves' partial sums are added in wave order through LDS (deterministic).
 // gemm_raw_kernel (Q4_K, IQ4_XS, Q6_K) reads X in the xq layout; see its own description below.
 #include "decode.h"
+#include "split_k.h"
 #include "xq.h"
 
 namespace gguf {
@@ -242,13 +243,11 @@ hipError_t launch_gemm(int type, const uint8_t* W, int64_t row_bytes, int nrows,
 //  * on weights of few 16-row tiles (fewer than two per CU) the K blocks are also split over S =
 //    gridDim.z workgroups per tile (raw_split): each writes its sums to a slot of the workspace,
 //    bumps the tile's counter, and the one that brings it to S adds the S slots in slot order and
-//    writes the output (the counters are cleared by the quantise launch before the GEMM; slots and
-//    counters are agent-scope atomics, with no cache-wide fence).
+//    writes the output (split_k.h).
 namespace {
 
 constexpr int kRawRows = 16;   // weight rows per workgroup (the MFMA A rows)
 constexpr int kRawWaves = 4;   // waves per workgroup, splitting its K blocks
-constexpr int kRawMaxSplit = 4;  // most workgroups one tile's K is split over (raw_split)
 
 template <int TYPE>
 struct RawFrag;
@@ -512,49 +511,7 @@ __global__ void __launch_bounds__(64 * KS) gemm_raw_kernel(const uint8_t* __rest
       sum[t][v] = acc[t][v];
       for (int w2 = 1; w2 < KS; ++w2) sum[t][v] += red[w2 - 1][t][v][lane];
     }
-  if (S > 1) {
-    // slot z of this (tile, column group); the workgroup that completes the count adds the S
-    // slots in slot order, so the result does not depend on which one finishes last. The slots
-    // and the count are agent-scope atomics (written through to the device-coherent level and
-    // read from it), so no fence has to write back or invalidate a whole L2: the stores are
-    // complete (vmcnt 0) before the count, and the reads follow the count's returned value.
-    const size_t tg = (size_t)blockIdx.x * gridDim.y + blockIdx.y;
-    constexpr int kSlot = NT * 4 * 64;
-    float* slot = part + (tg * S + z) * kSlot;
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-      for (int v = 0; v < 4; ++v)
-        __hip_atomic_store(slot + (t * 4 + v) * 64 + lane, sum[t][v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    uint32_t prev = 0;
-    if (lane == 0) prev = __hip_atomic_fetch_add(cnt + tg, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    prev = __builtin_amdgcn_readfirstlane(prev);
-    if (prev != (uint32_t)S - 1) return;
-    asm volatile("" ::: "memory");
-    // all S x NT x 4 loads in flight at once, then the sums in slot order
-    const float* first = part + tg * S * kSlot;
-    float pv[kRawMaxSplit][NT][4];
-#pragma unroll
-    for (int zz = 0; zz < kRawMaxSplit; ++zz)
-#pragma unroll
-      for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int v = 0; v < 4; ++v)
-          pv[zz][t][v] = zz < S ? __hip_atomic_load(first + zz * kSlot + (t * 4 + v) * 64 + lane, __ATOMIC_RELAXED,
-                                                    __HIP_MEMORY_SCOPE_AGENT)
-                                : 0.0f;
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        float tot = pv[0][t][v];
-#pragma unroll
-        for (int zz = 1; zz < kRawMaxSplit; ++zz)
-          if (zz < S) tot += pv[zz][t][v];
-        sum[t][v] = tot;
-      }
-  }
+  if (S > 1 && !split_fixup<NT>(sum, part, cnt, S, z, (size_t)blockIdx.x * gridDim.y + blockIdx.y, lane)) return;
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     const int col = (ct0 + t) * kXqCols + j;
@@ -779,18 +736,13 @@ void launch_raw_type(const uint8_t* W, int64_t row_bytes, int nrows, int k, cons
 
 bool raw_type(int type) { return type == kQ4_K || type == kIQ4_XS || type == kQ6_K; }
 
-// column tiles per workgroup of the raw GEMM's plan
-int raw_nt(int64_t n) {
-  const int nct = (int)xq_col_tiles(n);
-  return nct < 4 ? nct : 4;
-}
-
 }  // namespace
 
-// The raw GEMM's K split over workgroups (1: none), for grids of fewer than two (tile, column
-// group) workgroups per CU. A workgroup holds a CU alone (256 threads, up to 256 VGPRs), so G of
-// them run in ceil(G / CUs) rounds; split s over K they take ceil(G s / CUs) rounds of 1/s the
-// work. s in {2, 4} is taken where that time drops, the smaller s on a tie; each wave keeps 3
+// The raw GEMM's K split over workgroups (1: none; split_k.h), for grids of fewer than two (tile,
+// column group) workgroups per CU. From 3 column tiles a workgroup holds a CU alone (up to 256
+// VGPRs per lane), so G of them run in ceil(G / CUs) rounds, and split s over K they take
+// ceil(G s / CUs) rounds of 1/s the work; with fewer column tiles 2-3 workgroups share a CU and
+// the same count still picks the measured best. s in {2, 4} is taken where that time drops, the smaller s on a tie; each wave keeps 3
 // blocks of its split (the fixed costs of a workgroup outweigh fewer), or 1 where the time at
 // least halves (most CUs idle otherwise). Measured on the op (quantise included, graph replayed),
 // no split -> split: IQ4_XS 5120 x 17408 (320 tiles, s = 4) M = 16 / 32 / 48: 38.1 -> 30.4 /
@@ -801,13 +753,13 @@ int raw_nt(int64_t n) {
 int raw_split(int type, int64_t nrows, int64_t k, int64_t n) {
   if (!raw_type(type) || n <= 0) return 1;
   const int64_t tiles = (nrows + kRawRows - 1) / kRawRows, nb = k / kQK, cus = device_cus();
-  const int64_t groups = tiles * ((xq_col_tiles(n) + raw_nt(n) - 1) / raw_nt(n));
+  const int64_t groups = split_groups(tiles, n);
   if (groups >= 2 * cus) return 1;
   // time in quarter workgroup-times
   auto quarters = [&](int64_t s) { return (groups * s + cus - 1) / cus * 4 / s; };
   int best = 1;
   int64_t best_t = quarters(1);
-  for (int s = 2; s <= kRawMaxSplit; s *= 2) {
+  for (int s = 2; s <= kMaxSplit; s *= 2) {
     const int64_t t = quarters(s);
     const int64_t min_blocks = 2 * t <= quarters(1) ? kRawWaves : 3 * kRawWaves;
     if (t < best_t && nb / s >= min_blocks) best = s, best_t = t;
@@ -815,31 +767,16 @@ int raw_split(int type, int64_t nrows, int64_t k, int64_t n) {
   return best;
 }
 
-// Workspace of a split raw GEMM: the partial sums (one 256-B aligned slot of NT x 4 x 64 floats
-// per tile, column group and split), then one uint32 counter per tile and column group.
-size_t raw_split_part_bytes(int type, int64_t nrows, int64_t k, int64_t n) {
-  const int split = raw_split(type, nrows, k, n);
-  if (split == 1) return 0;
-  const int64_t tiles = (nrows + kRawRows - 1) / kRawRows, nt = raw_nt(n);
-  const int64_t groups = tiles * ((xq_col_tiles(n) + nt - 1) / nt);
-  return (size_t)(groups * split * nt * 4 * 64 * sizeof(float));
-}
-
-int raw_split_counters(int type, int64_t nrows, int64_t k, int64_t n) {
-  if (raw_split(type, nrows, k, n) == 1) return 0;
-  const int64_t tiles = (nrows + kRawRows - 1) / kRawRows, nt = raw_nt(n);
-  return (int)(tiles * ((xq_col_tiles(n) + nt - 1) / nt));
-}
-
 // Q4_K / IQ4_XS / Q6_K rows; xq: X in the xq layout (launch_quantize_xq). mmq: X quantised with
 // the product ops' MMQ arithmetic (for Q4_K the scale words then carry the fp16 sum of x).
-// split_ws: raw_split_part_bytes of partial sums followed by raw_split_counters zeroed counters,
-// when raw_split(...) > 1 (unused otherwise).
+// split_ws: the split's workspace (split_k.h) when raw_split(...) > 1, its counters zeroed
+// (unused otherwise).
 hipError_t launch_gemm_xq(int type, const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n,
                           void* y, int y_dtype, bool mmq, void* split_ws, hipStream_t stream) {
   const int split = raw_split(type, nrows, k, n);
   float* part = (float*)split_ws;
-  uint32_t* cnt = (uint32_t*)((uint8_t*)split_ws + raw_split_part_bytes(type, nrows, k, n));
+  uint32_t* cnt =
+      (uint32_t*)((uint8_t*)split_ws + split_part_bytes(split, (nrows + kRawRows - 1) / kRawRows, n));
   if (split > 1 && split_ws == nullptr) return hipErrorInvalidValue;
   switch (type) {
     case kQ4_K:

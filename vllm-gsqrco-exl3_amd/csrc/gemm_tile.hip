@@ -17,6 +17,7 @@
 //  * the next block's weight and activation loads are issued before the current block is
 //    computed (two named register sets); the waves' partial sums are added in wave order.
 #include "iq3_tile.h"
+#include "split_k.h"
 #include "xq.h"
 
 namespace gguf {
@@ -174,8 +175,10 @@ __device__ __forceinline__ void mma_block(const uint8_t* tbl, uint8_t* tr, const
 template <int NT, int RW, int KS>
 __global__ void __launch_bounds__(64 * KS) gemm_iq3s_tile_kernel(const uint8_t* __restrict__ W, int64_t row_bytes,
                                                                  int nrows, int k, const uint8_t* __restrict__ xq,
-                                                                 int nct, int n, void* __restrict__ y, int y_dtype) {
+                                                                 int nct, int n, void* __restrict__ y, int y_dtype,
+                                                                 float* part, uint32_t* cnt) {
   static_assert((KS - 1) * RW * NT * 4 * 64 * 4 <= 2048 * 16, "wave partials fit the table region");
+  static_assert(RW == 1, "the K split's slots hold one row tile");
   __shared__ uint4 table[2048];  // signed-grid table; the waves' partial sums at the end
   __shared__ uint4 trbuf[KS][kTrBytes / 16];
   const int lane = threadIdx.x & 63;
@@ -186,7 +189,10 @@ __global__ void __launch_bounds__(64 * KS) gemm_iq3s_tile_kernel(const uint8_t* 
   const int tile0 = blockIdx.x * RW;
   const int ct0 = blockIdx.y * NT;
   const int nb = k / kQK;
-  const int b_begin = wave * nb / KS, b_end = (wave + 1) * nb / KS;
+  // this workgroup's part of K (split z of S), then the wave's part of that
+  const int S = (int)gridDim.z, z = (int)blockIdx.z;
+  const int zb0 = z * nb / S, zb1 = (z + 1) * nb / S;
+  const int b_begin = zb0 + wave * (zb1 - zb0) / KS, b_end = zb0 + (wave + 1) * (zb1 - zb0) / KS;
   const int64_t tile_bytes = (int64_t)kTileRows * row_bytes;
   const int tiles_here = ntiles - tile0 < RW ? ntiles - tile0 : RW;
   // every load stays inside the workgroup's tiles and the xq buffer: a missing tile of the last
@@ -261,51 +267,75 @@ __global__ void __launch_bounds__(64 * KS) gemm_iq3s_tile_kernel(const uint8_t* 
         for (int v = 0; v < 4; ++v) red[((((wave - 1) * RW + r) * NT + t) * 4 + v) * 64 + lane] = acc[r][t][v];
   }
   __syncthreads();
-  if (wave == 0) {
+  if (wave != 0) return;
+  float sum[NT][4];
 #pragma unroll
-    for (int r = 0; r < RW; ++r) {
-      if (r >= tiles_here) break;
+  for (int t = 0; t < NT; ++t)
 #pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        const int col = (ct0 + t) * kXqCols + j;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          float sum = acc[r][t][v];
-          for (int w2 = 1; w2 < KS; ++w2) sum += red[((((w2 - 1) * RW + r) * NT + t) * 4 + v) * 64 + lane];
-          if (col < n) store_y(y, (int64_t)col * nrows + (int64_t)(tile0 + r) * kTileRows + 4 * q + v, sum, y_dtype);
-        }
-      }
+    for (int v = 0; v < 4; ++v) {
+      sum[t][v] = acc[0][t][v];
+      for (int w2 = 1; w2 < KS; ++w2) sum[t][v] += red[(((w2 - 1) * NT + t) * 4 + v) * 64 + lane];
     }
+  if (S > 1 && !split_fixup<NT>(sum, part, cnt, S, z, (size_t)blockIdx.x * gridDim.y + blockIdx.y, lane)) return;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int col = (ct0 + t) * kXqCols + j;
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      if (col < n) store_y(y, (int64_t)col * nrows + (int64_t)tile0 * kTileRows + 4 * q + v, sum[t][v], y_dtype);
   }
 }
 
 template <int NT, int RW, int KS>
 void launch_tile_gemm(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n, void* y,
-                      int y_dtype, hipStream_t stream) {
+                      int y_dtype, int split, float* part, uint32_t* cnt, hipStream_t stream) {
   const int nct = (int)xq_col_tiles(n);
-  const dim3 grid((unsigned)((nrows / kTileRows + RW - 1) / RW), (unsigned)((nct + NT - 1) / NT));
-  gemm_iq3s_tile_kernel<NT, RW, KS><<<grid, 64 * KS, 0, stream>>>(W, row_bytes, nrows, k, xq, nct, n, y, y_dtype);
+  const dim3 grid((unsigned)((nrows / kTileRows + RW - 1) / RW), (unsigned)((nct + NT - 1) / NT), (unsigned)split);
+  gemm_iq3s_tile_kernel<NT, RW, KS>
+      <<<grid, 64 * KS, 0, stream>>>(W, row_bytes, nrows, k, xq, nct, n, y, y_dtype, part, cnt);
 }
 
 }  // namespace
 
+// The tile GEMM's K split over workgroups (1: none; split_k.h). Two or three of its workgroups
+// share a CU (49.6 KB of LDS each), so an uneven grid costs less than on the raw GEMM; the split
+// pays on long K and on grids that leave most CUs idle. Measured on the op (quantise included,
+// graph replayed), no split -> split: IQ3_S 5120 x 17408 (320 tiles, 68 blocks) M = 8 / 16 (2
+// ways): 29.5 -> 27.6 / 29.5 -> 27.7 us, M = 24 / 32 / 48 (4 ways): 42.8 -> 37.9 / 42.8 -> 38.0 /
+// 56.7 -> 48.9; 1024 x 5120 (64 tiles, 2 ways) M = 16 / 48: 9.9 -> 9.7 / 16.7 -> 14.2. At 20
+// blocks on 384 tiles (6144 x 5120) a 2-way split loses (12.9 -> 14.2 us at M = 16, measured
+// without the fixup).
+int tile_split(int64_t nrows, int64_t k, int64_t n) {
+  if (n <= 0) return 1;
+  const int64_t tiles = nrows / kTileRows, nb = k / kQK, cus = device_cus();
+  const int64_t groups = split_groups(tiles, n);
+  if (groups >= 2 * cus) return 1;
+  if (nb >= 48) return xq_col_tiles(n) >= 2 ? 4 : 2;
+  return 2 * groups < cus && nb >= 16 ? 2 : 1;
+}
+
 // IQ3_S in the unit layout; nrows % 16 == 0; xq: X in the xq layout (launch_quantize_xq).
 // Launch shapes measured at 17408 x 5120, 5120 x 17408 and 5120 x 5120: four waves per tile,
 // eight for one column tile on matrices of fewer than 512 tiles (more waves per tile to fill
-// the GPU); above 64 activation rows the y grid walks groups of four column tiles.
+// the GPU); above 64 activation rows the y grid walks groups of four column tiles. split_ws: the
+// split's workspace (split_k.h) when tile_split(...) > 1, its counters zeroed.
 hipError_t launch_gemm_packed_xq(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n,
-                                 void* y, int y_dtype, hipStream_t stream) {
+                                 void* y, int y_dtype, void* split_ws, hipStream_t stream) {
   const int nct = (int)xq_col_tiles(n);
   const bool few = nrows / kTileRows < 512;
+  const int split = tile_split(nrows, k, n);
+  if (split > 1 && split_ws == nullptr) return hipErrorInvalidValue;
+  float* part = (float*)split_ws;
+  uint32_t* cnt = (uint32_t*)((uint8_t*)split_ws + split_part_bytes(split, nrows / kTileRows, n));
   if (nct == 1) {
-    if (few) launch_tile_gemm<1, 1, 8>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
-    else launch_tile_gemm<1, 1, 4>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
+    if (few) launch_tile_gemm<1, 1, 8>(W, row_bytes, nrows, k, xq, n, y, y_dtype, split, part, cnt, stream);
+    else launch_tile_gemm<1, 1, 4>(W, row_bytes, nrows, k, xq, n, y, y_dtype, split, part, cnt, stream);
   } else if (nct == 2) {
-    launch_tile_gemm<2, 1, 4>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
+    launch_tile_gemm<2, 1, 4>(W, row_bytes, nrows, k, xq, n, y, y_dtype, split, part, cnt, stream);
   } else if (nct == 3) {
-    launch_tile_gemm<3, 1, 4>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
+    launch_tile_gemm<3, 1, 4>(W, row_bytes, nrows, k, xq, n, y, y_dtype, split, part, cnt, stream);
   } else {
-    launch_tile_gemm<4, 1, 4>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
+    launch_tile_gemm<4, 1, 4>(W, row_bytes, nrows, k, xq, n, y, y_dtype, split, part, cnt, stream);
   }
   return hipGetLastError();
 }
