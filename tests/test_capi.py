@@ -103,6 +103,8 @@ def test_workspace_of_the_split_raw_gemm(lib):
     assert lib.gguf_op_workspace_bytes(vec, 23, 4096, 4096, 8, 0) == xq(8, 4096)
     assert lib.gguf_op_workspace_bytes(mmq, 12, 5120, 5120, 48, 0) == xq(48, 5120)
     assert lib.gguf_op_workspace_bytes(mmq, 23, 6144, 5120, 32, 0) == xq(32, 5120)
+    # 3 column tiles keep 4 blocks per wave: 24 blocks do not split 2 ways
+    assert lib.gguf_op_workspace_bytes(mmq, 14, 5120, 6144, 48, 0) == xq(48, 6144)
 
 
 def test_workspace_of_the_split_tile_gemm(lib):

@@ -742,14 +742,15 @@ bool raw_type(int type) { return type == kQ4_K || type == kIQ4_XS || type == kQ6
 // column group) workgroups per CU. From 3 column tiles a workgroup holds a CU alone (up to 256
 // VGPRs per lane), so G of them run in ceil(G / CUs) rounds, and split s over K they take
 // ceil(G s / CUs) rounds of 1/s the work; with fewer column tiles 2-3 workgroups share a CU and
-// the same count still picks the measured best. s in {2, 4} is taken where that time drops, the smaller s on a tie; each wave keeps 3
-// blocks of its split (the fixed costs of a workgroup outweigh fewer), or 1 where the time at
-// least halves (most CUs idle otherwise). Measured on the op (quantise included, graph replayed),
-// no split -> split: IQ4_XS 5120 x 17408 (320 tiles, s = 4) M = 16 / 32 / 48: 38.1 -> 30.4 /
-// 50.2 -> 41.1 / 65.9 -> 52.8 us; Q6_K 5120 x 6144 (s = 2) M = 16 / 32: 22.2 -> 19.2 /
-// 28.3 -> 23.7; Q6_K 1024 x 5120 (64 tiles, s = 4) M = 16: 11.7 -> 9.8. Left unsplit: 256
-// workgroups (one round either way: 4096 x 4096 IQ4_XS M = 8 11.2 -> 13.0 with s = 2), 20-block
-// K at 320 or 384 tiles (Q4_K 5120 x 5120 M = 48 27.0 -> 31.0).
+// the same count still picks the measured best. s in {2, 4} is taken where that time drops, the
+// smaller s on a tie; each wave keeps 3 blocks of its split (4 from 3 column tiles: the fixed
+// costs of a workgroup outweigh fewer), or 1 where the time at least halves (most CUs idle
+// otherwise). Measured on the op (quantise included, graph replayed), no split -> split: IQ4_XS
+// 5120 x 17408 (320 tiles, s = 4) M = 16 / 32 / 48: 38.1 -> 30.4 / 50.2 -> 41.1 / 65.9 -> 52.8
+// us; Q6_K 5120 x 6144 (s = 2) M = 16 / 32: 22.2 -> 19.2 / 28.3 -> 23.7; Q6_K 1024 x 5120 (64
+// tiles, s = 4) M = 16: 11.7 -> 9.8. Left unsplit: 256 workgroups (one round either way: 4096 x
+// 4096 IQ4_XS M = 8 11.2 -> 13.0 with s = 2), 20-block K at 320 or 384 tiles (Q4_K 5120 x 5120
+// M = 48 27.0 -> 31.0), 24 blocks at 3 column tiles (Q6_K 5120 x 6144 M = 48 37.1 -> 37.8).
 int raw_split(int type, int64_t nrows, int64_t k, int64_t n) {
   if (!raw_type(type) || n <= 0) return 1;
   const int64_t tiles = (nrows + kRawRows - 1) / kRawRows, nb = k / kQK, cus = device_cus();
@@ -759,9 +760,10 @@ int raw_split(int type, int64_t nrows, int64_t k, int64_t n) {
   auto quarters = [&](int64_t s) { return (groups * s + cus - 1) / cus * 4 / s; };
   int best = 1;
   int64_t best_t = quarters(1);
+  const int64_t per_wave = split_nt(n) >= 3 ? 4 : 3;
   for (int s = 2; s <= kMaxSplit; s *= 2) {
     const int64_t t = quarters(s);
-    const int64_t min_blocks = 2 * t <= quarters(1) ? kRawWaves : 3 * kRawWaves;
+    const int64_t min_blocks = 2 * t <= quarters(1) ? kRawWaves : per_wave * kRawWaves;
     if (t < best_t && nb / s >= min_blocks) best = s, best_t = t;
   }
   return best;
