@@ -55,13 +55,13 @@ __device__ __forceinline__ TileOffs unit_lane_offsets(int lane, int p, int s) {
 // the lane's bytes of one K block or unit-block: scalar field bases f (inside rs) + lane offsets o
 __device__ __forceinline__ void load_tile_frag(__amdgpu_buffer_rsrc_t rs, const Iq3Fields& f, const TileOffs& o,
                                                TileFrag& t) {
-  const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)o.qs, (int)f.qs, 0);
+  const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)o.qs, (int)f.qs, kWeightCpol);
   t.qs = make_uint4(q.x, q.y, q.z, q.w);
-  const auto e = __builtin_amdgcn_raw_buffer_load_b64(rs, (int)o.e8, (int)f.e8, 0);
+  const auto e = __builtin_amdgcn_raw_buffer_load_b64(rs, (int)o.e8, (int)f.e8, kWeightCpol);
   t.e8 = make_uint2(e[0], e[1]);
-  t.l2 = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)o.l2, (int)f.l2, 0);
-  t.sc = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)o.sc, (int)f.sc, 0);
-  t.dd = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)o.dd, (int)f.d, 0);
+  t.l2 = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)o.l2, (int)f.l2, kWeightCpol);
+  t.sc = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)o.sc, (int)f.sc, kWeightCpol);
+  t.dd = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)o.dd, (int)f.d, kWeightCpol);
 }
 
 template <int NC>

@@ -348,6 +348,15 @@ __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdg
 // zero. gfx9 descriptor word 3.
 constexpr int kBufDword3 = 0x00020000;
 
+// Cache policy of the IQ3_S decode GEMVs' weight loads (the aux operand of a raw buffer load on
+// gfx950: bit 0 sc0, bit 1 nt). Each weight byte is read once per launch by one lane, so the loads
+// are marked non-temporal; on the 17408 x 5120 and 5120 x 17408 stream GEMV this took 4-5 % off
+// each launch at 1 and 4 activation rows (sc0 alone changed nothing). The row-chunk GEMV of the
+// GGUF-row types keeps the default policy: its lanes read the header bytes of a block from lines
+// that other loads of the same block also touch, and nt made it slower (Q4_K 17408 x 5120 M = 1
+// 12.6 -> 14.1 us, Q6_K 5120 x 17408 23.6 -> 28.6 us).
+constexpr int kWeightCpol = 3;
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, kBufDword3);
 }
