@@ -26,6 +26,14 @@ shape, and the 64-layer decoder sweep under one CUDA graph with a replay bit-exa
 Under "eager": the headline op called eagerly (no graph) at M = 1 and a 512-row prefill chunk, with
 the host's time per call.
 
+Also measured on the GPU (--no-peaks skips them): the read floor, one streaming launch over a
+headline weight's bytes (38.3 MB) and a gate|up pair's (76.6 MB) with the decode GEMV's access
+pattern, and the dense MFMA rate (v_mfma_i32_16x16x64_i8, v_mfma_f32_16x16x32_f16), so that the
+roofline carries a measured peak beside the published one.
+
+Output: each detail section on a line of its own ({"bench_detail": name, "result": ...}), then
+the headline, a compact JSON object, as the last line of stdout.
+
 `traffic` (HBM bytes per launch of the dominant kernel) is read from the committed PMC summary
 profiles/gemv_iq3s_stream_17408x5120_m1.traffic.json when present (null otherwise). That summary
 comes from `rocprofv3 --pmc FETCH_SIZE` and `--pmc WRITE_SIZE` runs of `bench.py --kernel-only`,
@@ -289,7 +297,8 @@ def _cpu_path_times(torch, o, raw, qt, rows, k, ms, threads):
 
 
 def config_cpu_q4k(torch, C):
-    """benchmark configs[0]: Q4_K 4096x4096 at M = 1, fp32 X N(0,1): the GPU op next to the CPU
+    """benchmark configs[0]: Q4_K 4096x4096 at M = 1, fp32 X N(0,1): the GPU op (the routing
+    table's, lcpp_mul_mat_vec_q at one row) next to the CPU
     reference path (numpy dequantise + q8_1 round trip + torch fp32 matmul), seed 0; dequantise and
     matmul each the median of 5, the matmul on all threads and on one."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -305,9 +314,13 @@ def config_cpu_q4k(torch, C):
     x = np.random.default_rng(0).standard_normal((1, k)).astype(np.float32)
     wd = torch.from_numpy(raw).cuda()
     xd = torch.from_numpy(x).cuda()
-    g = graph(torch, [lambda: C.lcpp_mul_mat_vec_own(wd, xd, Q4_K, rows)] * 8)
+    from vllm_gguf_plugin.quantization import linear
+
+    op = linear._lcpp_op(1, Q4_K, rows, k, False)
+    fn = getattr(C, op)
+    g = graph(torch, [lambda: fn(wd, xd, Q4_K, rows)] * 8)
     us = time_graphs(torch, [g], 10) * 1e3 / 8
-    return {"shape": "4096x4096", "m": 1, "op": "lcpp_mul_mat_vec_own", "gpu_us_per_call": round(us, 2),
+    return {"shape": "4096x4096", "m": 1, "op": op, "gpu_us_per_call": round(us, 2),
             "cpu_us_per_call": round((t_deq + mm[(1, threads)]) * 1e6, 1),
             "cpu_us_per_call_1_thread": round((t_deq + mm[(1, 1)]) * 1e6, 1),
             "cpu_dequant_us": round(t_deq * 1e6, 1), "cpu_matmul_us": round(mm[(1, threads)] * 1e6, 1),
@@ -358,6 +371,65 @@ def cpu_baseline(torch):
                       f"{CPU_SAMPLE_ROWS} rows of each shape, numpy dequantise + q8_1 round trip + torch "
                       f"fp32 matmul, each part the median of 5, scaled to the full rows",
             "cases": cases}
+
+
+PEAKS_LIB = os.path.join(ROOT, "vllm-gsqrco-exl3_amd", "vllm_gguf_plugin", "libgguf_peaks.so")
+FLOOR_SIZES = (38297600, 76595200)  # one 17408 x 5120 IQ3_S weight; a gate|up pair
+
+
+def measured_peaks(torch, reps=5):
+    """The two denominators measured on this GPU (libgguf_peaks.so, csrc/bench/peaks.hip):
+    * read floor: one launch streaming FLOOR_SIZES bytes (a headline weight, and a gate|up pair),
+      each workgroup over a contiguous equal share with 16-byte buffer loads, as the decode GEMV
+      reads; graph replays of one launch per buffer over rotation_copies buffers (beyond the
+      MALL), HIP events; the fastest of a sweep of launch shapes (workgroups x threads x loads in
+      flight x cache policy), with the shape that gave it;
+    * MFMA peak: 2048 workgroups of 4 waves, each wave 8 independent chains of MFMAs with register
+      operands: v_mfma_i32_16x16x64_i8 (int8 TOP/s) and v_mfma_f32_16x16x32_f16 (TFLOP/s)."""
+    import ctypes
+
+    lib = ctypes.CDLL(PEAKS_LIB)
+    lib.gguf_peak_read.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                   ctypes.c_int, ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p]
+    lib.gguf_peak_mfma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                   ctypes.c_void_p]
+    key = 0x9E3779B9  # a sum the data never gives: the kernels' guard store stays unexecuted
+    sink = torch.zeros(2048 * 1024, dtype=torch.int32, device="cuda")
+    out = {"read_floor": [], "mfma": {}}
+    for nbytes in FLOOR_SIZES:
+        nbuf = rotation_copies(nbytes)
+        stride = (nbytes + 255) // 256 * 256
+        pool = torch.randint(0, 256, (nbuf * stride,), dtype=torch.uint8, device="cuda")
+        best = None
+        for grid in (256, 512, 1024):
+            for threads in (256, 512, 1024):
+                for unroll in (2, 4):
+                    for nt in (0, 1):
+                        def call(i, grid=grid, threads=threads, unroll=unroll, nt=nt):
+                            rc = lib.gguf_peak_read(pool.data_ptr() + i * stride, nbytes, grid, threads, unroll, nt,
+                                                    key, sink.data_ptr(), torch.cuda.current_stream().cuda_stream)
+                            assert rc == 0, rc
+                        g = graph(torch, [lambda i=i: call(i) for i in range(nbuf)])
+                        us = time_graphs(torch, [g], reps) * 1e3 / nbuf
+                        if best is None or us < best[0]:
+                            best = (us, grid, threads, unroll, nt)
+                        del g
+        us, grid, threads, unroll, nt = best
+        out["read_floor"].append({"bytes": nbytes, "us": round(us, 3), "gbps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                                  "shape": f"{grid}x{threads} u{unroll}{' nt' if nt else ''}"})
+        del pool
+    grid, iters = 2048, 2000
+    for kind, name, per in ((0, "i8_16x16x64_tops", 32768), (1, "f16_16x16x32_tflops", 16384)):
+        def mcall(kind=kind):
+            rc = lib.gguf_peak_mfma(kind, grid, iters, key, sink.data_ptr(), torch.cuda.current_stream().cuda_stream)
+            assert rc == 0, rc
+        g = graph(torch, [mcall] * 3)
+        ms = time_graphs(torch, [g], 3) / 3
+        out["mfma"][name] = round(grid * 4 * 8 * iters * per / (ms * 1e-3) / 1e12, 1)
+        del g
+    del sink
+    torch.cuda.empty_cache()
+    return out
 
 
 def load_traffic():
@@ -464,6 +536,7 @@ def main():
     ap.add_argument("--section", choices=["mtp", "prefill", "layers", "types"],
                     help="run only this benchmark config and print its JSON (for rocprofv3 counter runs)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-peaks", action="store_true", help="skip the measured read floor and MFMA peak")
     ap.add_argument("--kernel-only", action="store_true",
                     help="time only the dominant kernel, then run the counter-calibration copy (for rocprofv3)")
     args = ap.parse_args()
@@ -527,24 +600,41 @@ def main():
     eager = eager_calls(torch, C, weights[(17408, 5120)], 17408, 5120)
     del weights
     torch.cuda.empty_cache()
+    emit("headline_cases", detail)
+    emit("eager", eager)
+
+    # ------------------------------------------------------------------ measured denominators
+    peaks = None
+    if not args.no_peaks:
+        peaks = measured_peaks(torch)
+        emit("measured_peaks", peaks)
+        floor = peaks["read_floor"][0]  # one launch over the headline weight's bytes
+        roofline["peak_measured"] = floor["gbps"]
+        roofline["frac_measured"] = round(roofline["achieved"] / floor["gbps"], 4)
+        roofline["read_floor_us"] = floor["us"]
 
     # ------------------------------------------------------------------ the metric's other points
     points = []
     if not args.no_points:
         for qt in (IQ3_S, Q4_K):
             points += op_points(torch, C, iq3_pack, linear, qt, 17408, 5120, (1, 4, 16, 32, 48), seed=1000)
+        emit("points", points)
 
-    configs = None
     if not args.no_configs:
-        configs = {"cpu_q4k_4096": config_cpu_q4k(torch, C),
-                   "mtp_small_gemm": config_mtp(torch, C, iq3_pack, linear),
-                   "prefill": config_prefill(torch, C, iq3_pack, linear),
-                   "generic_types": config_types(torch, C, iq3_pack, linear),
-                   "layer_sweep_64": config_layers(torch, C, iq3_pack, linear, args.steps),
-                   "layer_sweep_64_runs": config_layers(torch, C, iq3_pack, linear, args.steps, merged=True)}
+        for name, fn in (("cpu_q4k_4096", lambda: config_cpu_q4k(torch, C)),
+                         ("mtp_small_gemm", lambda: config_mtp(torch, C, iq3_pack, linear)),
+                         ("prefill", lambda: config_prefill(torch, C, iq3_pack, linear)),
+                         ("generic_types", lambda: config_types(torch, C, iq3_pack, linear)),
+                         ("layer_sweep_64", lambda: config_layers(torch, C, iq3_pack, linear, args.steps)),
+                         ("layer_sweep_64_runs",
+                          lambda: config_layers(torch, C, iq3_pack, linear, args.steps, merged=True))):
+            emit(name, fn())
 
     cpu = None if args.no_cpu else cpu_baseline(torch)
+    if cpu is not None:
+        emit("cpu_baseline_cases", cpu.pop("cases"))
 
+    # the headline: one compact JSON object, the last line of stdout (the details are above)
     line = {
         "metric": "µs/call + achieved HBM GB/s (% of peak), IQ3_S/Q4_K matmul at M=1,4,16,32,48",
         "value": round(value, 2),
@@ -561,14 +651,21 @@ def main():
         "config": {"workload": "IQ3_S decode GEMV (packed unit layout) at M=1,4 on 17408x5120 and 5120x17408, "
                                "benchmark configs[1]; per shape, weight copies of at least 512 MiB in all",
                    "calls_per_step": sum(n for *_, n, _ in per_case), "bytes_per_step": step_bytes},
-        "detail": detail,
+        "us_per_call": {f"{c['shape']} M={c['m']}": c["us_per_call"] for c in detail},
         "roofline": roofline,
-        "eager": eager,
         "cpu_baseline": cpu,
-        "points": points,
-        "configs": configs,
     }
-    print(json.dumps(line), flush=True)
+    if points:
+        line["points_us"] = {TYPE_NAME[qt]: {str(p["m"]): p["us_per_call"] for p in points
+                                             if p["type"] == TYPE_NAME[qt]} for qt in (IQ3_S, Q4_K)}
+    if peaks is not None:
+        line["measured_peaks"] = {"read_floor_gbps": [f["gbps"] for f in peaks["read_floor"]], **peaks["mfma"]}
+    print(json.dumps(line, separators=(",", ":")), flush=True)
+
+
+def emit(name, result):
+    """One detail section of the full run, on its own stdout line before the headline."""
+    print(json.dumps({"bench_detail": name, "result": result}, separators=(",", ":")), flush=True)
 
 
 if __name__ == "__main__":

@@ -899,9 +899,10 @@ def test_full_size_iq3s_gate_packed(n):
 
 
 def test_full_size_q4k_cpu_config():
-    """The CPU-path benchmark case: Q4_K 4096 x 4096, X 1 x 4096 fp32 N(0,1), seed 0."""
+    """The CPU-path benchmark case: Q4_K 4096 x 4096 with d, dmin ~ |N(0, 1e-3)| (the config's
+    recipe), X 1 x 4096 fp32 N(0,1), seed 0."""
     rows = k = 4096
-    raw = _w(o.Q4_K, rows, k, seed=0)
+    raw = o.random_blocks(np.random.default_rng(0), o.Q4_K, rows, k, scale_sigma=1e-3)
     x = torch.from_numpy(np.random.default_rng(0).standard_normal((1, k)).astype(np.float32))
     y = C().lcpp_mul_mat_vec_q(_dev(raw), x.cuda(), o.Q4_K, rows).cpu().numpy()
     assert o.rel_l2(y, o.q81_model(raw, o.Q4_K, x)) <= 1e-3

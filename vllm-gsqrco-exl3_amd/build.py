@@ -7,7 +7,8 @@ Each csrc/*.hip is compiled to an object in _build/ (in parallel), then linked i
 vllm_gguf_plugin/libgguf_mi355x.so, in-tree, where vllm_gguf_plugin._capi loads it.
 csrc/torch_ops.cpp (host C++ against PyTorch-ROCm's headers) is compiled alongside into
 vllm_gguf_plugin/_C_gguf_ops.so, which links libgguf_mi355x.so next to it and registers
-torch.ops._C_gguf when vllm_gguf_plugin._C_gguf loads it.
+torch.ops._C_gguf when vllm_gguf_plugin._C_gguf loads it. csrc/bench/peaks.hip (bench.py's
+measurement kernels, outside the C ABI) is built into vllm_gguf_plugin/libgguf_peaks.so.
 """
 
 import argparse
@@ -21,6 +22,9 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 OUT = os.path.join(HERE, "vllm_gguf_plugin", "libgguf_mi355x.so")
 OPS_OUT = os.path.join(HERE, "vllm_gguf_plugin", "_C_gguf_ops.so")
+# bench.py's measurement kernels (streaming-read floor, MFMA peak): not part of the C ABI
+PEAKS_SRC = os.path.join(CSRC, "bench", "peaks.hip")
+PEAKS_OUT = os.path.join(HERE, "vllm_gguf_plugin", "libgguf_peaks.so")
 CXX = os.environ.get("CXX", "g++")
 ARCH = os.environ.get("GGUF_OFFLOAD_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -85,13 +89,25 @@ def _link_ops(obj):
     os.replace(tmp, OPS_OUT)
 
 
+def _build_peaks():
+    """csrc/bench/peaks.hip -> libgguf_peaks.so (one step: compile and link)."""
+    tmp = PEAKS_OUT + ".tmp"
+    cmd = [HIPCC, *FLAGS, "-shared", PEAKS_SRC, "-o", tmp]
+    p = subprocess.run(cmd, capture_output=True, text=True)
+    if p.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {PEAKS_SRC}:\n{p.stderr}")
+    os.replace(tmp, PEAKS_OUT)
+
+
 def build(jobs: int = 8, verbose: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
     srcs = sources()
-    with cf.ThreadPoolExecutor(max_workers=max(1, min(jobs, len(srcs) + 1))) as ex:
+    with cf.ThreadPoolExecutor(max_workers=max(1, min(jobs, len(srcs) + 2))) as ex:
         ops = ex.submit(_compile_ops)
+        peaks = ex.submit(_build_peaks)
         results = list(ex.map(_compile, srcs))
         ops_obj, ops_err = ops.result()
+        peaks.result()
     for _, err in results:
         if err.strip() and verbose:
             print(err, file=sys.stderr)

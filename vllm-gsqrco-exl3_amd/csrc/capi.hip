@@ -515,17 +515,19 @@ namespace {
 constexpr size_t kScratchBytes = GGUF_SCRATCH_BYTES;
 __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
-constexpr int kMaxDevices = 64;
-void* g_scratch_ptr[kMaxDevices] = {};
+void* g_scratch_ptr[gguf::kMaxDevices] = {};
 std::mutex g_scratch_mu;
 
-// The current device's scratch address (the caller has made X's device current).
+// The current device's scratch address (the caller has made X's device current). The first call
+// on a device may come inside a caller's stream capture: the symbol lookup runs with the capture
+// mode relaxed (gguf::outside_capture).
 hipError_t scratch_address(int device, void** out) {
-  if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+  if (device < 0 || device >= gguf::kMaxDevices) return hipErrorInvalidDevice;
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch_ptr[device]) {
     void* p = nullptr;
-    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    hipError_t e = hipSuccess;
+    gguf::outside_capture([&] { e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)); });
     if (e != hipSuccess) return e;
     g_scratch_ptr[device] = p;
   }

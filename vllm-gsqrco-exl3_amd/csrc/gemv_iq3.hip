@@ -391,7 +391,14 @@ __global__ void __launch_bounds__(64 * NW) gemv_iq3s_stream_kernel(const uint8_t
   const int nu = u1 - u0, items = nu * nkb;
   const uint32_t ubytes = (uint32_t)(kUnitRows * row_bytes), rbytes = (uint32_t)nu * ubytes;
   const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(W + (int64_t)u0 * ubytes, rbytes);
-  const TileOffs off = unit_lane_offsets(lane, p, s);
+  // a last unit-block of r = 2 blocks (nb % 4 == 2; K % 512 == 0 leaves r in {0, 2}): lanes of
+  // bi >= 2 load lane L - 32's bytes instead of bytes past the block's fields, so every load of
+  // the run stays inside it; their terms are zeroed below (d = 0)
+  const TileOffs off = unit_lane_offsets(lane, p, s), off_r = unit_lane_offsets(lane & 31, p & 3, s);
+  const bool ragged = (nb & 3) != 0;
+  // an empty range: loads past the wave's run read zeros without touching memory (the hardware
+  // range check sees only the lane offset, not the scalar field base)
+  const __amdgpu_buffer_rsrc_t nrs = buffer_rsrc(W, 0u);
   const uint8_t* tbl = (const uint8_t*)table;
   const int j0 = wave * items / NW, j1 = (wave + 1) * items / NW;
   const int cu0 = (int)((uint32_t)j0 / (uint32_t)nkb);
@@ -402,10 +409,11 @@ __global__ void __launch_bounds__(64 * NW) gemv_iq3s_stream_kernel(const uint8_t
     f.qs += ub; f.e8 += ub; f.l2 += ub; f.sc += ub; f.d += ub;
     return f;
   };
-  // past the run: the end of the range (every lane's load reads zeros)
+  // past the run: the empty range nrs (every lane's load reads zeros)
   auto load_next = [&](TileFrag& f) {
-    const Iq3Fields e = {rbytes, rbytes, rbytes, rbytes, rbytes};
-    load_tile_frag(wrs, lj < j1 ? fields(lu, lkb) : e, off, f);
+    const Iq3Fields e = {0u, 0u, 0u, 0u, 0u};
+    const bool in_run = lj < j1;
+    load_tile_frag(in_run ? wrs : nrs, in_run ? fields(lu, lkb) : e, ragged && lkb == nkb - 1 ? off_r : off, f);
     ++lj;
     if (++lkb == nkb) {
       lkb = 0;
@@ -509,18 +517,28 @@ constexpr size_t kStreamXMax = 96 * 1024;        // X staged in the stream kerne
 constexpr size_t kStreamLdsMin = 82 * 1024;      // dynamic LDS floor: one workgroup per CU
 constexpr int kStreamXpt[] = {1, 2, 3, 4, 5, 6, 9, 13, 17, 24};
 
+// dynamic LDS of a stream launch: X's q8_1 plus the partial-sum slots of the most units a
+// workgroup owns, at least kStreamLdsMin
+static size_t stream_lds(int64_t nrows, int64_t k, int64_t n, int64_t grid) {
+  const int64_t nu_max = (nrows / kUnitRows + grid - 1) / grid;
+  const size_t part = (size_t)nu_max * kStreamWaves * (size_t)n * 16 * sizeof(float);
+  return std::max(kStreamLdsMin, (size_t)n * (size_t)(k / kQ81) * 36 + part);
+}
+
+// the stream kernel's static LDS: the signed-grid table (2048 x 16 B) and the 16-B sink
+constexpr size_t kStreamStaticLds = sizeof(uint4) * 2049;
+constexpr size_t kStreamLdsMax = 160 * 1024 - kStreamStaticLds;  // the dynamic LDS a workgroup may take
+
 // The stream kernel takes 1..4 activation rows (fused X: 1..2 rows at K <= 8192) on weights of
-// at least one 4-row unit per CU, with X's q8_1 within its LDS budget.
+// at least one 4-row unit per CU, with X's q8_1 and the partial sums within its LDS budget (a
+// weight of many units per CU at 3-4 rows needs more partial-sum slots than fit: such shapes take
+// the tile kernel).
 static bool stream_supported(int64_t nrows, int64_t k, int64_t n, bool fused) {
   if (n < 1 || n > (fused ? 2 : 4) || (fused && k > 8192)) return false;
   if ((size_t)n * (size_t)(k / kQ81) * 36 > kStreamXMax) return false;
-  return nrows / kUnitRows >= device_cus();
-}
-
-static size_t stream_lds(int64_t nrows, int64_t k, int n, unsigned grid) {
-  const int64_t nu_max = (nrows / kUnitRows + grid - 1) / grid;
-  const size_t part = (size_t)nu_max * kStreamWaves * n * 16 * sizeof(float);
-  return std::max(kStreamLdsMin, (size_t)n * (size_t)(k / kQ81) * 36 + part);
+  const int64_t cus = device_cus();
+  if (nrows / kUnitRows < cus) return false;
+  return stream_lds(nrows, k, n, cus) <= kStreamLdsMax;
 }
 
 template <int NC, int XDT, int XPT>
@@ -528,12 +546,13 @@ static void launch_stream_k(const uint8_t* W, int64_t row_bytes, int nrows, int 
                             void* y, int y_dtype, hipStream_t stream) {
   const unsigned g = (unsigned)std::min<int64_t>(nrows / kUnitRows, device_cus());
   const size_t lds = stream_lds(nrows, k, NC, g);
-  static bool attr_set[64] = {false};
   int dev = 0;
-  if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64 && !attr_set[dev]) {
-    (void)hipFuncSetAttribute((const void*)gemv_iq3s_stream_kernel<NC, XDT, XPT>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - (int)sizeof(uint4) * 2049);
-    attr_set[dev] = true;
+  if (hipGetDevice(&dev) == hipSuccess) {
+    struct Tag;  // one set of per-device flags per kernel instantiation
+    once_per_device<Tag>(dev, [] {
+      (void)hipFuncSetAttribute((const void*)gemv_iq3s_stream_kernel<NC, XDT, XPT>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)kStreamLdsMax);
+    });
   }
   gemv_iq3s_stream_kernel<NC, XDT, XPT><<<g, 64 * kStreamWaves, lds, stream>>>(W, row_bytes, nrows, k, x, s01, y,
                                                                               y_dtype);

@@ -13,6 +13,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+#include <mutex>
+
 namespace gguf {
 
 // ggml type ids (gguf GGMLQuantizationType)
@@ -408,17 +411,44 @@ __device__ __forceinline__ int iq4nl(uint32_t q, int sh) {
   return (int)((hi & sel) | (lo & ~sel));
 }
 
+// Per-device one-time set-up (device queries, kernel attributes) runs lazily, on a product's first
+// call on a device, and that call may be made inside a caller's stream capture (a CUDA-graph
+// capture in torch). The set-up is run with this thread's capture mode exchanged for relaxed, so
+// that no capture in global mode (torch's default) rejects it, and is restored afterwards. The
+// reference makes the same first-call-in-capture promise (lcpp_owned_iq3_mma.cu:333-346,
+// lcpp_owned_mma_k.cu:551-569).
+template <class F>
+inline void outside_capture(F&& fn) {
+  hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+  const bool swapped = hipThreadExchangeStreamCaptureMode(&mode) == hipSuccess;
+  fn();
+  if (swapped) (void)hipThreadExchangeStreamCaptureMode(&mode);
+}
+
+constexpr int kMaxDevices = 64;
+
+// fn() once per device (device index dev < kMaxDevices), thread-safe: concurrent first calls from
+// several host threads run it once and the others wait for it.
+template <class Tag, class F>
+inline void once_per_device(int dev, F&& fn) {
+  static std::once_flag flags[kMaxDevices];
+  if (dev < 0 || dev >= kMaxDevices) return;
+  std::call_once(flags[dev], [&] { outside_capture(fn); });
+}
+
 // compute units of the current device (256 on MI355X; 256 when the query fails), cached per device
 inline int device_cus() {
-  static int cus[64] = {0};
+  static std::atomic<int> cus[kMaxDevices];  // zero-initialised (static storage)
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cus[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cus[dev] = n;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    outside_capture([&] {
+      if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    });
+    cus[dev].store(n, std::memory_order_relaxed);  // every thread that races here stores the same value
   }
-  return cus[dev];
+  return n;
 }
 
 }  // namespace gguf

@@ -4,8 +4,9 @@
 // allocates the output and the workspace with torch's caching allocator on X's device (so calls
 // are safe under graph capture), and calls the library on torch's current stream.
 //
-// Same namespace, op names and schemas as the reference. Implementations are registered for
-// CUDA (HIP tensors on ROCm) and, as in the reference (lcpp_shim.cu:997-1008), for CPU, where
+// Same namespace (registered as a fragment), op names and schemas as the reference.
+// Implementations are registered for CUDA (HIP tensors on ROCm) and, as in the reference
+// (lcpp_shim.cu:997-1008), for CPU, where
 // the library runs every guard and the call ends with "must be CUDA tensors". A guard that
 // fails raises RuntimeError with the library's message (the reference's message fragments, in
 // its order). The fake (meta) implementations for torch.compile are registered from Python
@@ -126,7 +127,10 @@ at::Tensor quantize_q8_1(const at::Tensor& X, int64_t type, bool mmq, bool vendo
 
 }  // namespace
 
-TORCH_LIBRARY(_C_gguf, m) {
+// A fragment of the namespace, as the reference adds its Route L ops to the _C_gguf library of its
+// stock ops (lcpp_shim.cu:973 beside torch_bindings.cpp:22): this registration loads beside any
+// other library that defines _C_gguf (the stock extension's ggml_dequantize, for one).
+TORCH_LIBRARY_FRAGMENT(_C_gguf, m) {
   m.def("lcpp_mul_mat_vec_q(Tensor W, Tensor X, int type, SymInt row, Tensor? x_q8=None) -> Tensor");
   m.def("lcpp_mul_mat_q(Tensor W, Tensor X, int type, SymInt row) -> Tensor");
   m.def("lcpp_mul_mat_vec_iq3(Tensor W, Tensor X, int type, SymInt row, Tensor? x_q8=None) -> Tensor");
