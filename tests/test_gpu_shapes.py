@@ -84,6 +84,21 @@ def test_full_size_iq3s_down_exact_integer():
         np.testing.assert_array_equal(y.astype(np.int64), exact_ref(raw, o.IQ3_S, x), err_msg=f"n={n}")
 
 
+@pytest.mark.parametrize("n", [3, 4])
+def test_stream_lds_limit(n):
+    """53264 x 5120 (13316 units, 53 per CU at 256 CUs): at 4 rows X's q8_1 and the partial-sum
+    slots of 53 units need 131,584 B of dynamic LDS, more than the 131,056 B a workgroup may take
+    beside the table, so the decode op takes the one-tile GEMV; at 3 rows (98,688 B) the stream
+    GEMV. Sampled rows against the q81 model, bf16 X."""
+    rows, k = 53264, 5120
+    raw = w_rand(o.IQ3_S, rows, k, seed=90 + n)
+    w = _pack(dev(raw))
+    x = x_rand(n, k, seed=91 + n, dtype=torch.bfloat16)
+    y = C().lcpp_mul_mat_vec_iq3_mma_packed(w, x.cuda(), o.IQ3_S, rows).float().cpu().numpy()
+    rs = _sampled(rows, 768, seed=92 + n)
+    assert o.rel_l2(y[:, rs], o.q81_model(raw[rs], o.IQ3_S, x)) <= TIGHT[torch.bfloat16]
+
+
 # ------------------------------------------------------------------------------------ tile GEMM, 4 waves
 # The packed IQ3_S GEMM runs one column tile (up to 16 activation rows) with four K-splitting
 # waves per 16-row tile on weights of 512 tiles or more (8192 rows), eight waves below.

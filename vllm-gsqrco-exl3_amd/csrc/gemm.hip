@@ -570,7 +570,8 @@ __global__ void __launch_bounds__(64 * KS) gemm_generic_kernel(const uint8_t* __
   const int nb = k / kQK;
   const int b_begin = wave * nb / KS, b_end = (wave + 1) * nb / KS;
   // rows past nrows, and the copy's read past the tile's last block-row, lie past the
-  // descriptor's size and read zeros
+  // descriptor's size and read zeros: the block's byte offset goes into the lane offset, which
+  // the hardware range check covers (a scalar offset is not checked)
   const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(W + (int64_t)row0 * row_bytes, (uint32_t)(rows_here * row_bytes));
   const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(xq, (uint32_t)xq_bytes((int64_t)nct * kXqCols, k));
   const int sbase = (int)xq_scale_base(nct, nb);
@@ -589,8 +590,9 @@ __global__ void __launch_bounds__(64 * KS) gemm_generic_kernel(const uint8_t* __
 
   auto load_rows = [&](int b, u32x4 (&r)[2]) {
     const int bb = b < b_end ? b : b_end - 1;  // past the wave's range: re-read its last block
-    r[0] = __builtin_amdgcn_raw_buffer_load_b128(wrs, copy_off, (bb * BS) & ~3, 0);
-    r[1] = __builtin_amdgcn_raw_buffer_load_b128(wrs, copy_off + 16, (bb * BS) & ~3, 0);
+    const int bo = (bb * BS) & ~3;
+    r[0] = __builtin_amdgcn_raw_buffer_load_b128(wrs, copy_off + bo, 0, 0);
+    r[1] = __builtin_amdgcn_raw_buffer_load_b128(wrs, copy_off + bo + 16, 0, 0);
   };
   // the block lands at byte 2 of its staged row whatever its alignment in W, so that its 4-byte
   // fields (at 2 mod 4 in every format here) are aligned LDS words
