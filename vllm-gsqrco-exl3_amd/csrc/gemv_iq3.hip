@@ -454,7 +454,8 @@ __global__ void __launch_bounds__(64 * NW) gemv_iq3s_stream_kernel(const uint8_t
       const uint4 a0 = *(const uint4*)(xq + o * 8), a1 = *(const uint4*)(xq + o * 8 + 4);
       x.q[c][0] = (int)a0.x; x.q[c][1] = (int)a0.y; x.q[c][2] = (int)a0.z; x.q[c][3] = (int)a0.w;
       x.q[c][4] = (int)a1.x; x.q[c][5] = (int)a1.y; x.q[c][6] = (int)a1.z; x.q[c][7] = (int)a1.w;
-      x.d[c] = live ? xd[o] : 0u;
+      const uint32_t dv = xd[o];  // read unconditionally (o is in range) and selected: no branch
+      x.d[c] = live ? dv : 0u;
     }
     TileFrag f = fc;
     f.dd = live ? f.dd : 0u;
@@ -532,7 +533,9 @@ constexpr size_t kStreamLdsMax = 160 * 1024 - kStreamStaticLds;  // the dynamic 
 // The stream kernel takes 1..4 activation rows (fused X: 1..2 rows at K <= 8192) on weights of
 // at least one 4-row unit per CU, with X's q8_1 and the partial sums within its LDS budget (a
 // weight of many units per CU at 3-4 rows needs more partial-sum slots than fit: such shapes take
-// the tile kernel).
+// the tile kernel). Quantising X in every workgroup costs more than the quantise launch at 3-4
+// rows (17408 x 5120, M = 4: 19.5 against 18.3 us) and at K = 17408 (5120 x 17408, M = 1: 13.5
+// against 12.8 us): those take the q8_1 path.
 static bool stream_supported(int64_t nrows, int64_t k, int64_t n, bool fused) {
   if (n < 1 || n > (fused ? 2 : 4) || (fused && k > 8192)) return false;
   if ((size_t)n * (size_t)(k / kQ81) * 36 > kStreamXMax) return false;
