@@ -384,8 +384,11 @@ def measured_peaks(torch, reps=5):
       reads; graph replays of one launch per buffer over rotation_copies buffers (beyond the
       MALL), HIP events; the fastest of a sweep of launch shapes (workgroups x threads x loads in
       flight x cache policy), with the shape that gave it;
-    * MFMA peak: 2048 workgroups of 4 waves, each wave 8 independent chains of MFMAs with register
-      operands: v_mfma_i32_16x16x64_i8 (int8 TOP/s) and v_mfma_f32_16x16x32_f16 (TFLOP/s)."""
+    * MFMA peak: 2048 workgroups of 4 waves, each wave 8 MFMAs per iteration in independent
+      chains with register operands, one kernel per shape: v_mfma_i32_16x16x64_i8,
+      v_mfma_f32_16x16x32_f16 (the shapes the GEMMs use), the 32 x 32 shapes
+      v_mfma_i32_32x32x32_i8 and v_mfma_f32_32x32x16_f16, v_mfma_i32_16x16x32_i8,
+      v_mfma_i32_4x4x4_16b_i8, and v_dot4_i32_i8 on the VALU (TOP/s or TFLOP/s)."""
     import ctypes
 
     lib = ctypes.CDLL(PEAKS_LIB)
@@ -401,9 +404,9 @@ def measured_peaks(torch, reps=5):
         stride = (nbytes + 255) // 256 * 256
         pool = torch.randint(0, 256, (nbuf * stride,), dtype=torch.uint8, device="cuda")
         best = None
-        for grid in (256, 512, 1024):
+        for grid in (256, 512, 1024, 2048):
             for threads in (256, 512, 1024):
-                for unroll in (2, 4):
+                for unroll in (1, 2, 4, 8):
                     for nt in (0, 1):
                         def call(i, grid=grid, threads=threads, unroll=unroll, nt=nt):
                             rc = lib.gguf_peak_read(pool.data_ptr() + i * stride, nbytes, grid, threads, unroll, nt,
@@ -419,7 +422,10 @@ def measured_peaks(torch, reps=5):
                                   "shape": f"{grid}x{threads} u{unroll}{' nt' if nt else ''}"})
         del pool
     grid, iters = 2048, 2000
-    for kind, name, per in ((0, "i8_16x16x64_tops", 32768), (1, "f16_16x16x32_tflops", 16384)):
+    for kind, name, per in ((0, "i8_16x16x64_tops", 32768), (1, "f16_16x16x32_tflops", 16384),
+                            (2, "i8_32x32x32_tops", 65536), (3, "f16_32x32x16_tflops", 32768),
+                            (4, "i8_16x16x32_tops", 16384), (5, "i8_4x4x4_16b_tops", 2048),
+                            (6, "valu_dot4_i8_tops", 512)):
         def mcall(kind=kind):
             rc = lib.gguf_peak_mfma(kind, grid, iters, key, sink.data_ptr(), torch.cuda.current_stream().cuda_stream)
             assert rc == 0, rc
@@ -533,7 +539,7 @@ def main():
     ap.add_argument("--no-points", action="store_true", help="skip the metric's other (type, M) points")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the other benchmark configs (CPU Q4_K, MTP small GEMM, prefill, 64-layer sweep)")
-    ap.add_argument("--section", choices=["mtp", "prefill", "layers", "types"],
+    ap.add_argument("--section", choices=["mtp", "prefill", "layers", "types", "peaks"],
                     help="run only this benchmark config and print its JSON (for rocprofv3 counter runs)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-peaks", action="store_true", help="skip the measured read floor and MFMA peak")
@@ -559,6 +565,7 @@ def main():
         fn = {"mtp": lambda: config_mtp(torch, C, iq3_pack, linear),
               "prefill": lambda: config_prefill(torch, C, iq3_pack, linear),
               "types": lambda: config_types(torch, C, iq3_pack, linear),
+              "peaks": lambda: measured_peaks(torch),
               "layers": lambda: {"layer_sweep_64": config_layers(torch, C, iq3_pack, linear, args.steps),
                                  "layer_sweep_64_runs": config_layers(torch, C, iq3_pack, linear, args.steps,
                                                                       merged=True)}}[args.section]
@@ -659,7 +666,10 @@ def main():
         line["points_us"] = {TYPE_NAME[qt]: {str(p["m"]): p["us_per_call"] for p in points
                                              if p["type"] == TYPE_NAME[qt]} for qt in (IQ3_S, Q4_K)}
     if peaks is not None:
-        line["measured_peaks"] = {"read_floor_gbps": [f["gbps"] for f in peaks["read_floor"]], **peaks["mfma"]}
+        line["measured_peaks"] = {"read_floor_gbps": [f["gbps"] for f in peaks["read_floor"]],
+                                  **{k: v for k, v in peaks["mfma"].items()
+                                     if k in ("i8_16x16x64_tops", "f16_16x16x32_tflops", "i8_32x32x32_tops",
+                                              "f16_32x32x16_tflops")}}
     print(json.dumps(line, separators=(",", ":")), flush=True)
 
 

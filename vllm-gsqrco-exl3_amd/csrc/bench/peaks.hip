@@ -6,9 +6,9 @@
 //    pattern of the decode GEMV (each workgroup reads one contiguous equal share with 16-byte
 //    buffer loads, U loads in flight per lane, optionally non-temporal), so that its time is the
 //    floor of a weight-streaming launch of that size: launch and ramp included.
-//  * gguf_peak_mfma: chains of independent MFMAs with operands in registers and no memory traffic
-//    (v_mfma_i32_16x16x64_i8, the gfx950 double-rate int8 shape, or v_mfma_f32_16x16x32_f16),
-//    for the dense MFMA rate the prefill GEMMs are priced against.
+//  * gguf_peak_mfma: chains of independent MFMAs (or v_dot4 on the VALU) with operands in
+//    registers and no memory traffic, one kernel per instruction shape: the dense MFMA rate each
+//    shape sustains, for the rate the GEMMs are priced against.
 // Results are kept live by a store that the data never triggers (the sum compared with a value
 // the host passes), so no load or MFMA is dropped by the compiler.
 #include <hip/hip_runtime.h>
@@ -20,6 +20,9 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
@@ -84,6 +87,73 @@ __global__ void __launch_bounds__(256) mfma_f16_kernel(int iters, int key, int* 
   if (__float_as_int(s) == key) sink[blockIdx.x * blockDim.x + threadIdx.x] = __float_as_int(s);
 }
 
+// the other shapes: K selects the instruction (see gguf_peak_mfma)
+template <int K>
+__global__ void __launch_bounds__(256) mfma_shape_kernel(int iters, int key, int* __restrict__ sink) {
+  int s = 0;
+  if constexpr (K == 2) {  // v_mfma_i32_32x32x32_i8: 4 chains of 16 accumulators
+    const i32x4 a = {(int)threadIdx.x, 1, 2, 3}, b = {(int)blockIdx.x, 5, 6, 7};
+    i32x16 c[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      c[i] = (i32x16){};
+      c[i][0] = i;
+    }
+    for (int it = 0; it < iters; ++it)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) c[i & 3] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c[i & 3], 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s += c[i][0] + c[i][15];
+  } else if constexpr (K == 3) {  // v_mfma_f32_32x32x16_f16
+    const _Float16 t = (_Float16)(threadIdx.x & 7) * (_Float16)0.125f;
+    const f16x8 a = {t, t, t, t, t, t, t, t}, b = {(_Float16)1.0f, t, t, t, t, t, t, (_Float16)0.5f};
+    f32x16 c[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      c[i] = (f32x16){};
+      c[i][0] = (float)i;
+    }
+    for (int it = 0; it < iters; ++it)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) c[i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c[i & 3], 0, 0, 0);
+    float f = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f += c[i][0] + c[i][15];
+    s = __float_as_int(f);
+  } else if constexpr (K == 4) {  // v_mfma_i32_16x16x32_i8
+    const long a = threadIdx.x, b = blockIdx.x * 3 + 1;
+    i32x4 c[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) c[i] = (i32x4){i, 0, 0, 0};
+    for (int it = 0; it < iters; ++it)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) c[i] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c[i], 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s += c[i].x + c[i].w;
+  } else if constexpr (K == 5) {  // v_mfma_i32_4x4x4_16b_i8
+    const int a = threadIdx.x, b = blockIdx.x * 3 + 1;
+    i32x4 c[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) c[i] = (i32x4){i, 0, 0, 0};
+    for (int it = 0; it < iters; ++it)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) c[i] = __builtin_amdgcn_mfma_i32_4x4x4i8(a, b, c[i], 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s += c[i].x + c[i].w;
+  } else {  // v_dot4_i32_i8 on the VALU
+    const int a = threadIdx.x, b = blockIdx.x * 3 + 1;
+    int c[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) c[i] = i;
+    for (int it = 0; it < iters; ++it)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) c[i] = __builtin_amdgcn_sdot4(a, b, c[i], false);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s += c[i];
+  }
+  if (s == key) sink[blockIdx.x * blockDim.x + threadIdx.x] = s;
+}
+
 }  // namespace
 
 extern "C" {
@@ -115,15 +185,26 @@ __attribute__((visibility("default"))) int gguf_peak_read(const void* src, uint6
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 
-// kind 0: v_mfma_i32_16x16x64_i8 (32,768 int8 ops each), kind 1: v_mfma_f32_16x16x32_f16 (16,384
-// flops each). grid workgroups of 4 waves, each wave 8 chains x iters MFMAs. sink: grid * 256 int.
+// grid workgroups of 4 waves, each wave 8 instructions x iters (8 independent chains; 4 chains
+// for the 32 x 32 shapes). Operations per instruction: kind 0 v_mfma_i32_16x16x64_i8 32,768;
+// 1 v_mfma_f32_16x16x32_f16 16,384; 2 v_mfma_i32_32x32x32_i8 65,536; 3 v_mfma_f32_32x32x16_f16
+// 32,768; 4 v_mfma_i32_16x16x32_i8 16,384; 5 v_mfma_i32_4x4x4_16b_i8 2,048; 6 v_dot4_i32_i8
+// 512 (64 lanes x 4 multiply-adds). sink: grid * 256 int.
 __attribute__((visibility("default"))) int gguf_peak_mfma(int kind, int grid, int iters, int key, void* sink,
                                                          void* stream) {
   if (!sink || grid < 1 || iters < 1) return 1;
   hipStream_t s = (hipStream_t)stream;
-  if (kind == 0) mfma_i8_kernel<8><<<grid, 256, 0, s>>>(iters, key, (int*)sink);
-  else if (kind == 1) mfma_f16_kernel<8><<<grid, 256, 0, s>>>(iters, key, (int*)sink);
-  else return 1;
+  int* k = (int*)sink;
+  switch (kind) {
+    case 0: mfma_i8_kernel<8><<<grid, 256, 0, s>>>(iters, key, k); break;
+    case 1: mfma_f16_kernel<8><<<grid, 256, 0, s>>>(iters, key, k); break;
+    case 2: mfma_shape_kernel<2><<<grid, 256, 0, s>>>(iters, key, k); break;
+    case 3: mfma_shape_kernel<3><<<grid, 256, 0, s>>>(iters, key, k); break;
+    case 4: mfma_shape_kernel<4><<<grid, 256, 0, s>>>(iters, key, k); break;
+    case 5: mfma_shape_kernel<5><<<grid, 256, 0, s>>>(iters, key, k); break;
+    case 6: mfma_shape_kernel<6><<<grid, 256, 0, s>>>(iters, key, k); break;
+    default: return 1;
+  }
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 
