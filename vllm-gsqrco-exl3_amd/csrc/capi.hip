@@ -42,6 +42,7 @@ bool gemv_packed_x_supported(int64_t nrows, int64_t k, int64_t n);
 hipError_t launch_gemv_rows_x(int type, const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x,
                               int x_dtype, int64_t s01, int n, void* y, int y_dtype, hipStream_t stream);
 bool gemv_rows_x_supported(int type, int64_t nrows, int64_t row_bytes, int64_t k, int64_t n);
+bool gemv_mfma4_supported(int type, int64_t nrows, int64_t row_bytes, int64_t k, int64_t n);
 hipError_t launch_gemm_packed_xq(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n,
                                  void* y, int y_dtype, void* split_ws, hipStream_t stream);
 hipError_t launch_quantize_xh(const void* x, int dtype, int64_t n, int64_t k, int64_t s01, int type, void* y,
@@ -259,17 +260,31 @@ int64_t vec_mma_from(int op, int64_t type) {
   return INT64_MAX;
 }
 
+// Bytes per 256-value block of the GGUF-row types with a row-chunk GEMV (0 for the others).
+int64_t rows_block_bytes(int64_t type) {
+  return type == gguf::kQ4_K ? 144 : type == gguf::kQ6_K ? 210 : type == gguf::kIQ4_XS ? 136 : 0;
+}
+
+// The MFMA decode GEMV (Q4_K at 2..4 rows, gemv_mfma4.hip) on a decode op's shape.
+bool decode_mfma4(int op, int64_t type, int64_t row, int64_t k, int64_t n) {
+  const int64_t bb = rows_block_bytes(type);
+  return !op_gemm(op) && !op_packed(op) && bb > 0 && gguf::gemv_mfma4_supported((int)type, row, k / 256 * bb, k, n);
+}
+
 // A decode op runs the int8-MFMA small GEMM from vec_mma_from rows on, except at up to four rows
-// of Q4_K / IQ4_XS / Q6_K where the row-chunk GEMV takes the shape (X's q8_1 in LDS).
+// of Q4_K / IQ4_XS / Q6_K where a GEMV takes the shape (X's q8_1 in LDS): the MFMA decode GEMV
+// where it applies, else the row-chunk GEMV.
 bool decode_mma(int op, int64_t type, int64_t row, int64_t k, int64_t n) {
-  if (n < vec_mma_from(op, type)) return false;
-  const int64_t bb = type == gguf::kQ4_K ? 144 : type == gguf::kQ6_K ? 210 : type == gguf::kIQ4_XS ? 136 : 0;
+  if (n < vec_mma_from(op, type) || decode_mfma4(op, type, row, k, n)) return false;
+  const int64_t bb = rows_block_bytes(type);
   return !(op_packed(op) == false && bb > 0 && gguf::gemv_rows_supported((int)type, row, k / 256 * bb, k, n));
 }
 
 bool rows_fused(int op, int64_t type, int64_t row, int64_t k, int64_t n, bool has_x_q8) {
-  if (op_gemm(op) || op_packed(op) || has_x_q8 || decode_mma(op, type, row, k, n)) return false;
-  const int64_t bb = type == gguf::kQ4_K ? 144 : type == gguf::kQ6_K ? 210 : type == gguf::kIQ4_XS ? 136 : 0;
+  if (op_gemm(op) || op_packed(op) || has_x_q8 || decode_mma(op, type, row, k, n) ||
+      decode_mfma4(op, type, row, k, n))
+    return false;
+  const int64_t bb = rows_block_bytes(type);
   return bb > 0 && gguf::gemv_rows_x_supported((int)type, row, k / 256 * bb, k, n);
 }
 

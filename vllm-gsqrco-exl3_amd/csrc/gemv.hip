@@ -814,6 +814,10 @@ hipError_t launch_gemv_rows_x(int type, const uint8_t* W, int64_t row_bytes, int
   return hipGetLastError();
 }
 
+bool gemv_mfma4_supported(int type, int64_t nrows, int64_t row_bytes, int64_t k, int64_t n);
+hipError_t launch_gemv_mfma4(int type, const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n,
+                             void* y, int y_dtype, hipStream_t stream);
+
 // n in 1..8 activation rows; q8: block_q8_1 of X; y: [n, nrows] in y_dtype.
 hipError_t launch_gemv_raw(int type, const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n,
                            void* y, int y_dtype, hipStream_t stream) {
@@ -822,6 +826,9 @@ hipError_t launch_gemv_raw(int type, const uint8_t* W, int64_t row_bytes, int nr
   // slice pair: Q4_K 13.8 us against 16.0, and 16.9 against 20.5 on 5120 x 17408; at 3-4 rows it
   // replaces the generic GEMV and the MMA small GEMM: IQ4_XS M = 4 18.8 us against 25.6, Q6_K
   // 26.2 against 37.1 + quantise)
+  // Q4_K at 2-4 rows: the MFMA decode GEMV where it applies (gemv_mfma4.hip)
+  if (gemv_mfma4_supported(type, nrows, row_bytes, k, n))
+    return launch_gemv_mfma4(type, W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);
   bool done = false;
   if (type == kQ4_K) done = launch_rows<kQ4_K>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);
   if (type == kIQ4_XS) done = launch_rows<kIQ4_XS>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);
