@@ -237,6 +237,37 @@ def test_full_size_decode(qt, n):
     assert np.isfinite(y).all()
 
 
+# the stream GEMV (gemv_generic_stream_kernel: 1-4 rows, rows % 4 == 0, a 4-row unit per CU or
+# more): one unit per CU at 256 CUs with two block pairs; 516 units (2 or 3 per CU); K = 17408
+# (34 block pairs per unit)
+STREAM_SHAPES = [(1024, 1024), (2064, 2560), (1024, 17408)]
+
+
+@pytest.mark.parametrize("qt", GENERIC, ids=lambda t: TN[t])
+@pytest.mark.parametrize("n", [1, 2, 3, 4])
+@pytest.mark.parametrize("rows,k", STREAM_SHAPES)
+def test_stream_decode_exact(qt, n, rows, k):
+    raw = exact_weights(qt, rows, k, seed=900 + 10 * n + qt)
+    x = exact_x(n, k, seed=901 + n, dtype=torch.float32)
+    y = C().lcpp_mul_mat_vec_q(dev(raw), x.cuda(), qt, rows).cpu().numpy()
+    np.testing.assert_array_equal(y.astype(np.float64), exact_ref(raw, qt, x, "mmvq"))
+
+
+@pytest.mark.parametrize("qt", GENERIC, ids=lambda t: TN[t])
+def test_stream_down_shape(qt):
+    """5120 x 17408 (5 units per CU, 34 block pairs) at 2 rows, bf16 X: sampled rows against the
+    q81 model; one graph replay equals the eager call."""
+    rows, k, n = 5120, 17408, 2
+    raw = w_rand(qt, rows, k, seed=950 + qt)
+    w = dev(raw)
+    x = x_rand(n, k, seed=951, dtype=torch.bfloat16).cuda()
+    y = C().lcpp_mul_mat_vec_q(w, x, qt, rows)
+    rs = np.unique(np.concatenate([[0, rows - 1], np.random.default_rng(qt).choice(rows, 254, replace=False)]))
+    assert o.rel_l2(y.float().cpu().numpy()[:, rs], o.q81_model(raw[rs], qt, x.cpu())) <= TIGHT[torch.bfloat16]
+    torch.cuda.synchronize()
+    graph_replays_equal(lambda: C().lcpp_mul_mat_vec_q(w, x, qt, rows), y)
+
+
 @pytest.mark.parametrize("qt", [o.Q2_K, o.IQ2_S, o.IQ3_XXS], ids=lambda t: TN[t])
 def test_down_shape_product(qt):
     """5120 x 17408 at 48 activation rows: sampled rows against the q81 model."""

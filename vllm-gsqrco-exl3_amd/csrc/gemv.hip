@@ -295,6 +295,174 @@ __global__ void __launch_bounds__(64 * kSlicesWaves) gemv_slices_kernel(const ui
   }
 }
 
+// The generic types at 1-4 activation rows on weights of at least one 4-row unit per CU: the
+// stream GEMV's split (gemv_iq3.hip). One workgroup per CU owns an equal run of 4-row units; its
+// items are (unit, pair of K blocks), unit-major, and each of its 8 waves a contiguous run of
+// them, so every CU reads the same number of bytes and no barrier falls inside the loop. Lane
+// l = 16r + 8kb + s decodes slice s of block kb of the pair in row r (raw_load / raw_decode, the
+// codebook in LDS): a row's 16 lanes read its two blocks' bytes contiguously and one load
+// instruction covers 4 rows. Three items are in flight while a fourth is computed. The codebook's
+// and X's loads are issued before the first weight load (a CU's loads return in order); X's
+// q8_1 goes to LDS as in gemv_slices_kernel. The slice term is mmvq_term; a lane adds its terms
+// over the wave's items of a unit, and on leaving the unit the 16 lanes of each row are summed
+// by DPP (xor 1, xor 2, half-row mirror, row mirror) into a (unit, wave) slot; the output adds
+// the slots in wave order.
+constexpr int kGsWaves = 8;
+constexpr int kGsXpt[] = {1, 2, 3, 5};  // X slices staged per thread (NC * K / 32 <= XPT * 512)
+
+template <int CTRL>
+__device__ __forceinline__ float gs_dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
+template <int TYPE, int NC, int XPT>
+__global__ void __launch_bounds__(64 * kGsWaves) gemv_generic_stream_kernel(const uint8_t* __restrict__ W,
+                                                                            int64_t row_bytes, int nrows, int k,
+                                                                            const uint8_t* __restrict__ q8,
+                                                                            void* __restrict__ y, int y_dtype) {
+  constexpr int NW = kGsWaves, NT = 64 * NW, BS = block_bytes(TYPE);
+  using CB = Codebook<TYPE>;
+  constexpr int CPT = (CB::n + NT - 1) / NT;  // codebook entries staged per thread
+  __shared__ typename CB::T grid[CB::n];
+  __shared__ uint4 sink;  // staging writes past the end
+  extern __shared__ uint4 xdyn[];
+  const int nslices = k / kQ81, nb = k / kQK, npair = nb >> 1;
+  uint32_t* xq = (uint32_t*)xdyn;               // [NC][nslices][8] q8 words
+  float* xd = (float*)(xq + NC * nslices * 8);  // [NC][nslices] d8
+  int* xs = (int*)(xd + NC * nslices);          // [NC][nslices] Q2_K: sums of the two halves
+  float* part = (float*)(xs + NC * nslices);    // [unit][wave][row][NC]
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane >> 4, kb = (lane >> 3) & 1, s = lane & 7;
+  // staging loads first: the codebook entries and X's q8_1 blocks (indices clamped into range)
+  typename CB::T cbv[CPT];
+#pragma unroll
+  for (int t = 0; t < CPT; ++t) cbv[t] = CB::at(min((int)threadIdx.x + t * NT, CB::n - 1));
+  const int nx = NC * nslices;
+  u32x4 xa[XPT], xb[XPT];
+  uint32_t xdb[XPT];
+#pragma unroll
+  for (int t = 0; t < XPT; ++t) {
+    const uint8_t* src = q8 + (int64_t)min((int)threadIdx.x + t * NT, nx - 1) * 36;
+    xdb[t] = *(const uint16_t*)src;
+    xa[t] = ld128a4(src + 4);
+    xb[t] = ld128a4(src + 20);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // the workgroup's units [u0, u1), the wave's items [j0, j1)
+  const uint32_t nunits = (uint32_t)nrows / 4, G = gridDim.x;
+  const int u0 = (int)(blockIdx.x * nunits / G), u1 = (int)((blockIdx.x + 1) * nunits / G);
+  const int nu = u1 - u0, items = nu * npair;
+  const int j0 = wave * items / NW, j1 = (wave + 1) * items / NW;
+  const int64_t ubytes = 4 * row_bytes;
+  const uint8_t* wl = W + ((int64_t)u0 * 4 + r) * row_bytes + kb * BS;  // pair 0 of the lane's row, unit u0
+  // the next item to load: unit lu, pair lp (past the run: the workgroup's last item again)
+  const int cu0 = j0 / npair;
+  int lj = j0, lu = cu0, lp = j0 - cu0 * npair;
+  auto load_next = [&](RawSlice<TYPE>& f) {
+    const bool in_run = lj < j1;
+    const int uu = in_run ? lu : nu - 1, pp = in_run ? lp : npair - 1;
+    raw_load<TYPE>(wl + (int64_t)uu * ubytes + (int64_t)pp * (2 * BS), s, f);
+    ++lj;
+    if (++lp == npair) {
+      lp = 0;
+      ++lu;
+    }
+  };
+  RawSlice<TYPE> f0, f1, f2, f3;
+  load_next(f0);
+  load_next(f1);
+  load_next(f2);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int t = 0; t < CPT; ++t) {
+    const int i = (int)threadIdx.x + t * NT;
+    if (CB::n % NT == 0 || i < CB::n) grid[i] = cbv[t];
+  }
+#pragma unroll
+  for (int t = 0; t < XPT; ++t) {
+    const int i = (int)threadIdx.x + t * NT;
+    const bool live = i < nx;
+    *(live ? (uint4*)(xq + 8 * i) : &sink) = make_uint4(xa[t][0], xa[t][1], xa[t][2], xa[t][3]);
+    *(live ? (uint4*)(xq + 8 * i + 4) : &sink) = make_uint4(xb[t][0], xb[t][1], xb[t][2], xb[t][3]);
+    *(live ? xd + i : (float*)&sink) = half_bits_to_float(xdb[t]);
+    if constexpr (TYPE == kQ2_K) {
+      int s0 = 0, s1 = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        s0 = dot4(0x01010101, (int)xa[t][e], s0);
+        s1 = dot4(0x01010101, (int)xb[t][e], s1);
+      }
+      *(live ? xs + i : (int*)&sink) = (s0 & 0xFFFF) | (s1 << 16);
+    }
+  }
+  for (int t = threadIdx.x; t < nu * NW * NC; t += NT) ((float4*)part)[t] = make_float4(0.f, 0.f, 0.f, 0.f);
+  __syncthreads();
+  float acc[NC];
+#pragma unroll
+  for (int cc = 0; cc < NC; ++cc) acc[cc] = 0.0f;
+  int cu = cu0, cp = j0 - cu0 * npair, j = j0;  // the item being computed
+  auto step = [&](const RawSlice<TYPE>& fc, RawSlice<TYPE>& fl) {
+    load_next(fl);
+    __builtin_amdgcn_sched_barrier(0);
+    int w[8];
+    SliceScale sc;
+    raw_decode<TYPE>(fc, s, grid, w, sc);
+    const int sl = (2 * cp + kb) * 8 + s;
+#pragma unroll
+    for (int cc = 0; cc < NC; ++cc) {
+      const int xi = cc * nslices + sl;
+      const uint4 x0 = *(const uint4*)(xq + 8 * xi), x1 = *(const uint4*)(xq + 8 * xi + 4);
+      const int xv[8] = {(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+      int sq = 0, sq2 = 0;
+      if constexpr (TYPE == kQ2_K) {
+        const int hsum = xs[xi];
+        sq = (int)(int16_t)(hsum & 0xFFFF);
+        sq2 = hsum >> 16;
+      }
+      acc[cc] += mmvq_term<TYPE>(w, xv, sc, xd[xi], sq, sq2);
+    }
+    ++j;
+    if (++cp == npair || j == j1) {  // leaving the unit: the row sums to the wave's slot
+      const int slot = cu * NW + wave;
+#pragma unroll
+      for (int cc = 0; cc < NC; ++cc) {
+        float v = acc[cc];
+        v += gs_dpp<0xB1>(v);   // quad xor 1
+        v += gs_dpp<0x4E>(v);   // quad xor 2
+        v += gs_dpp<0x141>(v);  // half-row mirror: the other quad of the 8
+        v += gs_dpp<0x140>(v);  // row mirror: the other 8 of the 16
+        if ((lane & 15) == 0) part[(slot * 4 + r) * NC + cc] = v;
+        acc[cc] = 0.0f;
+      }
+      if (cp == npair) {
+        cp = 0;
+        ++cu;
+      }
+    }
+  };
+  const int nmine = j1 - j0;
+  int i = 0;
+  for (; i + 4 <= nmine; i += 4) {
+    step(f0, f3);
+    step(f1, f0);
+    step(f2, f1);
+    step(f3, f2);
+  }
+  if (i < nmine) step(f0, f3);
+  if (i + 1 < nmine) step(f1, f0);
+  if (i + 2 < nmine) step(f2, f1);
+  __syncthreads();
+  const int nout = nu * 4 * NC;
+  for (int t = threadIdx.x; t < nout; t += NT) {
+    const int uu = t / (4 * NC), cc = (t >> 2) % NC, row = t & 3;
+    float v = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) v += part[((uu * NW + w) * 4 + row) * NC + cc];
+    store_y(y, (int64_t)cc * nrows + (int64_t)(u0 + uu) * 4 + row, v, y_dtype);
+  }
+}
+
 // X of the row-chunk GEMV, staged in LDS: q8 values [NC][slice][8 dwords], then (d8, sum of q)
 // [NC][slice]. Group g = part g & 3 (8 q bytes) of slice row g >> 2 of the block_q8_1 array; the
 // four lanes of a slice are consecutive, so the slice's sum of q is a quad sum (DPP).
@@ -361,11 +529,17 @@ struct RowsFrag<kIQ4_XS> {
   uint2 hdr[2];  // d | scales_h << 16, scales_l
   u32x4 qs[2];
 };
+// Q6_K blocks are 210 bytes: every odd block starts 2 bytes past a dword boundary, and 16-byte
+// loads there are split by the memory pipeline. The lane loads the dword-aligned 16 bytes at or
+// 2 below each 16-byte field (mis = 2 on odd blocks, wave-uniform) and the dword after them, and
+// takes the field with a byte align; the two scale bytes and d come from byte and 16-bit loads.
 template <>
 struct RowsFrag<kQ6_K> {
-  u32x4 ql[2], qh[2];
-  uint2 sc[2];  // scales[8n .. 8n + 8)
-  uint32_t d;   // fp16 d of row r | of row 8 + r << 16
+  u32x4 ql[2], qh[2];      // from ql[16c - mis], qh[32n + 16h - mis]
+  uint32_t qlx[2], qhx[2];  // the dword after each
+  uint8_t s0[2], s1[2];     // scales[8n + 2t + h], scales[8n + 4 + 2t + h]
+  uint16_t d[2];            // fp16 d of rows r, 8 + r
+  uint32_t mis;
 };
 
 // PH (kp_arg > 1): X's q8_1 does not fit the LDS budget, so K runs in kp phases of whole blocks;
@@ -407,7 +581,6 @@ __global__ void __launch_bounds__(64 * WPT) gemv_rows_kernel(const uint8_t* __re
     const __amdgpu_buffer_rsrc_t rs = t < ntiles ? wrs : nrs;
     const int t0 = (t < ntiles ? t : 0) * TR;
     const int bo = b * BS;
-    uint32_t d16[2] = {0u, 0u};
 #pragma unroll
     for (int i = 0; i < RPL; ++i) {
       const int o = min(t0 + 8 * i + r, nrows - 1) * (int)row_bytes;
@@ -418,16 +591,18 @@ __global__ void __launch_bounds__(64 * WPT) gemv_rows_kernel(const uint8_t* __re
         const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, o, bo, 0);
         f.hdr[i] = make_uint2(v[0], v[1]);
         f.qs[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 8 + 16 * c, bo, 0);
-      } else {
-        const int n = c >> 2;
-        f.ql[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 16 * c, bo, 0);
-        f.qh[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 128 + 16 * (2 * n + h), bo, 0);
-        const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, o + 192 + 8 * n, bo, 0);
-        f.sc[i] = make_uint2(v[0], v[1]);
-        d16[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, o + 208, bo, 0);
+      } else {  // row_bytes % 4 == 0 (an even number of blocks): mis = 2 on odd blocks
+        const int n = c >> 2, sb = (c >> 1 & 1) * 2 + h, mis = bo & 3;
+        f.ql[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 16 * c, bo - mis, 0);
+        f.qlx[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, o + 16 * c + 16, bo - mis, 0);
+        f.qh[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 128 + 16 * (2 * n + h), bo - mis, 0);
+        f.qhx[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, o + 144 + 16 * (2 * n + h), bo - mis, 0);
+        f.s0[i] = __builtin_amdgcn_raw_buffer_load_b8(rs, o + 192 + 8 * n + sb, bo, 0);
+        f.s1[i] = __builtin_amdgcn_raw_buffer_load_b8(rs, o + 196 + 8 * n + sb, bo, 0);
+        f.d[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, o + 208, bo, 0);
+        f.mis = (uint32_t)mis;
       }
     }
-    if constexpr (TYPE == kQ6_K) f.d = (d16[0] & 0xFFFFu) | (d16[1] << 16);
   };
   // phase p: blocks [ph0(p), ph0(p + 1)); this wave's part of it: [wb(p), we(p))
   auto ph0 = [&](int pp) { return pp * nb / kp; };
@@ -564,7 +739,7 @@ __global__ void __launch_bounds__(64 * WPT) gemv_rows_kernel(const uint8_t* __re
 #pragma unroll
           for (int e = 0; e < 4; ++e) sumi = dot4(iq4nl(f.qs[i][e], 4), xv[4 + e], sumi);
           const int ls = (int)(((f.hdr[i].y >> (4 * c)) & 0xF) | (((f.hdr[i].x >> (16 + 2 * c)) & 3u) << 4)) - 32;
-          acc[i][cc] = fmaf(half_bits_to_float(f.hdr[i].x & 0xFFFF) * (float)(sumi * ls), d8, acc[i][cc]);
+          acc[i][cc] = fmaf(half_bits_to_float(f.hdr[i].x & 0xFFFF) * (float)__mul24(sumi, ls), d8, acc[i][cc]);
         }
       } else {
         const uint4 x1 = *(const uint4*)(xq + s1 * 8 + 4 * h), x2 = *(const uint4*)(xq + s2 * 8 + 4 * h);
@@ -597,16 +772,16 @@ __global__ void __launch_bounds__(64 * WPT) gemv_rows_kernel(const uint8_t* __re
             const int sx1 = (int)(int16_t)((hs1 >> (16 * h)) & 0xFFFFu), sx2 = (int)(int16_t)((hs2 >> (16 * h)) & 0xFFFFu);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              const uint32_t l = f.ql[i][e], q = f.qh[i][e];
+              const uint32_t l = __builtin_amdgcn_alignbyte(e < 3 ? f.ql[i][e + 1] : f.qlx[i], f.ql[i][e], f.mis);
+              const uint32_t q = __builtin_amdgcn_alignbyte(e < 3 ? f.qh[i][e + 1] : f.qhx[i], f.qh[i][e], f.mis);
               const int w1 = (int)((l & 0x0F0F0F0Fu) | (__builtin_amdgcn_alignbit(q, q, (t2 + 28) & 31) & 0x30303030u));
               const int w2 = (int)(((l >> 4) & 0x0F0F0F0Fu) | (__builtin_amdgcn_alignbit(q, q, t2 & 31) & 0x30303030u));
               a1 = dot4(w1, xv1[e], a1);
               a2 = dot4(w2, xv2[e], a2);
             }
-            const int sc1 = (int)(int8_t)((f.sc[i].x >> (8 * ((c >> 1 & 1) * 2 + h))) & 0xFF);  // 8n + 2t + h
-            const int sc2 = (int)(int8_t)((f.sc[i].y >> (8 * ((c >> 1 & 1) * 2 + h))) & 0xFF);  // and 4 above
-            const int tot = join((a1 - 32 * sx1) * sc1, (a2 - 32 * sx2) * sc2);
-            const float dr = half_bits_to_float((f.d >> (16 * i)) & 0xFFFFu);
+            const int sc1 = (int)(int8_t)f.s0[i], sc2 = (int)(int8_t)f.s1[i];  // 8n + 2t + h, and 4 above
+            const int tot = join(__mul24(a1 - 32 * sx1, sc1), __mul24(a2 - 32 * sx2, sc2));  // 24-bit operands
+            const float dr = half_bits_to_float(f.d[i]);
             acc[i][cc] = fmaf(dr * (float)tot, d8, acc[i][cc]);
           }
         }
@@ -780,10 +955,76 @@ static void launch_slices(const uint8_t* W, int64_t row_bytes, int nrows, int k,
 #undef GGUF_SLICES
 }
 
+// The generic stream GEMV: X slices staged per thread, its dynamic LDS (X, then the partial-sum
+// slots of the most units a workgroup takes) and the most it may take beside the codebook.
+static int gs_xpt(int64_t k, int64_t n) {
+  const int64_t need = (n * (k / kQ81) + 511) / 512;
+  for (int x : kGsXpt)
+    if (x >= need) return x;
+  return 0;
+}
+
+static size_t gs_lds(int64_t nrows, int64_t k, int64_t n, int64_t grid) {
+  const int64_t units = (nrows / 4 + grid - 1) / grid;
+  return (size_t)(n * (k / kQ81) * 40 + units * kGsWaves * 4 * n * 4);
+}
+
+// 256 bytes are left for the alignment padding of the static arrays (the codebook and the 16-byte
+// sink); static plus dynamic LDS must stay within the 160 KB a workgroup may take.
+template <int TYPE>
+constexpr size_t gs_lds_max() {
+  return 160 * 1024 - sizeof(typename Codebook<TYPE>::T) * Codebook<TYPE>::n - 256;
+}
+
+template <int TYPE>
+static bool gs_supported(int64_t nrows, int64_t row_bytes, int64_t k, int64_t n) {
+  if (!generic_type(TYPE) || n < 1 || n > 4 || nrows % 4 != 0 || k % 512 != 0) return false;
+  if (row_bytes != k / kQK * block_bytes(TYPE) || gs_xpt(k, n) == 0) return false;
+  const int64_t cus = device_cus();
+  return nrows / 4 >= cus && gs_lds(nrows, k, n, cus) <= gs_lds_max<TYPE>();
+}
+
+template <int TYPE, int NC, int XPT>
+static void launch_gs_x(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, void* y,
+                        int y_dtype, hipStream_t stream) {
+  const int cus = device_cus();
+  const size_t lds = gs_lds(nrows, k, NC, cus);
+  int dev = 0;
+  if (lds > 64 * 1024 && hipGetDevice(&dev) == hipSuccess) {
+    struct Tag;
+    once_per_device<Tag>(dev, [] {
+      (void)hipFuncSetAttribute((const void*)gemv_generic_stream_kernel<TYPE, NC, XPT>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)gs_lds_max<TYPE>());
+    });
+  }
+  gemv_generic_stream_kernel<TYPE, NC, XPT><<<cus, 64 * kGsWaves, lds, stream>>>(W, row_bytes, nrows, k, q8, y,
+                                                                                 y_dtype);
+}
+
+template <int TYPE, int NC>
+static void launch_gs_nc(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, void* y,
+                         int y_dtype, hipStream_t stream) {
+  switch (gs_xpt(k, NC)) {
+    case 1: launch_gs_x<TYPE, NC, 1>(W, row_bytes, nrows, k, q8, y, y_dtype, stream); break;
+    case 2: launch_gs_x<TYPE, NC, 2>(W, row_bytes, nrows, k, q8, y, y_dtype, stream); break;
+    case 3: launch_gs_x<TYPE, NC, 3>(W, row_bytes, nrows, k, q8, y, y_dtype, stream); break;
+    default: launch_gs_x<TYPE, NC, 5>(W, row_bytes, nrows, k, q8, y, y_dtype, stream); break;
+  }
+}
+
 template <int TYPE>
 static void launch_type(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n, void* y,
                         int y_dtype, hipStream_t stream) {
   if constexpr (generic_type(TYPE)) {
+    if (gs_supported<TYPE>(nrows, row_bytes, k, n)) {
+      switch (n) {
+        case 1: launch_gs_nc<TYPE, 1>(W, row_bytes, nrows, k, q8, y, y_dtype, stream); break;
+        case 2: launch_gs_nc<TYPE, 2>(W, row_bytes, nrows, k, q8, y, y_dtype, stream); break;
+        case 3: launch_gs_nc<TYPE, 3>(W, row_bytes, nrows, k, q8, y, y_dtype, stream); break;
+        default: launch_gs_nc<TYPE, 4>(W, row_bytes, nrows, k, q8, y, y_dtype, stream); break;
+      }
+      return;
+    }
     if (slices_supported(TYPE, k, n)) {
       launch_slices<TYPE>(W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);
       return;
