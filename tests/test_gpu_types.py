@@ -254,6 +254,24 @@ def test_stream_decode_exact(qt, n, rows, k):
 
 
 @pytest.mark.parametrize("qt", GENERIC, ids=lambda t: TN[t])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16], ids=str)
+@pytest.mark.parametrize("n", [1, 2])
+def test_stream_fused_quantisation(qt, dtype, n):
+    """At 1-2 rows and K <= 8192 the stream GEMV quantises X itself: bit-identical to the q8_1
+    quantiser followed by the GEMV (the op given x_q8), for each X dtype, on X as rows of a wider
+    tensor (row stride above K) with an all-zero slice (d = 0)."""
+    rows, k = 2064, 5120
+    w = dev(w_rand(qt, rows, k, seed=960 + qt))
+    wide = x_rand(n, k + 512, seed=961 + n, dtype=dtype).cuda()
+    x = wide[:, 256:256 + k]
+    x[:, 64:96] = 0
+    q8 = C().lcpp_quantize_q8_1(x, qt, False, False)
+    a = C().lcpp_mul_mat_vec_q(w, x, qt, rows)
+    b = C().lcpp_mul_mat_vec_q(w, x, qt, rows, q8)
+    assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("qt", GENERIC, ids=lambda t: TN[t])
 def test_stream_down_shape(qt):
     """5120 x 17408 (5 units per CU, 34 block pairs) at 2 rows, bf16 X: sampled rows against the
     q81 model; one graph replay equals the eager call."""

@@ -43,6 +43,9 @@ hipError_t launch_gemv_rows_x(int type, const uint8_t* W, int64_t row_bytes, int
                               int x_dtype, int64_t s01, int n, void* y, int y_dtype, hipStream_t stream);
 bool gemv_rows_x_supported(int type, int64_t nrows, int64_t row_bytes, int64_t k, int64_t n);
 bool gemv_mfma4_supported(int type, int64_t nrows, int64_t row_bytes, int64_t k, int64_t n);
+bool gemv_generic_x_supported(int type, int64_t nrows, int64_t row_bytes, int64_t k, int64_t n);
+hipError_t launch_gemv_generic_x(int type, const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x,
+                                 int x_dtype, int64_t s01, int n, void* y, int y_dtype, hipStream_t stream);
 hipError_t launch_gemm_packed_xq(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n,
                                  void* y, int y_dtype, void* split_ws, hipStream_t stream);
 hipError_t launch_quantize_xh(const void* x, int dtype, int64_t n, int64_t k, int64_t s01, int type, void* y,
@@ -280,6 +283,11 @@ bool decode_mma(int op, int64_t type, int64_t row, int64_t k, int64_t n) {
   return !(op_packed(op) == false && bb > 0 && gguf::gemv_rows_supported((int)type, row, k / 256 * bb, k, n));
 }
 
+// A generic type's decode op with X quantised inside the stream GEMV (1-2 rows, K <= 8192).
+bool generic_fused(int64_t type, int64_t row, int64_t k, int64_t n) {
+  return gguf::gemv_generic_x_supported((int)type, row, k / 256 * gguf::block_bytes((int)type), k, n);
+}
+
 bool rows_fused(int op, int64_t type, int64_t row, int64_t k, int64_t n, bool has_x_q8) {
   if (op_gemm(op) || op_packed(op) || has_x_q8 || decode_mma(op, type, row, k, n) ||
       decode_mfma4(op, type, row, k, n))
@@ -340,7 +348,7 @@ size_t gguf_op_workspace_bytes(int op, int64_t type, int64_t row, int64_t k, int
   if (n <= 0) return 0;
   if (generic(type)) {
     if (op_gemm(op)) return align256(generic_xq(type) ? gguf::xq_bytes(n, k) : gguf_q8_1_bytes(n, k, 1));
-    return has_x_q8 ? 0 : align256(gguf_q8_1_bytes(n, k, 0));
+    return has_x_q8 || generic_fused(type, row, k, n) ? 0 : align256(gguf_q8_1_bytes(n, k, 0));
   }
   if (op_gemm(op)) {
     const bool mmq_layout = !op_packed(op) && type == gguf::kIQ3_S;
@@ -397,6 +405,12 @@ int run_checked(int op, const gguf_view* W, const gguf_view* X, int64_t type, in
       if (e != hipSuccess) return hip_fail(e, name, "quantize");
       e = gguf::launch_gemm((int)type, w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace, (int)n, y, ydt, s);
       if (e != hipSuccess) return hip_fail(e, name, "gemm");
+      return GGUF_OK;
+    }
+    if (!x_q8 && generic_fused(type, row, k, n)) {  // quantisation inside the stream GEMV
+      e = gguf::launch_gemv_generic_x((int)type, w, row_bytes, (int)row, (int)k, X->data, X->dtype, s01, (int)n, y,
+                                      ydt, s);
+      if (e != hipSuccess) return hip_fail(e, name, "gemv");
       return GGUF_OK;
     }
     const uint8_t* q8 = x_q8 ? (const uint8_t*)x_q8->data : (const uint8_t*)workspace;

@@ -315,11 +315,16 @@ __device__ __forceinline__ float gs_dpp(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
 }
 
-template <int TYPE, int NC, int XPT>
+// X: XDT < 0 the caller's block_q8_1 (xsrc), XPT q8_1 blocks staged per thread; XDT >= 0 X itself
+// (dtype XDT, row stride s01) quantised while staged, XPT groups of 8 values per thread, with the
+// q8_1 quantiser's arithmetic (xgroup_quantize: bit-identical bytes, and for Q2_K the sums of
+// each half formed from those bytes).
+template <int TYPE, int NC, int XPT, int XDT>
 __global__ void __launch_bounds__(64 * kGsWaves) gemv_generic_stream_kernel(const uint8_t* __restrict__ W,
                                                                             int64_t row_bytes, int nrows, int k,
-                                                                            const uint8_t* __restrict__ q8,
-                                                                            void* __restrict__ y, int y_dtype) {
+                                                                            const void* __restrict__ xsrc,
+                                                                            int64_t s01, void* __restrict__ y,
+                                                                            int y_dtype) {
   constexpr int NW = kGsWaves, NT = 64 * NW, BS = block_bytes(TYPE);
   using CB = Codebook<TYPE>;
   constexpr int CPT = (CB::n + NT - 1) / NT;  // codebook entries staged per thread
@@ -339,14 +344,24 @@ __global__ void __launch_bounds__(64 * kGsWaves) gemv_generic_stream_kernel(cons
 #pragma unroll
   for (int t = 0; t < CPT; ++t) cbv[t] = CB::at(min((int)threadIdx.x + t * NT, CB::n - 1));
   const int nx = NC * nslices;
-  u32x4 xa[XPT], xb[XPT];
-  uint32_t xdb[XPT];
+  constexpr int QX = XDT < 0 ? XPT : 1, RX = XDT < 0 ? 1 : XPT;
+  u32x4 xa[QX], xb[QX];
+  uint32_t xdb[QX];
+  XGroup<XDT < 0 ? kBF16 : XDT> xr[RX];
+  if constexpr (XDT < 0) {
+    const uint8_t* q8 = (const uint8_t*)xsrc;
 #pragma unroll
-  for (int t = 0; t < XPT; ++t) {
-    const uint8_t* src = q8 + (int64_t)min((int)threadIdx.x + t * NT, nx - 1) * 36;
-    xdb[t] = *(const uint16_t*)src;
-    xa[t] = ld128a4(src + 4);
-    xb[t] = ld128a4(src + 20);
+    for (int t = 0; t < XPT; ++t) {
+      const uint8_t* src = q8 + (int64_t)min((int)threadIdx.x + t * NT, nx - 1) * 36;
+      xdb[t] = *(const uint16_t*)src;
+      xa[t] = ld128a4(src + 4);
+      xb[t] = ld128a4(src + 20);
+    }
+  } else {
+    const __amdgpu_buffer_rsrc_t none = buffer_rsrc(xsrc, 0u);  // unused by the raw-X loads
+#pragma unroll
+    for (int t = 0; t < XPT; ++t)
+      xgroup_load<NC, XDT>(xsrc, none, s01, nslices, min((int)threadIdx.x + t * NT, 4 * nx - 1), xr[t]);
   }
   __builtin_amdgcn_sched_barrier(0);
   // the workgroup's units [u0, u1), the wave's items [j0, j1)
@@ -379,8 +394,25 @@ __global__ void __launch_bounds__(64 * kGsWaves) gemv_generic_stream_kernel(cons
     const int i = (int)threadIdx.x + t * NT;
     if (CB::n % NT == 0 || i < CB::n) grid[i] = cbv[t];
   }
+  if constexpr (XDT >= 0) {  // group g: part g & 3 (8 values) of slice row g >> 2; a slice is a quad
 #pragma unroll
-  for (int t = 0; t < XPT; ++t) {
+    for (int t = 0; t < XPT; ++t) {
+      const int g = (int)threadIdx.x + t * NT, sr = g >> 2, pt = g & 3;
+      const bool live = g < 4 * nx;
+      uint32_t lo, hi, dbits;
+      xgroup_quantize<XDT>(xr[t], lo, hi, dbits);
+      *(live ? (uint2*)(xq + 8 * sr + 2 * pt) : (uint2*)&sink) = make_uint2(lo, hi);
+      *(live && pt == 0 ? xd + sr : (float*)&sink) = half_bits_to_float(dbits);
+      if constexpr (TYPE == kQ2_K) {  // values 0..15 are parts 0, 1; 16..31 parts 2, 3
+        int hs = dot4(0x01010101, (int)hi, dot4(0x01010101, (int)lo, 0));
+        hs += __builtin_amdgcn_update_dpp(0, hs, 0xB1, 0xF, 0xF, true);             // quad xor 1
+        const int other = __builtin_amdgcn_update_dpp(0, hs, 0x4E, 0xF, 0xF, true);  // quad xor 2
+        *(live && pt == 0 ? xs + sr : (int*)&sink) = (hs & 0xFFFF) | (other << 16);
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < QX && XDT < 0; ++t) {
     const int i = (int)threadIdx.x + t * NT;
     const bool live = i < nx;
     *(live ? (uint4*)(xq + 8 * i) : &sink) = make_uint4(xa[t][0], xa[t][1], xa[t][2], xa[t][3]);
@@ -984,8 +1016,8 @@ static bool gs_supported(int64_t nrows, int64_t row_bytes, int64_t k, int64_t n)
   return nrows / 4 >= cus && gs_lds(nrows, k, n, cus) <= gs_lds_max<TYPE>();
 }
 
-template <int TYPE, int NC, int XPT>
-static void launch_gs_x(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, void* y,
+template <int TYPE, int NC, int XPT, int XDT>
+static void launch_gs_x(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x, int64_t s01, void* y,
                         int y_dtype, hipStream_t stream) {
   const int cus = device_cus();
   const size_t lds = gs_lds(nrows, k, NC, cus);
@@ -993,23 +1025,61 @@ static void launch_gs_x(const uint8_t* W, int64_t row_bytes, int nrows, int k, c
   if (lds > 64 * 1024 && hipGetDevice(&dev) == hipSuccess) {
     struct Tag;
     once_per_device<Tag>(dev, [] {
-      (void)hipFuncSetAttribute((const void*)gemv_generic_stream_kernel<TYPE, NC, XPT>,
+      (void)hipFuncSetAttribute((const void*)gemv_generic_stream_kernel<TYPE, NC, XPT, XDT>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)gs_lds_max<TYPE>());
     });
   }
-  gemv_generic_stream_kernel<TYPE, NC, XPT><<<cus, 64 * kGsWaves, lds, stream>>>(W, row_bytes, nrows, k, q8, y,
-                                                                                 y_dtype);
+  gemv_generic_stream_kernel<TYPE, NC, XPT, XDT><<<cus, 64 * kGsWaves, lds, stream>>>(W, row_bytes, nrows, k, x, s01,
+                                                                                      y, y_dtype);
 }
 
 template <int TYPE, int NC>
 static void launch_gs_nc(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, void* y,
                          int y_dtype, hipStream_t stream) {
   switch (gs_xpt(k, NC)) {
-    case 1: launch_gs_x<TYPE, NC, 1>(W, row_bytes, nrows, k, q8, y, y_dtype, stream); break;
-    case 2: launch_gs_x<TYPE, NC, 2>(W, row_bytes, nrows, k, q8, y, y_dtype, stream); break;
-    case 3: launch_gs_x<TYPE, NC, 3>(W, row_bytes, nrows, k, q8, y, y_dtype, stream); break;
-    default: launch_gs_x<TYPE, NC, 5>(W, row_bytes, nrows, k, q8, y, y_dtype, stream); break;
+    case 1: launch_gs_x<TYPE, NC, 1, -1>(W, row_bytes, nrows, k, q8, 0, y, y_dtype, stream); break;
+    case 2: launch_gs_x<TYPE, NC, 2, -1>(W, row_bytes, nrows, k, q8, 0, y, y_dtype, stream); break;
+    case 3: launch_gs_x<TYPE, NC, 3, -1>(W, row_bytes, nrows, k, q8, 0, y, y_dtype, stream); break;
+    default: launch_gs_x<TYPE, NC, 5, -1>(W, row_bytes, nrows, k, q8, 0, y, y_dtype, stream); break;
   }
+}
+
+// X quantised inside the generic stream GEMV: 1-2 activation rows at K <= 8192 (at most 4 groups
+// of 8 values per thread), where the quantisation each workgroup repeats costs less than the
+// quantise launch it saves.
+static int gs_fused_xpt(int64_t k, int64_t n) { return (int)((n * (k / kQ81) * 4 + 511) / 512); }
+
+template <int TYPE>
+static bool gs_x_supported(int64_t nrows, int64_t row_bytes, int64_t k, int64_t n) {
+  return n <= 2 && k <= 8192 && gs_supported<TYPE>(nrows, row_bytes, k, n);
+}
+
+template <int TYPE, int NC, int XDT>
+static void launch_gs_fused_dt(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x, int64_t s01,
+                               void* y, int y_dtype, hipStream_t stream) {
+  switch (gs_fused_xpt(k, NC)) {
+    case 1: launch_gs_x<TYPE, NC, 1, XDT>(W, row_bytes, nrows, k, x, s01, y, y_dtype, stream); break;
+    case 2: launch_gs_x<TYPE, NC, 2, XDT>(W, row_bytes, nrows, k, x, s01, y, y_dtype, stream); break;
+    case 3: launch_gs_x<TYPE, NC, 3, XDT>(W, row_bytes, nrows, k, x, s01, y, y_dtype, stream); break;
+    default: launch_gs_x<TYPE, NC, 4, XDT>(W, row_bytes, nrows, k, x, s01, y, y_dtype, stream); break;
+  }
+}
+
+template <int TYPE, int NC>
+static void launch_gs_fused_nc(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x, int x_dtype,
+                               int64_t s01, void* y, int y_dtype, hipStream_t stream) {
+  switch (x_dtype) {
+    case kF32: launch_gs_fused_dt<TYPE, NC, kF32>(W, row_bytes, nrows, k, x, s01, y, y_dtype, stream); break;
+    case kF16: launch_gs_fused_dt<TYPE, NC, kF16>(W, row_bytes, nrows, k, x, s01, y, y_dtype, stream); break;
+    default: launch_gs_fused_dt<TYPE, NC, kBF16>(W, row_bytes, nrows, k, x, s01, y, y_dtype, stream); break;
+  }
+}
+
+template <int TYPE>
+static void launch_gs_fused(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x, int x_dtype,
+                            int64_t s01, int n, void* y, int y_dtype, hipStream_t stream) {
+  if (n == 1) launch_gs_fused_nc<TYPE, 1>(W, row_bytes, nrows, k, x, x_dtype, s01, y, y_dtype, stream);
+  else launch_gs_fused_nc<TYPE, 2>(W, row_bytes, nrows, k, x, x_dtype, s01, y, y_dtype, stream);
 }
 
 template <int TYPE>
@@ -1067,7 +1137,7 @@ hipError_t launch_gemv_raw(int type, const uint8_t* W, int64_t row_bytes, int nr
   // slice pair: Q4_K 13.8 us against 16.0, and 16.9 against 20.5 on 5120 x 17408; at 3-4 rows it
   // replaces the generic GEMV and the MMA small GEMM: IQ4_XS M = 4 18.8 us against 25.6, Q6_K
   // 26.2 against 37.1 + quantise)
-  // Q4_K at 2-4 rows: the MFMA decode GEMV where it applies (gemv_mfma4.hip)
+  // Q4_K / IQ4_XS / Q6_K at 2-4 rows: the MFMA decode GEMV where it applies (gemv_mfma4.hip)
   if (gemv_mfma4_supported(type, nrows, row_bytes, k, n))
     return launch_gemv_mfma4(type, W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);
   bool done = false;
@@ -1091,5 +1161,33 @@ hipError_t launch_gemv_raw(int type, const uint8_t* W, int64_t row_bytes, int nr
   return hipGetLastError();
 }
 
+// The generic types' decode GEMV with X (dtype x_dtype, row stride s01) quantised inside the
+// stream GEMV, on the shapes gs_x_supported admits; bit-identical to the q8_1 quantiser +
+// launch_gemv_raw.
+bool gemv_generic_x_supported(int type, int64_t nrows, int64_t row_bytes, int64_t k, int64_t n) {
+  switch (type) {
+    case kQ2_K: return gs_x_supported<kQ2_K>(nrows, row_bytes, k, n);
+    case kIQ2_XXS: return gs_x_supported<kIQ2_XXS>(nrows, row_bytes, k, n);
+    case kIQ2_XS: return gs_x_supported<kIQ2_XS>(nrows, row_bytes, k, n);
+    case kIQ2_S: return gs_x_supported<kIQ2_S>(nrows, row_bytes, k, n);
+    case kIQ3_XXS: return gs_x_supported<kIQ3_XXS>(nrows, row_bytes, k, n);
+    case kIQ1_M: return gs_x_supported<kIQ1_M>(nrows, row_bytes, k, n);
+    default: return false;
+  }
+}
+
+hipError_t launch_gemv_generic_x(int type, const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x,
+                                 int x_dtype, int64_t s01, int n, void* y, int y_dtype, hipStream_t stream) {
+  if (!gemv_generic_x_supported(type, nrows, row_bytes, k, n)) return hipErrorInvalidValue;
+  switch (type) {
+    case kQ2_K: launch_gs_fused<kQ2_K>(W, row_bytes, nrows, k, x, x_dtype, s01, n, y, y_dtype, stream); break;
+    case kIQ2_XXS: launch_gs_fused<kIQ2_XXS>(W, row_bytes, nrows, k, x, x_dtype, s01, n, y, y_dtype, stream); break;
+    case kIQ2_XS: launch_gs_fused<kIQ2_XS>(W, row_bytes, nrows, k, x, x_dtype, s01, n, y, y_dtype, stream); break;
+    case kIQ2_S: launch_gs_fused<kIQ2_S>(W, row_bytes, nrows, k, x, x_dtype, s01, n, y, y_dtype, stream); break;
+    case kIQ3_XXS: launch_gs_fused<kIQ3_XXS>(W, row_bytes, nrows, k, x, x_dtype, s01, n, y, y_dtype, stream); break;
+    default: launch_gs_fused<kIQ1_M>(W, row_bytes, nrows, k, x, x_dtype, s01, n, y, y_dtype, stream); break;
+  }
+  return hipGetLastError();
+}
 
 }  // namespace gguf
