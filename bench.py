@@ -200,6 +200,18 @@ def config_types(torch, C, iq3_pack, linear):
     return out
 
 
+def config_decode(torch, C, iq3_pack, linear):
+    """The decode ops of every type with a dedicated decode GEMV at M = 1..4 on the FFN shapes
+    17408 x 5120 and 5120 x 17408: IQ3_S (packed: the stream GEMV), Q4_K, IQ4_XS and Q6_K (the
+    row-chunk GEMV at one row, the 4 x 4 x 4 MFMA GEMV at 2-4 rows), through the routing table's
+    op."""
+    out = []
+    for qt in (IQ3_S, Q4_K, IQ4_XS, Q6_K):
+        for rows, k in ((17408, 5120), (5120, 17408)):
+            out += op_points(torch, C, iq3_pack, linear, qt, rows, k, (1, 2, 3, 4), seed=5000)
+    return out
+
+
 def config_layers(torch, C, iq3_pack, linear, steps, ms=(1, 4, 16, 32), nlayers=64, merged=False):
     """benchmark configs[4]: a 64-layer synthetic 27B-style decoder's linear layers (hidden 5120,
     intermediate 17408, 48 query / 8 KV heads of dim 128) in the GSQ-RCO mix -- IQ3_S (packed)
@@ -544,7 +556,7 @@ def main():
     ap.add_argument("--no-points", action="store_true", help="skip the metric's other (type, M) points")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the other benchmark configs (CPU Q4_K, MTP small GEMM, prefill, 64-layer sweep)")
-    ap.add_argument("--section", choices=["mtp", "prefill", "layers", "types", "peaks"],
+    ap.add_argument("--section", choices=["mtp", "prefill", "layers", "types", "peaks", "decode"],
                     help="run only this benchmark config and print its JSON (for rocprofv3 counter runs)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-peaks", action="store_true", help="skip the measured read floor and MFMA peak")
@@ -570,6 +582,7 @@ def main():
         fn = {"mtp": lambda: config_mtp(torch, C, iq3_pack, linear),
               "prefill": lambda: config_prefill(torch, C, iq3_pack, linear),
               "types": lambda: config_types(torch, C, iq3_pack, linear),
+              "decode": lambda: config_decode(torch, C, iq3_pack, linear),
               "peaks": lambda: measured_peaks(torch),
               "layers": lambda: {"layer_sweep_64": config_layers(torch, C, iq3_pack, linear, args.steps),
                                  "layer_sweep_64_runs": config_layers(torch, C, iq3_pack, linear, args.steps,
