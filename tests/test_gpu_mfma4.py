@@ -1,12 +1,14 @@
 """The MFMA decode GEMV (csrc/gemv_mfma4.hip, gemv_mfma4_kernel): Q4_K, IQ4_XS and Q6_K decode
-ops at 2-4 activation rows on weights of at least one 4-row unit per CU, through the C ABI
-(torch.ops._C_gguf -> libgguf_mi355x.so). Needs an MI355X.
+ops at 2-4 activation rows (Q4_K / IQ4_XS also at one row on K > 8192) on weights of at least one
+4-row unit per CU, through the C ABI (torch.ops._C_gguf -> libgguf_mi355x.so); the one-row cases
+at K <= 8192 and of Q6_K exercise the row-chunk GEMV. Needs an MI355X.
 
   * exact-integer mode (block scales 1, Q6_K sub-scales within +-31, X integers with every q8_1
     d = 1): every output equals the oracle's int64 sum of the slice terms (Q4_K
     sc * sumi - m * sum(q8), IQ4_XS ls * sumi, Q6_K sc_a * sumi_a + sc_b * sumi_b), at the configs' shapes
     17408 x 5120 and 5120 x 17408 (K blocks 20 and 68: 10 and 34 block pairs, 17 and 5 units per
-    CU) and on smaller weights (one unit per CU, K = 1024 with two block pairs);
+    CU) and on smaller weights (one unit per CU, K = 1024 with two block pairs, K = 9216 at one
+    row);
   * the q81 model (MMVQ form) at the full shapes with bf16 (5e-3: the output is rounded to bf16)
     and fp32 (1e-3) activations;
   * the caller's x_q8 (lcpp_mul_mat_vec_q with x_q8) gives the same bytes as X quantised by the op;
@@ -44,8 +46,9 @@ def _routed(qt):
 
 
 @pytest.mark.parametrize("qt", TYPES, ids=lambda t: TN[t])
-@pytest.mark.parametrize("rows,k", [(17408, 5120), (5120, 17408), (1024, 4096), (1024, 1024), (2064, 2560)])
-@pytest.mark.parametrize("n", [2, 3, 4])
+@pytest.mark.parametrize("rows,k", [(17408, 5120), (5120, 17408), (1024, 4096), (1024, 1024), (2064, 2560),
+                                    (1024, 9216)])
+@pytest.mark.parametrize("n", [1, 2, 3, 4])
 def test_mfma4_exact_integer(qt, rows, k, n):
     raw = exact_weights(qt, rows, k, seed=300 + n + qt)
     w = dev(raw)
@@ -58,7 +61,7 @@ def test_mfma4_exact_integer(qt, rows, k, n):
 
 @pytest.mark.parametrize("qt", TYPES, ids=lambda t: TN[t])
 @pytest.mark.parametrize("rows,k", [(17408, 5120), (5120, 17408)])
-@pytest.mark.parametrize("n", [2, 3, 4])
+@pytest.mark.parametrize("n", [1, 2, 3, 4])
 def test_mfma4_full_size_q81(qt, rows, k, n):
     raw = w_rand(qt, rows, k, seed=310 + n + qt)
     w = dev(raw)

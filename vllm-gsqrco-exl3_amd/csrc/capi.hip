@@ -268,7 +268,8 @@ int64_t rows_block_bytes(int64_t type) {
   return type == gguf::kQ4_K ? 144 : type == gguf::kQ6_K ? 210 : type == gguf::kIQ4_XS ? 136 : 0;
 }
 
-// The MFMA decode GEMV (Q4_K at 2..4 rows, gemv_mfma4.hip) on a decode op's shape.
+// The MFMA decode GEMV (Q4_K / IQ4_XS / Q6_K at 2..4 rows, Q4_K / IQ4_XS at one row on long K;
+// gemv_mfma4.hip) on a decode op's shape.
 bool decode_mfma4(int op, int64_t type, int64_t row, int64_t k, int64_t n) {
   const int64_t bb = rows_block_bytes(type);
   return !op_gemm(op) && !op_packed(op) && bb > 0 && gguf::gemv_mfma4_supported((int)type, row, k / 256 * bb, k, n);

@@ -1137,7 +1137,8 @@ hipError_t launch_gemv_raw(int type, const uint8_t* W, int64_t row_bytes, int nr
   // slice pair: Q4_K 13.8 us against 16.0, and 16.9 against 20.5 on 5120 x 17408; at 3-4 rows it
   // replaces the generic GEMV and the MMA small GEMM: IQ4_XS M = 4 18.8 us against 25.6, Q6_K
   // 26.2 against 37.1 + quantise)
-  // Q4_K / IQ4_XS / Q6_K at 2-4 rows: the MFMA decode GEMV where it applies (gemv_mfma4.hip)
+  // Q4_K / IQ4_XS / Q6_K at 2-4 rows (Q4_K / IQ4_XS also at one row on K > 8192): the MFMA decode
+  // GEMV where it applies (gemv_mfma4.hip)
   if (gemv_mfma4_supported(type, nrows, row_bytes, k, n))
     return launch_gemv_mfma4(type, W, row_bytes, nrows, k, q8, n, y, y_dtype, stream);
   bool done = false;

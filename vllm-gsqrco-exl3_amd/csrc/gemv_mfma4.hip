@@ -1,5 +1,6 @@
 // Decode GEMV on v_mfma_i32_4x4x4_16b_i8 for 2-4 activation rows of Q4_K, IQ4_XS and Q6_K on GGUF
-// rows: Y[c, r] = sum_k X[c, k] * W[r, k], X given as block_q8_1.
+// rows (and one row of Q4_K / IQ4_XS on long K): Y[c, r] = sum_k X[c, k] * W[r, k], X given as
+// block_q8_1.
 //
 // Replaces the reference's 2..4-row decode products of these types (vendored MMVQ
 // mul_mat_vec_q, mmvq.cu:600-760; the owned dp4a kernel lcpp_owned_k4.cu:116-269) where the
@@ -344,11 +345,15 @@ static int m4_xpt(int64_t k, int64_t n) {
 
 static int64_t m4_units_per_wg(int64_t nrows, int64_t grid) { return (nrows / kM4UnitRows + grid - 1) / grid; }
 
-// Q4_K, IQ4_XS and Q6_K at 2-4 activation rows, rows % 4 == 0 with at least one unit per CU,
-// K % 512 == 0 (whole block pairs), a weight below 2 GiB, X within the staged groups and the LDS.
+// Q4_K, IQ4_XS and Q6_K at 2-4 activation rows, and Q4_K / IQ4_XS at one row on K > 8192 (where
+// the row-chunk GEMV does not quantise X itself and its 8-row tiles leave CUs uneven: 5120 x 17408
+// at one row 16.1 -> 14.7 us for Q4_K, 17.2 -> 16.5 for IQ4_XS; Q6_K's row-chunk GEMV stays
+// faster there); rows % 4 == 0 with at least one unit per CU, K % 512 == 0 (whole block pairs), a
+// weight below 2 GiB, X within the staged groups and the LDS.
 bool gemv_mfma4_supported(int type, int64_t nrows, int64_t row_bytes, int64_t k, int64_t n) {
   if (!(type == kQ4_K || type == kIQ4_XS || type == kQ6_K)) return false;
-  if (n < 2 || n > 4 || k % 512 != 0 || nrows % kM4UnitRows != 0) return false;
+  if (n == 1 && (k <= 8192 || type == kQ6_K)) return false;
+  if (n < 1 || n > 4 || k % 512 != 0 || nrows % kM4UnitRows != 0) return false;
   if (row_bytes != k / kQK * block_bytes(type) || nrows * row_bytes >= ((int64_t)1 << 31)) return false;
   const int64_t cus = device_cus();
   if (nrows / kM4UnitRows < cus || m4_xpt(k, n) == 0) return false;
@@ -388,13 +393,14 @@ template <int TYPE>
 static void launch_m4_type(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n, void* y,
                            int y_dtype, hipStream_t stream) {
   switch (n) {
+    case 1: launch_m4_nc<TYPE, 1>(W, row_bytes, nrows, k, q8, y, y_dtype, stream); break;
     case 2: launch_m4_nc<TYPE, 2>(W, row_bytes, nrows, k, q8, y, y_dtype, stream); break;
     case 3: launch_m4_nc<TYPE, 3>(W, row_bytes, nrows, k, q8, y, y_dtype, stream); break;
     default: launch_m4_nc<TYPE, 4>(W, row_bytes, nrows, k, q8, y, y_dtype, stream); break;
   }
 }
 
-// n in 2..4 activation rows on the shapes gemv_mfma4_supported admits; q8: block_q8_1 of X;
+// n in 1..4 activation rows on the shapes gemv_mfma4_supported admits; q8: block_q8_1 of X;
 // y: [n, nrows] in y_dtype.
 hipError_t launch_gemv_mfma4(int type, const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* q8, int n,
                              void* y, int y_dtype, hipStream_t stream) {
