@@ -3,8 +3,9 @@
 The reference promises that its kernels' one-time set-up (the max-dynamic-shared-memory attribute,
 the first device query) may run inside a capture (lcpp_owned_iq3_mma.cu:333-346,
 lcpp_owned_mma_k.cu:551-569) and tests it in a fresh process (tests/gpu/test_kernel_parity.py:
-655-698). Here the set-up is the stream GEMV's dynamic-LDS attribute, the compute-unit count the
-launch plans read, and the no-allocation entry point's scratch address. The child process touches
+655-698). Here the set-up is the stream GEMVs' dynamic-LDS attributes (IQ3_S, the 4x4x4 MFMA
+GEMV, the generic types' stream GEMV), the compute-unit count the launch plans read, and the
+no-allocation entry point's scratch address. The child process touches
 the GPU only through torch (inputs made and packed on the host, so that not even the repack
 kernel runs first), then for each case captures one op call as the first call of its kernel
 instance, replays the graph on new activations twice and compares both replays with an eager call
@@ -51,6 +52,11 @@ CASES = [
     (o.IQ2_S, 1024, 5120, 2, False),    # generic GEMV
     (o.IQ2_S, 1024, 5120, 16, False),   # generic MFMA GEMM
     (o.IQ3_S, 1024, 5120, 16, False),   # per-slice MFMA GEMM (unpacked IQ3_S)
+    (o.Q4_K, 5120, 17408, 4, False),    # 4x4x4 MFMA GEMV, 97 KB of dynamic LDS (the attribute)
+    (o.IQ4_XS, 1024, 17408, 3, False),  # 4x4x4 MFMA GEMV, 70 KB of dynamic LDS
+    (o.Q4_K, 1024, 17408, 1, False),    # 4x4x4 MFMA GEMV at one row (K > 8192)
+    (o.IQ3_XXS, 1024, 17408, 3, False), # generic stream GEMV, 65 KB of dynamic LDS
+    (o.IQ2_XXS, 1024, 2048, 1, False),  # generic stream GEMV, X quantised in the kernel
 ]
 
 fails = []
