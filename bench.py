@@ -135,7 +135,7 @@ def x_outliers(torch, m, k, seed):
 def op_points(torch, C, iq3_pack, linear, qt, rows, k, ms, ncopies=None, reps=5, seed=0, outliers=False):
     """us/call of the routing table's op for a qt weight [rows, k] at each M in ms (bf16 X N(0,1),
     with outliers: x_outliers), over ncopies weight copies (default: rotation_copies) captured in
-    one graph per M. IQ3_S in the packed unit layout (IQ3_XXS packed too: the identity)."""
+    one graph per M. IQ3_S and IQ3_XXS in their packed unit layouts."""
     if ncopies is None:
         ncopies = rotation_copies(rows * (k // 256) * BLOCK[qt])
     ws = [make_weights(torch, qt, rows, k, seed + i) for i in range(ncopies)]

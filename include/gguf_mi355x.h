@@ -145,12 +145,12 @@ GGUF_API int gguf_lcpp_mul_mat_vec_own(const gguf_view* W, const gguf_view* X, i
 /* replaces lcpp_mul_mat_mma_k (lcpp_shim.cu:931-933): Q4_K / IQ4_XS, 1..64 rows */
 GGUF_API int gguf_lcpp_mul_mat_mma_k(const gguf_view* W, const gguf_view* X, int64_t type, int64_t row, void* y,
                             size_t y_bytes, void* workspace, size_t workspace_bytes, void* stream);
-/* replaces lcpp_mul_mat_vec_iq3_mma_packed (lcpp_shim.cu:935-938): IQ3_S in the build's tile
- * layout (gguf_iq3_pack), 1..32 rows, row % 16 == 0 */
+/* replaces lcpp_mul_mat_vec_iq3_mma_packed (lcpp_shim.cu:935-938): IQ3_S or IQ3_XXS in the build's
+ * unit layout of its type (gguf_iq3_pack), 1..32 rows, row % 16 == 0 */
 GGUF_API int gguf_lcpp_mul_mat_vec_iq3_mma_packed(const gguf_view* W, const gguf_view* X, int64_t type, int64_t row,
                                          const gguf_view* x_q8, void* y, size_t y_bytes, void* workspace,
                                          size_t workspace_bytes, void* stream);
-/* replaces lcpp_mul_mat_iq3_packed (lcpp_shim.cu:940-942): IQ3_S tile layout, any rows */
+/* replaces lcpp_mul_mat_iq3_packed (lcpp_shim.cu:940-942): IQ3_S / IQ3_XXS unit layout, any rows */
 GGUF_API int gguf_lcpp_mul_mat_iq3_packed(const gguf_view* W, const gguf_view* X, int64_t type, int64_t row, void* y,
                                  size_t y_bytes, void* workspace, size_t workspace_bytes, void* stream);
 
@@ -162,12 +162,13 @@ GGUF_API size_t gguf_q8_1_bytes(int64_t n, int64_t k, int mmq);
 GGUF_API int gguf_lcpp_quantize_q8_1(const gguf_view* X, int64_t type, int mmq, int vendored, void* out, size_t out_bytes,
                             void* stream);
 
-/* The build's IQ3_S tile layout (the reference's load-time repack hook, quantization/iq3_pack.py
- * pack_ / unpack, replaced by a layout of this build's own). In place on rows % 16 == 0 GGUF
- * rows [rows, row_bytes] (contiguous, 16-byte aligned); scratch: >= gguf_iq3_pack_scratch_bytes. */
+/* The build's IQ3_S and IQ3_XXS unit layouts (the reference's load-time repack hook,
+ * quantization/iq3_pack.py pack_(w, weight_type) / unpack, replaced by layouts of this build's
+ * own). In place on rows % 16 == 0 GGUF rows [rows, row_bytes] of type 21 (IQ3_S) or 18 (IQ3_XXS)
+ * (contiguous, 16-byte aligned); scratch: >= gguf_iq3_pack_scratch_bytes. */
 GGUF_API size_t gguf_iq3_pack_scratch_bytes(int64_t rows, int64_t row_bytes);
-GGUF_API int gguf_iq3_pack(void* w, int64_t rows, int64_t row_bytes, int unpack, void* scratch, size_t scratch_bytes,
-                  void* stream);
+GGUF_API int gguf_iq3_pack(void* w, int64_t type, int64_t rows, int64_t row_bytes, int unpack, void* scratch,
+                           size_t scratch_bytes, void* stream);
 
 /* Dense product of a small unquantized weight: Y[n, rows] = X @ W.T in X's dtype, W [rows, K] and
  * X [n, K] of one float dtype (fp32 / fp16 / bf16), 1 <= n <= 8 (n == 0: nothing), K % 32 == 0,

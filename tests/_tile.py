@@ -102,3 +102,65 @@ def unpack(pk: np.ndarray) -> np.ndarray:
                 o = base + D * r + 4 * p + 2 * rr
                 out[:, 2 * rp + rr, b, 0:2] = t[:, o:o + 2]
     return out.astype(np.uint8).reshape(rows, rb)
+
+
+# ---------------------------------------------------------------------------------------------
+# The IQ3_XXS unit layout (csrc/iq3_tile.h): the same units, unit-blocks and lanes, 1568-byte
+# unit-blocks (392 r for a last one of r blocks). block_iq3_xxs: d[0:2], qs[2:66] (one grid index
+# per 4 values), per slice s a dword at 66 + 4s (four 7-bit sign indices, the scale in bits 28..31).
+#   [    0, 256 r) QS  16 B at 16L: qs[8s:8s+8] of row 2rp, then of row 2rp+1
+#   [256 r, 384 r) AUX  8 B at 8L : the slice's dword of row 2rp, then of row 2rp+1
+#   [384 r, 392 r) D    4 B at 4p : d of row 2rp, then of row 2rp+1
+
+XQS, XAUX, XD = 0, 256, 384   # field bases per block of the unit-block (times r)
+
+
+def xxs_unit_blocks(nb):
+    """(kb, r, byte offset in the unit) of each IQ3_XXS unit-block of a unit of nb blocks."""
+    out, off = [], 0
+    for kb in range((nb + 3) // 4):
+        r = min(4, nb - 4 * kb)
+        out.append((kb, r, off))
+        off += 392 * r
+    return out
+
+
+def _xxs_sources(nb):
+    """For every byte of a unit in the layout, (row in the unit, byte of that GGUF row)."""
+    src = []
+    for kb, r, base in xxs_unit_blocks(nb):
+        ub = [None] * (392 * r)
+        for L in range(16 * r):
+            bi, rp, s = L // 16, (L // 8) % 2, L % 8
+            b = 4 * kb + bi
+            for rr in range(2):
+                for i in range(8):
+                    ub[XQS * r + 16 * L + 8 * rr + i] = (2 * rp + rr, 98 * b + 2 + 8 * s + i)
+                for i in range(4):
+                    ub[XAUX * r + 8 * L + 4 * rr + i] = (2 * rp + rr, 98 * b + 66 + 4 * s + i)
+        for p in range(2 * r):
+            bi, rp = p // 2, p % 2
+            for rr in range(2):
+                for i in range(2):
+                    ub[XD * r + 4 * p + 2 * rr + i] = (2 * rp + rr, 98 * (4 * kb + bi) + i)
+        src += ub
+    return src
+
+
+def pack_xxs(w: np.ndarray) -> np.ndarray:
+    """[rows, row_bytes] GGUF IQ3_XXS rows (rows % 4 == 0) -> the unit layout."""
+    rows, rb = w.shape
+    nb, nu = rb // 98, rows // 4
+    src = _xxs_sources(nb)
+    ridx = np.array([r for r, _ in src]) * rb + np.array([c for _, c in src])
+    return w.reshape(nu, 4 * rb)[:, ridx].reshape(rows, rb)
+
+
+def unpack_xxs(pk: np.ndarray) -> np.ndarray:
+    rows, rb = pk.shape
+    nb, nu = rb // 98, rows // 4
+    src = _xxs_sources(nb)
+    ridx = np.array([r for r, _ in src]) * rb + np.array([c for _, c in src])
+    out = np.zeros((nu, 4 * rb), dtype=pk.dtype)
+    out[:, ridx] = pk.reshape(nu, 4 * rb)
+    return out.reshape(rows, rb)

@@ -55,7 +55,10 @@ CASES = [
     (o.Q4_K, 5120, 17408, 4, False),    # 4x4x4 MFMA GEMV, 97 KB of dynamic LDS (the attribute)
     (o.IQ4_XS, 1024, 17408, 3, False),  # 4x4x4 MFMA GEMV, 70 KB of dynamic LDS
     (o.Q4_K, 1024, 17408, 1, False),    # 4x4x4 MFMA GEMV at one row (K > 8192)
-    (o.IQ3_XXS, 1024, 17408, 3, False), # generic stream GEMV, 65 KB of dynamic LDS
+    (o.IQ2_XS, 1024, 17408, 3, False),  # generic stream GEMV, 65 KB of dynamic LDS
+    (o.IQ3_XXS, 1024, 17408, 3, True),  # IQ3 stream GEMV on the IQ3_XXS unit layout, 82 KB of LDS
+    (o.IQ3_XXS, 4096, 5120, 1, True),   # the same, X quantised in the kernel
+    (o.IQ3_XXS, 1024, 5120, 16, True),  # generic GEMM staging the IQ3_XXS unit layout
     (o.IQ2_XXS, 1024, 2048, 1, False),  # generic stream GEMV, X quantised in the kernel
 ]
 
@@ -63,7 +66,7 @@ fails = []
 for i, (qt, rows, k, n, packed) in enumerate(CASES):
     raw = o.random_blocks(np.random.default_rng(i), qt, rows, k)
     if packed:
-        raw = _tile.pack(raw)
+        raw = _tile.pack_xxs(raw) if qt == o.IQ3_XXS else _tile.pack(raw)
     w = torch.from_numpy(raw).cuda()
     g = torch.Generator().manual_seed(100 + i)
     x1, x2 = (torch.randn(n, k, generator=g).bfloat16().cuda() for _ in range(2))

@@ -442,6 +442,68 @@ def test_pack_is_the_tile_layout_and_roundtrips():
     np.testing.assert_array_equal(iq3_pack.unpack(p, o.IQ3_S).cpu().numpy(), raw)
 
 
+@pytest.mark.parametrize("rows,k", [(272, 1024), (32, 1536)])
+def test_pack_is_the_xxs_unit_layout_and_roundtrips(rows, k):
+    """IQ3_XXS: the GPU repack equals the numpy statement of the unit layout (a ragged last
+    unit-block at K = 1536) and unpacks back to the GGUF rows."""
+    from vllm_gguf_plugin.quantization import iq3_pack
+
+    raw = _w(o.IQ3_XXS, rows, k, seed=72)
+    p = iq3_pack.pack(_dev(raw), o.IQ3_XXS)
+    np.testing.assert_array_equal(p.cpu().numpy(), _tile.pack_xxs(raw))
+    np.testing.assert_array_equal(iq3_pack.unpack(p, o.IQ3_XXS).cpu().numpy(), raw)
+
+
+# Packed IQ3_XXS through both packed ops: the stream GEMV at 1..32 rows (q8_1 in groups of at most
+# 4 activation rows, fused at 1-2 rows for K <= 8192; 65536 x 5120 at 4 rows runs in two row
+# ranges, 61440 rows filling the partial-sum slots of LDS on 256 CUs) and the generic GEMM staging
+# the unit layout, against the q81 model of each op's arithmetic.
+@pytest.mark.parametrize("rows,k,n", [(64, 512, 1), (64, 1536, 3), (1024, 5120, 1), (1024, 5120, 2),
+                                      (4096, 5120, 4), (256, 17408, 1), (256, 17408, 5), (64, 5120, 32),
+                                      (17408, 5120, 2), (17408, 5120, 4), (65536, 5120, 4), (64, 1536, 33),
+                                      (1024, 5120, 300)])
+def test_packed_xxs_ops_vs_q81(rows, k, n):
+    from vllm_gguf_plugin.quantization import iq3_pack
+
+    raw = _w(o.IQ3_XXS, rows, k, seed=rows + k + n)
+    w = iq3_pack.pack(_dev(raw), o.IQ3_XXS)
+    x = _x(n, k, seed=n + 510)
+    gemm = n > 32
+    op = "lcpp_mul_mat_iq3_packed" if gemm else "lcpp_mul_mat_vec_iq3_mma_packed"
+    mid = min(61440, rows // 2)  # 65536 rows: where the second row range starts
+    sel = slice(None) if rows <= 4096 else np.r_[0:256, mid - 128:mid + 128, rows - 256:rows]
+    y = getattr(C(), op)(w, x.cuda(), o.IQ3_XXS, rows).cpu().numpy()
+    ref = o.q81_model(raw[sel], o.IQ3_XXS, x, layout="mmq" if gemm else "mmvq")
+    assert o.rel_l2(y[:, sel], ref) <= 1e-3
+
+
+def test_packed_xxs_decode_with_shared_q8_1_and_replays():
+    """The packed IQ3_XXS GEMV on the caller's x_q8 equals the op quantising X itself, and graph
+    replays of the fused op with new X equal eager calls."""
+    from vllm_gguf_plugin.quantization import iq3_pack
+
+    rows, k = 4096, 5120
+    raw = _w(o.IQ3_XXS, rows, k, seed=73)
+    w = iq3_pack.pack(_dev(raw), o.IQ3_XXS)
+    for n in (1, 2, 4):
+        x = _x(n, k, seed=520 + n).cuda()
+        q8 = C().lcpp_quantize_q8_1(x, o.IQ3_XXS, False, False)
+        a = C().lcpp_mul_mat_vec_iq3_mma_packed(w, x, o.IQ3_XXS, rows)
+        b = C().lcpp_mul_mat_vec_iq3_mma_packed(w, x, o.IQ3_XXS, rows, q8)
+        assert torch.equal(a, b)
+    xs = _x(1, k, seed=530).cuda()
+    C().lcpp_mul_mat_vec_iq3_mma_packed(w, xs, o.IQ3_XXS, rows)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ys = C().lcpp_mul_mat_vec_iq3_mma_packed(w, xs, o.IQ3_XXS, rows)
+    for i in range(3):
+        xs.copy_(_x(1, k, seed=540 + i).cuda())
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(ys, C().lcpp_mul_mat_vec_iq3_mma_packed(w, xs, o.IQ3_XXS, rows))
+
+
 def test_pack_inplace_inside_padded_buffer():
     from vllm_gguf_plugin.quantization import iq3_pack
 

@@ -67,13 +67,15 @@ def _ops():
 
 
 def _weights(raw, op, qt):
-    """W as the op reads it: the packed ops take iq3_pack's layout (the identity for IQ3_XXS)."""
+    """W as the op reads it: the packed ops take iq3_pack's layout (IQ3_XXS: its unit layout)."""
     w = dev(raw)
     if op.endswith("_packed"):
         from vllm_gguf_plugin.quantization import iq3_pack
 
+        import _tile
+
         w = iq3_pack.pack(w, qt)
-        assert torch.equal(w, dev(raw))
+        np.testing.assert_array_equal(w.cpu().numpy(), _tile.pack_xxs(raw) if qt == o.IQ3_XXS else _tile.pack(raw))
     return w
 
 
@@ -346,7 +348,7 @@ def test_iq1m_routing(n):
 
 @pytest.mark.parametrize("n", [1, 6, 9, 40])
 def test_iq3xxs_packed_layer(n):
-    """A qkv layer of IQ3_XXS q with IQ3_S k, v: the layer packs (IQ3_XXS as the identity) and
+    """A qkv layer of IQ3_XXS q with IQ3_S k, v: the layer packs both (each into its unit layout) and
     apply() equals each run's packed op on its own bytes."""
     from test_gpu_layers import build_layer, routed
 

@@ -1,4 +1,4 @@
-"""A host model of the IQ3_S stream GEMV's weight loads (csrc/gemv_iq3.hip,
+"""A host model of the IQ3_S and IQ3_XXS stream GEMV's weight loads (csrc/gemv_iq3.hip,
 gemv_iq3s_stream_kernel), checked on the CPU.
 
 The kernel reads W through one buffer descriptor per workgroup, with the unit-block's field bases
@@ -10,7 +10,9 @@ issues past its run (which must use the empty descriptor), and per lane the five
 E8 8 B, L2 2 B, SC 2 B, D 4 B). It checks that every in-run access lies inside the unit-block it
 belongs to, on full unit-blocks and on a ragged last one of two blocks (K % 1024 == 512), where the
 lanes of the absent blocks take the offsets of lane L - 32; and that the items of all waves cover
-each (unit, unit-block) of the weight exactly once.
+each (unit, unit-block) of the weight exactly once. The IQ3_XXS unit layout takes the same lane
+offsets for its three fields (QS 16 B at 16L, AUX 8 B at 8L, D 4 B at 4p) in unit-blocks of
+392 r bytes.
 """
 
 import numpy as np
@@ -90,3 +92,27 @@ def test_items_cover_each_unit_block_once(nrows, k, cus):
     hits, past, grid = enumerate_loads(nrows, k, cus)
     assert (hits == 1).all()
     assert past == 2 * WAVES * grid  # each wave's two trailing loads use the empty range
+
+
+XXS_FIELD_SIZE = {"qs": 16, "e8": 8, "d": 4}  # the kernel loads AUX with the E8 lane offset
+
+
+def xxs_unitblock_bases(r):
+    """Field bases of an IQ3_XXS unit-block of r blocks (xxs_unitblock_fields)."""
+    return {"qs": 0, "e8": 256 * r, "d": 384 * r}
+
+
+@pytest.mark.parametrize("blocks", [2, 4, 6, 10, 18, 20, 22, 24, 68, 70])
+def test_xxs_every_field_access_stays_in_its_unit_block(blocks):
+    for kb in range((blocks + 3) // 4):
+        r = unit_blocks(blocks, kb)
+        bases = xxs_unitblock_bases(r)
+        ragged = (blocks & 3) != 0 and kb == (blocks + 3) // 4 - 1
+        offs = OFF_RAGGED if ragged else OFF
+        for f, size in XXS_FIELD_SIZE.items():
+            lo = bases[f] + offs[f]
+            assert lo.min() >= 0 and (lo + size).max() <= 392 * r, (blocks, kb, f)
+        if not ragged:  # the 64 lanes' QS and AUX parts tile their fields exactly
+            assert sorted((bases["qs"] + OFF["qs"]).tolist()) == list(range(0, 256 * r, 16))
+            assert sorted((bases["e8"] + OFF["e8"]).tolist()) == list(range(256 * r, 384 * r, 8))
+            assert sorted(set((bases["d"] + OFF["d"]).tolist())) == list(range(384 * r, 392 * r, 4))

@@ -44,6 +44,11 @@ hipError_t launch_gemv_rows_x(int type, const uint8_t* W, int64_t row_bytes, int
 bool gemv_rows_x_supported(int type, int64_t nrows, int64_t row_bytes, int64_t k, int64_t n);
 bool gemv_mfma4_supported(int type, int64_t nrows, int64_t row_bytes, int64_t k, int64_t n);
 bool gemv_generic_x_supported(int type, int64_t nrows, int64_t row_bytes, int64_t k, int64_t n);
+bool gemv_iq3xxs_stream_supported(int64_t nrows, int64_t row_bytes, int64_t k, int64_t n, bool fused);
+hipError_t launch_gemv_iq3xxs_stream(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x,
+                                     int x_dtype, int64_t s01, int n, void* y, int y_dtype, hipStream_t stream);
+hipError_t launch_gemm_iq3xxs_packed(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n,
+                                     void* y, int y_dtype, hipStream_t stream);
 hipError_t launch_gemv_generic_x(int type, const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x,
                                  int x_dtype, int64_t s01, int n, void* y, int y_dtype, hipStream_t stream);
 hipError_t launch_gemm_packed_xq(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n,
@@ -57,7 +62,7 @@ hipError_t launch_gemm_small_h(int type, bool packed, const uint8_t* W, int64_t 
                                const uint8_t* xh, int n, void* y, int y_dtype, hipStream_t stream);
 hipError_t launch_gemm_prefill(int type, bool packed, const uint8_t* W, int64_t row_bytes, int nrows, int k,
                                const uint8_t* xq, int n, void* y, int y_dtype, hipStream_t stream);
-hipError_t launch_iq3_pack(uint8_t* w, int64_t rows, int64_t row_bytes, bool unpack, uint8_t* scratch,
+hipError_t launch_iq3_pack(int type, uint8_t* w, int64_t rows, int64_t row_bytes, bool unpack, uint8_t* scratch,
                            size_t scratch_bytes, hipStream_t stream);
 size_t iq3_pack_scratch_bytes(int64_t rows, int64_t row_bytes);
 hipError_t launch_dense(int dtype, const void* W, int64_t ws0, int rows, int k, const void* X, int64_t xs0, int n,
@@ -110,8 +115,8 @@ using gguf::kIQ2_S;
 using gguf::kIQ3_XXS;
 
 // Q2_K, the IQ2 types, IQ3_XXS and IQ1_M run on the generic kernels: the dot4 GEMV for the decode
-// ops, the per-slice MFMA GEMM for the product ops (IQ3_XXS keeps the GGUF layout in the packed
-// ops: its repack is the identity)
+// ops, the per-slice MFMA GEMM for the product ops; the packed ops on IQ3_XXS read its unit layout
+// (the IQ3 stream GEMV, and the generic GEMM staging the layout's fields into GGUF blocks)
 bool generic(int64_t t) { return gguf::generic_type((int)t); }
 
 // the generic types whose product ops run on the xq-layout GEMM (D4 scales); Q2_K's D2S6 layout
@@ -284,8 +289,12 @@ bool decode_mma(int op, int64_t type, int64_t row, int64_t k, int64_t n) {
   return !(op_packed(op) == false && bb > 0 && gguf::gemv_rows_supported((int)type, row, k / 256 * bb, k, n));
 }
 
+// A packed op on IQ3_XXS: the weight is in the build's IQ3_XXS unit layout (gguf_iq3_pack).
+bool xxs_packed(int op, int64_t type) { return op_packed(op) && type == kIQ3_XXS; }
+
 // A generic type's decode op with X quantised inside the stream GEMV (1-2 rows, K <= 8192).
-bool generic_fused(int64_t type, int64_t row, int64_t k, int64_t n) {
+bool generic_fused(int op, int64_t type, int64_t row, int64_t k, int64_t n) {
+  if (xxs_packed(op, type)) return gguf::gemv_iq3xxs_stream_supported(row, k / 256 * 98, k, n, true);
   return gguf::gemv_generic_x_supported((int)type, row, k / 256 * gguf::block_bytes((int)type), k, n);
 }
 
@@ -349,7 +358,7 @@ size_t gguf_op_workspace_bytes(int op, int64_t type, int64_t row, int64_t k, int
   if (n <= 0) return 0;
   if (generic(type)) {
     if (op_gemm(op)) return align256(generic_xq(type) ? gguf::xq_bytes(n, k) : gguf_q8_1_bytes(n, k, 1));
-    return has_x_q8 || generic_fused(type, row, k, n) ? 0 : align256(gguf_q8_1_bytes(n, k, 0));
+    return has_x_q8 || generic_fused(op, type, row, k, n) ? 0 : align256(gguf_q8_1_bytes(n, k, 0));
   }
   if (op_gemm(op)) {
     const bool mmq_layout = !op_packed(op) && type == gguf::kIQ3_S;
@@ -393,12 +402,32 @@ int run_checked(int op, const gguf_view* W, const gguf_view* X, int64_t type, in
   const int ydt = X->dtype;
 
   if (generic(type)) {
+    const bool xxs = xxs_packed(op, type);
     if (gemm && generic_xq(type)) {  // the product ops' MMQ arithmetic in the xq layout
       e = gguf::launch_quantize_xq(X->data, X->dtype, n, k, s01, (int)type, false, workspace, s);
       if (e != hipSuccess) return hip_fail(e, name, "quantize");
-      e = gguf::launch_gemm_xq((int)type, w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace, (int)n, y, ydt,
-                               true, nullptr, s);
+      e = xxs ? gguf::launch_gemm_iq3xxs_packed(w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace, (int)n, y,
+                                               ydt, s)
+              : gguf::launch_gemm_xq((int)type, w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace, (int)n, y,
+                                     ydt, true, nullptr, s);
       if (e != hipSuccess) return hip_fail(e, name, "gemm");
+      return GGUF_OK;
+    }
+    if (xxs) {  // IQ3_XXS unit layout: the IQ3 stream GEMV
+      if (!gguf::gemv_iq3xxs_stream_supported(row, row_bytes, k, 1, false))
+        return fail("%s: K=%lld is past the packed IQ3_XXS GEMV's X staging", name, (long long)k);
+      if (!x_q8 && generic_fused(op, type, row, k, n)) {
+        e = gguf::launch_gemv_iq3xxs_stream(w, row_bytes, (int)row, (int)k, X->data, X->dtype, s01, (int)n, y, ydt, s);
+        if (e != hipSuccess) return hip_fail(e, name, "gemv");
+        return GGUF_OK;
+      }
+      const uint8_t* q8 = x_q8 ? (const uint8_t*)x_q8->data : (const uint8_t*)workspace;
+      if (!x_q8) {
+        e = gguf::launch_quantize(X->data, X->dtype, n, k, s01, (int)type, false, workspace, s);
+        if (e != hipSuccess) return hip_fail(e, name, "quantize");
+      }
+      e = gguf::launch_gemv_iq3xxs_stream(w, row_bytes, (int)row, (int)k, q8, -1, 0, (int)n, y, ydt, s);
+      if (e != hipSuccess) return hip_fail(e, name, "gemv");
       return GGUF_OK;
     }
     if (gemm) {  // Q2_K: the product ops' MMQ arithmetic, block_q8_1_mmq and the per-slice MFMA GEMM
@@ -408,7 +437,7 @@ int run_checked(int op, const gguf_view* W, const gguf_view* X, int64_t type, in
       if (e != hipSuccess) return hip_fail(e, name, "gemm");
       return GGUF_OK;
     }
-    if (!x_q8 && generic_fused(type, row, k, n)) {  // quantisation inside the stream GEMV
+    if (!x_q8 && generic_fused(op, type, row, k, n)) {  // quantisation inside the stream GEMV
       e = gguf::launch_gemv_generic_x((int)type, w, row_bytes, (int)row, (int)k, X->data, X->dtype, s01, (int)n, y,
                                       ydt, s);
       if (e != hipSuccess) return hip_fail(e, name, "gemv");
@@ -663,15 +692,19 @@ int gguf_dense_mul_mat(const gguf_view* W, const gguf_view* X, void* y, size_t y
   return GGUF_OK;
 }
 
-int gguf_iq3_pack(void* w, int64_t rows, int64_t row_bytes, int unpack, void* scratch, size_t scratch_bytes,
-                  void* stream) {
+int gguf_iq3_pack(void* w, int64_t type, int64_t rows, int64_t row_bytes, int unpack, void* scratch,
+                  size_t scratch_bytes, void* stream) {
   g_err.clear();
-  if (!w || rows <= 0 || rows % 16 != 0 || row_bytes <= 0 || row_bytes % 110 != 0)
-    return fail("gguf_iq3_pack: rows must be a positive multiple of 16 and row bytes whole IQ3_S blocks");
+  if (type != gguf::kIQ3_S && type != kIQ3_XXS)
+    return fail("gguf_iq3_pack: IQ3_S or IQ3_XXS only, got type %lld", (long long)type);
+  const int64_t bs = type == kIQ3_XXS ? 98 : 110;
+  if (!w || rows <= 0 || rows % 16 != 0 || row_bytes <= 0 || row_bytes % bs != 0)
+    return fail("gguf_iq3_pack: rows must be a positive multiple of 16 and row bytes whole %s blocks",
+                type == kIQ3_XXS ? "IQ3_XXS" : "IQ3_S");
   if (reinterpret_cast<uintptr_t>(w) % 16 != 0) return fail("gguf_iq3_pack: W data must be 16-byte aligned");
   if (scratch_bytes < gguf::iq3_pack_scratch_bytes(rows, row_bytes) || !scratch)
     return fail("gguf_iq3_pack: scratch of %zu bytes needed", gguf::iq3_pack_scratch_bytes(rows, row_bytes));
-  const hipError_t e = gguf::launch_iq3_pack((uint8_t*)w, rows, row_bytes, unpack != 0, (uint8_t*)scratch,
+  const hipError_t e = gguf::launch_iq3_pack((int)type, (uint8_t*)w, rows, row_bytes, unpack != 0, (uint8_t*)scratch,
                                              scratch_bytes, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "gguf_iq3_pack", "pack");
   return GGUF_OK;

@@ -15,6 +15,7 @@
 //  * the 4 waves' partial sums are added in wave order through LDS (deterministic).
 // gemm_raw_kernel (Q4_K, IQ4_XS, Q6_K) reads X in the xq layout; see its own description below.
 #include "decode.h"
+#include "iq3_tile.h"
 #include "split_k.h"
 #include "xq.h"
 
@@ -551,7 +552,13 @@ __device__ __forceinline__ void gen_row_scales(const uint8_t* rowp, int u, int& 
   }
 }
 
-template <int TYPE, int NT, int KS>
+// PK (IQ3_XXS only): W in the build's IQ3_XXS unit layout (iq3_tile.h). Lane 16u + 8rp + s loads
+// unit u's QS 16 B, AUX 8 B and D 4 B of block b's lanes 8 (2 bi + rp) + s (rows 2rp, 2rp+1,
+// slice s: each field contiguous across the 16 lanes of a unit) and writes them to the staged
+// rows 4u + 2rp, 4u + 2rp + 1 as the GGUF block, at byte 2 of each (the fields are then at the
+// same places as in the GGUF path: d at 2, the slice's indices at 4 + 8s, its sign / scale word at
+// 68 + 4s).
+template <int TYPE, int NT, int KS, bool PK = false>
 __global__ void __launch_bounds__(64 * KS) gemm_generic_kernel(const uint8_t* __restrict__ W, int64_t row_bytes,
                                                                int nrows, int k, const uint8_t* __restrict__ xq,
                                                                int nct, int n, void* __restrict__ y, int y_dtype) {
@@ -588,19 +595,42 @@ __global__ void __launch_bounds__(64 * KS) gemm_generic_kernel(const uint8_t* __
 #pragma unroll
     for (int v = 0; v < 4; ++v) acc[t][v] = 0.0f;
 
+  static_assert(!PK || TYPE == kIQ3_XXS, "the packed layout is IQ3_XXS's");
+  const int pu = lane >> 4, prp = (lane >> 3) & 1, ps = lane & 7;  // PK: unit, row pair, slice
+  const int pk_off = pu * 4 * (int)row_bytes + 16 * (8 * prp + ps);
   auto load_rows = [&](int b, u32x4 (&r)[2]) {
     const int bb = b < b_end ? b : b_end - 1;  // past the wave's range: re-read its last block
-    const int bo = (bb * BS) & ~3;
-    r[0] = __builtin_amdgcn_raw_buffer_load_b128(wrs, copy_off + bo, 0, 0);
-    r[1] = __builtin_amdgcn_raw_buffer_load_b128(wrs, copy_off + bo + 16, 0, 0);
+    if constexpr (PK) {
+      const XxsFields f = xxs_block_fields(nb, bb);
+      r[0] = __builtin_amdgcn_raw_buffer_load_b128(wrs, pk_off + (int)f.qs, 0, 0);
+      const auto a = __builtin_amdgcn_raw_buffer_load_b64(wrs, pu * 4 * (int)row_bytes + (int)f.aux + 8 * (8 * prp + ps),
+                                                         0, 0);
+      const uint32_t d = __builtin_amdgcn_raw_buffer_load_b32(wrs, pu * 4 * (int)row_bytes + (int)f.d + 4 * prp, 0, 0);
+      r[1] = u32x4{a[0], a[1], d, 0u};
+    } else {
+      const int bo = (bb * BS) & ~3;
+      r[0] = __builtin_amdgcn_raw_buffer_load_b128(wrs, copy_off + bo, 0, 0);
+      r[1] = __builtin_amdgcn_raw_buffer_load_b128(wrs, copy_off + bo + 16, 0, 0);
+    }
   };
   // the block lands at byte 2 of its staged row whatever its alignment in W, so that its 4-byte
   // fields (at 2 mod 4 in every format here) are aligned LDS words
   auto store_rows = [&](uint8_t* buf, int b, const u32x4 (&r)[2]) {
-    const int bb = b < b_end ? b : b_end - 1;
-    uint4* d = (uint4*)(buf + 2 - ((bb * BS) & 3) + (lane >> 2) * kGenRowStride + 32 * (lane & 3));
-    d[0] = make_uint4(r[0][0], r[0][1], r[0][2], r[0][3]);
-    d[1] = make_uint4(r[1][0], r[1][1], r[1][2], r[1][3]);
+    if constexpr (PK) {
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr) {
+        uint8_t* row = buf + 2 + (4 * pu + 2 * prp + rr) * kGenRowStride;
+        *(uint32_t*)(row + 2 + 8 * ps) = r[0][2 * rr];
+        *(uint32_t*)(row + 6 + 8 * ps) = r[0][2 * rr + 1];
+        *(uint32_t*)(row + 66 + 4 * ps) = r[1][rr];
+        *(uint16_t*)row = (uint16_t)(r[1][2] >> (16 * rr));  // the 8 lanes of a row pair write the same d
+      }
+    } else {
+      const int bb = b < b_end ? b : b_end - 1;
+      uint4* d = (uint4*)(buf + 2 - ((bb * BS) & 3) + (lane >> 2) * kGenRowStride + 32 * (lane & 3));
+      d[0] = make_uint4(r[0][0], r[0][1], r[0][2], r[0][3]);
+      d[1] = make_uint4(r[1][0], r[1][1], r[1][2], r[1][3]);
+    }
   };
   auto compute = [&](const uint8_t* buf0_, int b, const XRawFrag<NT>& x) {
     const uint8_t* buf = buf0_ + 2;  // the block's first byte in each staged row
@@ -699,22 +729,22 @@ __global__ void __launch_bounds__(64 * KS) gemm_generic_kernel(const uint8_t* __
   }
 }
 
-template <int TYPE, int NT>
+template <int TYPE, int NT, bool PK = false>
 void launch_generic_t(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n, void* y,
                       int y_dtype, hipStream_t stream) {
   const int nct = (int)xq_col_tiles(n);
   const dim3 grid((unsigned)((nrows + kRawRows - 1) / kRawRows), (unsigned)((nct + NT - 1) / NT));
-  gemm_generic_kernel<TYPE, NT, 4><<<grid, 256, 0, stream>>>(W, row_bytes, nrows, k, xq, nct, n, y, y_dtype);
+  gemm_generic_kernel<TYPE, NT, 4, PK><<<grid, 256, 0, stream>>>(W, row_bytes, nrows, k, xq, nct, n, y, y_dtype);
 }
 
-template <int TYPE>
+template <int TYPE, bool PK = false>
 void launch_generic_type(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n, void* y,
                          int y_dtype, hipStream_t stream) {
   const int nct = (int)xq_col_tiles(n);
-  if (nct == 1) launch_generic_t<TYPE, 1>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
-  else if (nct == 2) launch_generic_t<TYPE, 2>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
-  else if (nct == 3) launch_generic_t<TYPE, 3>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
-  else launch_generic_t<TYPE, 4>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
+  if (nct == 1) launch_generic_t<TYPE, 1, PK>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
+  else if (nct == 2) launch_generic_t<TYPE, 2, PK>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
+  else if (nct == 3) launch_generic_t<TYPE, 3, PK>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
+  else launch_generic_t<TYPE, 4, PK>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
 }
 
 template <int TYPE, int NT, int KS, bool SX>
@@ -795,6 +825,15 @@ hipError_t launch_gemm_xq(int type, const uint8_t* W, int64_t row_bytes, int nro
     case kIQ3_XXS: launch_generic_type<kIQ3_XXS>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream); break;
     default: return hipErrorInvalidValue;
   }
+  return hipGetLastError();
+}
+
+// IQ3_XXS in the build's unit layout (rows % 16 == 0), the product ops' MMQ arithmetic; xq: X in
+// the xq layout
+hipError_t launch_gemm_iq3xxs_packed(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n,
+                                     void* y, int y_dtype, hipStream_t stream) {
+  if (nrows % kRawRows != 0) return hipErrorInvalidValue;
+  launch_generic_type<kIQ3_XXS, true>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
   return hipGetLastError();
 }
 

@@ -17,6 +17,7 @@
 //  * gemv_iq3s_tile_kernel (the other shapes): one 16-row tile per workgroup, its waves split the
 //    K blocks; X as q8_1 or quantised block by block.
 #include <algorithm>
+#include <type_traits>
 
 #include "gemv_x.h"
 #include "iq3_tile.h"
@@ -69,6 +70,127 @@ struct XFrag {
   int q[NC][8];
   uint32_t d[NC];  // fp16 bits (converted where used, so a prefetch does not wait for its load)
 };
+
+// ---------------------------------------------------------------------------------------------
+// IQ3_XXS in the build's unit layout (iq3_tile.h): the stream kernel below serves it with the
+// lanes of the IQ3_S layout. Lane L = 8p + s loads its 16 QS bytes (row 2rp's 8 grid indices of
+// slice s, then row 2rp+1's), its 8 AUX bytes (the two rows' sign / scale words) and the 4 D bytes
+// of its row pair, each field contiguous across the wave.
+__device__ const Lattice32<256> kIq3xxsGridDev = kIq3xxsGrid;
+
+struct XxsFrag {
+  uint4 qs;
+  uint2 aux;
+  uint32_t dd;  // fp16 d of row 2rp (low half) and 2rp+1 (high half)
+};
+
+// f: the unit-block's field bases inside rs (scalar offsets); o: the lane's offsets (unit_lane_offsets:
+// qs 16L, e8 8L, dd 4p)
+__device__ __forceinline__ void load_xxs_frag(__amdgpu_buffer_rsrc_t rs, const XxsFields& f, const TileOffs& o,
+                                              XxsFrag& t) {
+  const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)o.qs, (int)f.qs, kWeightCpol);
+  t.qs = make_uint4(q.x, q.y, q.z, q.w);
+  const auto e = __builtin_amdgcn_raw_buffer_load_b64(rs, (int)o.e8, (int)f.aux, kWeightCpol);
+  t.aux = make_uint2(e[0], e[1]);
+  t.dd = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)o.dd, (int)f.d, kWeightCpol);
+}
+
+// The 4096-entry IQ3_XXS signed table in LDS (entry g | n << 8: grid word g with the bytes whose
+// bit is set in the nibble n negated; the kIq3xxsSigned entries), built from the 1 KB grid:
+// thread i < 512 holds grid word i & 255 and writes the 8 entries of the nibbles 8 (i >> 8) ..
+// 8 (i >> 8) + 7. Every grid byte is nonzero, so the bytewise negation is 0x01010100 - g.
+constexpr bool iq3xxs_table_formula_holds() {
+  for (int i = 0; i < 4096; ++i) {
+    const uint32_t g = kIq3xxsGrid.v[i & 255], neg = 0x01010100u - g, n = (uint32_t)i >> 8;
+    const uint32_t m = ((n & 1) ? 0xFFu : 0u) | ((n & 2) ? 0xFF00u : 0u) | ((n & 4) ? 0xFF0000u : 0u) |
+                       ((n & 8) ? 0xFF000000u : 0u);
+    if (((neg & m) | (g & ~m)) != kIq3xxsSigned.v[i]) return false;
+  }
+  return true;
+}
+static_assert(iq3xxs_table_formula_holds(), "IQ3_XXS signed table from the grid");
+
+__device__ __forceinline__ void iq3xxs_table_from_grid(uint4* table, uint32_t gword, int i) {
+  const uint32_t neg = 0x01010100u - gword;
+  const uint32_t top = (i >> 8) & 1 ? 0xFF000000u : 0u;  // nibble bit 3
+  uint32_t* t32 = (uint32_t*)table;
+  const uint32_t base = (uint32_t)(i & 255) | ((uint32_t)((i >> 8) & 1) << 11);
+#pragma unroll
+  for (int sg = 0; sg < 8; ++sg) {
+    const uint32_t m = ((sg & 1) ? 0xFFu : 0u) | ((sg & 2) ? 0xFF00u : 0u) | ((sg & 4) ? 0xFF0000u : 0u) | top;
+    t32[base | ((uint32_t)sg << 8)] = (neg & m) | (gword & ~m);
+  }
+}
+
+// byte B of v times 4 (a table entry's byte offset): one SDWA shift
+template <int B>
+__device__ __forceinline__ uint32_t byte_x4(uint32_t v) {
+  uint32_t o;
+  if constexpr (B == 0)
+    asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0" : "=v"(o) : "v"(v));
+  else if constexpr (B == 1)
+    asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1" : "=v"(o) : "v"(v));
+  else if constexpr (B == 2)
+    asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2" : "=v"(o) : "v"(v));
+  else
+    asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3" : "=v"(o) : "v"(v));
+  return o;
+}
+
+// a ^ b ^ c in one gfx950 three-input bit operation (truth table 0x96: odd parity)
+__device__ __forceinline__ uint32_t xor3(uint32_t a, uint32_t b, uint32_t c) {
+  uint32_t o;
+  asm("v_bitop3_b32 %0, %1, %2, %3 bitop3:0x96" : "=v"(o) : "v"(a), "v"(b), "v"(c));
+  return o;
+}
+
+// bits 7g..7g+3 of v at bits 10..13 (the nibble's place in a table byte offset)
+template <int G>
+__device__ __forceinline__ uint32_t nib_x1024(uint32_t v) {
+  constexpr int sh = 10 - 7 * G;
+  return (sh >= 0 ? v << sh : v >> -sh) & 0x3C00u;
+}
+
+// The lane's two rows of one item. Sign index g (bits 7g..7g+6 of aux) gives the first word of
+// group g its nibble (bits 7g..7g+3) and the second word bits 7g+4..7g+6 plus the parity of all
+// seven as bit 3 (ksigns_iq2xs). The four parities come from two three-way xors: with
+// t_i = a_i ^ a_i+1 ^ a_i+2, t_i ^ t_i+3 ^ a_i+6 is the xor of a_i..a_i+6, which at i = 7g reads
+// only sign index g's bits. A table read's byte offset is (index byte) * 4 | nibble * 1024. The
+// slice term is the decode ops' (s4 sumi + sumi / 2) / 2 with s4 = aux >> 28 (ls = 2 s4 + 1),
+// times d and X's d.
+template <int NC>
+__device__ __forceinline__ void xxs_compute(const uint8_t* tbl, const XxsFrag& f, const XFrag<NC>& x,
+                                            float (&acc)[2][NC]) {
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const uint32_t a = r == 0 ? f.aux.x : f.aux.y;
+    const uint32_t t = xor3(a, a >> 1, a >> 2);
+    const uint32_t par = xor3(t, t >> 3, a >> 6);                              // bit 7g: parity of index g
+    const uint32_t hi = ((par << 3) & 0x01020408u) | ((a >> 4) & ~0x01020408u);  // bits 7g..7g+3
+    const uint32_t q0 = r == 0 ? f.qs.x : f.qs.z, q1 = r == 0 ? f.qs.y : f.qs.w;
+    int w[8];
+    w[0] = *(const int*)(tbl + (byte_x4<0>(q0) | nib_x1024<0>(a)));
+    w[1] = *(const int*)(tbl + (byte_x4<1>(q0) | nib_x1024<0>(hi)));
+    w[2] = *(const int*)(tbl + (byte_x4<2>(q0) | nib_x1024<1>(a)));
+    w[3] = *(const int*)(tbl + (byte_x4<3>(q0) | nib_x1024<1>(hi)));
+    w[4] = *(const int*)(tbl + (byte_x4<0>(q1) | nib_x1024<2>(a)));
+    w[5] = *(const int*)(tbl + (byte_x4<1>(q1) | nib_x1024<2>(hi)));
+    w[6] = *(const int*)(tbl + (byte_x4<2>(q1) | nib_x1024<3>(a)));
+    w[7] = *(const int*)(tbl + (byte_x4<3>(q1) | nib_x1024<3>(hi)));
+    const float lsq = (float)(2 * (int)(a >> 28) + 1) * 0.25f;  // ls / 4
+    const float dw = half_bits_to_float((f.dd >> (16 * r)) & 0xFFFFu);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      int sumi = 0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sumi = dot4(w[e], x.q[c][e], sumi);
+      // (s4 sumi + sumi / 2) / 2 in C's truncating division equals trunc(sumi ls / 4), and
+      // sumi ls (|sumi| <= 32 * 62 * 127, ls <= 31) is below 2^24: exact in fp32
+      const float v = truncf((float)sumi * lsq);
+      acc[r][c] = fmaf(v, dw * half_bits_to_float(x.d[c]), acc[r][c]);
+    }
+  }
+}
 
 // q8_1 blocks of X at slice `slice0 + s` for every activation row c (row c starts nslices
 // blocks after row c-1): rs describes the whole q8_1 buffer, lane_off = 36 * s
@@ -347,15 +469,21 @@ constexpr int kStreamWaves = 8;
 // X: XDT < 0 the caller's block_q8_1 copied into LDS, XDT >= 0 X itself (row stride s01)
 // quantised into LDS with the q8_1 arithmetic. Each thread stages XPT groups of 8 values, their
 // loads issued first, then the grid word, then the wave's first two unit-blocks.
-template <int NC, int XDT, int XPT, int NW = kStreamWaves>
+// TYPE kIQ3_XXS: the same split, items and lanes over the IQ3_XXS unit layout (1568-B unit-blocks;
+// XxsFrag), its 16 KB signed table built from the 1 KB grid.
+// Y's activation rows are ys elements apart (the launch may cover a run of the weight's rows).
+template <int TYPE, int NC, int XDT, int XPT, int NW = kStreamWaves>
 __global__ void __launch_bounds__(64 * NW) gemv_iq3s_stream_kernel(const uint8_t* __restrict__ W,
                                                                               int64_t row_bytes, int nrows, int k,
                                                                               const void* __restrict__ xsrc,
                                                                               int64_t s01, void* __restrict__ y,
-                                                                              int y_dtype) {
+                                                                              int64_t ys, int y_dtype) {
   constexpr int NT = 64 * NW;
+  constexpr bool XXS = TYPE == kIQ3_XXS;
+  static_assert(TYPE == kIQ3_S || XXS, "IQ3_S or IQ3_XXS, each in its unit layout");
   static_assert(NT >= 512, "the table build takes 512 threads");
-  __shared__ uint4 table[2048];
+  using Frag = typename std::conditional<XXS, XxsFrag, TileFrag>::type;
+  __shared__ uint4 table[XXS ? 1024 : 2048];
   __shared__ uint4 sink;    // staging writes of groups past the end of X
   extern __shared__ uint4 xdyn[];  // X: q [NC][slice][8 dwords], d [NC][slice]; then the partial sums
   const int lane = threadIdx.x & 63;
@@ -382,7 +510,8 @@ __global__ void __launch_bounds__(64 * NW) gemv_iq3s_stream_kernel(const uint8_t
 #pragma unroll
   for (int j = 0; j < XPT; ++j) xgroup_load<NC, XDT>(xsrc, xrs, s01, nslices, xg[j], xa[j]);
   const uint32_t gword =
-      __builtin_amdgcn_raw_buffer_load_b32(buffer_rsrc(&kIq3sGridDev, 2048), 4 * (threadIdx.x & 511), 0, 0);
+      XXS ? __builtin_amdgcn_raw_buffer_load_b32(buffer_rsrc(&kIq3xxsGridDev, 1024), 4 * (threadIdx.x & 255), 0, 0)
+          : __builtin_amdgcn_raw_buffer_load_b32(buffer_rsrc(&kIq3sGridDev, 2048), 4 * (threadIdx.x & 511), 0, 0);
   __builtin_amdgcn_sched_barrier(0);
   // the workgroup's units [u0, u1) and the wave's run of items [j0, j1) (32-bit: units * grid
   // < 2^31 for any weight of fewer than 2^23 rows)
@@ -410,10 +539,20 @@ __global__ void __launch_bounds__(64 * NW) gemv_iq3s_stream_kernel(const uint8_t
     return f;
   };
   // past the run: the empty range nrs (every lane's load reads zeros)
-  auto load_next = [&](TileFrag& f) {
-    const Iq3Fields e = {0u, 0u, 0u, 0u, 0u};
+  auto load_next = [&](Frag& f) {
     const bool in_run = lj < j1;
-    load_tile_frag(in_run ? wrs : nrs, in_run ? fields(lu, lkb) : e, ragged && lkb == nkb - 1 ? off_r : off, f);
+    if constexpr (XXS) {
+      XxsFields x = {0u, 0u, 0u};
+      if (in_run) {
+        x = xxs_unitblock_fields(nb, lkb);
+        const uint32_t ub = (uint32_t)lu * ubytes;
+        x.qs += ub; x.aux += ub; x.d += ub;
+      }
+      load_xxs_frag(in_run ? wrs : nrs, x, ragged && lkb == nkb - 1 ? off_r : off, f);
+    } else {
+      const Iq3Fields e = {0u, 0u, 0u, 0u, 0u};
+      load_tile_frag(in_run ? wrs : nrs, in_run ? fields(lu, lkb) : e, ragged && lkb == nkb - 1 ? off_r : off, f);
+    }
     ++lj;
     if (++lkb == nkb) {
       lkb = 0;
@@ -421,11 +560,14 @@ __global__ void __launch_bounds__(64 * NW) gemv_iq3s_stream_kernel(const uint8_t
     }
   };
   __syncthreads();
-  TileFrag f0, f1, f2;
+  Frag f0, f1, f2;
   load_next(f0);
   load_next(f1);
   __builtin_amdgcn_sched_barrier(0);
-  if (NT == 512 || threadIdx.x < 512) iq3_table_from_grid(table, gword, threadIdx.x);
+  if (NT == 512 || threadIdx.x < 512) {
+    if constexpr (XXS) iq3xxs_table_from_grid(table, gword, threadIdx.x);
+    else iq3_table_from_grid(table, gword, threadIdx.x);
+  }
 #pragma unroll
   for (int j = 0; j < XPT; ++j) {
     if (wave * 64 + j * NT < ngroups)  // waves with no group left skip the (fused) quantisation
@@ -441,7 +583,7 @@ __global__ void __launch_bounds__(64 * NW) gemv_iq3s_stream_kernel(const uint8_t
   for (int r = 0; r < 2; ++r)
 #pragma unroll
     for (int c = 0; c < NC; ++c) acc[r][c] = 0.0f;
-  auto step = [&](const TileFrag& fc, TileFrag& fl) {
+  auto step = [&](const Frag& fc, Frag& fl) {
     load_next(fl);
     __builtin_amdgcn_sched_barrier(0);
     // lanes of blocks past a last unit-block of r < 4 blocks: d = 0 and X's d = 0
@@ -457,9 +599,10 @@ __global__ void __launch_bounds__(64 * NW) gemv_iq3s_stream_kernel(const uint8_t
       const uint32_t dv = xd[o];  // read unconditionally (o is in range) and selected: no branch
       x.d[c] = live ? dv : 0u;
     }
-    TileFrag f = fc;
+    Frag f = fc;
     f.dd = live ? f.dd : 0u;
-    tile_compute<NC>(tbl, f, x, s, acc);
+    if constexpr (XXS) xxs_compute<NC>(tbl, f, x, acc);
+    else tile_compute<NC>(tbl, f, x, s, acc);
     ++j;
     if (++ckb == nkb || j == j1) {  // leaving the unit: its partial sums to the wave's slot
       const int slot = cu * NW + wave;
@@ -507,7 +650,7 @@ __global__ void __launch_bounds__(64 * NW) gemv_iq3s_stream_kernel(const uint8_t
     v += dpp_f<0xB1>(v);
     v += dpp_f<0x4E>(v);
     if (q == 0 && o < nout)
-      store_y(y, (int64_t)c * nrows + (int64_t)(u0 + uu) * kUnitRows + row, v, y_dtype);
+      store_y(y, (int64_t)c * ys + (int64_t)(u0 + uu) * kUnitRows + row, v, y_dtype);
   }
 }
 
@@ -526,9 +669,12 @@ static size_t stream_lds(int64_t nrows, int64_t k, int64_t n, int64_t grid) {
   return std::max(kStreamLdsMin, (size_t)n * (size_t)(k / kQ81) * 36 + part);
 }
 
-// the stream kernel's static LDS: the signed-grid table (2048 x 16 B) and the 16-B sink
-constexpr size_t kStreamStaticLds = sizeof(uint4) * 2049;
-constexpr size_t kStreamLdsMax = 160 * 1024 - kStreamStaticLds;  // the dynamic LDS a workgroup may take
+// the stream kernel's static LDS: the signed-grid table (IQ3_S 2048, IQ3_XXS 1024 x 16 B) and the
+// 16-B sink; the dynamic LDS a workgroup may take beside it
+template <int TYPE>
+constexpr size_t stream_lds_max() {
+  return 160 * 1024 - sizeof(uint4) * ((TYPE == kIQ3_XXS ? 1024 : 2048) + 1);
+}
 
 // The stream kernel takes 1..4 activation rows (fused X: 1..2 rows at K <= 8192) on weights of
 // at least one 4-row unit per CU, with X's q8_1 and the partial sums within its LDS budget (a
@@ -536,39 +682,40 @@ constexpr size_t kStreamLdsMax = 160 * 1024 - kStreamStaticLds;  // the dynamic 
 // the tile kernel). Quantising X in every workgroup costs more than the quantise launch at 3-4
 // rows (17408 x 5120, M = 4: 19.5 against 18.3 us) and at K = 17408 (5120 x 17408, M = 1: 13.5
 // against 12.8 us): those take the q8_1 path.
+template <int TYPE = kIQ3_S>
 static bool stream_supported(int64_t nrows, int64_t k, int64_t n, bool fused) {
   if (n < 1 || n > (fused ? 2 : 4) || (fused && k > 8192)) return false;
   if ((size_t)n * (size_t)(k / kQ81) * 36 > kStreamXMax) return false;
   const int64_t cus = device_cus();
   if (nrows / kUnitRows < cus) return false;
-  return stream_lds(nrows, k, n, cus) <= kStreamLdsMax;
+  return stream_lds(nrows, k, n, cus) <= stream_lds_max<TYPE>();
 }
 
-template <int NC, int XDT, int XPT>
+template <int TYPE, int NC, int XDT, int XPT>
 static void launch_stream_k(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x, int64_t s01,
-                            void* y, int y_dtype, hipStream_t stream) {
+                            void* y, int64_t ys, int y_dtype, hipStream_t stream) {
   const unsigned g = (unsigned)std::min<int64_t>(nrows / kUnitRows, device_cus());
   const size_t lds = stream_lds(nrows, k, NC, g);
   int dev = 0;
   if (hipGetDevice(&dev) == hipSuccess) {
     struct Tag;  // one set of per-device flags per kernel instantiation
     once_per_device<Tag>(dev, [] {
-      (void)hipFuncSetAttribute((const void*)gemv_iq3s_stream_kernel<NC, XDT, XPT>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)kStreamLdsMax);
+      (void)hipFuncSetAttribute((const void*)gemv_iq3s_stream_kernel<TYPE, NC, XDT, XPT>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)stream_lds_max<TYPE>());
     });
   }
-  gemv_iq3s_stream_kernel<NC, XDT, XPT><<<g, 64 * kStreamWaves, lds, stream>>>(W, row_bytes, nrows, k, x, s01, y,
-                                                                              y_dtype);
+  gemv_iq3s_stream_kernel<TYPE, NC, XDT, XPT><<<g, 64 * kStreamWaves, lds, stream>>>(W, row_bytes, nrows, k, x, s01,
+                                                                                    y, ys, y_dtype);
 }
 
-template <int NC, int XDT>
+template <int TYPE, int NC, int XDT>
 static hipError_t launch_stream_nc(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x,
-                                   int64_t s01, void* y, int y_dtype, hipStream_t stream) {
+                                   int64_t s01, void* y, int64_t ys, int y_dtype, hipStream_t stream) {
   const int need = (NC * (k / kQ81) * 4 + 64 * kStreamWaves - 1) / (64 * kStreamWaves);
-#define GGUF_XPT(X)                                                                     \
-  if (need <= X) {                                                                      \
-    launch_stream_k<NC, XDT, X>(W, row_bytes, nrows, k, x, s01, y, y_dtype, stream);    \
-    return hipSuccess;                                                                  \
+#define GGUF_XPT(X)                                                                         \
+  if (need <= X) {                                                                          \
+    launch_stream_k<TYPE, NC, XDT, X>(W, row_bytes, nrows, k, x, s01, y, ys, y_dtype, stream);  \
+    return hipSuccess;                                                                      \
   }
   if constexpr (XDT >= 0) {  // fused: K <= 8192, at most 4 groups per thread
     GGUF_XPT(1) GGUF_XPT(2) GGUF_XPT(3) GGUF_XPT(4)
@@ -580,14 +727,16 @@ static hipError_t launch_stream_nc(const uint8_t* W, int64_t row_bytes, int nrow
   return hipErrorInvalidValue;  // no instantiation stages this much of X (stream_supported excludes it)
 }
 
-template <int XDT>
+// ys: Y's row stride in elements (the weight's rows, or more where a launch covers a run of them)
+template <int XDT, int TYPE = kIQ3_S>
 static hipError_t launch_stream(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x, int64_t s01,
-                                int n, void* y, int y_dtype, hipStream_t stream) {
-  if (n == 1) return launch_stream_nc<1, XDT>(W, row_bytes, nrows, k, x, s01, y, y_dtype, stream);
-  if (n == 2) return launch_stream_nc<2, XDT>(W, row_bytes, nrows, k, x, s01, y, y_dtype, stream);
+                                int n, void* y, int y_dtype, hipStream_t stream, int64_t ys = -1) {
+  if (ys < 0) ys = nrows;
+  if (n == 1) return launch_stream_nc<TYPE, 1, XDT>(W, row_bytes, nrows, k, x, s01, y, ys, y_dtype, stream);
+  if (n == 2) return launch_stream_nc<TYPE, 2, XDT>(W, row_bytes, nrows, k, x, s01, y, ys, y_dtype, stream);
   if constexpr (XDT < 0) {
-    if (n == 3) return launch_stream_nc<3, XDT>(W, row_bytes, nrows, k, x, s01, y, y_dtype, stream);
-    if (n == 4) return launch_stream_nc<4, XDT>(W, row_bytes, nrows, k, x, s01, y, y_dtype, stream);
+    if (n == 3) return launch_stream_nc<TYPE, 3, XDT>(W, row_bytes, nrows, k, x, s01, y, ys, y_dtype, stream);
+    if (n == 4) return launch_stream_nc<TYPE, 4, XDT>(W, row_bytes, nrows, k, x, s01, y, ys, y_dtype, stream);
   }
   return hipErrorInvalidValue;
 }
@@ -665,6 +814,64 @@ hipError_t launch_gemv_packed_x(const uint8_t* W, int64_t row_bytes, int nrows, 
         launch_tile<8, kBF16>(W, row_bytes, nrows, k, x, s01, n, y, y_dtype, stream);
       }
       break;
+  }
+  return hipGetLastError();
+}
+
+// IQ3_XXS decode in its unit layout (packed; rows % 16 == 0, K % 512 == 0) through the stream
+// kernel, on any number of rows: launches take at most 4 activation rows (fused, X quantised
+// inside: 1-2 rows at K <= 8192, bit-identical to the q8_1 quantiser followed by the q8_1
+// launch), and a weight of more units per CU than the partial-sum slots of LDS hold runs in
+// consecutive row ranges, one launch each. X's q8_1 of one activation row must fit the kernel's
+// X staging (K <= 87,381).
+static int64_t xxs_rows_per_launch(int64_t nrows, int64_t k, int64_t n) {
+  const int64_t cus = device_cus();
+  const size_t x = (size_t)n * (size_t)(k / kQ81) * 36;
+  if (x > kStreamXMax) return 0;
+  const size_t slot = (size_t)kStreamWaves * (size_t)n * 16 * sizeof(float);  // per unit
+  const int64_t nu_fit = (int64_t)((stream_lds_max<kIQ3_XXS>() - x) / slot);
+  if (nu_fit < 1) return 0;
+  return std::min<int64_t>(nrows, nu_fit * cus * kUnitRows);
+}
+
+static int xxs_rows_per_group(int64_t k, bool fused) {
+  int g = fused ? 2 : 4;
+  while (g > 1 && (size_t)g * (size_t)(k / kQ81) * 36 > kStreamXMax) --g;
+  return g;
+}
+
+bool gemv_iq3xxs_stream_supported(int64_t nrows, int64_t row_bytes, int64_t k, int64_t n, bool fused) {
+  if (nrows < kTileRows || nrows % kTileRows != 0 || k < 512 || k % 512 != 0 || row_bytes != k / kQK * 98) return false;
+  if (n < 1 || (fused && (n > 2 || k > 8192))) return false;
+  return xxs_rows_per_launch(nrows, k, 1) > 0;
+}
+
+// x_dtype < 0: x is X's block_q8_1; else X itself (dtype x_dtype, row stride s01)
+hipError_t launch_gemv_iq3xxs_stream(const uint8_t* W, int64_t row_bytes, int nrows, int k, const void* x,
+                                     int x_dtype, int64_t s01, int n, void* y, int y_dtype, hipStream_t stream) {
+  const bool fused = x_dtype >= 0;
+  if (!gemv_iq3xxs_stream_supported(nrows, row_bytes, k, n, fused)) return hipErrorInvalidValue;
+  const int group = xxs_rows_per_group(k, fused);
+  const int64_t ysz = y_dtype == kF32 ? 4 : 2, xsz = x_dtype == kF32 ? 4 : 2;
+  for (int c0 = 0; c0 < n; c0 += group) {
+    const int nc = std::min(group, n - c0);
+    const int64_t run = xxs_rows_per_launch(nrows, k, nc);
+    if (run <= 0) return hipErrorInvalidValue;
+    const void* xc = fused ? (const void*)((const uint8_t*)x + (int64_t)c0 * s01 * xsz)
+                           : (const void*)((const uint8_t*)x + (int64_t)c0 * (k / kQ81) * 36);
+    for (int64_t r0 = 0; r0 < nrows; r0 += run) {
+      const int rows = (int)std::min<int64_t>(run, nrows - r0);
+      const uint8_t* wc = W + r0 * row_bytes;
+      void* yc = (uint8_t*)y + ((int64_t)c0 * nrows + r0) * ysz;
+      hipError_t e;
+      switch (x_dtype) {
+        case kF32: e = launch_stream<kF32, kIQ3_XXS>(wc, row_bytes, rows, k, xc, s01, nc, yc, y_dtype, stream, nrows); break;
+        case kF16: e = launch_stream<kF16, kIQ3_XXS>(wc, row_bytes, rows, k, xc, s01, nc, yc, y_dtype, stream, nrows); break;
+        case kBF16: e = launch_stream<kBF16, kIQ3_XXS>(wc, row_bytes, rows, k, xc, s01, nc, yc, y_dtype, stream, nrows); break;
+        default: e = launch_stream<-1, kIQ3_XXS>(wc, row_bytes, rows, k, xc, 0, nc, yc, y_dtype, stream, nrows); break;
+      }
+      if (e != hipSuccess) return e;
+    }
   }
   return hipGetLastError();
 }

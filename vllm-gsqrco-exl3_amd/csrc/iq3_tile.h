@@ -158,6 +158,63 @@ __host__ __device__ inline void iq3_tile_scale_source(int j, int r, int& row, in
 }
 
 // ---------------------------------------------------------------------------------------------
+// The build's IQ3_XXS unit layout (its own, as the IQ3_S one above): the same 4-row units and
+// unit-blocks of 4 K blocks (4 x 4 x 98 = 1568 B; a last unit-block of r = nb % 4 blocks takes
+// 392 r bytes, fields scaled by r/4), the same lanes L = 8p + s (p = 2 bi + rp: rows 2rp, 2rp+1 of
+// the unit in slice s of block 4kb + bi). block_iq3_xxs is d[0:2], qs[2:66] (one grid index per 4
+// values), then per slice s a dword at 66 + 4s (four 7-bit sign indices, the scale in bits 28..31).
+//   [   0, 256 r) QS  16 B at 16L: qs[8s..8s+8) of row 2rp, then of row 2rp+1
+//   [256 r, 384 r) AUX  8 B at 8L : the slice's dword of row 2rp, then of row 2rp+1
+//   [384 r, 392 r) D    4 B at 4p : d of row 2rp, then of row 2rp+1
+// A byte permutation local to each unit, bijective; every decode-wave load is contiguous across
+// the wave (16 / 8 B per lane, 4 B per 8 lanes). The data of K block b = 4kb + bi sits, inside its
+// unit-block, at QS 256 bi, AUX 128 bi and D 8 bi.
+constexpr int kXxsUnitBlockBytes = 4 * 4 * 98;  // 1568
+
+__host__ __device__ constexpr uint32_t xxs_aux_base(int r) { return 256u * r; }
+__host__ __device__ constexpr uint32_t xxs_d_base(int r) { return 384u * r; }
+
+struct XxsFields {
+  uint32_t qs, aux, d;
+};
+
+// unit-block kb of a unit of nb blocks: field bases from the unit's first byte
+__host__ __device__ inline XxsFields xxs_unitblock_fields(int nb, int kb) {
+  const int r = iq3_unit_blocks(nb, kb);
+  const uint32_t u = (uint32_t)kXxsUnitBlockBytes * kb;
+  return {u, u + xxs_aux_base(r), u + xxs_d_base(r)};
+}
+
+// K block b of a unit of nb blocks: its QS / AUX / D bytes from the unit's first byte (QS: 16
+// lanes x 16 B, AUX 16 x 8 B, D 2 x 4 B, lanes 16 bi .. 16 bi + 15 in order)
+__host__ __device__ inline XxsFields xxs_block_fields(int nb, int b) {
+  const int kb = b >> 2, bi = b & 3, r = iq3_unit_blocks(nb, kb);
+  const uint32_t u = (uint32_t)kXxsUnitBlockBytes * kb;
+  return {u + 256u * bi, u + xxs_aux_base(r) + 128u * bi, u + xxs_d_base(r) + 8u * bi};
+}
+
+// Byte j of a unit-block of r blocks <- (row in the unit, block bi in the unit-block, byte o of
+// that row's GGUF block)
+__host__ __device__ inline void xxs_unit_source(int j, int r, int& row, int& bi, int& o) {
+  if (j < (int)xxs_aux_base(r)) {
+    const int L = j >> 4, w = j & 15, s = L & 7;
+    bi = L >> 4;
+    row = 2 * ((L >> 3) & 1) + (w >> 3);
+    o = 2 + 8 * s + (w & 7);
+  } else if (j < (int)xxs_d_base(r)) {
+    const int jj = j - (int)xxs_aux_base(r), L = jj >> 3, w = jj & 7, s = L & 7;
+    bi = L >> 4;
+    row = 2 * ((L >> 3) & 1) + (w >> 2);
+    o = 66 + 4 * s + (w & 3);
+  } else {
+    const int jj = j - (int)xxs_d_base(r), p = jj >> 2, w = jj & 3;
+    bi = p >> 1;
+    row = 2 * (p & 1) + (w >> 1);
+    o = w & 1;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // Decode helpers of the kernels
 
 // ex of the 4 groups 0..3 (lo) and 4..7 (hi) of row r, one per byte, from a lane's E8 dword of

@@ -1,8 +1,9 @@
-// In-place conversion between GGUF IQ3_S rows and the build's unit layout (iq3_tile.h), the
+// In-place conversion between GGUF IQ3_S / IQ3_XXS rows and the build's unit layouts (iq3_tile.h), the
 // load-time repack behind GGUFLinearMethod._pack_iq3 (reference: quantization/iq3_pack.py
 // pack_ / unpack, linear.py:437-457). Whole 4-row units are copied to scratch in chunks and
-// converted back; per unit-block of r K blocks, 16 r threads handle the lanes' QS / E8 / L2 bytes
-// and 24 r threads the scale and d bytes.
+// converted back. IQ3_S: per unit-block of r K blocks, 16 r threads handle the lanes' QS / E8 / L2
+// bytes and 24 r threads the scale and d bytes; IQ3_XXS (a plain byte permutation): one thread per
+// byte.
 #include "iq3_tile.h"
 
 namespace gguf {
@@ -49,20 +50,44 @@ __global__ void iq3_unit_convert_kernel(const uint8_t* __restrict__ src, uint8_t
   }
 }
 
-hipError_t launch_iq3_pack(uint8_t* w, int64_t rows, int64_t row_bytes, bool unpack, uint8_t* scratch,
+// IQ3_XXS: one thread per byte of the unit layout (xxs_unit_source names its GGUF byte); unpack
+// writes each GGUF byte back from its place in the unit layout.
+__global__ void iq3xxs_unit_convert_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
+                                           int64_t row_bytes, int64_t nunits, int nb, bool unpack) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t unit_bytes = kUnitRows * row_bytes;
+  if (i >= nunits * unit_bytes) return;
+  const int64_t u = i / unit_bytes;
+  const int jb = (int)(i - u * unit_bytes);  // byte of the unit (layout side)
+  const int kb = jb / kXxsUnitBlockBytes, j = jb - kb * kXxsUnitBlockBytes;
+  int row, bi, o;
+  xxs_unit_source(j, iq3_unit_blocks(nb, kb), row, bi, o);
+  const int64_t g = u * unit_bytes + row * row_bytes + (int64_t)(4 * kb + bi) * 98 + o;
+  if (!unpack) dst[i] = src[g];
+  else dst[g] = src[i];
+}
+
+hipError_t launch_iq3_pack(int type, uint8_t* w, int64_t rows, int64_t row_bytes, bool unpack, uint8_t* scratch,
                            size_t scratch_bytes, hipStream_t stream) {
   const int64_t unit_bytes = (int64_t)kUnitRows * row_bytes;
   const int64_t units_per_chunk = (int64_t)(scratch_bytes / (size_t)unit_bytes);
   const int64_t nunits = rows / kUnitRows;
-  const int nb = (int)(row_bytes / 110);
+  const bool xxs = type == kIQ3_XXS;
+  const int nb = (int)(row_bytes / (xxs ? 98 : 110));
   for (int64_t u0 = 0; u0 < nunits; u0 += units_per_chunk) {
     const int64_t nu = nunits - u0 < units_per_chunk ? nunits - u0 : units_per_chunk;
     uint8_t* chunk = w + u0 * unit_bytes;
     hipError_t e = hipMemcpyAsync(scratch, chunk, (size_t)(nu * unit_bytes), hipMemcpyDeviceToDevice, stream);
     if (e != hipSuccess) return e;
-    const int64_t threads = nu * 40 * nb;
-    iq3_unit_convert_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, stream>>>(scratch, chunk, row_bytes, nu, nb,
-                                                                                   unpack);
+    if (xxs) {
+      const int64_t threads = nu * unit_bytes;
+      iq3xxs_unit_convert_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, stream>>>(scratch, chunk, row_bytes, nu,
+                                                                                        nb, unpack);
+    } else {
+      const int64_t threads = nu * 40 * nb;
+      iq3_unit_convert_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, stream>>>(scratch, chunk, row_bytes, nu,
+                                                                                     nb, unpack);
+    }
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }

@@ -83,7 +83,7 @@ def load():
     lib.gguf_lcpp_quantize_q8_1.argtypes = [P, I64, I32, I32, VP, SZ, VP]
     lib.gguf_iq3_pack_scratch_bytes.argtypes = [I64, I64]
     lib.gguf_iq3_pack_scratch_bytes.restype = SZ
-    lib.gguf_iq3_pack.argtypes = [VP, I64, I64, I32, VP, SZ, VP]
+    lib.gguf_iq3_pack.argtypes = [VP, I64, I64, I64, I32, VP, SZ, VP]
     lib.gguf_scratch_bytes.restype = SZ
     lib.gguf_mul_mat_noalloc.argtypes = [I32, P, P, I64, I64, P, VP, SZ, VP]
     lib.gguf_dense_mul_mat.argtypes = [P, P, VP, SZ, VP]

@@ -2,12 +2,12 @@
 
 Replaces the reference's quantization/iq3_pack.py (ROWS 36, pack_ 121-131, pack 134-138,
 unpack 141-181) with the same interface over layouts of this build's own:
-  * IQ3_S: 16-row tiles whose 1760-byte tile-blocks are ordered for the gfx950 decode GEMV's
-    coalesced 16-byte loads (csrc/iq3_tile.h documents the byte map). The permutation runs on the
-    GPU (gguf_iq3_pack in libgguf_mi355x.so); it is a bijection (unpack(pack(w)) == w) that keeps
-    every 16-row tile inside its own rows' bytes.
-  * IQ3_XXS: the GGUF block layout itself (the identity map): this build's packed ops read IQ3_XXS
-    rows as stored, with the generic kernels.
+  * IQ3_S: 4-row units whose 1760-byte unit-blocks (4 rows x 4 K blocks) are ordered for the
+    gfx950 decode GEMV's coalesced 16-byte loads (csrc/iq3_tile.h documents the byte map).
+  * IQ3_XXS: the same units, 1568-byte unit-blocks with the grid indices, the sign / scale words
+    and the d values of a unit-block's 16 blocks each in one field (csrc/iq3_tile.h).
+The permutations run on the GPU (gguf_iq3_pack in libgguf_mi355x.so); each is a bijection
+(unpack(pack(w)) == w) that keeps every 4-row unit inside its own rows' bytes.
 """
 
 import torch
@@ -30,14 +30,12 @@ def _run(w: torch.Tensor, weight_type: int, unpack: bool) -> None:
     assert rows == 1 or w.stride(0) == rb, "rows must be contiguous"
     if not w.is_cuda:
         raise RuntimeError("iq3_pack: W must be a CUDA tensor (the repack runs on the GPU)")
-    if weight_type == WeightType.IQ3_XXS:
-        return
     lib = _capi.load()
     sb = lib.gguf_iq3_pack_scratch_bytes(rows, rb)
     scratch = torch.empty(sb, dtype=torch.uint8, device=w.device)
     with torch.cuda.device(w.device):
-        _capi.check(lib, lib.gguf_iq3_pack(w.data_ptr(), rows, rb, int(unpack), scratch.data_ptr(), sb,
-                                           _capi.stream_of(w)))
+        _capi.check(lib, lib.gguf_iq3_pack(w.data_ptr(), int(weight_type), rows, rb, int(unpack), scratch.data_ptr(),
+                                           sb, _capi.stream_of(w)))
 
 
 def pack_(w: torch.Tensor, weight_type: int) -> None:

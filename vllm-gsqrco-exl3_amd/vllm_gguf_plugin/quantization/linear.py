@@ -37,6 +37,9 @@ from .params import (
 from .utils import DEQUANT_TYPES, UNQUANTIZED_TYPES, WeightType
 
 _IQ3_TYPES = (WeightType.IQ3_S, WeightType.IQ3_XXS)
+# The packed IQ3_XXS GEMV stages one activation row's q8_1 (36 bytes per 32 values) in at most
+# 96 KB of LDS: K <= 87040 (K % 512 == 0).
+_XXS_PACK_MAX_K = 87040
 # fewest activation rows at which lcpp_mul_mat_vec_own is routed (up to 8)
 _OWN_MIN_ROWS = {WeightType.Q4_K: 3, WeightType.IQ2_S: 1}
 # most activation rows at which IQ1_M is routed to MMVQ (in 8-row calls above 8)
@@ -324,7 +327,8 @@ class GGUFLinearMethod(LinearMethodBase):
         """Store the layer's IQ3_S / IQ3_XXS runs in iq3_pack's layout, in place, and set
         weight.iq3_packed (reference linear.py:437-457); apply() then routes them to the packed
         ops. All or nothing per layer: every IQ3 run must have a multiple of 16 rows and 16-byte
-        aligned bytes, and be on the GPU (the repack runs there)."""
+        aligned bytes, and be on the GPU (the repack runs there); an IQ3_XXS run's K must fit the
+        packed GEMV's X staging (_XXS_PACK_MAX_K)."""
         weight = layer.weight
         if getattr(weight, "iq3_packed", False):
             return
@@ -336,6 +340,8 @@ class GGUFLinearMethod(LinearMethodBase):
             runs = [(weight.data, layer.weight_type.weight_type)]
         runs = [(w, t) for w, t in runs if t in _IQ3_TYPES]
         if not runs or any(w.shape[0] % iq3_pack.ROWS or w.data_ptr() % 16 or not w.is_cuda for w, _ in runs):
+            return
+        if any(t == WeightType.IQ3_XXS and w.shape[1] // 98 * 256 > _XXS_PACK_MAX_K for w, t in runs):
             return
         for w, t in runs:
             iq3_pack.pack_(w, t)
