@@ -47,24 +47,28 @@ __device__ __forceinline__ float mmvq_term(const int (&w)[8], const int (&x)[8],
     for (int e = 0; e < 4; ++e) sa = dot4(w[e], x[e], sa);
 #pragma unroll
     for (int e = 4; e < 8; ++e) sb = dot4(w[e], x[e], sb);
-    if constexpr (TYPE == kQ6_K) return (float)(sa * sc.ls + sb * sc.ls2) * (sc.d * d8);
+    // every integer product here has operands within 24 bits (slice dots below 2^20 in magnitude,
+    // scales and half-slice sums of q8 below 2^12): __mul24 is exact and full rate (a 32-bit
+    // v_mul_lo_u32 is quarter rate)
+    if constexpr (TYPE == kQ6_K) return (float)(__mul24(sa, sc.ls) + __mul24(sb, sc.ls2)) * (sc.d * d8);
     if constexpr (TYPE == kQ2_K)
-      return d8 * (sc.d * (float)(sa * sc.ls + sb * sc.ls2) - sc.dmin * (float)(sq * sc.m + sq2 * sc.m2));
-    if constexpr (TYPE == kIQ1_M) return (float)(sa * sc.ls + sb * sc.ls2) * ((sc.d * d8) * 0.125f);
+      return d8 * (sc.d * (float)(__mul24(sa, sc.ls) + __mul24(sb, sc.ls2)) -
+                   sc.dmin * (float)(__mul24(sq, sc.m) + __mul24(sq2, sc.m2)));
+    if constexpr (TYPE == kIQ1_M) return (float)(__mul24(sa, sc.ls) + __mul24(sb, sc.ls2)) * ((sc.d * d8) * 0.125f);
     const int s0 = (sc.ls - 1) >> 1, s1 = (sc.ls2 - 1) >> 1;  // IQ2_XS, IQ2_S
-    return (float)((sa * s0 + sb * s1 + (sa + sb) / 2) / 4) * (sc.d * d8);
+    return (float)((__mul24(sa, s0) + __mul24(sb, s1) + (sa + sb) / 2) / 4) * (sc.d * d8);
   } else {
     int sumi = 0;
 #pragma unroll
     for (int e = 0; e < 8; ++e) sumi = dot4(w[e], x[e], sumi);
     if constexpr (TYPE == kQ4_K)
       return ((sc.d * (float)sc.ls) * (float)sumi - (sc.dmin * (float)sc.ls2) * (float)sq) * d8;
-    if constexpr (TYPE == kIQ2_XXS) return (float)(sumi * sc.ls / 8) * (sc.d * d8);
+    if constexpr (TYPE == kIQ2_XXS) return (float)(__mul24(sumi, sc.ls) / 8) * (sc.d * d8);
     if constexpr (TYPE == kIQ3_XXS) {
       const int s4 = (sc.ls - 1) >> 1;
-      return (float)((s4 * sumi + sumi / 2) / 2) * (sc.d * d8);
+      return (float)((__mul24(s4, sumi) + sumi / 2) / 2) * (sc.d * d8);
     }
-    return (float)(sumi * sc.ls) * (sc.d * d8);  // IQ3_S, IQ4_XS
+    return (float)__mul24(sumi, sc.ls) * (sc.d * d8);  // IQ3_S, IQ4_XS
   }
 }
 
