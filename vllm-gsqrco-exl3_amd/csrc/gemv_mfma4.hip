@@ -353,6 +353,11 @@ static int64_t m4_units_per_wg(int64_t nrows, int64_t grid) { return (nrows / kM
 bool gemv_mfma4_supported(int type, int64_t nrows, int64_t row_bytes, int64_t k, int64_t n) {
   if (!(type == kQ4_K || type == kIQ4_XS || type == kQ6_K)) return false;
   if (n == 1 && (k <= 8192 || type == kQ6_K)) return false;
+  // Q6_K at two rows: the row-chunk GEMV (X quantised inside at K <= 8192) is faster, measured
+  // in graph replays (op with X): 17408 x 5120 22.1-22.8 against 23.8 us, 5120 x 17408 24.1-24.3
+  // against 26.9; from three rows this kernel is (24.8 against 24.2-24.6 us and 28.0 against
+  // 36.9 at three, 24.7 / 29.0 against 27.1 / 40.7 at four)
+  if (type == kQ6_K && n == 2) return false;
   if (n < 1 || n > 4 || k % 512 != 0 || nrows % kM4UnitRows != 0) return false;
   if (row_bytes != k / kQK * block_bytes(type) || nrows * row_bytes >= ((int64_t)1 << 31)) return false;
   const int64_t cus = device_cus();
