@@ -356,7 +356,9 @@ bool gemv_mfma4_supported(int type, int64_t nrows, int64_t row_bytes, int64_t k,
   // Q6_K at two rows: the row-chunk GEMV (X quantised inside at K <= 8192) is faster, measured
   // in graph replays (op with X): 17408 x 5120 22.1-22.8 against 23.8 us, 5120 x 17408 24.1-24.3
   // against 26.9; from three rows this kernel is (24.8 against 24.2-24.6 us and 28.0 against
-  // 36.9 at three, 24.7 / 29.0 against 27.1 / 40.7 at four)
+  // 36.9 at three, 24.7 / 29.0 against 27.1 / 40.7 at four). Q4_K and IQ4_XS at two rows stay
+  // here: the row-chunk GEMV measured 19.1 / 20.1 against 14.5 / 16.8 us (Q4_K 17408 x 5120 /
+  // 5120 x 17408) and 17.9 / 19.6 against 16.3 / 17.2 (IQ4_XS).
   if (type == kQ6_K && n == 2) return false;
   if (n < 1 || n > 4 || k % 512 != 0 || nrows % kM4UnitRows != 0) return false;
   if (row_bytes != k / kQK * block_bytes(type) || nrows * row_bytes >= ((int64_t)1 << 31)) return false;
