@@ -472,7 +472,11 @@ constexpr int kStreamWaves = 8;
 // TYPE kIQ3_XXS: the same split, items and lanes over the IQ3_XXS unit layout (1568-B unit-blocks;
 // XxsFrag), its 16 KB signed table built from the 1 KB grid.
 // Y's activation rows are ys elements apart (the launch may cover a run of the weight's rows).
-template <int TYPE, int NC, int XDT, int XPT, int NW = kStreamWaves>
+// RG: K's last unit-block is ragged (nb % 4 == 2); without it no lane needs the remapped offsets
+// or the zeroed scales, and neither is computed (11 of 177 VALU instructions per item at 4 rows,
+// 9 of 90 at one; in one run of graph replays 17408 x 5120 M = 1 10.9-11.2 against 11.3-11.9 us
+// with the ragged code, 5120 x 17408 12.7 against 12.9-13.1).
+template <int TYPE, int NC, int XDT, int XPT, bool RG, int NW = kStreamWaves>
 __global__ void __launch_bounds__(64 * NW) gemv_iq3s_stream_kernel(const uint8_t* __restrict__ W,
                                                                               int64_t row_bytes, int nrows, int k,
                                                                               const void* __restrict__ xsrc,
@@ -524,7 +528,7 @@ __global__ void __launch_bounds__(64 * NW) gemv_iq3s_stream_kernel(const uint8_t
   // bi >= 2 load lane L - 32's bytes instead of bytes past the block's fields, so every load of
   // the run stays inside it; their terms are zeroed below (d = 0)
   const TileOffs off = unit_lane_offsets(lane, p, s), off_r = unit_lane_offsets(lane & 31, p & 3, s);
-  const bool ragged = (nb & 3) != 0;
+  constexpr bool ragged = RG;  // the launch passes RG == (nb % 4 != 0)
   // an empty range: loads past the wave's run read zeros without touching memory (the hardware
   // range check sees only the lane offset, not the scalar field base)
   const __amdgpu_buffer_rsrc_t nrs = buffer_rsrc(W, 0u);
@@ -587,7 +591,7 @@ __global__ void __launch_bounds__(64 * NW) gemv_iq3s_stream_kernel(const uint8_t
     load_next(fl);
     __builtin_amdgcn_sched_barrier(0);
     // lanes of blocks past a last unit-block of r < 4 blocks: d = 0 and X's d = 0
-    const bool live = bi < iq3_unit_blocks(nb, ckb);
+    const bool live = !RG || bi < iq3_unit_blocks(nb, ckb);
     const int sl = live ? 32 * ckb + xl : 0;
     XFrag<NC> x;
 #pragma unroll
@@ -700,12 +704,18 @@ static void launch_stream_k(const uint8_t* W, int64_t row_bytes, int nrows, int 
   if (hipGetDevice(&dev) == hipSuccess) {
     struct Tag;  // one set of per-device flags per kernel instantiation
     once_per_device<Tag>(dev, [] {
-      (void)hipFuncSetAttribute((const void*)gemv_iq3s_stream_kernel<TYPE, NC, XDT, XPT>,
+      (void)hipFuncSetAttribute((const void*)gemv_iq3s_stream_kernel<TYPE, NC, XDT, XPT, false>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)stream_lds_max<TYPE>());
+      (void)hipFuncSetAttribute((const void*)gemv_iq3s_stream_kernel<TYPE, NC, XDT, XPT, true>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)stream_lds_max<TYPE>());
     });
   }
-  gemv_iq3s_stream_kernel<TYPE, NC, XDT, XPT><<<g, 64 * kStreamWaves, lds, stream>>>(W, row_bytes, nrows, k, x, s01,
-                                                                                    y, ys, y_dtype);
+  if ((k / kQK) % 4 != 0)
+    gemv_iq3s_stream_kernel<TYPE, NC, XDT, XPT, true><<<g, 64 * kStreamWaves, lds, stream>>>(W, row_bytes, nrows, k, x,
+                                                                                            s01, y, ys, y_dtype);
+  else
+    gemv_iq3s_stream_kernel<TYPE, NC, XDT, XPT, false><<<g, 64 * kStreamWaves, lds, stream>>>(W, row_bytes, nrows, k, x,
+                                                                                             s01, y, ys, y_dtype);
 }
 
 template <int TYPE, int NC, int XDT>
