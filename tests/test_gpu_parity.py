@@ -613,6 +613,36 @@ def test_prefill_q6k_largest_subscales():
 
 
 @pytest.mark.parametrize("n", PREFILL_N)
+@pytest.mark.parametrize("k", [512, 1536])
+def test_prefill_packed_xxs_exact(n, k):
+    """IQ3_XXS in its unit layout on the fp16 prefill GEMM (operand w * ls, row scale d / 4), in
+    the exact mode: the product ops' slice values dot / 4 summed, multiples of 1/4 exact in fp32;
+    144 rows (a partial last 128-row group) and K = 1536 (a ragged last unit-block)."""
+    from vllm_gguf_plugin.quantization import iq3_pack
+
+    rows = 144
+    raw = _exact_weights(o.IQ3_XXS, rows, k, seed=160 + n + k)
+    x = _exact_x(n, k, seed=170 + n, dtype=torch.float32)
+    want = _exact_ref(raw, o.IQ3_XXS, x, form="mmq")
+    w = iq3_pack.pack(_dev(raw), o.IQ3_XXS)
+    y = C().lcpp_mul_mat_iq3_packed(w, x.cuda(), o.IQ3_XXS, rows).cpu().numpy()
+    np.testing.assert_array_equal(y.astype(np.float64), want)
+
+
+@pytest.mark.parametrize("rows,k,n", [(272, 5120, 256), (272, 5120, 600), (2048, 5120, 2048)])
+def test_prefill_packed_xxs_vs_q81(rows, k, n):
+    """IQ3_XXS prefill (the 4-wave and the 8-wave plans) against the q81 model of the product ops."""
+    from vllm_gguf_plugin.quantization import iq3_pack
+
+    raw = _w(o.IQ3_XXS, rows, k, seed=rows + n + 9)
+    x = _x(n, k, seed=n + 710)
+    x[-1, 256:288] = 0  # an all-zero slice
+    y = C().lcpp_mul_mat_iq3_packed(iq3_pack.pack(_dev(raw), o.IQ3_XXS), x.cuda(), o.IQ3_XXS, rows).cpu().numpy()
+    ref = o.q81_model(raw, o.IQ3_XXS, x, layout="mmq")
+    assert o.rel_l2(y, ref) <= 1e-3, o.rel_l2(y, ref)
+
+
+@pytest.mark.parametrize("n", PREFILL_N)
 @pytest.mark.parametrize("k", [512, 5120])
 def test_prefill_packed_vs_q81(n, k):
     from vllm_gguf_plugin.quantization import iq3_pack

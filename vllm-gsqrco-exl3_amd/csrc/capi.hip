@@ -357,6 +357,7 @@ size_t split_ws(int op, int64_t type, int64_t row, int64_t k, int64_t n) {
 size_t gguf_op_workspace_bytes(int op, int64_t type, int64_t row, int64_t k, int64_t n, int has_x_q8) {
   if (n <= 0) return 0;
   if (generic(type)) {
+    if (op_gemm(op) && xxs_packed(op, type) && n >= kPrefillFrom) return align256(gguf::xh_bytes(n, k));
     if (op_gemm(op)) return align256(generic_xq(type) ? gguf::xq_bytes(n, k) : gguf_q8_1_bytes(n, k, 1));
     return has_x_q8 || generic_fused(op, type, row, k, n) ? 0 : align256(gguf_q8_1_bytes(n, k, 0));
   }
@@ -403,6 +404,14 @@ int run_checked(int op, const gguf_view* W, const gguf_view* X, int64_t type, in
 
   if (generic(type)) {
     const bool xxs = xxs_packed(op, type);
+    if (gemm && xxs && n >= kPrefillFrom) {  // IQ3_XXS unit layout: the fp16 prefill GEMM (xh layout)
+      e = gguf::launch_quantize_xh(X->data, X->dtype, n, k, s01, (int)type, workspace, s);
+      if (e != hipSuccess) return hip_fail(e, name, "quantize");
+      e = gguf::launch_gemm_prefill((int)type, true, w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace, (int)n,
+                                    y, ydt, s);
+      if (e != hipSuccess) return hip_fail(e, name, "gemm");
+      return GGUF_OK;
+    }
     if (gemm && generic_xq(type)) {  // the product ops' MMQ arithmetic in the xq layout
       e = gguf::launch_quantize_xq(X->data, X->dtype, n, k, s01, (int)type, false, workspace, s);
       if (e != hipSuccess) return hip_fail(e, name, "quantize");

@@ -330,10 +330,13 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW) gemm_prefill_h_kernel(const u
                                                                          int64_t row_bytes, int nrows, int k,
                                                                          const uint8_t* __restrict__ xh, int nct,
                                                                          int n, void* __restrict__ y, int y_dtype) {
-  constexpr bool IQ3 = TYPE == kIQ3_S;
+  constexpr bool XXS = TYPE == kIQ3_XXS;
+  constexpr bool IQ3 = TYPE == kIQ3_S || XXS;  // the unit layouts: a 16-row tile is 4 units
   constexpr bool MIN = TYPE == kQ4_K;  // the min term
   constexpr int TPW = 8 / NW;  // row tiles a wave decodes per step
-  using Raw = typename std::conditional<IQ3, RawIq3, typename std::conditional<MIN, RawQ4k, RawQ6k>::type>::type;
+  using Raw = typename std::conditional<
+      XXS, RawXxsH,
+      typename std::conditional<IQ3, RawIq3, typename std::conditional<MIN, RawQ4k, RawQ6k>::type>::type>::type;
   __shared__ __attribute__((aligned(16))) uint8_t A[2 * kHA];
   __shared__ __attribute__((aligned(16))) float RT[128];
   __shared__ __attribute__((aligned(16))) float EF[128];
@@ -347,7 +350,7 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW) gemm_prefill_h_kernel(const u
   const int tile0 = blockIdx.x * kPfRowTiles;
   const int nb = k / kQK;
   if constexpr (IQ3) {
-    iq3_half_tables_to_lds(GH, SM, threadIdx.x, 64 * NW);
+    iq3_half_tables_to_lds(GH, SM, threadIdx.x, 64 * NW, XXS);
   }
 
   // this wave's column tiles (past nct: the last one again, never stored)
@@ -557,11 +560,12 @@ void launch_prefill_t(const uint8_t* W, int64_t row_bytes, int nrows, int k, con
 bool prefill_uses_xh(int type, bool packed) { return packed || type == kQ4_K || type == kQ6_K; }
 
 // Large-M products; xq: X in the xq layout, or the xh layout where prefill_uses_xh. packed: IQ3_S
-// in the tile layout (nrows % 16 == 0).
+// or IQ3_XXS in its unit layout (nrows % 16 == 0).
 hipError_t launch_gemm_prefill(int type, bool packed, const uint8_t* W, int64_t row_bytes, int nrows, int k,
                                const uint8_t* xq, int n, void* y, int y_dtype, hipStream_t stream) {
   if (packed) {
-    launch_prefill_h<kIQ3_S>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
+    if (type == kIQ3_XXS) launch_prefill_h<kIQ3_XXS>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
+    else launch_prefill_h<kIQ3_S>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream);
   } else {
     switch (type) {
       case kQ4_K: launch_prefill_h<kQ4_K>(W, row_bytes, nrows, k, xq, n, y, y_dtype, stream); break;

@@ -1,5 +1,6 @@
 // fp16 decode of weight blocks for the fp16-operand MFMA GEMMs (the prefill GEMM's fp16 variant
-// and the small GEMM): IQ3_S in the tile layout (iq3_tile.h), Q4_K and Q6_K rows, decoded to fp16
+// and the small GEMM): IQ3_S and IQ3_XXS in their unit layouts (iq3_tile.h), Q4_K and Q6_K rows,
+// decoded to fp16
 // values with the slice (Q6_K: 16-value) sub-scale applied (exact integers: at most 465 for
 // IQ3_S, 945 for Q4_K; Q6_K's up to 4064 round above 2048), in the A-operand order of
 // v_mfma_f32_16x16x32_f16.
@@ -51,6 +52,18 @@ constexpr Iq3sGridHalf make_iq3s_grid_half() {
 }
 __device__ const Iq3sGridHalf kIq3sGridHalf = make_iq3s_grid_half();
 
+// The IQ3_XXS grid as fp16 (entries 0..255 in the first 512 dwords)
+constexpr Iq3sGridHalf make_iq3xxs_grid_half() {
+  Iq3sGridHalf g{};
+  for (int i = 0; i < 256; ++i) {
+    const uint32_t w = kIq3xxsGrid.v[i];
+    g.v[2 * i] = small_int_half(w & 0xFF) | (small_int_half((w >> 8) & 0xFF) << 16);
+    g.v[2 * i + 1] = small_int_half((w >> 16) & 0xFF) | (small_int_half(w >> 24) << 16);
+  }
+  return g;
+}
+__device__ const Iq3sGridHalf kIq3xxsGridHalf = make_iq3xxs_grid_half();
+
 // A slot of (row tile t, slice u of the half block, row j, quarter q): the quarter's 16 bytes sit
 // in slot q ^ g(j) of the row, g(j) = ((j >> 1) ^ (j >> 3)) & 3, which keeps the operand reads
 // (lane (j, q)) free of bank conflicts.
@@ -71,6 +84,11 @@ struct RawIq3 {
   uint8_t sc;   // SC byte (two 4-bit sub-scales)
   uint16_t d;   // fp16 d of the row
 };
+struct RawXxsH {
+  uint2 qs;      // the 8 grid indices of the lane's row and slice
+  uint32_t aux;  // the slice's four 7-bit sign indices and 4-bit scale
+  uint16_t d;    // fp16 d of the row
+};
 struct RawQ4k {
   u32x4 hdr;    // d, dmin, scales[12]
   uint2 v0, v1; // quarter q of the two 32-byte quant groups of the half block
@@ -88,6 +106,18 @@ __device__ __forceinline__ void load_step(RawIq3& w, const uint8_t* tile, int64_
   w.l2 = *(const uint16_t*)(u + f.l2 + l.l2);
   w.sc = u[f.sc + l.sc + 2 * (s >> 1) + r];
   w.d = *(const uint16_t*)(u + f.d + l.d + 2 * r);
+}
+
+// IQ3_XXS lane (row j, slice 4h + sp) of K block b of a 16-row tile in the IQ3_XXS unit layout:
+// the block's 16 lanes 8 rp + s hold rows 2rp, 2rp+1 of the unit
+__device__ __forceinline__ void load_step(RawXxsH& w, const uint8_t* tile, int64_t row_bytes, int nb, int b, int h,
+                                          int j, int sp) {
+  const int r = j & 1, rp = (j >> 1) & 1, s = 4 * h + sp, L = 8 * rp + s;
+  const XxsFields f = xxs_block_fields(nb, b);
+  const uint8_t* u = tile + (int64_t)(j >> 2) * kUnitRows * row_bytes;
+  w.qs = *(const uint2*)(u + f.qs + 16 * L + 8 * r);
+  w.aux = *(const uint32_t*)(u + f.aux + 8 * L + 4 * r);
+  w.d = *(const uint16_t*)(u + f.d + 4 * rp + 2 * r);
 }
 
 // Q4_K lane (row j, quarter q) of the row's block
@@ -126,6 +156,37 @@ __device__ __forceinline__ void decode_step(const RawIq3& w, int h, const uint32
     const uint2 sg = sm[ex & 0xF];
     v[2 * g] = h2_bits(bits_h2(gv.x ^ sg.x) * lsh);
     v[2 * g + 1] = h2_bits(bits_h2(gv.y ^ sg.y) * lsh);
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    *(uint4*)(A + h_off(t, sp, j, q)) = make_uint4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+}
+
+// IQ3_XXS: value = d * ls * w / 4 (ls = 2 * scale + 1, w the signed grid byte): the operand is
+// w * ls (at most 62 * 31 = 1922, exact in fp16) and the row's scale d / 4. The second word of
+// each 8-value group takes bits 4..6 of the group's 7-bit sign index and their parity with bits
+// 0..3 (ksigns_iq2xs), all four parities from two three-way xors (bit 7g of t ^ t >> 3 ^ a >> 6,
+// t = a ^ a >> 1 ^ a >> 2, is the xor of bits 7g..7g+6).
+__device__ __forceinline__ void decode_step(const RawXxsH& w, int h, const uint32_t* gh, const uint2* sm, uint8_t* A,
+                                            float* RT, float* EF, float& e, int t, int j, int sp) {
+  const float d = half_bits_to_float(w.d) * 0.25f;
+  if (h == 0) next_scale(d, e, RT, EF, t * 16 + j);
+  const uint32_t a = w.aux;
+  const uint32_t t3 = a ^ (a >> 1) ^ (a >> 2);
+  const uint32_t par = t3 ^ (t3 >> 3) ^ (a >> 6);
+  const uint32_t hi = ((par << 3) & 0x01020408u) | ((a >> 4) & ~0x01020408u);
+  const _Float16 ls = d != 0.0f ? (_Float16)(float)(2 * (a >> 28) + 1) : (_Float16)0.0f;
+  const h2 lsh = {ls, ls};
+  uint32_t v[16];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const uint32_t qw = (g < 2 ? w.qs.x : w.qs.y) >> (16 * (g & 1));
+    const uint2 g0 = *(const uint2*)(gh + 2 * (qw & 0xFF)), g1 = *(const uint2*)(gh + 2 * ((qw >> 8) & 0xFF));
+    const uint2 s0 = sm[(a >> (7 * g)) & 0xF], s1 = sm[(hi >> (7 * g)) & 0xF];
+    v[4 * g] = h2_bits(bits_h2(g0.x ^ s0.x) * lsh);
+    v[4 * g + 1] = h2_bits(bits_h2(g0.y ^ s0.y) * lsh);
+    v[4 * g + 2] = h2_bits(bits_h2(g1.x ^ s1.x) * lsh);
+    v[4 * g + 3] = h2_bits(bits_h2(g1.y ^ s1.y) * lsh);
   }
 #pragma unroll
   for (int q = 0; q < 4; ++q)
@@ -216,8 +277,12 @@ __device__ __forceinline__ void decode_step(const RawQ6k& w, int h, uint8_t* A, 
 
 // The IQ3_S decode tables in LDS: the fp16 grid (GH, 1024 dwords) and the 16 sign masks (SM),
 // written by threads tid = 0 .. nt - 1 of the workgroup; the caller synchronises.
-__device__ __forceinline__ void iq3_half_tables_to_lds(uint32_t* GH, uint2* SM, int tid, int nt) {
-  for (int i = tid; i < 1024; i += nt) GH[i] = kIq3sGridHalf.v[i];
+__device__ __forceinline__ void iq3_half_tables_to_lds(uint32_t* GH, uint2* SM, int tid, int nt, bool xxs = false) {
+  if (xxs) {
+    for (int i = tid; i < 512; i += nt) GH[i] = kIq3xxsGridHalf.v[i];
+  } else {
+    for (int i = tid; i < 1024; i += nt) GH[i] = kIq3sGridHalf.v[i];
+  }
   if (tid < 16) {
     const uint32_t nib = tid;
     SM[nib] = make_uint2(((nib & 1u) << 15) | ((nib & 2u) << 30), ((nib & 4u) << 13) | ((nib & 8u) << 28));
