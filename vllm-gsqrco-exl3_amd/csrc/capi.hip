@@ -261,6 +261,31 @@ bool rows_fused(int op, int64_t type, int64_t row, int64_t k, int64_t n, bool ha
 // GEMMs' one-column-tile-group plans re-decode the weights once per 16..64 activation rows).
 constexpr int64_t kPrefillFrom = 256;
 
+bool xxs_packed(int op, int64_t type);
+
+// Whether a product op runs the prefill GEMM (128 weight rows x 256 activation rows per
+// workgroup; 128 on grids of fewer than 256). Its grid must hold enough workgroups: per
+// workgroup it walks all of K, so on a small grid most CUs idle while the small GEMMs (16-row
+// tiles) spread the same work. Measured (µs per op, graph replays, prefill / small GEMM):
+//   1024 x 5120, M = 256 / 512 (8 / 16 groups): IQ3_S 106 / 109 against 26 / 38, Q6_K 113 / 114
+//   against 28 / 49; M = 2048 (64 groups): IQ3_S 124 against 134, Q6_K 127 against 166;
+//   6144 x 5120, M = 256 (48): IQ3_S 108 against 95, Q4_K 117 against 96; M = 512 (96): 114
+//   against 168, 123 against 184; 5120 x 17408, M = 256 (40): IQ3_S 314 against 224; M = 512
+//   (80): 323 against 430; 17408 x 5120, M = 256 (136): 152 against 158.
+// So from 64 groups on (128 for IQ4_XS, whose prefill GEMM is the int8 one: 5120 x 6144 M = 512,
+// 80 groups, 219 against 182; 17408 x 5120 M = 256, 136 groups, 242 against 263). Packed IQ3_XXS,
+// whose small GEMM (the generic one) is slower, from 32 groups at 256 rows and on grids of 128
+// groups from 64 rows (17408 x 5120 M = 64 / 128 / 255: 92 / 93 / 135 against 97 / 166 / 309;
+// 6144 x 5120 M = 256, 48 groups: 96 against 114; 5120 x 17408 M = 128, 40 groups: 275 against
+// 148).
+bool prefill_route(int op, int64_t type, int64_t row, int64_t k, int64_t n) {
+  if (!op_gemm(op) || n < 64) return false;
+  const int64_t groups = (row + 127) / 128 * ((n + 255) / 256);
+  if (xxs_packed(op, type)) return (n >= kPrefillFrom && groups >= 32) || groups >= 128;
+  if (n < kPrefillFrom) return false;
+  return groups >= (type == gguf::kIQ4_XS ? 128 : 64);
+}
+
 int64_t vec_mma_from(int op, int64_t type) {
   if (op_packed(op)) return 5;
   if (type == gguf::kQ4_K || type == gguf::kQ6_K) return 3;
@@ -292,6 +317,7 @@ bool decode_mma(int op, int64_t type, int64_t row, int64_t k, int64_t n) {
 // A packed op on IQ3_XXS: the weight is in the build's IQ3_XXS unit layout (gguf_iq3_pack).
 bool xxs_packed(int op, int64_t type) { return op_packed(op) && type == kIQ3_XXS; }
 
+
 // A generic type's decode op with X quantised inside the stream GEMV (1-2 rows, K <= 8192).
 bool generic_fused(int op, int64_t type, int64_t row, int64_t k, int64_t n) {
   if (xxs_packed(op, type)) return gguf::gemv_iq3xxs_stream_supported(row, k / 256 * 98, k, n, true);
@@ -315,21 +341,21 @@ bool rows_fused(int op, int64_t type, int64_t row, int64_t k, int64_t n, bool ha
 // workgroups) the int8 GEMM's K split across waves is faster.
 bool small_fp16(int op, int64_t type, int64_t row, int64_t k, int64_t n) {
   if (!op_gemm(op) || k > 8192 || !gguf::small_h_supported((int)type, op_packed(op))) return false;
-  return (n >= 64 && n < kPrefillFrom) || gguf::small_h_range((int)type, row, n);
+  return (n >= 64 && !prefill_route(op, type, row, k, n)) || gguf::small_h_range((int)type, row, n);
 }
 
 // The int8 small GEMM on Q4_K / IQ4_XS / Q6_K rows (gemm_raw_kernel): product ops below the
 // prefill rows off the fp16 GEMM's plans, and decode ops from vec_mma_from rows on.
 bool raw_gemm(int op, int64_t type, int64_t row, int64_t k, int64_t n) {
   if (op_packed(op) || !(type == gguf::kQ4_K || type == gguf::kIQ4_XS || type == gguf::kQ6_K)) return false;
-  if (op_gemm(op)) return n < kPrefillFrom && !small_fp16(op, type, row, k, n);
+  if (op_gemm(op)) return !prefill_route(op, type, row, k, n) && !small_fp16(op, type, row, k, n);
   return decode_mma(op, type, row, k, n);
 }
 
 // The int8 tile GEMM on packed IQ3_S (gemm_iq3s_tile_kernel), on the same terms.
 bool tile_gemm(int op, int64_t type, int64_t row, int64_t k, int64_t n) {
   if (!op_packed(op) || type != gguf::kIQ3_S) return false;
-  if (op_gemm(op)) return n < kPrefillFrom && !small_fp16(op, type, row, k, n);
+  if (op_gemm(op)) return !prefill_route(op, type, row, k, n) && !small_fp16(op, type, row, k, n);
   return decode_mma(op, type, row, k, n);
 }
 
@@ -357,13 +383,13 @@ size_t split_ws(int op, int64_t type, int64_t row, int64_t k, int64_t n) {
 size_t gguf_op_workspace_bytes(int op, int64_t type, int64_t row, int64_t k, int64_t n, int has_x_q8) {
   if (n <= 0) return 0;
   if (generic(type)) {
-    if (op_gemm(op) && xxs_packed(op, type) && n >= kPrefillFrom) return align256(gguf::xh_bytes(n, k));
+    if (xxs_packed(op, type) && prefill_route(op, type, row, k, n)) return align256(gguf::xh_bytes(n, k));
     if (op_gemm(op)) return align256(generic_xq(type) ? gguf::xq_bytes(n, k) : gguf_q8_1_bytes(n, k, 1));
     return has_x_q8 || generic_fused(op, type, row, k, n) ? 0 : align256(gguf_q8_1_bytes(n, k, 0));
   }
   if (op_gemm(op)) {
     const bool mmq_layout = !op_packed(op) && type == gguf::kIQ3_S;
-    if (!mmq_layout && ((n >= kPrefillFrom && gguf::prefill_uses_xh((int)type, op_packed(op))) ||
+    if (!mmq_layout && ((prefill_route(op, type, row, k, n) && gguf::prefill_uses_xh((int)type, op_packed(op))) ||
                         small_fp16(op, type, row, k, n)))
       return align256(gguf::xh_bytes(n, k));
     return align256(mmq_layout ? gguf_q8_1_bytes(n, k, 1) : gguf::xq_bytes(n, k)) + split_ws(op, type, row, k, n);
@@ -404,7 +430,7 @@ int run_checked(int op, const gguf_view* W, const gguf_view* X, int64_t type, in
 
   if (generic(type)) {
     const bool xxs = xxs_packed(op, type);
-    if (gemm && xxs && n >= kPrefillFrom) {  // IQ3_XXS unit layout: the fp16 prefill GEMM (xh layout)
+    if (xxs && prefill_route(op, type, row, k, n)) {  // IQ3_XXS unit layout: the fp16 prefill GEMM (xh layout)
       e = gguf::launch_quantize_xh(X->data, X->dtype, n, k, s01, (int)type, workspace, s);
       if (e != hipSuccess) return hip_fail(e, name, "quantize");
       e = gguf::launch_gemm_prefill((int)type, true, w, row_bytes, (int)row, (int)k, (const uint8_t*)workspace, (int)n,
@@ -471,7 +497,7 @@ int run_checked(int op, const gguf_view* W, const gguf_view* X, int64_t type, in
   // (from vec_mma_from rows on, see decode_mma) with the decode ops' q8_1 arithmetic or the
   // caller's x_q8
   if ((gemm && (packed || type != gguf::kIQ3_S)) || (!gemm && decode_mma(op, type, row, k, n))) {
-    const bool prefill = gemm && n >= kPrefillFrom;
+    const bool prefill = prefill_route(op, type, row, k, n);
     const bool fp16 = small_fp16(op, type, row, k, n);
     const bool xh = fp16 || (prefill && gguf::prefill_uses_xh((int)type, packed));
     // a K-split GEMM's slots and counters follow the xq copy; the quantise launch clears the
