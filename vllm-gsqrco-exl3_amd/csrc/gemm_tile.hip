@@ -333,7 +333,13 @@ hipError_t launch_gemm_packed_xq(const uint8_t* W, int64_t row_bytes, int nrows,
   } else if (nct == 2) {
     launch_tile_gemm<2, 1, 4>(W, row_bytes, nrows, k, xq, n, y, y_dtype, split, part, cnt, stream);
   } else if (nct == 3) {
-    launch_tile_gemm<3, 1, 4>(W, row_bytes, nrows, k, xq, n, y, y_dtype, split, part, cnt, stream);
+    // unsplit on fewer than two tiles per CU: one column tile per workgroup, three times the
+    // workgroups (each decodes the tile again). Measured on the op (graph replays, M = 48): IQ3_S
+    // 5120 x 6144 26.9 -> 23.1 us, 6144 x 5120 24.0 -> 23.5; two column tiles per workgroup
+    // (2 + 1) 27.4 and 24.7
+    if (split == 1 && nrows / kTileRows < 2 * device_cus())
+      launch_tile_gemm<1, 1, 4>(W, row_bytes, nrows, k, xq, n, y, y_dtype, split, part, cnt, stream);
+    else launch_tile_gemm<3, 1, 4>(W, row_bytes, nrows, k, xq, n, y, y_dtype, split, part, cnt, stream);
   } else {
     launch_tile_gemm<4, 1, 4>(W, row_bytes, nrows, k, xq, n, y, y_dtype, split, part, cnt, stream);
   }
