@@ -327,19 +327,18 @@ hipError_t launch_gemm_packed_xq(const uint8_t* W, int64_t row_bytes, int nrows,
   if (split > 1 && split_ws == nullptr) return hipErrorInvalidValue;
   float* part = (float*)split_ws;
   uint32_t* cnt = (uint32_t*)((uint8_t*)split_ws + split_part_bytes(split, nrows / kTileRows, n));
-  if (nct == 1) {
-    if (few) launch_tile_gemm<1, 1, 8>(W, row_bytes, nrows, k, xq, n, y, y_dtype, split, part, cnt, stream);
+  // 2-3 column tiles unsplit on fewer than two tiles per CU: one column tile per workgroup, two or
+  // three times the workgroups (each decodes its tile again). Measured on the op (graph
+  // replays): IQ3_S M = 48 5120 x 6144 26.9 -> 23.1 us, 6144 x 5120 24.0 -> 23.5 (groups of two
+  // column tiles: 27.4, 24.7); M = 32 5120 x 6144 21.1 -> 19.9, 6144 x 5120 19.0 -> 18.4
+  const bool one_ct = nct <= 3 && split == 1 && nrows / kTileRows < 2 * device_cus();
+  if (nct == 1 || one_ct) {
+    if (few && nct == 1) launch_tile_gemm<1, 1, 8>(W, row_bytes, nrows, k, xq, n, y, y_dtype, split, part, cnt, stream);
     else launch_tile_gemm<1, 1, 4>(W, row_bytes, nrows, k, xq, n, y, y_dtype, split, part, cnt, stream);
   } else if (nct == 2) {
     launch_tile_gemm<2, 1, 4>(W, row_bytes, nrows, k, xq, n, y, y_dtype, split, part, cnt, stream);
   } else if (nct == 3) {
-    // unsplit on fewer than two tiles per CU: one column tile per workgroup, three times the
-    // workgroups (each decodes the tile again). Measured on the op (graph replays, M = 48): IQ3_S
-    // 5120 x 6144 26.9 -> 23.1 us, 6144 x 5120 24.0 -> 23.5; two column tiles per workgroup
-    // (2 + 1) 27.4 and 24.7
-    if (split == 1 && nrows / kTileRows < 2 * device_cus())
-      launch_tile_gemm<1, 1, 4>(W, row_bytes, nrows, k, xq, n, y, y_dtype, split, part, cnt, stream);
-    else launch_tile_gemm<3, 1, 4>(W, row_bytes, nrows, k, xq, n, y, y_dtype, split, part, cnt, stream);
+    launch_tile_gemm<3, 1, 4>(W, row_bytes, nrows, k, xq, n, y, y_dtype, split, part, cnt, stream);
   } else {
     launch_tile_gemm<4, 1, 4>(W, row_bytes, nrows, k, xq, n, y, y_dtype, split, part, cnt, stream);
   }
