@@ -467,8 +467,8 @@ def load_traffic():
 def dominant_kernel(torch, C, ws, steps):
     """The headline's dominant kernel alone: the packed decode op at 17408 x 5120, M = 1, bf16 X,
     which is one launch of the stream GEMV that quantises X itself
-    (gemv_iq3s_stream_kernel<1, bf16, 2>); one graph of one launch per weight copy, timed with
-    HIP events on the stream the op launches on."""
+    (gemv_iq3s_stream_kernel<IQ3_S, 1, bf16, 2, false, 8>); one graph of one launch per weight copy,
+    timed with HIP events on the stream the op launches on."""
     rows, k, m = 17408, 5120, 1
     x = torch.randn(m, k, device="cuda", dtype=torch.bfloat16)
     kg = graph(torch, [lambda w=w: C.lcpp_mul_mat_vec_iq3_mma_packed(w, x, IQ3_S, rows) for w in ws])
@@ -481,7 +481,7 @@ def dominant_kernel(torch, C, ws, steps):
     floor_us = time_graphs(torch, [fg], max(5, steps)) * 1e3 / len(ws)
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic(),
-            "kernel": "gemv_iq3s_stream_kernel<1,bf16,2> (17408x5120, M=1, X quantised in the kernel)",
+            "kernel": "gemv_iq3s_stream_kernel<IQ3_S,1,bf16,2,false,8> (17408x5120, M=1, X quantised in the kernel)",
             "us_per_launch": round(kernel_us, 3), "alg_bytes_per_launch": alg_bytes,
             "launch_floor_us": round(floor_us, 3)}
 

@@ -430,8 +430,13 @@ __device__ __forceinline__ void raw_block(const RawFrag<TYPE>& f, const XRawFrag
   }
 }
 
+// Up to two column tiles the kernel is held to two workgroups per CU (256 registers per lane):
+// Q4_K at two column tiles otherwise takes 257 and runs alone on its CU (measured, op level:
+// 5120 x 17408 M = 24 / 32 52.4 / 51.8 -> 38.8 / 38.9 us, 6144 x 5120 22.2 / 22.0 -> 19.6 /
+// 19.5). At three column tiles Q6_K's 263 registers squeezed to 256 spill 15 dwords and lose on
+// K = 5120 / 6144 (33.6 -> 35.1 us, 37.1 -> 40.6 at M = 48), so three stay unconstrained.
 template <int TYPE, int NT, int KS, bool SX>
-__global__ void __launch_bounds__(64 * KS) gemm_raw_kernel(const uint8_t* __restrict__ W, int64_t row_bytes, int nrows,
+__global__ void __launch_bounds__(64 * KS, NT <= 2 ? 2 : 1) gemm_raw_kernel(const uint8_t* __restrict__ W, int64_t row_bytes, int nrows,
                                                            int k, const uint8_t* __restrict__ xq, int nct, int n,
                                                            void* __restrict__ y, int y_dtype, float* part,
                                                            uint32_t* cnt) {
@@ -558,8 +563,12 @@ __device__ __forceinline__ void gen_row_scales(const uint8_t* rowp, int u, int& 
 // rows 4u + 2rp, 4u + 2rp + 1 as the GGUF block, at byte 2 of each (the fields are then at the
 // same places as in the GGUF path: d at 2, the slice's indices at 4 + 8s, its sign / scale word at
 // 68 + 4s).
+// Up to three column tiles the kernel is held to two workgroups per CU (256 registers per lane):
+// IQ2_S at three column tiles otherwise takes 271 and runs alone on its CU; squeezed it spills 3
+// dwords and its 48-row op at 17408 x 5120 goes from 81.8 to 56.3 us (IQ2_XS 58.6 -> 55.0,
+// IQ3_XXS at 16 rows 30.8 -> 28.8).
 template <int TYPE, int NT, int KS, bool PK = false>
-__global__ void __launch_bounds__(64 * KS) gemm_generic_kernel(const uint8_t* __restrict__ W, int64_t row_bytes,
+__global__ void __launch_bounds__(64 * KS, NT <= 3 ? 2 : 1) gemm_generic_kernel(const uint8_t* __restrict__ W, int64_t row_bytes,
                                                                int nrows, int k, const uint8_t* __restrict__ xq,
                                                                int nct, int n, void* __restrict__ y, int y_dtype) {
   constexpr int BS = block_bytes(TYPE);

@@ -172,8 +172,11 @@ __device__ __forceinline__ void mma_block(const uint8_t* tbl, uint8_t* tr, const
   }
 }
 
+// Two column tiles on four waves: held to three workgroups per CU (168 registers per lane, 3
+// dwords spilled; the LDS admits three): 17408 x 5120 M = 20 / 32 39.1 / 38.6 -> 35.9 / 35.5 us,
+// 5120 x 17408 39.3 / 38.4 -> 36.4 / 36.2 (172 registers and two workgroups per CU before).
 template <int NT, int RW, int KS>
-__global__ void __launch_bounds__(64 * KS) gemm_iq3s_tile_kernel(const uint8_t* __restrict__ W, int64_t row_bytes,
+__global__ void __launch_bounds__(64 * KS, KS == 4 && NT == 2 ? 3 : 1) gemm_iq3s_tile_kernel(const uint8_t* __restrict__ W, int64_t row_bytes,
                                                                  int nrows, int k, const uint8_t* __restrict__ xq,
                                                                  int nct, int n, void* __restrict__ y, int y_dtype,
                                                                  float* part, uint32_t* cnt) {
