@@ -566,9 +566,11 @@ __device__ __forceinline__ void gen_row_scales(const uint8_t* rowp, int u, int& 
 // Up to three column tiles the kernel is held to two workgroups per CU (256 registers per lane):
 // IQ2_S at three column tiles otherwise takes 271 and runs alone on its CU; squeezed it spills 3
 // dwords and its 48-row op at 17408 x 5120 goes from 81.8 to 56.3 us (IQ2_XS 58.6 -> 55.0,
-// IQ3_XXS at 16 rows 30.8 -> 28.8).
+// IQ3_XXS at 16 rows 30.8 -> 28.8). IQ3_XXS at two column tiles is held to three per CU (172 ->
+// 168 registers, 4 dwords spilled): 17408 x 5120 M = 24 / 32 43.8 / 43.5 -> 40.2 / 39.6 us, at a
+// cost of 0.4-0.6 us on 5120 x 17408 and 6144 x 5120 (45.5 -> 45.9, 19.5 -> 20.0 at M = 32).
 template <int TYPE, int NT, int KS, bool PK = false>
-__global__ void __launch_bounds__(64 * KS, NT <= 3 ? 2 : 1) gemm_generic_kernel(const uint8_t* __restrict__ W, int64_t row_bytes,
+__global__ void __launch_bounds__(64 * KS, NT == 2 && TYPE == kIQ3_XXS ? 3 : NT <= 3 ? 2 : 1) gemm_generic_kernel(const uint8_t* __restrict__ W, int64_t row_bytes,
                                                                int nrows, int k, const uint8_t* __restrict__ xq,
                                                                int nct, int n, void* __restrict__ y, int y_dtype) {
   constexpr int BS = block_bytes(TYPE);
