@@ -773,7 +773,18 @@ void launch_raw_type(const uint8_t* W, int64_t row_bytes, int nrows, int k, cons
   const int nct = (int)xq_col_tiles(n);
   if (nct == 1) launch_raw_t<TYPE, 1, kRawWaves, SX>(W, row_bytes, nrows, k, xq, n, y, y_dtype, split, part, cnt, stream);
   else if (nct == 2) launch_raw_t<TYPE, 2, kRawWaves, SX>(W, row_bytes, nrows, k, xq, n, y, y_dtype, split, part, cnt, stream);
-  else if (nct == 3) launch_raw_t<TYPE, 3, kRawWaves, SX>(W, row_bytes, nrows, k, xq, n, y, y_dtype, split, part, cnt, stream);
+  else if (nct == 3) {
+    // Q4_K / Q6_K unsplit on fewer than two tiles per CU: groups of two column tiles (2 + 1), at
+    // two workgroups per CU instead of one workgroup of three alone on its CU (263-354
+    // registers). Measured on the op, M = 40 / 48: Q4_K 6144 x 5120 29.0 / 28.5 -> 25.7 / 25.2
+    // us, 5120 x 6144 32.6 / 32.1 -> 30.1 / 29.5; Q6_K 6144 x 5120 34.2 / 33.7 -> 31.4 / 31.1.
+    // On 768 tiles (12288 x 5120) it lost (Q4_K 41.9 -> 43.5, Q6_K 49.8 -> 53.9 at M = 48), and
+    // IQ4_XS, whose three-tile workgroups already share a CU, lost everywhere (26.5 -> 27.1,
+    // 37.2 -> 46.3).
+    const bool pairs = TYPE != kIQ4_XS && split == 1 && (nrows + kRawRows - 1) / kRawRows < 2 * device_cus();
+    if (pairs) launch_raw_t<TYPE, 2, kRawWaves, SX>(W, row_bytes, nrows, k, xq, n, y, y_dtype, split, part, cnt, stream);
+    else launch_raw_t<TYPE, 3, kRawWaves, SX>(W, row_bytes, nrows, k, xq, n, y, y_dtype, split, part, cnt, stream);
+  }
   else launch_raw_t<TYPE, 4, kRawWaves, SX>(W, row_bytes, nrows, k, xq, n, y, y_dtype, split, part, cnt, stream);
 }
 
