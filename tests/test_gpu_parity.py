@@ -157,9 +157,15 @@ RAW_TYPES = [o.Q4_K, o.IQ4_XS, o.Q6_K]
 
 
 def _split_ws(lib, op, qt, rows, k, n, has_q8=0):
-    """Asserts that the op's plan splits K: its workspace holds more than the xq copy of X."""
+    """Asserts that the op's plan splits K: its workspace holds more than the xq copy of X. Q4_K
+    at 33-48 rows on these weights (fewer than two tiles per CU) is planned unsplit instead, in
+    groups of two column tiles: there the workspace is exactly the xq copy."""
     xq = -(-n // 16) * (k // 256) * 4608
-    assert lib.gguf_op_workspace_bytes(op, qt, rows, k, n, has_q8) > xq
+    ws = lib.gguf_op_workspace_bytes(op, qt, rows, k, n, has_q8)
+    if qt == o.Q4_K and 33 <= n <= 48:
+        assert ws == xq, (ws, xq)
+    else:
+        assert ws > xq, (ws, xq)
 
 
 @pytest.mark.parametrize("qt", RAW_TYPES, ids=lambda t: TN[t])

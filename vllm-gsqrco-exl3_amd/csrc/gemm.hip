@@ -808,6 +808,11 @@ bool raw_type(int type) { return type == kQ4_K || type == kIQ4_XS || type == kQ6
 int raw_split(int type, int64_t nrows, int64_t k, int64_t n) {
   if (!raw_type(type) || n <= 0) return 1;
   const int64_t tiles = (nrows + kRawRows - 1) / kRawRows, nb = k / kQK, cus = device_cus();
+  // Q4_K at three column tiles on fewer than two tiles per CU: unsplit, in two-column-tile groups
+  // (launch_raw_type), which beat the split (M = 40 / 48: 5120 x 17408 69.0 / 68.3 -> 64.6 / 63.5
+  // us, 2048 x 5120 14.5 / 14.3 -> 13.0 / 12.8); for Q6_K the split stays faster (5120 x 17408
+  // 80.7 against 85.1 at M = 48)
+  if (type == kQ4_K && xq_col_tiles(n) == 3 && tiles < 2 * cus) return 1;
   const int64_t groups = split_groups(tiles, n);
   if (groups >= 2 * cus) return 1;
   // time in quarter workgroup-times
