@@ -825,6 +825,10 @@ int raw_split(int type, int64_t nrows, int64_t k, int64_t n) {
     const int64_t min_blocks = 2 * t <= quarters(1) ? kRawWaves : per_wave * kRawWaves;
     if (t < best_t && nb / s >= min_blocks) best = s, best_t = t;
   }
+  // IQ4_XS at three column tiles (whose workgroups share a CU two by two) on fewer than two tiles
+  // per CU: two ways where the rule above leaves it unsplit (M = 40 / 48: 5120 x 6144 31.0 / 30.6
+  // -> 26.4 / 25.8 us, 6144 x 5120 26.5 / 26.5 -> 26.1 / 25.7); Q6_K lost with it (30.9 -> 37.6)
+  if (best == 1 && type == kIQ4_XS && split_nt(n) == 3 && tiles < 2 * cus && nb >= 2 * kRawWaves) return 2;
   return best;
 }
 
