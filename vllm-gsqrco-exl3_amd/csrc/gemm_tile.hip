@@ -320,7 +320,8 @@ int tile_split(int64_t nrows, int64_t k, int64_t n) {
 // IQ3_S in the unit layout; nrows % 16 == 0; xq: X in the xq layout (launch_quantize_xq).
 // Launch shapes measured at 17408 x 5120, 5120 x 17408 and 5120 x 5120: four waves per tile,
 // eight for one column tile on matrices of fewer than 512 tiles (more waves per tile to fill
-// the GPU); above 64 activation rows the y grid walks groups of four column tiles. split_ws: the
+// the GPU; on more tiles eight waves lost: 17408 x 5120 M = 16 26.5 -> 28.1 us, 12288 x 5120
+// 19.5 -> 20.4); above 64 activation rows the y grid walks groups of four column tiles. split_ws: the
 // split's workspace (split_k.h) when tile_split(...) > 1, its counters zeroed.
 hipError_t launch_gemm_packed_xq(const uint8_t* W, int64_t row_bytes, int nrows, int k, const uint8_t* xq, int n,
                                  void* y, int y_dtype, void* split_ws, hipStream_t stream) {
